@@ -1,0 +1,350 @@
+// extern "C" entry points of liblutmoe.so: argument validation (before any
+// HIP call, so every rejection is testable without a GPU), workspace
+// carving, and dispatch to the kernel launchers.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+
+#include <cstdio>
+
+#include "../../include/lutmoe.h"
+#include "kernels.h"
+
+namespace lutmoe_host {
+
+hipStream_t stream_of(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+int check_launch() {
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? LUTMOE_OK : LUTMOE_EHIP;
+}
+
+}  // namespace lutmoe_host
+
+using namespace lutmoe_host;
+
+namespace {
+
+thread_local char g_last_error[256] = "";
+
+void set_last_error(const char* fn, int code) {
+    if (code == LUTMOE_OK) { g_last_error[0] = 0; return; }
+    snprintf(g_last_error, sizeof(g_last_error), "%s: %s", fn, lutmoe_strerror(code));
+}
+
+inline bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+int validate_weights(const lutmoe_weights* w) {
+    if (!w || !w->codes || !w->tables) return LUTMOE_EINVAL;
+    if (w->num_experts <= 0 || w->rows <= 0 || w->cols <= 0) return LUTMOE_EINVAL;
+    switch (w->format) {
+        case LUTMOE_FMT_REF:
+            if (!w->codebook || w->block_size <= 0 || w->absmax_per_expert <= 0) return LUTMOE_EINVAL;
+            if ((int64_t)w->rows * w->cols >= (1ll << 31)) return LUTMOE_EUNSUPPORTED;
+            return LUTMOE_OK;
+        case LUTMOE_FMT_BL4:
+            if (w->cols % 64) return LUTMOE_EINVAL;
+            if (!aligned(w->codes, 16) || !aligned(w->tables, 16)) return LUTMOE_EALIGN;
+            return LUTMOE_OK;
+        case LUTMOE_FMT_NESTED:
+            if (w->cols % 64 || !w->tier_bits) return LUTMOE_EINVAL;
+            return LUTMOE_OK;
+        default:
+            return LUTMOE_EINVAL;
+    }
+}
+
+// Preconditions of the vectorised REF paths (grouped GEMV / MFMA): whole
+// 64-column blocks and absmax blocks made of whole 64-column steps.
+int validate_ref_vector(const lutmoe_weights* w) {
+    if (w->cols % 64 || w->block_size % 64) return LUTMOE_EUNSUPPORTED;
+    if (!aligned(w->codes, 16)) return LUTMOE_EALIGN;
+    return LUTMOE_OK;
+}
+
+size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
+
+struct MoeLayout {
+    size_t pair_ids, pair_w, offsets, perm, inv, active, act, y, total;
+};
+
+MoeLayout moe_layout(const lutmoe_moe_desc* d, int T, int k) {
+    const int E_tot = d->num_routed + d->num_shared;
+    const size_t P = (size_t)T * (k + d->num_shared);
+    MoeLayout L{};
+    size_t o = 0;
+    L.pair_ids = o; o = align_up(o + P * 4);
+    L.pair_w = o;   o = align_up(o + P * 4);
+    L.offsets = o;  o = align_up(o + (E_tot + 1) * 4);
+    L.perm = o;     o = align_up(o + P * 4);
+    L.inv = o;      o = align_up(o + P * 4);
+    L.active = o;   o = align_up(o + (E_tot + 1) * 4);
+    L.act = o;      o = align_up(o + P * d->inter * 2);
+    L.y = o;        o = align_up(o + P * d->hidden * 4);
+    L.total = o;
+    return L;
+}
+
+int validate_moe(const lutmoe_moe_desc* d) {
+    if (!d) return LUTMOE_EINVAL;
+    int rc = validate_weights(&d->w13);
+    if (rc) return rc;
+    rc = validate_weights(&d->w2);
+    if (rc) return rc;
+    const int H = d->hidden, I = d->inter;
+    if (H <= 0 || I <= 0 || d->num_routed <= 0 || d->num_shared < 0) return LUTMOE_EINVAL;
+    if (d->w13.rows != 2 * I || d->w13.cols != H || d->w2.rows != H || d->w2.cols != I)
+        return LUTMOE_EINVAL;
+    const int E_tot = d->num_routed + d->num_shared;
+    if (d->w13.num_experts < E_tot || d->w2.num_experts < E_tot) return LUTMOE_EINVAL;
+    if (d->w13.format != d->w2.format) return LUTMOE_EUNSUPPORTED;
+    if (d->w13.format == LUTMOE_FMT_NESTED) return LUTMOE_EUNSUPPORTED;
+    if (H % 64 || I % 64) return LUTMOE_EUNSUPPORTED;
+    if (d->w13.format == LUTMOE_FMT_REF) {
+        if ((rc = validate_ref_vector(&d->w13)) || (rc = validate_ref_vector(&d->w2))) return rc;
+    }
+    return LUTMOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* lutmoe_strerror(int code) {
+    switch (code) {
+        case LUTMOE_OK: return "ok";
+        case LUTMOE_EINVAL: return "invalid argument";
+        case LUTMOE_EUNSUPPORTED: return "unsupported shape or format combination";
+        case LUTMOE_EHIP: return "HIP runtime error";
+        case LUTMOE_EWORKSPACE: return "workspace too small";
+        case LUTMOE_EALIGN: return "pointer not aligned for vector access";
+        default: return "unknown error";
+    }
+}
+
+const char* lutmoe_version(void) { return "lutmoe 0.1.0 gfx950"; }
+
+const char* lutmoe_last_error(void) { return g_last_error; }
+
+// ------------------------------------------------------ reference-compatible
+
+int launch_blocklut_decompress(void* output, const void* indices, const void* absmax,
+                               const void* codebook, int N, int block_size, void* stream) {
+    if (N < 0 || block_size <= 0 || (N > 0 && (!output || !indices || !absmax || !codebook)))
+        return -1;
+    if (N == 0) return 0;
+    const int64_t nb = ((int64_t)N + block_size - 1) / block_size;
+    const int rc = launch_ref_dequant((uint16_t*)output, (const uint8_t*)indices,
+                                      (const uint16_t*)absmax, (const uint16_t*)codebook, N, nb,
+                                      block_size, 1, 0, 0, stream_of(stream));
+    return rc == LUTMOE_OK ? 0 : -1;
+}
+
+int launch_batch_blocklut_decompress(void* output, const void* indices, const void* absmax,
+                                     const void* codebook, int num_experts,
+                                     int elements_per_expert, int blocks_per_expert,
+                                     int block_size, void* stream) {
+    if (num_experts < 0 || elements_per_expert < 0 || blocks_per_expert <= 0 || block_size <= 0)
+        return -1;
+    if (num_experts == 0 || elements_per_expert == 0) return 0;
+    if (!output || !indices || !absmax || !codebook) return -1;
+    // The reference kernel leaves elements whose block index reaches
+    // blocks_per_expert unwritten; callers size absmax so that never happens,
+    // which is the only case accepted here.
+    if (((int64_t)elements_per_expert + block_size - 1) / block_size > blocks_per_expert) return -1;
+    const int rc = launch_ref_dequant((uint16_t*)output, (const uint8_t*)indices,
+                                      (const uint16_t*)absmax, (const uint16_t*)codebook,
+                                      elements_per_expert, blocks_per_expert, block_size,
+                                      num_experts, elements_per_expert, elements_per_expert,
+                                      stream_of(stream));
+    return rc == LUTMOE_OK ? 0 : -1;
+}
+
+void lut_moe_launch_blocklut_recover(uint16_t* out, const uint8_t* idx, const uint16_t* absmax,
+                                     const uint16_t* lut, size_t n, void* stream) {
+    int rc = LUTMOE_OK;
+    if (n == 0) { set_last_error(__func__, rc); return; }
+    if (!out || !idx || !absmax || !lut || n >= (1ull << 31)) rc = LUTMOE_EINVAL;
+    else rc = launch_ref_dequant(out, idx, absmax, lut, (int64_t)n, ((int64_t)n + 127) / 128, 128,
+                                 1, 0, 0, stream_of(stream));
+    set_last_error(__func__, rc);
+}
+
+void lut_moe_launch_unpack_4bit(uint8_t* data, size_t n, void* stream) {
+    int rc = LUTMOE_OK;
+    if (n == 0) { set_last_error(__func__, rc); return; }
+    if (!data || (n & 1)) rc = LUTMOE_EINVAL;
+    else rc = launch_unpack_4bit_inplace(data, (int64_t)n, stream_of(stream));
+    set_last_error(__func__, rc);
+}
+
+void launch_lut_gemv_kernel(const void* input, const void* indices, const void* codebook,
+                            const void* absmax, void* output, int M, int K, int num_blocks) {
+    int rc = LUTMOE_OK;
+    if (M <= 0 || K <= 0 || num_blocks <= 0 || !input || !indices || !codebook || !absmax || !output)
+        rc = LUTMOE_EINVAL;
+    else
+        rc = launch_ref_gemv((const uint16_t*)input, (const uint8_t*)indices, nullptr,
+                             (const float*)codebook, (const uint16_t*)absmax, output, M, K, 1,
+                             num_blocks, 128, LUTMOE_DTYPE_BF16, nullptr);
+    set_last_error(__func__, rc);
+}
+
+// ------------------------------------------------------------------- REF
+
+int lutmoe_ref_gemv(const void* x, const void* indices, const void* codebook, const void* absmax,
+                    void* y, int M, int K, int T, int num_blocks, int block_size, int y_dtype,
+                    void* stream) {
+    if (M <= 0 || K <= 0 || T < 0 || num_blocks <= 0 || block_size <= 0) return LUTMOE_EINVAL;
+    if (y_dtype != LUTMOE_DTYPE_BF16 && y_dtype != LUTMOE_DTYPE_F32) return LUTMOE_EINVAL;
+    if (!x || !indices || !codebook || !absmax || !y) return LUTMOE_EINVAL;
+    if ((int64_t)M * K >= (1ll << 31)) return LUTMOE_EUNSUPPORTED;
+    if (T == 0) return LUTMOE_OK;
+    return launch_ref_gemv((const uint16_t*)x, (const uint8_t*)indices, (const uint16_t*)codebook,
+                           nullptr, (const uint16_t*)absmax, y, M, K, T, num_blocks, block_size,
+                           y_dtype, stream_of(stream));
+}
+
+int lutmoe_unpack_6bit(const uint8_t* packed, uint8_t* out, int64_t n, void* stream) {
+    if (n < 0 || (n % 4)) return LUTMOE_EINVAL;
+    if (n == 0) return LUTMOE_OK;
+    if (!packed || !out) return LUTMOE_EINVAL;
+    return launch_unpack_6bit(packed, out, n, stream_of(stream));
+}
+
+// ---------------------------------------------------------------- generic
+
+int lutmoe_dequant(const lutmoe_weights* w, int e0, int ne, void* out, void* stream) {
+    int rc = validate_weights(w);
+    if (rc) return rc;
+    if (!out || e0 < 0 || ne < 0 || e0 + ne > w->num_experts) return LUTMOE_EINVAL;
+    if (ne == 0) return LUTMOE_OK;
+    const int64_t n = (int64_t)w->rows * w->cols;
+    switch (w->format) {
+        case LUTMOE_FMT_REF:
+            return launch_ref_dequant((uint16_t*)out, (const uint8_t*)w->codes + e0 * n,
+                                      (const uint16_t*)w->tables + e0 * w->absmax_per_expert,
+                                      (const uint16_t*)w->codebook, n, w->absmax_per_expert,
+                                      w->block_size, ne, n, n, stream_of(stream));
+        case LUTMOE_FMT_BL4: {
+            if (!aligned(out, 16)) return LUTMOE_EALIGN;
+            const int64_t nbl = n / 64;
+            return launch_bl4_dequant((uint16_t*)out, (const uint8_t*)w->codes + e0 * (n / 2),
+                                      (const uint16_t*)w->tables + e0 * (n / 4), ne * nbl,
+                                      stream_of(stream));
+        }
+        default:
+            if (!aligned(out, 16)) return LUTMOE_EALIGN;
+            return launch_nested_dequant((uint16_t*)out, w, e0, ne, stream_of(stream));
+    }
+}
+
+int lutmoe_gemv(const lutmoe_weights* w, int expert, const void* x, int T, void* y, int y_dtype,
+                void* stream) {
+    int rc = validate_weights(w);
+    if (rc) return rc;
+    if (!x || !y || T < 0 || expert < 0 || expert >= w->num_experts) return LUTMOE_EINVAL;
+    if (y_dtype != LUTMOE_DTYPE_BF16 && y_dtype != LUTMOE_DTYPE_F32) return LUTMOE_EINVAL;
+    if (!aligned(x, 16) || w->cols % 8) return LUTMOE_EALIGN;
+    if (T == 0) return LUTMOE_OK;
+    if (w->format == LUTMOE_FMT_NESTED)
+        return launch_nested_gemv(w, expert, (const uint16_t*)x, T, y, y_dtype, stream_of(stream));
+    if (w->format == LUTMOE_FMT_REF && (rc = validate_ref_vector(w))) return rc;
+    return launch_bl4_gemv(w, expert, (const uint16_t*)x, T, y, y_dtype, stream_of(stream));
+}
+
+int lutmoe_bl4_tables_from_f16(const uint16_t* f16, uint16_t* bf16, int64_t n, void* stream) {
+    if (n < 0) return LUTMOE_EINVAL;
+    if (n == 0) return LUTMOE_OK;
+    if (!f16 || !bf16) return LUTMOE_EINVAL;
+    if (!aligned(f16, 16) || !aligned(bf16, 16)) return LUTMOE_EALIGN;
+    return launch_f16_to_bf16(f16, bf16, n, stream_of(stream));
+}
+
+// ---------------------------------------------------------------- routing
+
+int lutmoe_route_topk(const float* logits, int T, int E, int k, int renormalize, float scaling,
+                      float* topk_w, int32_t* topk_ids, void* stream) {
+    if (T < 0 || E <= 0 || k <= 0 || k > E || k > 16) return LUTMOE_EINVAL;
+    if (T == 0) return LUTMOE_OK;
+    if (!logits || !topk_w || !topk_ids) return LUTMOE_EINVAL;
+    return launch_route_topk(logits, T, E, k, renormalize, scaling, topk_w, topk_ids,
+                             stream_of(stream));
+}
+
+int lutmoe_permute(const int32_t* topk_ids, int T, int k, int E, int32_t* offsets, int32_t* perm,
+                   int32_t* inv, int32_t* active, void* stream) {
+    if (T < 0 || k <= 0 || E <= 0 || E > 4096) return LUTMOE_EINVAL;
+    if (!topk_ids || !offsets || !perm || !inv || !active) return LUTMOE_EINVAL;
+    if ((int64_t)T * k >= (1ll << 31)) return LUTMOE_EUNSUPPORTED;
+    return launch_permute(topk_ids, T, k, E, offsets, perm, inv, active, stream_of(stream));
+}
+
+// -------------------------------------------------------------- MoE layer
+
+size_t lutmoe_moe_workspace_size(const lutmoe_moe_desc* d, int T, int k) {
+    if (!d || T < 0 || k <= 0) return 0;
+    return moe_layout(d, T, k).total;
+}
+
+int lutmoe_moe_forward(const lutmoe_moe_desc* d, const void* x, const float* topk_w,
+                       const int32_t* topk_ids, int T, int k, void* out, int out_dtype,
+                       void* workspace, size_t ws_bytes, int force_path, void* stream) {
+    int rc = validate_moe(d);
+    if (rc) return rc;
+    if (T < 0 || k <= 0 || k > d->num_routed || k + d->num_shared > 16) return LUTMOE_EINVAL;
+    if (out_dtype != LUTMOE_DTYPE_BF16 && out_dtype != LUTMOE_DTYPE_F32) return LUTMOE_EINVAL;
+    if (force_path < 0 || force_path > 2) return LUTMOE_EINVAL;
+    if (T == 0) return LUTMOE_OK;
+    if (!x || !topk_w || !topk_ids || !out || !workspace) return LUTMOE_EINVAL;
+    if (!aligned(x, 16) || !aligned(out, 16) || !aligned(workspace, 256)) return LUTMOE_EALIGN;
+    const MoeLayout L = moe_layout(d, T, k);
+    if (ws_bytes < L.total) return LUTMOE_EWORKSPACE;
+    const int S = d->num_shared, E = d->num_routed, E_tot = E + S, ke = k + S;
+    const int64_t P = (int64_t)T * ke;
+    if (P >= (1ll << 31) / (d->hidden > d->inter ? d->hidden : d->inter)) return LUTMOE_EUNSUPPORTED;
+    const bool lds_ok = P * 8 * 4 <= 48 * 1024;
+    bool gemv = force_path == 1 || (force_path == 0 && T <= 32 && lds_ok);
+    if (gemv && !lds_ok) return LUTMOE_EUNSUPPORTED;
+
+    char* ws = (char*)workspace;
+    int32_t* pair_ids = (int32_t*)(ws + L.pair_ids);
+    float* pair_w = (float*)(ws + L.pair_w);
+    MoeRouting r;
+    r.offsets = (int32_t*)(ws + L.offsets);
+    r.perm = (int32_t*)(ws + L.perm);
+    r.inv = (int32_t*)(ws + L.inv);
+    r.active = (int32_t*)(ws + L.active);
+    r.pair_w = pair_w;
+    r.T = T;
+    r.k_eff = ke;
+    r.num_experts_total = E_tot;
+    uint16_t* act = (uint16_t*)(ws + L.act);
+    float* y = (float*)(ws + L.y);
+    hipStream_t s = stream_of(stream);
+
+    if ((rc = launch_build_pairs(topk_ids, topk_w, T, k, E, S, pair_ids, pair_w, s))) return rc;
+    if ((rc = launch_permute(pair_ids, T, ke, E_tot, (int32_t*)r.offsets, (int32_t*)r.perm,
+                             (int32_t*)r.inv, (int32_t*)r.active, s)))
+        return rc;
+    const int max_active = (int)(P < E_tot ? P : E_tot);
+    if (gemv) {
+        if ((rc = launch_decode_gate_up(d, (const uint16_t*)x, r, act, max_active, s))) return rc;
+        return launch_decode_down_combine(d, act, r, out, out_dtype, max_active, s);
+    }
+    if ((rc = launch_prefill_gate_up(d, (const uint16_t*)x, r, act, (int)P, s))) return rc;
+    if ((rc = launch_prefill_down(d, act, r, y, (int)P, s))) return rc;
+    return launch_combine(y, r.inv, T, ke, d->hidden, out, out_dtype, s);
+}
+
+// --------------------------------------------------------------- encoders
+
+int lutmoe_bl4_encode(const float* w, int64_t nblocks, int n_iter, uint8_t* codes,
+                      uint16_t* tables_f16, void* stream) {
+    if (nblocks < 0 || n_iter < 1 || n_iter > 1000) return LUTMOE_EINVAL;
+    if (nblocks == 0) return LUTMOE_OK;
+    if (!w || !codes || !tables_f16) return LUTMOE_EINVAL;
+    return launch_bl4_encode(w, nblocks, n_iter, codes, tables_f16, stream_of(stream));
+}
+
+}  // extern "C"

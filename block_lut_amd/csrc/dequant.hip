@@ -1,0 +1,263 @@
+// Dequantisation and code-unpack kernels (memory-bound byte work).
+//
+//  ref_dequant   : REF codes -> bf16, out = bf16(f32(cb[c]) * f32(absmax[blk]))
+//                  (csrc/kernels/tensor_recover.cu:101-142 rule; batched over
+//                  experts like lut_decompress_kernel.cu:87-120).
+//  bl4_dequant   : BL4 codes -> bf16 through per-block bf16 tables staged in LDS.
+//  nested_dequant: NestedLUT tier-b bit-plane sections -> bf16.
+//  unpack_4bit   : in-place low-nibble unpack (tensor_recover.cu:161-192),
+//                  done as a race-free halving sequence instead of the
+//                  reference's copy-to-upper-half + expand.
+//  unpack_6bit   : the 6-bit tier unpack the reference runs on the CPU
+//                  (csrc/tensor_engine/tensor_engine.cpp:535-548).
+#include "common.h"
+#include "kernels.h"
+
+using namespace lutmoe;
+
+namespace {
+
+constexpr int kRefVec = 16;   // codes per thread in ref_dequant
+
+__global__ __launch_bounds__(256) void ref_dequant_kernel(
+    uint16_t* __restrict__ out, const uint8_t* __restrict__ idx,
+    const uint16_t* __restrict__ absmax, const uint16_t* __restrict__ cb, int n, int nb,
+    int bs, int64_t out_stride, int64_t idx_stride, int vec_ok) {
+    __shared__ float s_cb[256];
+    s_cb[threadIdx.x] = bf16_to_f32(cb[threadIdx.x]);
+    __syncthreads();
+    const int e = blockIdx.y;
+    const uint8_t* ip = idx + e * idx_stride;
+    const uint16_t* ap = absmax + (int64_t)e * nb;
+    uint16_t* op = out + e * out_stride;
+    const int i0 = (blockIdx.x * 256 + threadIdx.x) * kRefVec;
+    if (i0 >= n) return;
+    if (vec_ok && i0 + kRefVec <= n) {
+        const uint4 c = *reinterpret_cast<const uint4*>(ip + i0);
+        const uint32_t cw[4] = {c.x, c.y, c.z, c.w};
+        uint32_t o[8];
+        int b = i0 / bs;
+        int next = (b + 1) * bs;
+        float am = bf16_to_f32(ap[min(b, nb - 1)]);
+#pragma unroll
+        for (int j = 0; j < kRefVec; ++j) {
+            if (i0 + j == next) {            // crossed into the next absmax block
+                ++b;
+                next += bs;
+                am = bf16_to_f32(ap[min(b, nb - 1)]);
+            }
+            const uint32_t code = (cw[j >> 2] >> (8 * (j & 3))) & 0xffu;
+            const uint32_t v = f32_to_bf16(s_cb[code] * am);
+            if (j & 1) o[j >> 1] |= v << 16; else o[j >> 1] = v;
+        }
+        uint4* dst = reinterpret_cast<uint4*>(op + i0);
+        dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
+        dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
+    } else {
+        const int end = min(n, i0 + kRefVec);
+        for (int i = i0; i < end; ++i) {
+            const int b = min(i / bs, nb - 1);
+            op[i] = (uint16_t)f32_to_bf16(s_cb[ip[i]] * bf16_to_f32(ap[b]));
+        }
+    }
+}
+
+// 256 threads handle 128 blocks of 64 weights; tables staged in LDS.
+__global__ __launch_bounds__(256) void bl4_dequant_kernel(
+    uint16_t* __restrict__ out, const uint8_t* __restrict__ codes,
+    const uint16_t* __restrict__ tables, int64_t nblocks) {
+    __shared__ uint16_t s_tab[128 * 16];
+    const int64_t b0 = (int64_t)blockIdx.x * 128;
+    const int t = threadIdx.x;
+    const int64_t nloc = min((int64_t)128, nblocks - b0);
+    // table load: thread t loads entries [8t, 8t+8) of the CTA's 128*16 entries
+    if (t < nloc * 2) {
+        *reinterpret_cast<uint4*>(&s_tab[t * 8]) =
+            *reinterpret_cast<const uint4*>(tables + b0 * 16 + t * 8);
+    }
+    __syncthreads();
+    const int lb = t >> 1, h = t & 1;
+    if (lb >= nloc) return;
+    const uint4 c = *reinterpret_cast<const uint4*>(codes + (b0 + lb) * 32 + h * 16);
+    const uint32_t cw[4] = {c.x, c.y, c.z, c.w};
+    const uint16_t* tab = &s_tab[lb * 16];
+    uint32_t o[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const uint32_t byte = (cw[j >> 2] >> (8 * (j & 3))) & 0xffu;
+        o[j] = (uint32_t)tab[byte & 15u] | ((uint32_t)tab[byte >> 4] << 16);
+    }
+    uint4* dst = reinterpret_cast<uint4*>(out + (b0 + lb) * 64 + h * 32);
+    dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
+    dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
+    dst[2] = make_uint4(o[8], o[9], o[10], o[11]);
+    dst[3] = make_uint4(o[12], o[13], o[14], o[15]);
+}
+
+// Nested: thread handles 32 consecutive weights (half a 64-block).
+__global__ __launch_bounds__(256) void nested_dequant_kernel(
+    uint16_t* __restrict__ out, const uint8_t* const* __restrict__ code_ptrs,
+    const uint16_t* const* __restrict__ table_ptrs, const int8_t* __restrict__ bits,
+    int e0, int64_t n_per_expert) {
+    const int e = e0 + blockIdx.y;
+    const int b = bits[e];
+    const uint8_t* p01 = code_ptrs[e];
+    const uint8_t* p2 = p01 + n_per_expert / 4;
+    const uint8_t* p3 = p2 + n_per_expert / 8;
+    const uint16_t* tab = table_ptrs[e];
+    const int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 32;
+    if (i0 >= n_per_expert) return;
+    const uint2 q01 = *reinterpret_cast<const uint2*>(p01 + i0 / 4);
+    const uint64_t f01 = (uint64_t)q01.x | ((uint64_t)q01.y << 32);
+    const uint32_t f2 = b >= 3 ? *reinterpret_cast<const uint32_t*>(p2 + i0 / 8) : 0u;
+    const uint32_t f3 = b >= 4 ? *reinterpret_cast<const uint32_t*>(p3 + i0 / 8) : 0u;
+    const uint16_t* t = tab + (i0 / kBlockBL) * (1 << b);
+    uint32_t o[16];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+        const uint32_t c = (uint32_t)((f01 >> (2 * j)) & 3u) | (((f2 >> j) & 1u) << 2) |
+                           (((f3 >> j) & 1u) << 3);
+        const uint32_t v = t[c];
+        if (j & 1) o[j >> 1] |= v << 16; else o[j >> 1] = v;
+    }
+    uint4* dst = reinterpret_cast<uint4*>(out + (int64_t)blockIdx.y * n_per_expert + i0);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) dst[q] = make_uint4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]);
+}
+
+__global__ __launch_bounds__(256) void f16_to_bf16_kernel(const uint16_t* __restrict__ in,
+                                                          uint16_t* __restrict__ out, int64_t n) {
+    const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+    if (i + 8 <= n) {
+        const uint4 v = *reinterpret_cast<const uint4*>(in + i);
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+        uint32_t o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            o[j] = f32_to_bf16(f16_to_f32(w[j] & 0xffffu)) |
+                   (f32_to_bf16(f16_to_f32(w[j] >> 16)) << 16);
+        *reinterpret_cast<uint4*>(out + i) = make_uint4(o[0], o[1], o[2], o[3]);
+    } else {
+        for (int64_t j = i; j < n; ++j) out[j] = (uint16_t)f32_to_bf16(f16_to_f32(in[j]));
+    }
+}
+
+// out[2i] = src[i] & 15, out[2i+1] = src[i] >> 4 for i in [0, nsrc); src and
+// dst ranges are disjoint.
+__global__ __launch_bounds__(256) void expand_nibbles_kernel(uint8_t* __restrict__ dst,
+                                                             const uint8_t* __restrict__ src,
+                                                             int64_t nsrc) {
+    const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    const int64_t end = min(nsrc, i + 4);
+    for (int64_t j = i; j < end; ++j) {
+        const uint8_t p = src[j];
+        dst[2 * j] = p & 0x0f;
+        dst[2 * j + 1] = p >> 4;
+    }
+}
+
+constexpr int kUnpackBase = 8192;   // outputs finished by one CTA
+
+// Final in-place step on a region of m <= kUnpackBase outputs: every packed
+// byte is read before the CTA barrier, every output written after it.
+__global__ __launch_bounds__(1024) void unpack_base_kernel(uint8_t* data, int m) {
+    uint8_t v[kUnpackBase / 2 / 1024];
+    const int np = m / 2;
+#pragma unroll
+    for (int q = 0; q < kUnpackBase / 2 / 1024; ++q) {
+        const int i = threadIdx.x + q * 1024;
+        v[q] = i < np ? data[i] : 0;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < kUnpackBase / 2 / 1024; ++q) {
+        const int i = threadIdx.x + q * 1024;
+        if (i < np) {
+            data[2 * i] = v[q] & 0x0f;
+            data[2 * i + 1] = v[q] >> 4;
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void unpack_6bit_kernel(const uint8_t* __restrict__ packed,
+                                                          uint8_t* __restrict__ out, int64_t n) {
+    const int64_t e0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 16;
+    if (e0 >= n) return;
+    const int64_t end = min(n, e0 + 16);
+    const uint8_t* low = packed;
+    const uint8_t* mid = packed + n / 2;
+    for (int64_t e = e0; e < end; ++e) {
+        const uint8_t lb = low[e >> 1];
+        const uint8_t nib = (e & 1) ? (lb >> 4) : (lb & 0x0f);
+        const uint8_t m2 = (mid[e >> 2] >> (2 * (e & 3))) & 0x03;
+        out[e] = nib | (m2 << 4);
+    }
+}
+
+inline int grid1(int64_t work, int per_cta) { return (int)((work + per_cta - 1) / per_cta); }
+
+}  // namespace
+
+namespace lutmoe_host {
+
+int launch_ref_dequant(uint16_t* out, const uint8_t* idx, const uint16_t* absmax,
+                       const uint16_t* cb, int64_t n_per_expert, int64_t nb_per_expert,
+                       int block_size, int num_experts, int64_t out_stride,
+                       int64_t idx_stride, hipStream_t s) {
+    const int vec_ok = ((uintptr_t)idx % 16 == 0) && ((uintptr_t)out % 16 == 0) &&
+                       (idx_stride % 16 == 0) && (out_stride % 8 == 0);
+    dim3 grid(grid1(n_per_expert, 256 * kRefVec), num_experts);
+    hipLaunchKernelGGL(ref_dequant_kernel, grid, dim3(256), 0, s, out, idx, absmax, cb,
+                       (int)n_per_expert, (int)nb_per_expert, block_size, out_stride,
+                       idx_stride, vec_ok);
+    return check_launch();
+}
+
+int launch_bl4_dequant(uint16_t* out, const uint8_t* codes, const uint16_t* tables,
+                       int64_t nblocks, hipStream_t s) {
+    hipLaunchKernelGGL(bl4_dequant_kernel, dim3(grid1(nblocks, 128)), dim3(256), 0, s, out,
+                       codes, tables, nblocks);
+    return check_launch();
+}
+
+int launch_nested_dequant(uint16_t* out, const lutmoe_weights* w, int e0, int ne,
+                          hipStream_t s) {
+    const int64_t n = (int64_t)w->rows * w->cols;
+    dim3 grid(grid1(n, 256 * 32), ne);
+    hipLaunchKernelGGL(nested_dequant_kernel, grid, dim3(256), 0, s, out,
+                       (const uint8_t* const*)w->codes, (const uint16_t* const*)w->tables,
+                       w->tier_bits, e0, n);
+    return check_launch();
+}
+
+int launch_f16_to_bf16(const uint16_t* in, uint16_t* out, int64_t n, hipStream_t s) {
+    hipLaunchKernelGGL(f16_to_bf16_kernel, dim3(grid1(n, 256 * 8)), dim3(256), 0, s, in, out,
+                       n);
+    return check_launch();
+}
+
+int launch_unpack_4bit_inplace(uint8_t* data, int64_t n, hipStream_t s) {
+    // Region [0, m) holds its packed bytes in [0, m/2).  Peel the upper
+    // outputs [h, m) from the packed bytes [h/2, m/2) (disjoint from the
+    // writes since h >= m/2), then continue on [0, h).
+    int64_t m = n;
+    while (m > kUnpackBase) {
+        const int64_t h = ((m / 2) + 1) & ~(int64_t)1;
+        const int64_t nsrc = m / 2 - h / 2;
+        hipLaunchKernelGGL(expand_nibbles_kernel, dim3(grid1(nsrc, 1024)), dim3(256), 0, s,
+                           data + h, data + h / 2, nsrc);
+        const int rc = check_launch();
+        if (rc) return rc;
+        m = h;
+    }
+    hipLaunchKernelGGL(unpack_base_kernel, dim3(1), dim3(1024), 0, s, data, (int)m);
+    return check_launch();
+}
+
+int launch_unpack_6bit(const uint8_t* packed, uint8_t* out, int64_t n, hipStream_t s) {
+    hipLaunchKernelGGL(unpack_6bit_kernel, dim3(grid1(n, 256 * 16)), dim3(256), 0, s, packed,
+                       out, n);
+    return check_launch();
+}
+
+}  // namespace lutmoe_host

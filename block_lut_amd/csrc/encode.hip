@@ -1,0 +1,186 @@
+// BL4 encoder on the GPU: per-64-weight-block k-means (k = 16), one
+// wavefront per block, lane j holding weight j.
+//
+// The procedure is LUTQuantizer._train_kmeans (vllm_lut/quantizer.py:120-178)
+// applied per block: Lloyd iterations with argmin |x - c| (first minimum),
+// mean update leaving empty clusters unchanged, final sort, cast to the
+// storage dtype (fp16), codes re-assigned against the stored codebook
+// (quantize(), quantizer.py:292-296).  Initialisation is a binary-splitting
+// tree (4-means from the quantile start sorted[16i+8], then every cell split
+// by 2-means twice) instead of a random pick, so CPU and GPU agree exactly.
+// Cluster sums are the xor-butterfly over the 64 lanes (non-members add +0)
+// and every lane divides the same uniform sum by the same count, so the
+// result is bit-identical to the CPU restatement run in the same order.
+#include "common.h"
+#include "kernels.h"
+
+using namespace lutmoe;
+
+namespace {
+
+__device__ __forceinline__ float butterfly(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, kWave);
+    return v;
+}
+
+template <int K>
+__device__ __forceinline__ int argmin_abs(float x, const float (&c)[K]) {
+    int best = 0;
+    float bd = fabsf(x - c[0]);
+#pragma unroll
+    for (int i = 1; i < K; ++i) {
+        const float dd = fabsf(x - c[i]);
+        if (dd < bd) { bd = dd; best = i; }
+    }
+    return best;
+}
+
+// Lloyd on the member lanes; c[] is uniform across the wave.
+template <int K>
+__device__ void lloyd(float x, bool member, float (&c)[K], int n_iter, int& assign) {
+    assign = -1;
+    for (int it = 0; it < n_iter; ++it) {
+        const int a = member ? argmin_abs<K>(x, c) : -1;
+        const bool changed = member && a != assign;
+        assign = a;
+        if (!__any(changed)) break;
+#pragma unroll
+        for (int i = 0; i < K; ++i) {
+            const bool in = member && assign == i;
+            const float s = butterfly(in ? x : 0.0f);
+            const int cnt = __popcll(__ballot(in));
+            if (cnt) c[i] = s / (float)cnt;
+        }
+    }
+}
+
+template <int K>
+__device__ __forceinline__ void sort_small(float (&c)[K]) {
+#pragma unroll
+    for (int i = 1; i < K; ++i) {
+        const float v = c[i];
+        int j = i - 1;
+        while (j >= 0 && c[j] > v) { c[j + 1] = c[j]; --j; }
+        c[j + 1] = v;
+    }
+}
+
+__device__ void split2(float x, bool member, float parent, int n_iter, float (&ch)[2]) {
+    const bool any = __any(member);
+    if (!any) { ch[0] = ch[1] = parent; return; }
+    float lo = member ? x : INFINITY, hi = member ? x : -INFINITY;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        lo = fminf(lo, __shfl_xor(lo, off, kWave));
+        hi = fmaxf(hi, __shfl_xor(hi, off, kWave));
+    }
+    ch[0] = lo;
+    ch[1] = hi;
+    int a;
+    lloyd<2>(x, member, ch, n_iter, a);
+    if (ch[1] < ch[0]) { const float t = ch[0]; ch[0] = ch[1]; ch[1] = t; }
+}
+
+template <int K>
+__device__ __forceinline__ float pick(const float (&c)[K], int i) {
+    float v = c[0];
+#pragma unroll
+    for (int q = 1; q < K; ++q) v = (i == q) ? c[q] : v;
+    return v;
+}
+
+__global__ __launch_bounds__(256) void bl4_encode_kernel(const float* __restrict__ w,
+                                                         int64_t nblocks, int n_iter,
+                                                         uint8_t* __restrict__ codes,
+                                                         uint16_t* __restrict__ tables) {
+    __shared__ float s_x[4][64];
+    __shared__ float s_sorted[4][64];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    for (int64_t b = (int64_t)blockIdx.x * 4 + wv; b < nblocks; b += (int64_t)gridDim.x * 4) {
+        const float x = w[b * 64 + lane];
+        s_x[wv][lane] = x;
+        wave_lds_sync();
+        int r = 0;
+        for (int i = 0; i < 64; ++i) {
+            const float xi = s_x[wv][i];
+            r += (xi < x) || (xi == x && i < lane);
+        }
+        s_sorted[wv][r] = x;
+        wave_lds_sync();
+        float c2[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) c2[i] = s_sorted[wv][16 * i + 8];
+        wave_lds_sync();
+        int a2;
+        lloyd<4>(x, true, c2, n_iter, a2);
+        // order level-2 cells by centroid (stable insertion order of indices)
+        int order[4] = {0, 1, 2, 3};
+#pragma unroll
+        for (int i = 1; i < 4; ++i) {
+            const int v = order[i];
+            int j = i - 1;
+            while (j >= 0 && pick(c2, order[j]) > pick(c2, v)) { order[j + 1] = order[j]; --j; }
+            order[j + 1] = v;
+        }
+        float c2s[4];
+        int rank = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            c2s[i] = pick(c2, order[i]);
+            rank = (order[i] == a2) ? i : rank;
+        }
+        a2 = rank;
+        float c3[8];
+#pragma unroll
+        for (int j2 = 0; j2 < 4; ++j2) {
+            float ch[2];
+            split2(x, a2 == j2, c2s[j2], n_iter, ch);
+            c3[j2] = ch[0];
+            c3[j2 | 4] = ch[1];
+        }
+        int cell3;
+        {
+            const float two[2] = {pick(c3, a2), pick(c3, a2 | 4)};
+            cell3 = a2 | (argmin_abs<2>(x, two) << 2);
+        }
+        float c[16];
+#pragma unroll
+        for (int k3 = 0; k3 < 8; ++k3) {
+            float ch[2];
+            split2(x, cell3 == k3, c3[k3], n_iter, ch);
+            c[k3] = ch[0];
+            c[k3 | 8] = ch[1];
+        }
+        int a16;
+        lloyd<16>(x, true, c, n_iter, a16);
+        sort_small<16>(c);
+        float cf[16];
+        uint32_t h_mine = 0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const uint32_t h = f32_to_f16(c[i]);
+            cf[i] = f16_to_f32(h);
+            if (lane == i) h_mine = h;
+        }
+        const uint32_t code = (uint32_t)argmin_abs<16>(x, cf);
+        const uint32_t nb = (uint32_t)__shfl_down((int)code, 1, kWave);
+        if ((lane & 1) == 0) codes[b * 32 + (lane >> 1)] = (uint8_t)(code | (nb << 4));
+        if (lane < 16) tables[b * 16 + lane] = (uint16_t)h_mine;
+    }
+}
+
+}  // namespace
+
+namespace lutmoe_host {
+
+int launch_bl4_encode(const float* w, int64_t nblocks, int n_iter, uint8_t* codes,
+                      uint16_t* tables, hipStream_t s) {
+    int64_t ctas = (nblocks + 3) / 4;
+    if (ctas > 65536) ctas = 65536;
+    hipLaunchKernelGGL(bl4_encode_kernel, dim3((unsigned)ctas), dim3(256), 0, s, w, nblocks,
+                       n_iter, codes, tables);
+    return check_launch();
+}
+
+}  // namespace lutmoe_host

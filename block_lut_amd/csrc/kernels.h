@@ -1,0 +1,71 @@
+// Launchers of the gfx950 kernels (one translation unit per kernel family).
+// Arguments are validated by api.cpp before any of these is called.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/lutmoe.h"
+
+namespace lutmoe_host {
+
+// dequant.hip
+int launch_ref_dequant(uint16_t* out, const uint8_t* idx, const uint16_t* absmax,
+                       const uint16_t* cb, int64_t n_per_expert, int64_t nb_per_expert,
+                       int block_size, int num_experts, int64_t out_stride,
+                       int64_t idx_stride, hipStream_t s);
+int launch_bl4_dequant(uint16_t* out, const uint8_t* codes, const uint16_t* tables,
+                       int64_t nblocks, hipStream_t s);
+int launch_nested_dequant(uint16_t* out, const lutmoe_weights* w, int e0, int ne,
+                          hipStream_t s);
+int launch_f16_to_bf16(const uint16_t* in, uint16_t* out, int64_t n, hipStream_t s);
+int launch_unpack_4bit_inplace(uint8_t* data, int64_t n, hipStream_t s);
+int launch_unpack_6bit(const uint8_t* packed, uint8_t* out, int64_t n, hipStream_t s);
+
+// gemv.hip
+int launch_ref_gemv(const uint16_t* x, const uint8_t* idx, const uint16_t* cb_bf16,
+                    const float* cb_f32, const uint16_t* absmax, void* y, int M, int K,
+                    int T, int num_blocks, int block_size, int y_dtype, hipStream_t s);
+int launch_bl4_gemv(const lutmoe_weights* w, int expert, const uint16_t* x, int T, void* y,
+                    int y_dtype, hipStream_t s);
+int launch_nested_gemv(const lutmoe_weights* w, int expert, const uint16_t* x, int T,
+                       void* y, int y_dtype, hipStream_t s);
+
+// Decode MoE stages (grouped LUT-GEMV).  Pairs are (token, slot) with
+// k_eff = k + num_shared slots per token; positions are permuted pairs.
+struct MoeRouting {
+    const int32_t* offsets;   // [E_tot+1]
+    const int32_t* perm;      // [P] pair index at each position
+    const int32_t* inv;       // [P] position of each pair
+    const int32_t* active;    // [1 + E_tot]: count, then active expert ids
+    const float* pair_w;      // [P] routing weight of each pair (by pair index)
+    int T;
+    int k_eff;
+    int num_experts_total;    // E + S
+};
+int launch_decode_gate_up(const lutmoe_moe_desc* d, const uint16_t* x, const MoeRouting& r,
+                          uint16_t* act, int max_active, hipStream_t s);
+int launch_decode_down_combine(const lutmoe_moe_desc* d, const uint16_t* act,
+                               const MoeRouting& r, void* out, int out_dtype,
+                               int max_active, hipStream_t s);
+
+// route.hip
+int launch_route_topk(const float* logits, int T, int E, int k, int renorm, float scaling,
+                      float* w, int32_t* ids, hipStream_t s);
+int launch_build_pairs(const int32_t* topk_ids, const float* topk_w, int T, int k,
+                       int E, int S, int32_t* pair_ids, float* pair_w, hipStream_t s);
+int launch_permute(const int32_t* pair_ids, int T, int k_eff, int E_tot, int32_t* offsets,
+                   int32_t* perm, int32_t* inv, int32_t* active, hipStream_t s);
+int launch_combine(const float* y_pos, const int32_t* inv, int T, int k_eff, int H,
+                   void* out, int out_dtype, hipStream_t s);
+
+// gemm.hip (prefill, MFMA)
+int launch_prefill_gate_up(const lutmoe_moe_desc* d, const uint16_t* x, const MoeRouting& r,
+                           uint16_t* act, int P, hipStream_t s);
+int launch_prefill_down(const lutmoe_moe_desc* d, const uint16_t* act, const MoeRouting& r,
+                        float* y_pos, int P, hipStream_t s);
+
+// encode.hip
+int launch_bl4_encode(const float* w, int64_t nblocks, int n_iter, uint8_t* codes,
+                      uint16_t* tables, hipStream_t s);
+
+}  // namespace lutmoe_host

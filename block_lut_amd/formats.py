@@ -1,0 +1,222 @@
+"""Device-resident LUT weight stacks and their C-ABI descriptors.
+
+REF  (the reference's format, vllm_lut/quant_method.py:117-163):
+     codes uint8 [E, M, K], absmax bf16 [E, nb] (nb = ceil(M*K/block_size)),
+     codebook bf16 [256].
+BL4  (4-bit, per-64-block codebooks): codes uint8 [E, M, K/2] (even element in
+     the low nibble), tables bf16 [E, M, K/64, 16] holding the dequantised
+     entries bf16(fp16 codebook) -- the fp16 codebooks are the wire format,
+     converted once by ``BL4Stack.from_fp16``.
+NL   (NestedLUT 2/3/4-bit tiers): per expert, bit-plane sections
+     [p01 | p2 | p3] (a tier-b expert keeps the first 2, 3 or all of them) and
+     a bf16 table [M, K/64, 2^b].
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import List, Optional
+
+import torch
+
+from . import _native as N
+
+
+def _dev(t: torch.Tensor, dtype: torch.dtype, name: str) -> torch.Tensor:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device (cuda/HIP) tensor")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    return t
+
+
+class WeightStack:
+    format: int
+    num_experts: int
+    rows: int
+    cols: int
+
+    def desc(self) -> N.lutmoe_weights:
+        raise NotImplementedError
+
+    def hbm_bytes_per_expert(self) -> int:
+        raise NotImplementedError
+
+
+class RefStack(WeightStack):
+    """The reference's uint8 + bf16 absmax + global bf16[256] codebook stack."""
+
+    format = N.FMT_REF
+
+    def __init__(self, codes: torch.Tensor, absmax: torch.Tensor, codebook: torch.Tensor,
+                 block_size: int = 128):
+        if codes.dim() == 2:
+            codes = codes.unsqueeze(0)
+        if absmax.dim() == 1:
+            absmax = absmax.unsqueeze(0)
+        self.codes = _dev(codes, torch.uint8, "codes")
+        self.absmax = _dev(absmax, torch.bfloat16, "absmax")
+        self.codebook = _dev(codebook, torch.bfloat16, "codebook")
+        if self.codebook.numel() != 256:
+            raise ValueError("REF codebook must have 256 entries")
+        self.num_experts, self.rows, self.cols = self.codes.shape
+        self.block_size = int(block_size)
+        if self.absmax.shape[0] != self.num_experts:
+            raise ValueError("absmax must have one row per expert")
+        need = math.ceil(self.rows * self.cols / self.block_size)
+        if self.absmax.shape[1] < need:
+            raise ValueError(f"absmax has {self.absmax.shape[1]} blocks per expert, need {need}")
+
+    def desc(self) -> N.lutmoe_weights:
+        d = N.lutmoe_weights()
+        d.format = N.FMT_REF
+        d.num_experts, d.rows, d.cols = self.num_experts, self.rows, self.cols
+        d.codes = self.codes.data_ptr()
+        d.tables = self.absmax.data_ptr()
+        d.codebook = self.codebook.data_ptr()
+        d.tier_bits = None
+        d.absmax_per_expert = self.absmax.shape[1]
+        d.block_size = self.block_size
+        return d
+
+    def hbm_bytes_per_expert(self) -> int:
+        return self.rows * self.cols + 2 * self.absmax.shape[1]
+
+
+class BL4Stack(WeightStack):
+    """4-bit codes + per-64-block bf16 tables."""
+
+    format = N.FMT_BL4
+
+    def __init__(self, codes: torch.Tensor, tables_bf16: torch.Tensor):
+        if codes.dim() == 2:
+            codes = codes.unsqueeze(0)
+        if tables_bf16.dim() == 3:
+            tables_bf16 = tables_bf16.unsqueeze(0)
+        self.codes = _dev(codes, torch.uint8, "codes")
+        self.tables = _dev(tables_bf16, torch.bfloat16, "tables")
+        E, M, Kh = self.codes.shape
+        K = 2 * Kh
+        if K % 64:
+            raise ValueError("BL4 needs K % 64 == 0")
+        if tuple(self.tables.shape) != (E, M, K // 64, 16):
+            raise ValueError(f"tables shape {tuple(self.tables.shape)} != {(E, M, K // 64, 16)}")
+        self.num_experts, self.rows, self.cols = E, M, K
+
+    @classmethod
+    def from_fp16(cls, codes: torch.Tensor, tables_f16: torch.Tensor) -> "BL4Stack":
+        """Wire format (fp16 codebooks) -> device format (bf16 dequantised entries)."""
+        t = _dev(tables_f16, torch.float16, "tables_f16")
+        out = torch.empty(t.shape, dtype=torch.bfloat16, device=t.device)
+        N.check("lutmoe_bl4_tables_from_f16",
+                N.lib().lutmoe_bl4_tables_from_f16(t.data_ptr(), out.data_ptr(), t.numel(),
+                                                   _stream()))
+        return cls(codes, out)
+
+    def desc(self) -> N.lutmoe_weights:
+        d = N.lutmoe_weights()
+        d.format = N.FMT_BL4
+        d.num_experts, d.rows, d.cols = self.num_experts, self.rows, self.cols
+        d.codes = self.codes.data_ptr()
+        d.tables = self.tables.data_ptr()
+        d.codebook = None
+        d.tier_bits = None
+        d.absmax_per_expert = 0
+        d.block_size = 64
+        return d
+
+    def hbm_bytes_per_expert(self) -> int:
+        return self.rows * self.cols // 2 + self.rows * (self.cols // 64) * 32
+
+
+@dataclass
+class NestedExpert:
+    bits: int
+    planes: torch.Tensor     # uint8 [M*K/4 + (bits>=3)*M*K/8 + (bits>=4)*M*K/8]
+    table: torch.Tensor      # bf16 [M, K/64, 2^bits]
+
+
+class NestedStack(WeightStack):
+    """Per-expert NestedLUT tiers (2/3/4 bits)."""
+
+    format = N.FMT_NESTED
+
+    def __init__(self, experts: List[NestedExpert], rows: int, cols: int):
+        if cols % 64:
+            raise ValueError("NestedLUT needs K % 64 == 0")
+        self.experts = experts
+        self.num_experts, self.rows, self.cols = len(experts), rows, cols
+        n = rows * cols
+        for i, e in enumerate(experts):
+            if e.bits not in (2, 3, 4):
+                raise ValueError(f"expert {i}: tier bits must be 2, 3 or 4")
+            need = n // 4 + (n // 8 if e.bits >= 3 else 0) + (n // 8 if e.bits >= 4 else 0)
+            _dev(e.planes, torch.uint8, "planes")
+            _dev(e.table, torch.bfloat16, "table")
+            if e.planes.numel() != need:
+                raise ValueError(f"expert {i}: planes hold {e.planes.numel()} bytes, need {need}")
+            if tuple(e.table.shape) != (rows, cols // 64, 1 << e.bits):
+                raise ValueError(f"expert {i}: table shape {tuple(e.table.shape)}")
+        dev = experts[0].planes.device
+        self._code_ptrs = torch.tensor([e.planes.data_ptr() for e in experts], dtype=torch.int64,
+                                       device=dev)
+        self._table_ptrs = torch.tensor([e.table.data_ptr() for e in experts], dtype=torch.int64,
+                                        device=dev)
+        self._bits = torch.tensor([e.bits for e in experts], dtype=torch.int8, device=dev)
+
+    def desc(self) -> N.lutmoe_weights:
+        d = N.lutmoe_weights()
+        d.format = N.FMT_NESTED
+        d.num_experts, d.rows, d.cols = self.num_experts, self.rows, self.cols
+        d.codes = self._code_ptrs.data_ptr()
+        d.tables = self._table_ptrs.data_ptr()
+        d.codebook = None
+        d.tier_bits = self._bits.data_ptr()
+        d.absmax_per_expert = 0
+        d.block_size = 64
+        return d
+
+    def hbm_bytes_expert(self, e: int) -> int:
+        b = self.experts[e].bits
+        n = self.rows * self.cols
+        return n * b // 8 + (n // 64) * (1 << b) * 2
+
+
+@dataclass
+class MoEWeights:
+    """Routed experts 0..E-1 followed by num_shared always-on experts."""
+
+    w13: WeightStack
+    w2: WeightStack
+    hidden: int
+    inter: int
+    num_routed: int
+    num_shared: int = 0
+    _desc: Optional[N.lutmoe_moe_desc] = field(default=None, repr=False)
+
+    def __post_init__(self):
+        if self.w13.rows != 2 * self.inter or self.w13.cols != self.hidden:
+            raise ValueError("w13 must be [E, 2I, H]")
+        if self.w2.rows != self.hidden or self.w2.cols != self.inter:
+            raise ValueError("w2 must be [E, H, I]")
+        tot = self.num_routed + self.num_shared
+        if self.w13.num_experts < tot or self.w2.num_experts < tot:
+            raise ValueError("weight stacks hold fewer experts than routed + shared")
+
+    def desc(self) -> N.lutmoe_moe_desc:
+        if self._desc is None:
+            d = N.lutmoe_moe_desc()
+            d.w13 = self.w13.desc()
+            d.w2 = self.w2.desc()
+            d.hidden, d.inter = self.hidden, self.inter
+            d.num_routed, d.num_shared = self.num_routed, self.num_shared
+            self._desc = d
+        return self._desc
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream

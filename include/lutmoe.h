@@ -1,0 +1,194 @@
+/*
+ * lutmoe.h -- C ABI of the MI355X (gfx950) LUT-dequant MoE expert library
+ * (block_lut_amd/liblutmoe.so).
+ *
+ * Plain pointers and sizes only.  Every pointer argument named *_dev is a
+ * device pointer; `stream` is a hipStream_t passed as void* (NULL = the
+ * default stream).  All entry points are asynchronous on `stream` and never
+ * synchronise the device.  Argument validation happens before any HIP call,
+ * so an invalid call returns an error code without touching the GPU.
+ *
+ * Return convention of the int-returning functions: 0 = success, negative =
+ * one of the LUTMOE_E* codes below (lutmoe_strerror gives the text).
+ *
+ * Formats (device layouts):
+ *   REF  : codes uint8 [E][M][K] (one code per weight), absmax bf16 [E][nb]
+ *          with nb = ceil(M*K/block_size) per expert, codebook bf16[256].
+ *   BL4  : codes uint8 [E][M][K/2] (two 4-bit codes per byte, even element in
+ *          the low nibble), tables bf16 [E][M][K/64][16] (the dequantised
+ *          entries; lutmoe_bl4_tables_from_f16 converts the fp16 codebooks).
+ *   NL   : NestedLUT tier b in {2,3,4} per expert: codes are bit-plane
+ *          sections [p01 M*K/4 | p2 M*K/8 | p3 M*K/8] (a tier-b expert holds
+ *          the first 2, 3 or all sections), tables bf16 [M][K/64][2^b].
+ */
+#ifndef LUTMOE_H
+#define LUTMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- error codes ---------------------------------------------------- */
+#define LUTMOE_OK             0
+#define LUTMOE_EINVAL        -1   /* bad argument (null pointer, size, dtype) */
+#define LUTMOE_EUNSUPPORTED  -2   /* valid but unsupported combination        */
+#define LUTMOE_EHIP          -3   /* a HIP runtime call failed                */
+#define LUTMOE_EWORKSPACE    -4   /* workspace too small                      */
+#define LUTMOE_EALIGN        -5   /* pointer misaligned for vector access     */
+
+/* ---- formats and dtypes ---------------------------------------------- */
+#define LUTMOE_FMT_REF        0
+#define LUTMOE_FMT_BL4        1
+#define LUTMOE_FMT_NESTED     2
+
+#define LUTMOE_DTYPE_BF16     0
+#define LUTMOE_DTYPE_F32      1
+
+/* One stack of per-expert LUT-quantised matrices W[e] of shape [rows, cols]
+ * (rows = output features, cols = K = input features). */
+typedef struct lutmoe_weights {
+    int32_t format;            /* LUTMOE_FMT_*                                   */
+    int32_t num_experts;       /* E                                              */
+    int32_t rows;              /* M                                              */
+    int32_t cols;              /* K                                              */
+    const void* codes;         /* REF/BL4: device base of [E] code arrays.
+                                  NL: device array of E pointers (uint8_t*) to
+                                  each expert's bit-plane sections.              */
+    const void* tables;        /* REF: bf16 absmax [E][absmax_per_expert].
+                                  BL4: bf16 tables [E][M][K/64][16].
+                                  NL: device array of E pointers (uint16_t*) to
+                                  each expert's bf16 table [M][K/64][2^b].       */
+    const void* codebook;      /* REF: bf16[256] global codebook; else NULL.     */
+    const int8_t* tier_bits;   /* NL: device int8 [E] with b in {2,3,4}.         */
+    int64_t absmax_per_expert; /* REF: absmax entries per expert.                */
+    int32_t block_size;        /* REF: absmax block (reference default 128).     */
+    int32_t reserved;
+} lutmoe_weights;
+
+/* Fused-MoE layer description: routed experts 0..E-1, plus num_shared
+ * always-on experts stored after them (expert ids E..E+S-1 of the same
+ * stacks), each applied with weight 1.0 (customized/deepseek.py:111-115). */
+typedef struct lutmoe_moe_desc {
+    lutmoe_weights w13;        /* [E+S][2I][H]: gate rows [0,I), up rows [I,2I) */
+    lutmoe_weights w2;         /* [E+S][H][I]                                   */
+    int32_t hidden;            /* H                                             */
+    int32_t inter;             /* I                                             */
+    int32_t num_routed;        /* E                                             */
+    int32_t num_shared;        /* S                                             */
+} lutmoe_moe_desc;
+
+/* ---- library ---------------------------------------------------------- */
+const char* lutmoe_strerror(int code);
+const char* lutmoe_version(void);
+/* Last error text recorded by a void-returning reference-compatible entry
+ * point on the calling thread ("" when none). */
+const char* lutmoe_last_error(void);
+
+/* ---- reference-compatible entry points --------------------------------
+ * Same names, argument meaning and error behaviour as the reference's
+ * native surface (asynchronous here: no device synchronisation). */
+
+/* vllm_lut/cuda/lut_decompress_kernel.cu:125-154.
+ * out[i] = bf16(cb[idx[i]] * absmax[i / block_size]); 0 ok, -1 on error. */
+int launch_blocklut_decompress(void* output, const void* indices, const void* absmax,
+                               const void* codebook, int N, int block_size, void* stream);
+
+/* vllm_lut/cuda/lut_decompress_kernel.cu:156-180 (any elements_per_expert;
+ * the reference's one-thread-per-element launch is limited to 1024). */
+int launch_batch_blocklut_decompress(void* output, const void* indices, const void* absmax,
+                                     const void* codebook, int num_experts,
+                                     int elements_per_expert, int blocks_per_expert,
+                                     int block_size, void* stream);
+
+/* csrc/kernels/tensor_recover.hpp (lut_moe_launch_blocklut_recover,
+ * tensor_recover.cu:144-159): 128-element absmax blocks, bf16 out. */
+void lut_moe_launch_blocklut_recover(uint16_t* gpu_output_tensor,
+                                     const uint8_t* gpu_indices_ptr,
+                                     const uint16_t* gpu_absmax_ptr,
+                                     const uint16_t* gpu_lut_ptr,
+                                     size_t num_elements, void* tensor_stream);
+
+/* csrc/kernels/tensor_recover.hpp (lut_moe_launch_unpack_4bit,
+ * tensor_recover.cu:182-192): in place, the first n/2 bytes (low nibble
+ * section) become n one-byte codes. */
+void lut_moe_launch_unpack_4bit(uint8_t* gpu_data, size_t num_elements, void* tensor_stream);
+
+/* vllm_lut/cuda_lut_gemv.py:199-215 (launch_lut_gemv_kernel): fp32 codebook
+ * [256], bf16 input [K], uint8 indices [M][K], bf16 absmax [num_blocks]
+ * (128-element blocks), bf16 output [M]; default stream. */
+void launch_lut_gemv_kernel(const void* input, const void* indices, const void* codebook,
+                            const void* absmax, void* output, int M, int K, int num_blocks);
+
+/* ---- REF format ----------------------------------------------------------- */
+
+/* lut_gemv (vllm_lut/cuda_lut_gemv.py:153-169) with a bf16 codebook and an
+ * explicit stream.  y[T][M] (dtype y_dtype) = sum_k x[T][K] * cb[idx]*absmax,
+ * fp32 accumulation in the reference's (x*cb)*absmax product order. */
+int lutmoe_ref_gemv(const void* x_dev, const void* indices_dev, const void* codebook_dev,
+                    const void* absmax_dev, void* y_dev, int M, int K, int T,
+                    int num_blocks, int block_size, int y_dtype, void* stream);
+
+/* CPU-side tier unpack of the reference, on the GPU (csrc/tensor_engine/
+ * tensor_engine.cpp:535-548): 6-bit codes = low nibble | mid 2 bits << 4 from
+ * the [low | mid] sections of `packed`, written to `out` (n bytes). */
+int lutmoe_unpack_6bit(const uint8_t* packed_dev, uint8_t* out_dev, int64_t n, void* stream);
+
+/* ---- generic (all formats) --------------------------------------------- */
+
+/* Dequantise experts [e0, e0+ne) of a weight stack to bf16 [ne][M][K]. */
+int lutmoe_dequant(const lutmoe_weights* w, int e0, int ne, void* out_dev, void* stream);
+
+/* y[T][M] = x[T][K] . W[expert]^T for one expert (fp32 accumulation). */
+int lutmoe_gemv(const lutmoe_weights* w, int expert, const void* x_dev, int T,
+                void* y_dev, int y_dtype, void* stream);
+
+/* BL4 repack: fp16 codebook entries -> bf16 dequantised entries. */
+int lutmoe_bl4_tables_from_f16(const uint16_t* f16_dev, uint16_t* bf16_dev, int64_t n,
+                               void* stream);
+
+/* ---- routing and permutation ------------------------------------------ */
+
+/* softmax(fp32 logits [T][E]) -> top-k (sorted descending, ties to the lower
+ * id), optional renormalisation, times `scaling`; weights fp32 [T][k],
+ * ids int32 [T][k] (vllm_lut/moe_layer.py:358-376). */
+int lutmoe_route_topk(const float* logits_dev, int T, int E, int k, int renormalize,
+                      float scaling, float* topk_w_dev, int32_t* topk_ids_dev, void* stream);
+
+/* Expert-major, pair-ascending permutation of the T*k (token, slot) pairs.
+ * offsets int32 [E+1], perm int32 [T*k] (pair index t*k+slot at each
+ * position), inv int32 [T*k] (position of each pair), active int32 [E+1]
+ * (active[0] = number of experts with tokens, then their ids ascending). */
+int lutmoe_permute(const int32_t* topk_ids_dev, int T, int k, int E, int32_t* offsets_dev,
+                   int32_t* perm_dev, int32_t* inv_dev, int32_t* active_dev, void* stream);
+
+/* ---- fused MoE layer ------------------------------------------------------ */
+
+/* Workspace bytes lutmoe_moe_forward needs for T tokens and top-k. */
+size_t lutmoe_moe_workspace_size(const lutmoe_moe_desc* d, int T, int k);
+
+/* out[T][H] (out_dtype) = sum_k topk_w[t][k] * FFN_{ids[t][k]}(x[t])
+ *                         + sum_s FFN_{E+s}(x[t]),
+ * FFN(x) = W2 . bf16(silu(W13_gate x) * (W13_up x)), fp32 accumulation.
+ * x bf16 [T][H]; topk_w fp32 [T][k]; topk_ids int32 [T][k] in [0, E).
+ * Decode (small T) uses the grouped LUT-GEMV kernels, prefill the grouped
+ * MFMA LUT-GEMM; `force_path` 0 = auto, 1 = GEMV, 2 = MFMA. */
+int lutmoe_moe_forward(const lutmoe_moe_desc* d, const void* x_dev, const float* topk_w_dev,
+                       const int32_t* topk_ids_dev, int T, int k, void* out_dev,
+                       int out_dtype, void* workspace_dev, size_t workspace_bytes,
+                       int force_path, void* stream);
+
+/* ---- encoders (format producers) ----------------------------------------- */
+
+/* BL4 per-64-block k-means encoder on the GPU: w fp32 [nblocks*64] ->
+ * packed codes [nblocks*32] and fp16 tables [nblocks*16]. */
+int lutmoe_bl4_encode(const float* w_dev, int64_t nblocks, int n_iter, uint8_t* codes_dev,
+                      uint16_t* tables_f16_dev, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LUTMOE_H */

@@ -1,0 +1,88 @@
+"""Shared helpers for the parity tests: seeded inputs, host<->device bf16 moves,
+and the oracle-side builders of the same weights the GPU sees."""
+from __future__ import annotations
+
+import os
+
+import numpy as np
+
+import oracle as O
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def to_dev_bf16(bits: np.ndarray, device):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(bits, np.uint16).view(np.int16)).view(
+        torch.bfloat16).to(device)
+
+
+def to_dev_f16(bits: np.ndarray, device):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(bits, np.uint16).view(np.float16)).to(device)
+
+
+def bf16_bits(t) -> np.ndarray:
+    import torch
+    return t.detach().contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def rel_maxabs(got, ref) -> float:
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    den = np.abs(ref).max()
+    return float(np.abs(got - ref).max() / (den if den > 0 else 1.0))
+
+
+def golden_codebook() -> np.ndarray:
+    """bf16 bits of the reference's shipped Qwen blocklut_256 codebook (derived fixture)."""
+    return np.load(os.path.join(GOLDEN, "codebooks.npz"))["qwen_blocklut_256_bf16"]
+
+
+class BL4Expertset:
+    """E BL4-encoded matrices [M, K] built by the CPU oracle from seeded N(0, std) weights."""
+
+    def __init__(self, E, M, K, seed, std=0.02, n_iter=20):
+        rng = np.random.default_rng(seed)
+        self.E, self.M, self.K = E, M, K
+        self.codes = np.empty((E, M, K // 2), np.uint8)
+        self.tables = np.empty((E, M, K // 64, 16), np.uint16)
+        for e in range(E):
+            w = (rng.standard_normal((M, K)) * std).astype(np.float32)
+            self.codes[e], self.tables[e] = O.bl4_encode(w, n_iter=n_iter)
+
+    def deq_f32(self, e) -> np.ndarray:
+        return O.bf16_to_f32(O.bl4_dequant(self.codes[e], self.tables[e]))
+
+    def stack(self, device):
+        import torch
+        from block_lut_amd.formats import BL4Stack
+        return BL4Stack.from_fp16(torch.from_numpy(self.codes).to(device),
+                                  to_dev_f16(self.tables, device))
+
+
+class RefExpertset:
+    """E REF matrices quantized by the oracle's restatement of LUTQuantizer.quantize."""
+
+    def __init__(self, E, M, K, seed, std=0.02, block_size=128):
+        rng = np.random.default_rng(seed)
+        self.E, self.M, self.K, self.bs = E, M, K, block_size
+        self.cb = golden_codebook()
+        nb = -(-M * K // block_size)
+        self.codes = np.empty((E, M, K), np.uint8)
+        self.absmax = np.empty((E, nb), np.uint16)
+        for e in range(E):
+            w = (rng.standard_normal((M, K)) * std).astype(np.float32)
+            idx, am = O.ref_quantize(w, self.cb, block_size)
+            self.codes[e] = idx.reshape(M, K)
+            self.absmax[e] = am
+
+    def deq_f32(self, e) -> np.ndarray:
+        return O.bf16_to_f32(O.ref_dequant(self.codes[e], self.absmax[e], self.cb, self.bs)).reshape(
+            self.M, self.K)
+
+    def stack(self, device):
+        import torch
+        from block_lut_amd.formats import RefStack
+        return RefStack(torch.from_numpy(self.codes).to(device), to_dev_bf16(self.absmax, device),
+                        to_dev_bf16(self.cb, device), self.bs)

@@ -1,0 +1,288 @@
+"""GPU parity of the HIP kernels against the CPU oracle (seeded inputs).
+
+Bar: bit-exact for codes, dequantised weights, routing ids and permutations;
+GEMV / layer outputs (fp32 accumulation, fp32 output) within max-abs 1e-3
+relative to the oracle's float64 result, i.e.
+    max|y - y_ref| / max|y_ref| <= 1e-3.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from lutmoe_testutil import (BL4Expertset, RefExpertset, bf16_bits, golden_codebook, rel_maxabs,
+                             to_dev_bf16, to_dev_f16)
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+def _x(rng, T, K):
+    return O.f32_to_bf16(rng.standard_normal((T, K)).astype(np.float32))
+
+
+# ------------------------------------------------------------------ encoder
+
+@pytest.mark.parametrize("M,K,n_iter", [(16, 768, 50), (64, 2048, 20)])
+def test_bl4_encode_bitexact(gpu, M, K, n_iter):
+    import torch
+    from block_lut_amd import ops
+    rng = np.random.default_rng(100 + M)
+    w = (rng.standard_normal((M, K)) * 0.02).astype(np.float32)
+    w[0, :64] = 0.0                       # degenerate block: all equal
+    w[1, :64] = np.repeat(w[1, :16], 4)   # heavy duplicates
+    codes, tables = ops.bl4_encode(torch.from_numpy(w).to(gpu), n_iter=n_iter)
+    rc, rt = O.bl4_encode(w, n_iter=n_iter)
+    torch.cuda.synchronize()
+    assert np.array_equal(codes.cpu().numpy(), rc)
+    assert np.array_equal(tables.cpu().numpy().view(np.uint16), rt)
+
+
+# ------------------------------------------------------------------ dequant
+
+def test_bl4_dequant_bitexact(gpu):
+    from block_lut_amd import ops
+    es = BL4Expertset(3, 96, 1408, seed=1)
+    st = es.stack(gpu)
+    got = bf16_bits(ops.dequant(st))
+    for e in range(3):
+        assert np.array_equal(got[e], O.bl4_dequant(es.codes[e], es.tables[e]))
+    # table conversion alone: every fp16 pattern (incl. subnormals, inf, nan)
+    import torch
+    from block_lut_amd.formats import BL4Stack
+    allh = np.arange(65536, dtype=np.uint16).reshape(1, 1, 64, 16 * 64)[..., :16 * 64]
+    t = allh.reshape(1, 64, 64, 16)
+    c = torch.zeros((1, 64, 2048), dtype=torch.uint8, device=gpu)
+    st2 = BL4Stack.from_fp16(c, to_dev_f16(t, gpu))
+    got_t = bf16_bits(st2.tables)
+    assert np.array_equal(got_t, O.bl4_tables_bf16(t))
+
+
+def test_ref_dequant_bitexact(gpu):
+    import torch
+    from block_lut_amd import ops
+    rng = np.random.default_rng(2)
+    cb = golden_codebook()
+    for n, bs in ((4096, 128), (1000, 128), (2816 * 64, 128), (777, 64)):
+        idx = rng.integers(0, 256, n, dtype=np.uint8)
+        nb = -(-n // bs)
+        am = O.f32_to_bf16(np.abs(rng.standard_normal(nb)).astype(np.float32) * 0.05)
+        got = ops.blocklut_decompress(torch.from_numpy(idx).to(gpu), to_dev_bf16(am, gpu),
+                                      to_dev_bf16(cb, gpu), bs)
+        assert np.array_equal(bf16_bits(got), O.ref_dequant(idx, am, cb, bs)), (n, bs)
+        if bs == 128:
+            got2 = ops.blocklut_recover(torch.from_numpy(idx).to(gpu), to_dev_bf16(am, gpu),
+                                        to_dev_bf16(cb, gpu))
+            assert np.array_equal(bf16_bits(got2), O.ref_dequant(idx, am, cb, bs))
+
+
+def test_ref_dequant_all_codes_all_scales(gpu):
+    """Brute force: every code x a spread of absmax values (incl. zero, subnormal, large)."""
+    import torch
+    from block_lut_amd import ops
+    cb = golden_codebook()
+    scales = np.array([0.0, 1e-40, 1e-10, 3e-3, 0.02, 0.5, 1.0, 3.0, 1e4, 3e38], np.float32)
+    am = O.f32_to_bf16(scales)
+    idx = np.concatenate([np.roll(np.arange(256, dtype=np.uint8), s)[:128] for s in range(0, 20, 2)])
+    got = ops.blocklut_decompress(torch.from_numpy(idx).to(gpu), to_dev_bf16(am, gpu),
+                                  to_dev_bf16(cb, gpu), 128)
+    assert np.array_equal(bf16_bits(got), O.ref_dequant(idx, am, cb, 128))
+
+
+def test_ref_batch_decompress(gpu):
+    import ctypes
+    import torch
+    from block_lut_amd import _native as N
+    rng = np.random.default_rng(3)
+    cb = golden_codebook()
+    E, n, bs = 4, 5000, 128
+    nb = -(-n // bs)
+    idx = rng.integers(0, 256, (E, n), dtype=np.uint8)
+    am = O.f32_to_bf16(np.abs(rng.standard_normal((E, nb))).astype(np.float32))
+    out = torch.empty((E, n), dtype=torch.bfloat16, device=gpu)
+    di = torch.from_numpy(idx).to(gpu)
+    da = to_dev_bf16(am, gpu)
+    dc = to_dev_bf16(cb, gpu)
+    rc = N.lib().launch_batch_blocklut_decompress(out.data_ptr(), di.data_ptr(), da.data_ptr(),
+                                                  dc.data_ptr(), E, n, nb, bs, None)
+    assert rc == 0
+    got = bf16_bits(out)
+    for e in range(E):
+        assert np.array_equal(got[e], O.ref_dequant(idx[e], am[e], cb, bs))
+
+
+@pytest.mark.parametrize("n", [16, 8190, 8192, 8194, 100002, 5767168])
+def test_unpack_4bit_inplace(gpu, n):
+    import torch
+    from block_lut_amd import ops
+    rng = np.random.default_rng(n)
+    codes = rng.integers(0, 256, n, dtype=np.uint8)
+    packed = (codes[0::2] & 0x0F) | ((codes[1::2] & 0x0F) << 4)
+    buf = torch.zeros(n, dtype=torch.uint8, device=gpu)
+    buf[: n // 2] = torch.from_numpy(packed.astype(np.uint8)).to(gpu)
+    ops.unpack_4bit_(buf, n)
+    assert np.array_equal(buf.cpu().numpy(), O.unpack_4bit_ref(packed, n))
+
+
+def test_unpack_6bit(gpu):
+    import torch
+    from block_lut_amd import ops
+    rng = np.random.default_rng(6)
+    n = 4096 * 3
+    codes = rng.integers(0, 256, n, dtype=np.uint8)
+    packed = O.bitplane_pack_ref(codes)
+    got = ops.unpack_6bit(torch.from_numpy(packed).to(gpu), n)
+    assert np.array_equal(got.cpu().numpy(), O.unpack_6bit_ref(packed, n))
+    assert np.array_equal(got.cpu().numpy(), codes & 0x3F)
+
+
+# --------------------------------------------------------------------- GEMV
+
+@pytest.mark.parametrize("T", [1, 2, 3, 5])
+def test_bl4_gemv_c1_shape(gpu, T):
+    """Switch-base-8 expert FFN shape: W [3072, 768], 64-weight blocks."""
+    import torch
+    from block_lut_amd import ops
+    es = BL4Expertset(1, 3072, 768, seed=0, n_iter=10)
+    st = es.stack(gpu)
+    rng = np.random.default_rng(1)
+    xb = _x(rng, T, 768)
+    y = ops.gemv(st, to_dev_bf16(xb, gpu), 0, out_dtype=torch.float32).cpu().numpy()
+    ref = O.bf16_to_f32(xb).astype(np.float64) @ es.deq_f32(0).astype(np.float64).T
+    assert rel_maxabs(y, ref) <= TOL
+
+
+@pytest.mark.parametrize("M,K,T", [(2816, 2048, 1), (2048, 1408, 1), (300, 640, 3)])
+def test_ref_gemv(gpu, M, K, T):
+    import torch
+    from block_lut_amd import ops
+    rng = np.random.default_rng(M + K)
+    cb = golden_codebook()
+    idx = rng.integers(0, 256, (M, K), dtype=np.uint8)
+    nb = -(-M * K // 128)
+    am = O.f32_to_bf16(np.abs(rng.standard_normal(nb)).astype(np.float32) * 0.02)
+    xb = _x(rng, T, K)
+    y = ops.ref_gemv(to_dev_bf16(xb, gpu), torch.from_numpy(idx).to(gpu), to_dev_bf16(cb, gpu),
+                     to_dev_bf16(am, gpu), out_dtype=torch.float32).cpu().numpy()
+    for t in range(T):
+        ref = O.ref_gemv(xb[t], idx, cb, am)
+        assert rel_maxabs(y[t], ref) <= TOL
+
+
+def test_ref_gemv_generic_path(gpu):
+    """K not a multiple of 8 and 100-element absmax blocks spanning rows."""
+    import torch
+    from block_lut_amd import ops
+    rng = np.random.default_rng(9)
+    cb = golden_codebook()
+    M, K, bs = 37, 203, 100
+    idx = rng.integers(0, 256, (M, K), dtype=np.uint8)
+    nb = -(-M * K // bs)
+    am = O.f32_to_bf16(np.abs(rng.standard_normal(nb)).astype(np.float32))
+    xb = _x(rng, 1, K)
+    y = ops.ref_gemv(to_dev_bf16(xb, gpu), torch.from_numpy(idx).to(gpu), to_dev_bf16(cb, gpu),
+                     to_dev_bf16(am, gpu), block_size=bs, out_dtype=torch.float32)
+    deq = O.bf16_to_f32(cb)[idx] * O.bf16_to_f32(am)[np.minimum(np.arange(M * K) // bs, nb - 1)].reshape(M, K)
+    ref = deq.astype(np.float64) @ O.bf16_to_f32(xb[0]).astype(np.float64)
+    assert rel_maxabs(y.cpu().numpy()[0], ref) <= TOL
+
+
+def test_lut_gemv_reference_signature(gpu):
+    """launch_lut_gemv_kernel: fp32 codebook, default stream, bf16 out."""
+    import torch
+    from block_lut_amd import _native as N
+    rng = np.random.default_rng(10)
+    cb = golden_codebook()
+    M, K = 512, 1024
+    idx = rng.integers(0, 256, (M, K), dtype=np.uint8)
+    nb = M * K // 128
+    am = O.f32_to_bf16(np.abs(rng.standard_normal(nb)).astype(np.float32) * 0.02)
+    xb = _x(rng, 1, K)
+    di = torch.from_numpy(idx).to(gpu)
+    dcb = torch.from_numpy(O.bf16_to_f32(cb)).to(gpu)
+    dx, da = to_dev_bf16(xb, gpu), to_dev_bf16(am, gpu)
+    out = torch.empty(M, dtype=torch.bfloat16, device=gpu)
+    torch.cuda.synchronize()
+    N.lib().launch_lut_gemv_kernel(dx.data_ptr(), di.data_ptr(), dcb.data_ptr(), da.data_ptr(),
+                                   out.data_ptr(), M, K, nb)
+    N.check_last("launch_lut_gemv_kernel")
+    torch.cuda.synchronize()
+    ref = O.ref_gemv(xb[0], idx, cb, am)
+    # bf16 output: one bf16 rounding of the fp32 sum on top of the tolerance
+    assert rel_maxabs(O.bf16_to_f32(bf16_bits(out)), ref) <= TOL + 2.0 ** -8
+
+
+# ------------------------------------------------------------------ routing
+
+@pytest.mark.parametrize("T,E,k,renorm", [(1, 60, 4, False), (37, 64, 6, False), (513, 8, 2, True)])
+def test_route_topk(gpu, T, E, k, renorm):
+    import torch
+    from block_lut_amd import ops
+    rng = np.random.default_rng(T * E)
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    lg[0, :3] = 1.5                       # a tie: lower expert id first
+    w, ids = ops.route_topk(torch.from_numpy(lg).to(gpu), k, renormalize=renorm)
+    rw, rids = O.route(lg, k, renormalize=renorm)
+    assert np.array_equal(ids.cpu().numpy(), rids)
+    np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=2e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("T,k,E", [(1, 4, 60), (32, 4, 60), (2048, 8, 66), (300, 2, 8)])
+def test_permute(gpu, T, k, E):
+    import torch
+    from block_lut_amd import ops
+    rng = np.random.default_rng(T + E)
+    ids = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
+    off, perm, inv, act = [t.cpu().numpy() for t in ops.permute(torch.from_numpy(ids).to(gpu), E)]
+    roff, rperm, rinv = O.permute(ids, E)
+    assert np.array_equal(off, roff)
+    assert np.array_equal(perm, rperm)
+    assert np.array_equal(inv, rinv)
+    nz = np.nonzero(np.diff(roff))[0]
+    assert act[0] == nz.size and np.array_equal(act[1:1 + nz.size], nz)
+
+
+# --------------------------------------------------------------- MoE layer
+
+def _moe_case(fmt, E, S, H, I, seed):
+    cls = BL4Expertset if fmt == "bl4" else RefExpertset
+    w13 = cls(E + S, 2 * I, H, seed=seed)
+    w2 = cls(E + S, H, I, seed=seed + 1)
+    return w13, w2
+
+
+@pytest.mark.parametrize("fmt,T,path", [("bl4", 1, 1), ("bl4", 4, 1), ("bl4", 9, 1),
+                                        ("bl4", 200, 2), ("bl4", 5, 2),
+                                        ("ref", 1, 1), ("ref", 3, 1), ("ref", 150, 2)])
+def test_moe_layer(gpu, fmt, T, path):
+    import torch
+    from block_lut_amd import ops
+    from block_lut_amd.formats import MoEWeights
+    E, S, k, H, I = 8, 1, 2, 512, 320
+    w13, w2 = _moe_case(fmt, E, S, H, I, seed=20 + T)
+    moe = MoEWeights(w13.stack(gpu), w2.stack(gpu), H, I, E, S)
+    rng = np.random.default_rng(T)
+    xb = _x(rng, T, H)
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    rw, rids = O.route(lg, k)
+    out = ops.moe_forward(moe, to_dev_bf16(xb, gpu), torch.from_numpy(rw).to(gpu),
+                          torch.from_numpy(rids).to(gpu), out_dtype=torch.float32, path=path)
+    ref = O.moe_layer(xb, rids, rw, w13.deq_f32, w2.deq_f32,
+                      shared=[(w13.deq_f32(E + s), w2.deq_f32(E + s)) for s in range(S)])
+    assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
+
+
+def test_moe_layer_paths_agree(gpu):
+    """GEMV and MFMA paths on the same inputs (both fp32 accumulation)."""
+    import torch
+    from block_lut_amd import ops
+    from block_lut_amd.formats import MoEWeights
+    E, S, k, H, I, T = 8, 0, 2, 512, 320, 16
+    w13, w2 = _moe_case("bl4", E, S, H, I, seed=5)
+    moe = MoEWeights(w13.stack(gpu), w2.stack(gpu), H, I, E, S)
+    rng = np.random.default_rng(55)
+    xb = _x(rng, T, H)
+    rw, rids = O.route(rng.standard_normal((T, E)).astype(np.float32), k)
+    args = (moe, to_dev_bf16(xb, gpu), torch.from_numpy(rw).to(gpu), torch.from_numpy(rids).to(gpu))
+    a = ops.moe_forward(*args, out_dtype=torch.float32, path=1).cpu().numpy()
+    b = ops.moe_forward(*args, out_dtype=torch.float32, path=2).cpu().numpy()
+    assert rel_maxabs(a, b) <= TOL
