@@ -24,6 +24,11 @@ FMT_REF = 0
 FMT_BL4 = 1
 FMT_NESTED = 2
 
+STAGE_ROUTE = 1
+STAGE_GATE_UP = 2
+STAGE_DOWN = 4
+STAGE_ALL = 7
+
 DTYPE_BF16 = 0
 DTYPE_F32 = 1
 
@@ -92,6 +97,7 @@ PROTOTYPES = {
     "lutmoe_permute": (I32, [P, I32, I32, I32, P, P, P, P, P]),
     "lutmoe_moe_workspace_size": (SZ, [DP, I32, I32]),
     "lutmoe_moe_forward": (I32, [DP, P, P, P, I32, I32, P, I32, P, SZ, I32, P]),
+    "lutmoe_moe_forward_stages": (I32, [DP, P, P, P, I32, I32, P, I32, P, SZ, I32, I32, P]),
     "lutmoe_bl4_encode": (I32, [P, I64, I32, P, P, P]),
 }
 

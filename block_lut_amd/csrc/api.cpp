@@ -290,6 +290,15 @@ size_t lutmoe_moe_workspace_size(const lutmoe_moe_desc* d, int T, int k) {
 int lutmoe_moe_forward(const lutmoe_moe_desc* d, const void* x, const float* topk_w,
                        const int32_t* topk_ids, int T, int k, void* out, int out_dtype,
                        void* workspace, size_t ws_bytes, int force_path, void* stream) {
+    return lutmoe_moe_forward_stages(d, x, topk_w, topk_ids, T, k, out, out_dtype, workspace,
+                                     ws_bytes, force_path, LUTMOE_STAGE_ALL, stream);
+}
+
+int lutmoe_moe_forward_stages(const lutmoe_moe_desc* d, const void* x, const float* topk_w,
+                              const int32_t* topk_ids, int T, int k, void* out, int out_dtype,
+                              void* workspace, size_t ws_bytes, int force_path, int stages,
+                              void* stream) {
+    if (stages <= 0 || stages > LUTMOE_STAGE_ALL) return LUTMOE_EINVAL;
     int rc = validate_moe(d);
     if (rc) return rc;
     if (T < 0 || k <= 0 || k > d->num_routed || k + d->num_shared > 16) return LUTMOE_EINVAL;
@@ -323,18 +332,29 @@ int lutmoe_moe_forward(const lutmoe_moe_desc* d, const void* x, const float* top
     float* y = (float*)(ws + L.y);
     hipStream_t s = stream_of(stream);
 
-    if ((rc = launch_build_pairs(topk_ids, topk_w, T, k, E, S, pair_ids, pair_w, s))) return rc;
-    if ((rc = launch_permute(pair_ids, T, ke, E_tot, (int32_t*)r.offsets, (int32_t*)r.perm,
-                             (int32_t*)r.inv, (int32_t*)r.active, s)))
-        return rc;
+    if (stages & LUTMOE_STAGE_ROUTE) {
+        if ((rc = launch_build_pairs(topk_ids, topk_w, T, k, E, S, pair_ids, pair_w, s))) return rc;
+        if ((rc = launch_permute(pair_ids, T, ke, E_tot, (int32_t*)r.offsets, (int32_t*)r.perm,
+                                 (int32_t*)r.inv, (int32_t*)r.active, s)))
+            return rc;
+    }
     const int max_active = (int)(P < E_tot ? P : E_tot);
     if (gemv) {
-        if ((rc = launch_decode_gate_up(d, (const uint16_t*)x, r, act, max_active, s))) return rc;
-        return launch_decode_down_combine(d, act, r, out, out_dtype, max_active, s);
+        if ((stages & LUTMOE_STAGE_GATE_UP) &&
+            (rc = launch_decode_gate_up(d, (const uint16_t*)x, r, act, max_active, s)))
+            return rc;
+        if (stages & LUTMOE_STAGE_DOWN)
+            return launch_decode_down_combine(d, act, r, out, out_dtype, max_active, s);
+        return LUTMOE_OK;
     }
-    if ((rc = launch_prefill_gate_up(d, (const uint16_t*)x, r, act, (int)P, s))) return rc;
-    if ((rc = launch_prefill_down(d, act, r, y, (int)P, s))) return rc;
-    return launch_combine(y, r.inv, T, ke, d->hidden, out, out_dtype, s);
+    if ((stages & LUTMOE_STAGE_GATE_UP) &&
+        (rc = launch_prefill_gate_up(d, (const uint16_t*)x, r, act, (int)P, s)))
+        return rc;
+    if (stages & LUTMOE_STAGE_DOWN) {
+        if ((rc = launch_prefill_down(d, act, r, y, (int)P, s))) return rc;
+        return launch_combine(y, r.inv, T, ke, d->hidden, out, out_dtype, s);
+    }
+    return LUTMOE_OK;
 }
 
 // --------------------------------------------------------------- encoders

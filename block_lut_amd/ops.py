@@ -173,7 +173,7 @@ def moe_workspace_bytes(moe: MoEWeights, T: int, k: int) -> int:
 def moe_forward(moe: MoEWeights, x: torch.Tensor, topk_weights: torch.Tensor,
                 topk_ids: torch.Tensor, out: Optional[torch.Tensor] = None,
                 out_dtype: torch.dtype = torch.bfloat16, path: int = PATH_AUTO,
-                workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+                workspace: Optional[torch.Tensor] = None, stages: int = N.STAGE_ALL) -> torch.Tensor:
     """Fused LUT MoE layer: out[T, H] = sum_k w * FFN_{ids}(x) + shared experts."""
     _dev(x, torch.bfloat16, "x")
     T, H = x.shape
@@ -194,9 +194,10 @@ def moe_forward(moe: MoEWeights, x: torch.Tensor, topk_weights: torch.Tensor,
         workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=x.device)
     d = moe.desc()
     N.check("lutmoe_moe_forward",
-            N.lib().lutmoe_moe_forward(ctypes.byref(d), x.data_ptr(), w.data_ptr(), ids.data_ptr(),
-                                       T, k, out.data_ptr(), _out_code(out_dtype),
-                                       workspace.data_ptr(), workspace.numel(), path, _stream()))
+            N.lib().lutmoe_moe_forward_stages(ctypes.byref(d), x.data_ptr(), w.data_ptr(),
+                                              ids.data_ptr(), T, k, out.data_ptr(),
+                                              _out_code(out_dtype), workspace.data_ptr(),
+                                              workspace.numel(), path, stages, _stream()))
     return out
 
 

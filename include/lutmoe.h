@@ -180,6 +180,20 @@ int lutmoe_moe_forward(const lutmoe_moe_desc* d, const void* x_dev, const float*
                        int out_dtype, void* workspace_dev, size_t workspace_bytes,
                        int force_path, void* stream);
 
+/* Stage bits of lutmoe_moe_forward_stages. */
+#define LUTMOE_STAGE_ROUTE    1   /* pair build + permutation into the workspace   */
+#define LUTMOE_STAGE_GATE_UP  2   /* gate/up LUT-GEMV or GEMM + SwiGLU -> act      */
+#define LUTMOE_STAGE_DOWN     4   /* down projection + weighted combine -> out     */
+#define LUTMOE_STAGE_ALL      7
+
+/* lutmoe_moe_forward restricted to some stages; a later stage reads what an
+ * earlier call left in the same workspace (same T, k, routing).  Used to time
+ * each kernel family on its own. */
+int lutmoe_moe_forward_stages(const lutmoe_moe_desc* d, const void* x_dev, const float* topk_w_dev,
+                              const int32_t* topk_ids_dev, int T, int k, void* out_dev,
+                              int out_dtype, void* workspace_dev, size_t workspace_bytes,
+                              int force_path, int stages, void* stream);
+
 /* ---- encoders (format producers) ----------------------------------------- */
 
 /* BL4 per-64-block k-means encoder on the GPU: w fp32 [nblocks*64] ->

@@ -81,6 +81,14 @@ class RefExpertset:
         return O.bf16_to_f32(O.ref_dequant(self.codes[e], self.absmax[e], self.cb, self.bs)).reshape(
             self.M, self.K)
 
+    def gemv_f32(self, e) -> np.ndarray:
+        """Weights as the reference's decode GEMV sees them: f32(cb[c]) * f32(absmax)
+        without the bf16 rounding of the dequantised tensor (vllm_lut/cuda_lut_gemv.py:50-57)."""
+        cb = O.bf16_to_f32(self.cb)
+        am = O.bf16_to_f32(self.absmax[e])
+        blk = np.minimum(np.arange(self.M * self.K) // self.bs, am.size - 1)
+        return (cb[self.codes[e].reshape(-1)] * am[blk]).astype(np.float32).reshape(self.M, self.K)
+
     def stack(self, device):
         import torch
         from block_lut_amd.formats import RefStack

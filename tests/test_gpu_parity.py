@@ -266,8 +266,11 @@ def test_moe_layer(gpu, fmt, T, path):
     rw, rids = O.route(lg, k)
     out = ops.moe_forward(moe, to_dev_bf16(xb, gpu), torch.from_numpy(rw).to(gpu),
                           torch.from_numpy(rids).to(gpu), out_dtype=torch.float32, path=path)
-    ref = O.moe_layer(xb, rids, rw, w13.deq_f32, w2.deq_f32,
-                      shared=[(w13.deq_f32(E + s), w2.deq_f32(E + s)) for s in range(S)])
+    # REF decode follows the reference's lut_gemv (unrounded cb*absmax products),
+    # REF prefill its dequant-then-GEMM branch (bf16 weights); BL4 weights are the
+    # bf16 table entries on both paths.
+    f13, f2 = (w13.gemv_f32, w2.gemv_f32) if (fmt == "ref" and path == 1) else (w13.deq_f32, w2.deq_f32)
+    ref = O.moe_layer(xb, rids, rw, f13, f2, shared=[(f13(E + s), f2(E + s)) for s in range(S)])
     assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
 
 
