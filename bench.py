@@ -1,0 +1,305 @@
+#!/usr/bin/env python3
+"""Benchmark of the LUT-MoE hot path on one MI355X.
+
+Default workload (one step = one MoE layer decode step):
+  Qwen1.5-MoE-A2.7B-shaped layer, hidden 2048, moe_intermediate 1408, 60
+  routed experts, top-4 softmax routing of N(0,1) logits, SwiGLU gate/up/down
+  all BL4 4-bit (64-weight blocks, 16-entry codebooks), T = 1 token of bf16
+  N(0,1) activations.  Each step is one call of the MoE block forward from
+  router logits: two kernels, each recomputing the softmax/top-k routing and
+  the token permutation in-CTA, the first running the grouped LUT-GEMV gate/up
+  + SwiGLU, the second the down projection + weighted combine.  Steps rotate over 16 distinct layer weight copies (8.3 GB,
+  each step with its own routing) so the touched bytes per rotation exceed
+  the 256 MB Infinity Cache: the figure is cold-HBM, not MALL.
+
+value      = algorithmic HBM bytes of the timed steps / timed seconds (TB/s);
+             algorithmic bytes per step = sum over the step's distinct routed
+             experts of 8,650,752 B (codes 0.5 B/weight + bf16 tables
+             32 B per 64 weights) + 2*T*H*2 B of activations.
+roofline   = the gate/up + SwiGLU kernel (the dominant kernel) timed alone with
+             HIP events over a captured graph of its launches.
+cpu_baseline = the reference's CPU dequant + matmul path restated with torch
+             on the host (oracle/cpu_baseline.py), on a bounded sample of the
+             same steps.
+extra      = the other configurations (decode T=8/32, DeepSeek-V2-Lite prefill
+             grouped GEMM TFLOP/s, switch-base-8 single linear, hot-cache decode).
+
+Weights are synthetic BL4 data of the configured shapes (uniform random 4-bit
+codes, sorted N(0, 0.02) codebook entries): throughput does not depend on the
+values.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "LUT-MoE layer µs/token + achieved HBM TB/s (bs=1); prefill grouped-GEMM TFLOP/s"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+QWEN = dict(H=2048, I=1408, E=60, k=4, S=0)
+DSV2 = dict(H=2048, I=1408, E=64, k=6, S=2)
+BYTES_PER_WEIGHT = 1.0   # BL4: 0.5 B codes + 32 B table per 64 weights
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=480)
+    p.add_argument("--warmup", type=int, default=32)
+    p.add_argument("--tokens", type=int, default=1)
+    p.add_argument("--layers", type=int, default=16, help="rotating layer weight copies")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--no-extra", action="store_true", help="skip the other configurations")
+    p.add_argument("--cpu-seconds", type=float, default=12.0)
+    return p.parse_args()
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU only (every box here has one GPU); --gpus {a.gpus} "
+              "is not supported", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from block_lut_amd import ops
+    from block_lut_amd import _native as N
+    from block_lut_amd.formats import BL4Stack, MoEWeights
+
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    gen = torch.Generator(device="cpu").manual_seed(1234)
+
+    def rand_stack(E, M, K):
+        codes = torch.randint(0, 256, (E, M, K // 2), dtype=torch.uint8, device=dev)
+        tabs = torch.randn((E, M, K // 64, 16), device=dev) * 0.02
+        tabs = torch.sort(tabs, dim=-1).values.to(torch.bfloat16)
+        return BL4Stack(codes, tabs)
+
+    def rand_layer(c):
+        E = c["E"] + c["S"]
+        return MoEWeights(rand_stack(E, 2 * c["I"], c["H"]), rand_stack(E, c["H"], c["I"]),
+                          c["H"], c["I"], c["E"], c["S"])
+
+    def expert_bytes(c):
+        return 3 * c["H"] * c["I"] * BYTES_PER_WEIGHT
+
+    class Step:
+        """Preallocated inputs/outputs of one layer step (graph-capturable)."""
+
+        def __init__(self, layer, c, T):
+            self.layer, self.c, self.T = layer, c, T
+            self.logits = torch.randn((T, c["E"]), generator=gen).to(dev)
+            self.x = torch.randn((T, c["H"]), generator=gen).to(torch.bfloat16).to(dev)
+            self.w = torch.empty((T, c["k"]), dtype=torch.float32, device=dev)
+            self.ids = torch.empty((T, c["k"]), dtype=torch.int32, device=dev)
+            self.out = torch.empty((T, c["H"]), dtype=torch.bfloat16, device=dev)
+            self.ws = torch.empty(ops.moe_workspace_bytes(layer, T, c["k"]), dtype=torch.uint8,
+                                  device=dev)
+            ops.route_topk(self.logits, c["k"], out_w=self.w, out_ids=self.ids)
+            torch.cuda.synchronize()
+            ids = self.ids.cpu()
+            self.U = int(torch.unique(ids).numel()) + c["S"]
+            self.bytes = self.U * expert_bytes(c) + 2 * T * c["H"] * 2
+            self.bytes_gate_up = self.U * 2 * c["H"] * c["I"] * BYTES_PER_WEIGHT + T * c["H"] * 2
+
+        def run(self, path=ops.PATH_AUTO, stages=N.STAGE_ALL):
+            ops.moe_forward_logits(self.layer, self.x, self.logits, self.c["k"], out=self.out,
+                                   workspace=self.ws, path=path, stages=stages)
+
+    def graph_of(fns):
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for f in fns:
+                f()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for f in fns:
+                f()
+        torch.cuda.synchronize()
+        return g
+
+    def time_graph(g, reps):
+        st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        st.record()
+        for _ in range(reps):
+            g.replay()
+        en.record()
+        torch.cuda.synchronize()
+        return st.elapsed_time(en) / 1e3   # seconds
+
+    # ------------------------------------------------------------ main leg
+    c = QWEN
+    T = a.tokens
+    log(f"[bench] building {a.layers} Qwen-shaped BL4 layers ({a.layers * c['E'] * expert_bytes(c) / 1e9:.1f} GB)")
+    layers = [rand_layer(c) for _ in range(a.layers)]
+    steps = [Step(L, c, T) for L in layers]
+    g_step = graph_of([s.run for s in steps])
+    reps_w = max(1, -(-a.warmup // len(steps)))
+    reps = max(1, -(-a.steps // len(steps)))
+    K = reps * len(steps)
+    W = reps_w * len(steps)
+    time_graph(g_step, reps_w)
+    log(f"[bench] warmup {W} steps done; timing {K} steps")
+    secs = time_graph(g_step, reps)
+    bytes_total = reps * sum(s.bytes for s in steps)
+    value_tbs = bytes_total / secs / 1e12
+    ms_per_step = secs / K * 1e3
+    us_per_token = ms_per_step * 1e3 / T
+    log(f"[bench] {ms_per_step * 1e3:.2f} us/layer-step, {value_tbs:.3f} TB/s")
+
+    # dominant kernel alone: gate/up + SwiGLU grouped LUT-GEMV
+    g_gu = graph_of([lambda s=s: s.run(stages=N.STAGE_GATE_UP) for s in steps])
+    time_graph(g_gu, 4)
+    r_gu = max(8, reps // 2)
+    secs_gu = time_graph(g_gu, r_gu)
+    dur_gu = secs_gu / (r_gu * len(steps))
+    bytes_gu = sum(s.bytes_gate_up for s in steps) / len(steps)
+    ach_gu = bytes_gu / dur_gu / 1e9
+    g_dn = graph_of([lambda s=s: s.run(stages=N.STAGE_DOWN) for s in steps])
+    secs_dn = time_graph(g_dn, r_gu)
+    dur_dn = secs_dn / (r_gu * len(steps))
+    bytes_dn = sum(s.U * c["H"] * c["I"] * BYTES_PER_WEIGHT for s in steps) / len(steps)
+    log(f"[bench] gate_up kernel {dur_gu * 1e6:.2f} us ({ach_gu:.0f} GB/s); "
+        f"down+combine {dur_dn * 1e6:.2f} us ({bytes_dn / dur_dn / 1e9:.0f} GB/s)")
+
+    result = {
+        "metric": METRIC,
+        "value": round(value_tbs, 4),
+        "unit": "TB/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random BL4 codes and sorted N(0,0.02) codebooks of the configured "
+                "shapes; N(0,1) bf16 activations and router logits)",
+        "config": {"workload": f"Qwen1.5-MoE-A2.7B-shaped MoE layer decode, T={T} token(s): "
+                               "H2048 I1408 E60 top-4 softmax, SwiGLU BL4 4-bit (64-weight "
+                               f"blocks, 16-entry codebooks); {a.layers} rotating layer copies "
+                               "(cold HBM)",
+                   "tokens": T, "rotating_layers": a.layers,
+                   "avg_distinct_experts": round(sum(s.U for s in steps) / len(steps), 3)},
+        "us_per_token": round(us_per_token, 3),
+        "tokens_per_s": round(T / (ms_per_step / 1e3), 1),
+        "roofline": {"bound": "hbm", "kernel": "bl4_decode_gate_up<1>",
+                     "achieved": round(ach_gu, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(ach_gu / HBM_PEAK_GBS, 4), "traffic": None,
+                     "avg_launch_us": round(dur_gu * 1e6, 3),
+                     "algorithmic_bytes_per_launch": int(bytes_gu)},
+        "kernels": {"decode_down_combine_us": round(dur_dn * 1e6, 3),
+                    "decode_down_combine_GBs": round(bytes_dn / dur_dn / 1e9, 1)},
+    }
+
+    # ---------------------------------------------------------- extra configs
+    if not a.no_extra:
+        extra = {}
+        # hot cache: one layer, same routing every step
+        g_hot = graph_of([steps[0].run] * 16)
+        time_graph(g_hot, 4)
+        sh = time_graph(g_hot, 16) / (16 * 16)
+        extra["decode_T1_hot_cache_us"] = round(sh * 1e6, 3)
+        extra["decode_T1_hot_cache_TBs"] = round(steps[0].bytes / sh / 1e12, 3)
+        for Tn in (8, 32):
+            ss = [Step(L, c, Tn) for L in layers]
+            g = graph_of([s.run for s in ss])
+            time_graph(g, 2)
+            sec = time_graph(g, 8) / (8 * len(ss))
+            b = sum(s.bytes for s in ss) / len(ss)
+            extra[f"decode_T{Tn}_us_per_layer"] = round(sec * 1e6, 2)
+            extra[f"decode_T{Tn}_TBs"] = round(b / sec / 1e12, 3)
+            extra[f"decode_T{Tn}_avg_distinct_experts"] = round(sum(s.U for s in ss) / len(ss), 2)
+            log(f"[bench] decode T={Tn}: {sec * 1e6:.1f} us/layer, {b / sec / 1e12:.3f} TB/s")
+            del ss, g
+        del layers, steps, g_step, g_gu, g_dn, g_hot
+        torch.cuda.empty_cache()
+        # DeepSeek-V2-Lite prefill, 2048 tokens, grouped MFMA GEMM
+        d = DSV2
+        lay = rand_layer(d)
+        sp = Step(lay, d, 2048)
+        g = graph_of([lambda: sp.run(path=ops.PATH_MFMA)])
+        time_graph(g, 2)
+        sec = time_graph(g, 10) / 10
+        flops = 6 * d["H"] * d["I"] * 2048 * (d["k"] + d["S"])
+        extra["prefill_dsv2_T2048_us"] = round(sec * 1e6, 1)
+        extra["prefill_dsv2_T2048_TFLOPs"] = round(flops / sec / 1e12, 1)
+        extra["prefill_dsv2_T2048_frac_bf16_peak"] = round(flops / sec / 1e12 / BF16_PEAK_TFLOPS, 4)
+        log(f"[bench] prefill DeepSeek T=2048: {sec * 1e6:.0f} us, {flops / sec / 1e12:.1f} TFLOP/s")
+        # switch-base-8 single BL4 linear 768 -> 3072, one token
+        st1 = rand_stack(1, 3072, 768)
+        x1 = torch.randn((1, 768), device=dev).to(torch.bfloat16)
+        y1 = torch.empty((1, 3072), dtype=torch.bfloat16, device=dev)
+
+        def c1():
+            y1.copy_(ops.gemv(st1, x1))
+        g = graph_of([c1] * 32)
+        time_graph(g, 2)
+        sec = time_graph(g, 10) / (10 * 32)
+        extra["switch_linear_768x3072_us"] = round(sec * 1e6, 3)
+        result["extra"] = extra
+
+    # ------------------------------------------------------------ CPU leg
+    if not a.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(a, c, T)
+
+    print(json.dumps(result), flush=True)
+
+
+def cpu_baseline(a, c, T):
+    """The reference's CPU dequant + matmul path on a bounded sample of the
+    same workload (Qwen layer decode, T tokens, top-4 of 60 experts)."""
+    import torch
+    from oracle.cpu_baseline import moe_layer_step
+    ncores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(ncores)
+    g = torch.Generator().manual_seed(99)
+    H, I, E, k = c["H"], c["I"], c["E"], c["k"]
+    experts13, experts2 = {}, {}
+
+    def expert(e):
+        if e not in experts13:
+            experts13[e] = (torch.randint(0, 256, (2 * I, H // 2), dtype=torch.uint8, generator=g),
+                            torch.sort(torch.randn((2 * I, H // 64, 16), generator=g) * 0.02,
+                                       dim=-1).values.to(torch.bfloat16))
+            experts2[e] = (torch.randint(0, 256, (H, I // 2), dtype=torch.uint8, generator=g),
+                           torch.sort(torch.randn((H, I // 64, 16), generator=g) * 0.02,
+                                      dim=-1).values.to(torch.bfloat16))
+
+    steps, nbytes, t_total = 0, 0, 0.0
+    while t_total < a.cpu_seconds and steps < 1000:
+        logits = torch.randn((T, E), generator=g)
+        w, ids = torch.topk(torch.softmax(logits, -1), k, dim=-1)
+        for e in torch.unique(ids).tolist():
+            expert(e)
+        x = torch.randn((T, H), generator=g).to(torch.bfloat16)
+        t0 = time.perf_counter()
+        moe_layer_step(x, ids, w, experts13, experts2)
+        t_total += time.perf_counter() - t0
+        nbytes += int(torch.unique(ids).numel()) * 3 * H * I * BYTES_PER_WEIGHT + 2 * T * H * 2
+        steps += 1
+    return {"value": round(nbytes / t_total / 1e12, 6), "unit": "TB/s", "cores": ncores,
+            "kind": "port",
+            "us_per_token": round(t_total / steps / T * 1e6, 1),
+            "sample": f"{steps} Qwen-shaped layer decode steps (T={T}, top-4 of 60 BL4 experts), "
+                      "torch CPU dequant gather + bf16 F.linear, "
+                      f"{t_total:.1f} s"}
+
+
+if __name__ == "__main__":
+    main()

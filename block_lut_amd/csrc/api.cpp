@@ -65,7 +65,7 @@ int validate_ref_vector(const lutmoe_weights* w) {
 size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct MoeLayout {
-    size_t pair_ids, pair_w, offsets, perm, inv, active, act, y, total;
+    size_t route, topk_w, topk_ids, pair_ids, pair_w, offsets, perm, inv, active, act, y, total;
 };
 
 MoeLayout moe_layout(const lutmoe_moe_desc* d, int T, int k) {
@@ -73,6 +73,9 @@ MoeLayout moe_layout(const lutmoe_moe_desc* d, int T, int k) {
     const size_t P = (size_t)T * (k + d->num_shared);
     MoeLayout L{};
     size_t o = 0;
+    L.route = o;    o = align_up(o + decode_route_bytes());
+    L.topk_w = o;   o = align_up(o + (size_t)T * k * 4);
+    L.topk_ids = o; o = align_up(o + (size_t)T * k * 4);
     L.pair_ids = o; o = align_up(o + P * 4);
     L.pair_w = o;   o = align_up(o + P * 4);
     L.offsets = o;  o = align_up(o + (E_tot + 1) * 4);
@@ -287,17 +290,14 @@ size_t lutmoe_moe_workspace_size(const lutmoe_moe_desc* d, int T, int k) {
     return moe_layout(d, T, k).total;
 }
 
-int lutmoe_moe_forward(const lutmoe_moe_desc* d, const void* x, const float* topk_w,
-                       const int32_t* topk_ids, int T, int k, void* out, int out_dtype,
-                       void* workspace, size_t ws_bytes, int force_path, void* stream) {
-    return lutmoe_moe_forward_stages(d, x, topk_w, topk_ids, T, k, out, out_dtype, workspace,
-                                     ws_bytes, force_path, LUTMOE_STAGE_ALL, stream);
-}
+namespace {
 
-int lutmoe_moe_forward_stages(const lutmoe_moe_desc* d, const void* x, const float* topk_w,
-                              const int32_t* topk_ids, int T, int k, void* out, int out_dtype,
-                              void* workspace, size_t ws_bytes, int force_path, int stages,
-                              void* stream) {
+// Shared body of the MoE entry points.  Exactly one of (topk_w, topk_ids) and
+// logits is given.
+int moe_forward_impl(const lutmoe_moe_desc* d, const void* x, const float* topk_w,
+                     const int32_t* topk_ids, const float* logits, int T, int k, int renorm,
+                     float scaling, void* out, int out_dtype, void* workspace, size_t ws_bytes,
+                     int force_path, int stages, void* stream) {
     if (stages <= 0 || stages > LUTMOE_STAGE_ALL) return LUTMOE_EINVAL;
     int rc = validate_moe(d);
     if (rc) return rc;
@@ -305,7 +305,9 @@ int lutmoe_moe_forward_stages(const lutmoe_moe_desc* d, const void* x, const flo
     if (out_dtype != LUTMOE_DTYPE_BF16 && out_dtype != LUTMOE_DTYPE_F32) return LUTMOE_EINVAL;
     if (force_path < 0 || force_path > 2) return LUTMOE_EINVAL;
     if (T == 0) return LUTMOE_OK;
-    if (!x || !topk_w || !topk_ids || !out || !workspace) return LUTMOE_EINVAL;
+    const bool by_logits = logits != nullptr;
+    if (!x || !out || !workspace || (!by_logits && (!topk_w || !topk_ids))) return LUTMOE_EINVAL;
+    if (by_logits && d->num_routed > 320) return LUTMOE_EUNSUPPORTED;
     if (!aligned(x, 16) || !aligned(out, 16) || !aligned(workspace, 256)) return LUTMOE_EALIGN;
     const MoeLayout L = moe_layout(d, T, k);
     if (ws_bytes < L.total) return LUTMOE_EWORKSPACE;
@@ -313,10 +315,17 @@ int lutmoe_moe_forward_stages(const lutmoe_moe_desc* d, const void* x, const flo
     const int64_t P = (int64_t)T * ke;
     if (P >= (1ll << 31) / (d->hidden > d->inter ? d->hidden : d->inter)) return LUTMOE_EUNSUPPORTED;
     const bool lds_ok = P * 8 * 4 <= 48 * 1024;
-    bool gemv = force_path == 1 || (force_path == 0 && T <= 32 && lds_ok);
+    const bool gemv = force_path == 1 || (force_path == 0 && T <= 32 && lds_ok);
     if (gemv && !lds_ok) return LUTMOE_EUNSUPPORTED;
 
     char* ws = (char*)workspace;
+    uint16_t* act = (uint16_t*)(ws + L.act);
+    hipStream_t s = stream_of(stream);
+    if (gemv && decode_v2_supported(d, T, k)) {
+        // routing + permutation happen inside both decode kernels
+        return launch_decode_v2(d, (const uint16_t*)x, topk_w, topk_ids, logits, T, k, renorm,
+                                scaling, act, ws + L.route, out, out_dtype, stages, s);
+    }
     int32_t* pair_ids = (int32_t*)(ws + L.pair_ids);
     float* pair_w = (float*)(ws + L.pair_w);
     MoeRouting r;
@@ -328,11 +337,15 @@ int lutmoe_moe_forward_stages(const lutmoe_moe_desc* d, const void* x, const flo
     r.T = T;
     r.k_eff = ke;
     r.num_experts_total = E_tot;
-    uint16_t* act = (uint16_t*)(ws + L.act);
     float* y = (float*)(ws + L.y);
-    hipStream_t s = stream_of(stream);
-
     if (stages & LUTMOE_STAGE_ROUTE) {
+        if (by_logits) {
+            float* tw = (float*)(ws + L.topk_w);
+            int32_t* ti = (int32_t*)(ws + L.topk_ids);
+            if ((rc = launch_route_topk(logits, T, E, k, renorm, scaling, tw, ti, s))) return rc;
+            topk_w = tw;
+            topk_ids = ti;
+        }
         if ((rc = launch_build_pairs(topk_ids, topk_w, T, k, E, S, pair_ids, pair_w, s))) return rc;
         if ((rc = launch_permute(pair_ids, T, ke, E_tot, (int32_t*)r.offsets, (int32_t*)r.perm,
                                  (int32_t*)r.inv, (int32_t*)r.active, s)))
@@ -355,6 +368,34 @@ int lutmoe_moe_forward_stages(const lutmoe_moe_desc* d, const void* x, const flo
         return launch_combine(y, r.inv, T, ke, d->hidden, out, out_dtype, s);
     }
     return LUTMOE_OK;
+}
+
+}  // namespace
+
+int lutmoe_moe_forward(const lutmoe_moe_desc* d, const void* x, const float* topk_w,
+                       const int32_t* topk_ids, int T, int k, void* out, int out_dtype,
+                       void* workspace, size_t ws_bytes, int force_path, void* stream) {
+    if (!topk_w || !topk_ids) return T == 0 ? LUTMOE_OK : LUTMOE_EINVAL;
+    return moe_forward_impl(d, x, topk_w, topk_ids, nullptr, T, k, 0, 1.0f, out, out_dtype,
+                            workspace, ws_bytes, force_path, LUTMOE_STAGE_ALL, stream);
+}
+
+int lutmoe_moe_forward_stages(const lutmoe_moe_desc* d, const void* x, const float* topk_w,
+                              const int32_t* topk_ids, int T, int k, void* out, int out_dtype,
+                              void* workspace, size_t ws_bytes, int force_path, int stages,
+                              void* stream) {
+    if (!topk_w || !topk_ids) return T == 0 ? LUTMOE_OK : LUTMOE_EINVAL;
+    return moe_forward_impl(d, x, topk_w, topk_ids, nullptr, T, k, 0, 1.0f, out, out_dtype,
+                            workspace, ws_bytes, force_path, stages, stream);
+}
+
+int lutmoe_moe_forward_logits(const lutmoe_moe_desc* d, const void* x, const float* logits,
+                              int T, int k, int renormalize, float scaling, void* out,
+                              int out_dtype, void* workspace, size_t ws_bytes, int force_path,
+                              int stages, void* stream) {
+    if (!logits) return T == 0 ? LUTMOE_OK : LUTMOE_EINVAL;
+    return moe_forward_impl(d, x, nullptr, nullptr, logits, T, k, renormalize, scaling, out,
+                            out_dtype, workspace, ws_bytes, force_path, stages, stream);
 }
 
 // --------------------------------------------------------------- encoders

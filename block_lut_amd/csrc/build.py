@@ -17,7 +17,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
 ROOT = os.path.dirname(PKG)
 LIB = os.path.join(PKG, "liblutmoe.so")
-SOURCES = ["api.cpp", "dequant.hip", "gemv.hip", "route.hip", "gemm.hip", "encode.hip"]
+SOURCES = ["api.cpp", "dequant.hip", "gemv.hip", "decode.hip", "route.hip", "gemm.hip",
+           "encode.hip"]
 ARCH = "gfx950"
 
 

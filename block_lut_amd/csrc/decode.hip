@@ -1,0 +1,586 @@
+// Decode-time fused MoE layer on BL4 weights: two kernels per layer.
+//
+//   bl4_decode_gate_up : routing + permutation (recomputed in every CTA from
+//                        top-k ids or router logits; T*k is small at decode)
+//                        -> grouped LUT-GEMV over W13 rows -> SwiGLU
+//                        -> act[position][I] (bf16)
+//   bl4_decode_down    : the same routing -> grouped LUT-GEMV over W2 rows
+//                        of every active expert -> per-position results meet
+//                        in LDS -> weighted sum per token in slot order -> out
+//
+// Reference behaviour: LUTFusedMoEMethod.apply, decode branch
+// (vllm_lut/quant_method.py:250-260), routing of moe_layer._routing
+// (vllm_lut/moe_layer.py:358-376), shared experts added with weight 1
+// (customized/deepseek.py:111-115).
+//
+// GEMV layout (see lut_core.h): a wave owns 8 weight rows; in a 512-column
+// chunk lane l = 8g + q reads the code dword q of block g of every row and
+// the same-offset dword of that block's bf16 table (codes and tables are both
+// K/2 bytes per row), stages the tables in its LDS slot and looks each
+// nibble up there.  All chunk loads of a chunk group are issued before any is
+// consumed so a wave keeps up to 16 KB in flight.
+#include <utility>
+
+#include "common.h"
+#include "kernels.h"
+#include "lut_core.h"
+
+using namespace lutmoe;
+
+namespace {
+
+constexpr int kChunk = 512;
+constexpr int kRows = 8;
+constexpr int kSlot = kRows * 256;
+constexpr int kMaxEtot = 320;
+constexpr int kMaxP = 512;
+
+// Routing result: active experts (ascending), per-expert position offsets,
+// the expert-major position -> pair map and its inverse, pair weights.  Lives
+// in LDS; the same layout is the global copy written by decode_route_kernel.
+struct RouteOut {
+    int nact;
+    int act[kMaxEtot];                  // active expert ids, ascending
+    int aoff[kMaxEtot];                 // first position of active slot a
+    int an[kMaxEtot];                   // positions (pairs) of active slot a
+    int off[kMaxEtot + 1];
+    int perm[kMaxP];
+    int inv[kMaxP];
+    float pw[kMaxP];
+};
+
+struct RouteScratch {
+    int pid[kMaxP];                     // expert of each pair (-1: dropped)
+    int rin[kMaxP];                     // rank among same-expert pairs of its 64-pair chunk
+    int ccnt[kMaxP / 64][kMaxEtot];     // per chunk, per expert count -> exclusive prefix
+};
+
+struct DecodeArgs {
+    lutmoe_moe_desc d;
+    const uint16_t* x;         // [T][H] bf16
+    const float* topk_w;       // [T][k] (ids mode)
+    const int32_t* topk_ids;   // [T][k] (ids mode)
+    const float* logits;       // [T][E] fp32 (logits mode: topk_ids == nullptr)
+    int T, k, renorm;
+    float scaling;
+    uint16_t* act;             // [P][I] bf16
+    void* out;
+    int out_dtype;
+    RouteOut* route;           // global copy (precomputed-routing mode)
+};
+
+template <int Q>
+__device__ __forceinline__ int rdl(int v) { return __builtin_amdgcn_readlane(v, Q); }
+template <int Q>
+__device__ __forceinline__ float rdlf(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), Q));
+}
+
+// r += #{lanes q : (v_q > v) or (v_q == v and q < lane)} over the wave; the
+// other lanes' values are read back with readlane (no LDS).
+template <int Q>
+__device__ __forceinline__ void rank_step(float v, int lane, int& r) {
+    const float uq = rdlf<Q>(v);
+    r += (uq > v) || (uq == v && Q < lane);
+}
+template <int... Q>
+__device__ __forceinline__ void rank_all(float v, int lane, int& r, std::integer_sequence<int, Q...>) {
+    (rank_step<Q>(v, lane, r), ...);
+}
+
+// in-chunk stable rank of each lane's expert id, and whether it is the last
+// lane of that expert in the chunk.
+template <int Q>
+__device__ __forceinline__ void match_step(int e, int lane, int& before, int& after) {
+    const int u = rdl<Q>(e);
+    before += (Q < lane) & (u == e);
+    after += (Q > lane) & (u == e);
+}
+template <int... Q>
+__device__ __forceinline__ void match_all(int e, int lane, int& before, int& after,
+                                          std::integer_sequence<int, Q...>) {
+    (match_step<Q>(e, lane, before, after), ...);
+}
+
+// Routing + permutation of all T*(k+S) pairs into LDS; identical in every CTA
+// that runs it.  Cross-lane work is readlane/DPP only (no LDS round trips in
+// the rank loops).
+__device__ void cta_route(const DecodeArgs& A, RouteOut& R, RouteScratch& X) {
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int E = A.d.num_routed, S = A.d.num_shared, E_tot = E + S;
+    const int k = A.k, ke = k + S, T = A.T, P = T * ke;
+    const int nchunk = (P + 63) / 64;
+    for (int i = tid; i < nchunk * E_tot; i += 256) X.ccnt[i / E_tot][i % E_tot] = 0;
+    if (A.topk_ids) {
+        for (int p = tid; p < P; p += 256) {
+            const int t = p / ke, s = p - t * ke;
+            int e;
+            float w;
+            if (s < k) {
+                e = A.topk_ids[t * k + s];
+                w = A.topk_w[t * k + s];
+                if (e < 0 || e >= E) e = -1;
+            } else {
+                e = E + s - k;
+                w = 1.0f;
+            }
+            X.pid[p] = e;
+            R.pw[p] = w;
+        }
+    } else {
+        // logits mode, wave per token: softmax in fp32; top-k by logit (softmax
+        // is monotone): rank(e) = #{e' : l[e'] > l[e] or (l[e'] == l[e], e' < e)}.
+        for (int t = wv; t < T; t += 4) {
+            const float* src = A.logits + (int64_t)t * E;
+            float mx = -INFINITY;
+            for (int e = lane; e < E; e += 64) mx = fmaxf(mx, src[e]);
+            mx = wave_reduce_max(mx);
+            float ps = 0.f;
+            for (int e = lane; e < E; e += 64) ps += expf(src[e] - mx);
+            const float sum = wave_reduce(ps);
+            float wsum = 0.f;
+            if (E <= 64) {
+                // one logit per lane; ranks from readlane (no LDS round trips)
+                const float v = lane < E ? src[lane] : -INFINITY;
+                int r = 0;
+                rank_all(v, lane, r, std::make_integer_sequence<int, 64>{});
+                const bool sel = lane < E && r < k;
+                const float pj = sel ? expf(v - mx) / sum : 0.f;
+                wsum = wave_reduce(pj);
+                if (sel) {
+                    X.pid[t * ke + r] = lane;
+                    R.pw[t * ke + r] = (A.renorm ? pj / wsum : pj) * A.scaling;
+                }
+            } else {
+                float lsum = 0.f;
+                for (int e = lane; e < E; e += 64) {
+                    const float v = src[e];
+                    int r = 0;
+#pragma unroll 8
+                    for (int q = 0; q < E; ++q) {
+                        const float u = src[q];
+                        r += (u > v) || (u == v && q < e);
+                    }
+                    if (r < k) {
+                        const float pj = expf(v - mx) / sum;
+                        X.pid[t * ke + r] = e;
+                        R.pw[t * ke + r] = pj;
+                        lsum += pj;
+                    }
+                }
+                wsum = wave_reduce(lsum);
+                wave_lds_sync();
+                if (lane < k) {
+                    const float pj = R.pw[t * ke + lane];
+                    R.pw[t * ke + lane] = (A.renorm ? pj / wsum : pj) * A.scaling;
+                }
+            }
+            if (lane < S) {
+                X.pid[t * ke + k + lane] = E + lane;
+                R.pw[t * ke + k + lane] = 1.0f;
+            }
+        }
+    }
+    __syncthreads();
+    // stable ranks inside 64-pair chunks + per-chunk expert counts
+    for (int c = wv; c < nchunk; c += 4) {
+        const int p = c * 64 + lane;
+        const int e = p < P ? X.pid[p] : -1;
+        int before = 0, after = 0;
+        match_all(e, lane, before, after, std::make_integer_sequence<int, 64>{});
+        if (p < P) X.rin[p] = before;
+        if (e >= 0 && after == 0) X.ccnt[c][e] = before + 1;
+    }
+    __syncthreads();
+    if (wv == 0) {
+        // lane l owns experts [l*per, l*per+per): totals, chunk prefixes
+        const int per = (E_tot + 63) / 64;
+        int c = 0, a = 0;
+        for (int q = 0; q < per; ++q) {
+            const int e = lane * per + q;
+            if (e < E_tot) {
+                int run = 0;
+                for (int ch = 0; ch < nchunk; ++ch) {
+                    const int v = X.ccnt[ch][e];
+                    X.ccnt[ch][e] = run;
+                    run += v;
+                }
+                c += run;
+                a += run > 0;
+                R.off[e] = run;   // total for now
+            }
+        }
+        const int ic = wave_scan_incl(c), ia = wave_scan_incl(a);
+        int oc = ic - c, oa = ia - a;
+        for (int q = 0; q < per; ++q) {
+            const int e = lane * per + q;
+            if (e < E_tot) {
+                const int n = R.off[e];
+                R.off[e] = oc;
+                if (n > 0) R.act[oa++] = e;
+                oc += n;
+            }
+        }
+        if (lane == 63) { R.off[E_tot] = ic; R.nact = ia; }
+    }
+    __syncthreads();
+    for (int a = tid; a < R.nact; a += 256) {
+        const int e = R.act[a];
+        R.aoff[a] = R.off[e];
+        R.an[a] = R.off[e + 1] - R.off[e];
+    }
+    for (int p = tid; p < P; p += 256) {
+        const int e = X.pid[p];
+        if (e < 0) { R.inv[p] = -1; continue; }
+        const int pos = R.off[e] + X.ccnt[p >> 6][e] + X.rin[p];
+        R.perm[pos] = p;
+        R.inv[p] = pos;
+    }
+    __syncthreads();
+}
+
+// Single-wave routing for P = T*(k+S) <= 64 pairs (the decode case): lane p
+// holds pair p.  Top-k from logits needs E <= 64 (lane = expert): k rounds of
+// a DPP wave max, the lowest lane holding it wins (ties -> lower id).
+// Positions and the active list come from runtime-bounded readlane loops over
+// the P pairs.  Only wave 0 works; the others wait at the CTA barrier.
+__device__ void wave_route_small(const DecodeArgs& A, RouteOut& R) {
+    const int lane = threadIdx.x & 63;
+    const int E = A.d.num_routed, S = A.d.num_shared;
+    const int k = A.k, ke = k + S, T = A.T, P = T * ke;
+    int e = -1;
+    float w = 0.f;
+    if (A.topk_ids) {
+        if (lane < P) {
+            const int t = lane / ke, sl = lane - t * ke;
+            if (sl < k) {
+                e = A.topk_ids[t * k + sl];
+                w = A.topk_w[t * k + sl];
+                if (e < 0 || e >= E) e = -1;
+            } else {
+                e = E + sl - k;
+                w = 1.0f;
+            }
+        }
+    } else {
+        for (int t = 0; t < T; ++t) {
+            float v = lane < E ? A.logits[(int64_t)t * E + lane] : -INFINITY;
+            const float mx = wave_reduce_max(v);
+            const float sum = wave_reduce(lane < E ? expf(v - mx) : 0.f);
+            float wsum = 0.f;
+            for (int j = 0; j < k; ++j) {
+                const float m = wave_reduce_max(v);
+                const uint64_t b = __ballot(lane < E && v == m);
+                const int sel = (int)__builtin_ctzll(b);
+                const float pj = expf(m - mx) / sum;
+                wsum += pj;
+                if (lane == t * ke + j) { e = sel; w = pj; }
+                if (lane == sel) v = -INFINITY;
+            }
+            if (lane >= t * ke && lane < t * ke + k) w = (A.renorm ? w / wsum : w) * A.scaling;
+            if (lane >= t * ke + k && lane < (t + 1) * ke) { e = E + lane - t * ke - k; w = 1.0f; }
+        }
+    }
+    int less = 0, before = 0, cnt = 0;
+    for (int q = 0; q < P; ++q) {
+        const int u = __builtin_amdgcn_readlane(e, q);
+        less += (u >= 0) & (u < e);
+        before += (u == e) & (q < lane);
+        cnt += (u == e);
+    }
+    const bool valid = lane < P && e >= 0;
+    const uint64_t first = __ballot(valid && before == 0);
+    int arank = 0;
+    for (int q = 0; q < P; ++q) {
+        const int u = __builtin_amdgcn_readlane(e, q);
+        arank += (int)((first >> q) & 1ull) & (u < e);
+    }
+    if (valid && before == 0) {
+        R.act[arank] = e;
+        R.aoff[arank] = less;
+        R.an[arank] = cnt;
+    }
+    if (lane < P) {
+        const int pos = valid ? less + before : -1;
+        R.inv[lane] = pos;
+        R.pw[lane] = w;
+        if (valid) R.perm[pos] = lane;
+    }
+    if (lane == 0) R.nact = __popcll(first);
+}
+
+// Routing into LDS: computed here, or copied from the precomputed global copy.
+template <bool kPre>
+__device__ __forceinline__ void get_route(const DecodeArgs& A, RouteOut& R, RouteScratch& X) {
+    if constexpr (kPre) {
+        const int E_tot = A.d.num_routed + A.d.num_shared;
+        const int P = A.T * (A.k + A.d.num_shared);
+        const RouteOut* g = A.route;
+        for (int i = threadIdx.x; i < E_tot; i += 256) {
+            R.act[i] = g->act[i];
+            R.aoff[i] = g->aoff[i];
+            R.an[i] = g->an[i];
+        }
+        for (int i = threadIdx.x; i < P; i += 256) {
+            R.perm[i] = g->perm[i];
+            R.inv[i] = g->inv[i];
+            R.pw[i] = g->pw[i];
+        }
+        if (threadIdx.x == 0) R.nact = g->nact;
+        __syncthreads();
+    } else {
+        const int P = A.T * (A.k + A.d.num_shared);
+        if (P <= 64 && (A.topk_ids || A.d.num_routed <= 64)) {
+            if (threadIdx.x < 64) wave_route_small(A, R);
+            __syncthreads();
+        } else {
+            cta_route(A, R, X);
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void decode_route_kernel(DecodeArgs A) {
+    __shared__ RouteOut R;
+    __shared__ RouteScratch X;
+    cta_route(A, R, X);
+    const int E_tot = A.d.num_routed + A.d.num_shared;
+    const int P = A.T * (A.k + A.d.num_shared);
+    RouteOut* g = A.route;
+    for (int i = threadIdx.x; i < E_tot; i += 256) {
+        g->act[i] = R.act[i];
+        g->aoff[i] = R.aoff[i];
+        g->an[i] = R.an[i];
+    }
+    for (int i = threadIdx.x; i < P; i += 256) {
+        g->perm[i] = R.perm[i];
+        g->inv[i] = R.inv[i];
+        g->pw[i] = R.pw[i];
+    }
+    if (threadIdx.x == 0) g->nact = R.nact;
+}
+
+// One wave, 8 rows, chunks [c0, c0+CG) of K: loads first, then per chunk
+// stage tables in the wave's LDS slot and accumulate.
+template <int TB, int CG>
+__device__ __forceinline__ void bl4_rows8(const uint8_t* __restrict__ codes,
+                                          const uint8_t* __restrict__ tabs, const int (&rows)[kRows],
+                                          int K, int c0, int nch, int lane, uint8_t* slot,
+                                          const uint16_t* const (&xrow)[TB], int nt,
+                                          float (&acc)[kRows][TB]) {
+    const int nblk = K / kBlockBL;
+    uint32_t cw[CG][kRows], tw[CG][kRows];
+    uint32_t xs[CG][TB][4];
+#pragma unroll
+    for (int c = 0; c < CG; ++c) {
+        const int cc = c0 + c;
+        const bool ok = cc < nch && (cc * 8 + (lane >> 3)) < nblk;
+#pragma unroll
+        for (int r = 0; r < kRows; ++r) {
+            const int64_t off = (int64_t)rows[r] * (K / 2) + cc * 256 + 4 * lane;
+            cw[c][r] = ok ? *reinterpret_cast<const uint32_t*>(codes + off) : 0u;
+            tw[c][r] = ok ? *reinterpret_cast<const uint32_t*>(tabs + off) : 0u;
+        }
+#pragma unroll
+        for (int t = 0; t < TB; ++t) {
+            uint4 q = make_uint4(0u, 0u, 0u, 0u);
+            if (ok && t < nt) q = *reinterpret_cast<const uint4*>(xrow[t] + cc * kChunk + 8 * lane);
+            xs[c][t][0] = q.x; xs[c][t][1] = q.y; xs[c][t][2] = q.z; xs[c][t][3] = q.w;
+        }
+    }
+    const uint32_t gbase = lds_addr(slot) + ((lane >> 3) << 5);
+#pragma unroll
+    for (int c = 0; c < CG; ++c) {
+        if (c0 + c >= nch) break;
+#pragma unroll
+        for (int r = 0; r < kRows; ++r) *reinterpret_cast<uint32_t*>(slot + r * 256 + 4 * lane) = tw[c][r];
+        wave_lds_sync();
+#pragma unroll
+        for (int r = 0; r < kRows; ++r) bl4_dot8<TB>(cw[c][r], gbase + r * 256, xs[c], nt, acc[r]);
+        wave_lds_sync();
+    }
+}
+
+template <int TB, bool kPre>
+__global__ __launch_bounds__(256) void bl4_decode_gate_up(DecodeArgs A) {
+    __shared__ RouteOut R;
+    __shared__ RouteScratch X;
+    __shared__ __attribute__((aligned(16))) uint8_t s_slot[4 * kSlot];
+    get_route<kPre>(A, R, X);
+    const int a = blockIdx.y;
+    if (a >= R.nact) return;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int I = A.d.inter, H = A.d.hidden, ke = A.k + A.d.num_shared;
+    const int i0 = (blockIdx.x * 4 + wv) * 4;
+    if (i0 >= I) return;
+    const int e = R.act[a];
+    const int p0 = R.aoff[a], n = R.an[a];
+    int rows[kRows];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int i = min(i0 + j, I - 1);
+        rows[j] = i;
+        rows[4 + j] = I + i;
+    }
+    const int64_t per = (int64_t)A.d.w13.rows * (H / 2);
+    const uint8_t* codes = (const uint8_t*)A.d.w13.codes + e * per;
+    const uint8_t* tabs = (const uint8_t*)A.d.w13.tables + e * per;
+    const int nch = (H + kChunk - 1) / kChunk;
+    constexpr int CG = TB <= 2 ? 4 : 2;
+    uint8_t* slot = s_slot + wv * kSlot;
+    for (int tb = 0; tb < n; tb += TB) {
+        const int nt = min(TB, n - tb);
+        const uint16_t* xrow[TB];
+#pragma unroll
+        for (int t = 0; t < TB; ++t) xrow[t] = A.x + (int64_t)(R.perm[p0 + tb + min(t, nt - 1)] / ke) * H;
+        float acc[kRows][TB];
+#pragma unroll
+        for (int r = 0; r < kRows; ++r)
+#pragma unroll
+            for (int t = 0; t < TB; ++t) acc[r][t] = 0.f;
+        for (int c0 = 0; c0 < nch; c0 += CG)
+            bl4_rows8<TB, CG>(codes, tabs, rows, H, c0, nch, lane, slot, xrow, nt, acc);
+        float g[4][TB], u[4][TB];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int t = 0; t < TB; ++t) {
+                g[j][t] = wave_reduce(acc[j][t]);
+                u[j][t] = wave_reduce(acc[4 + j][t]);
+            }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int t = 0; t < TB; ++t)
+                if (lane == j * TB + t && t < nt && i0 + j < I)
+                    A.act[(int64_t)(p0 + tb + t) * I + i0 + j] = (uint16_t)f32_to_bf16(silu_mul(g[j][t], u[j][t]));
+    }
+}
+
+template <int TB, bool kPre>
+__global__ __launch_bounds__(256) void bl4_decode_down(DecodeArgs A) {
+    __shared__ RouteOut R;
+    __shared__ RouteScratch X;
+    __shared__ __attribute__((aligned(16))) uint8_t s_slot[4 * kSlot];
+    extern __shared__ float s_y[];   // [P][8]
+    get_route<kPre>(A, R, X);
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int I = A.d.inter, H = A.d.hidden, ke = A.k + A.d.num_shared;
+    const int h0 = blockIdx.x * kRows;
+    int rows[kRows];
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) rows[r] = min(h0 + r, H - 1);
+    const int64_t per = (int64_t)A.d.w2.rows * (I / 2);
+    const int nch = (I + kChunk - 1) / kChunk;
+    constexpr int CG = TB <= 2 ? 4 : 2;
+    uint8_t* slot = s_slot + wv * kSlot;
+    for (int a = wv; a < R.nact; a += 4) {
+        const int e = R.act[a];
+        const int p0 = R.aoff[a], n = R.an[a];
+        const uint8_t* codes = (const uint8_t*)A.d.w2.codes + e * per;
+        const uint8_t* tabs = (const uint8_t*)A.d.w2.tables + e * per;
+        for (int tb = 0; tb < n; tb += TB) {
+            const int nt = min(TB, n - tb);
+            const uint16_t* xrow[TB];
+#pragma unroll
+            for (int t = 0; t < TB; ++t) xrow[t] = A.act + (int64_t)(p0 + tb + min(t, nt - 1)) * I;
+            float acc[kRows][TB];
+#pragma unroll
+            for (int r = 0; r < kRows; ++r)
+#pragma unroll
+                for (int t = 0; t < TB; ++t) acc[r][t] = 0.f;
+            for (int c0 = 0; c0 < nch; c0 += CG)
+                bl4_rows8<TB, CG>(codes, tabs, rows, I, c0, nch, lane, slot, xrow, nt, acc);
+#pragma unroll
+            for (int t = 0; t < TB; ++t) {
+                const int p = p0 + tb + min(t, nt - 1);
+                const float pw = R.pw[R.perm[p]];
+#pragma unroll
+                for (int r = 0; r < kRows; ++r) {
+                    const float v = wave_reduce(acc[r][t]);
+                    if (lane == r && t < nt) s_y[p * kRows + r] = v * pw;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    const int T = A.T;
+    for (int idx = threadIdx.x; idx < T * kRows; idx += 256) {
+        const int t = idx / kRows, r = idx % kRows;
+        if (h0 + r >= H) continue;
+        float s = 0.f;
+        for (int q = 0; q < ke; ++q) {
+            const int pos = R.inv[t * ke + q];
+            if (pos >= 0) s += s_y[pos * kRows + r];
+        }
+        const int64_t o = (int64_t)t * H + h0 + r;
+        if (A.out_dtype == LUTMOE_DTYPE_F32) ((float*)A.out)[o] = s;
+        else ((uint16_t*)A.out)[o] = (uint16_t)f32_to_bf16(s);
+    }
+}
+
+// tokens per pass: T=1 and T=2 recompute routing per CTA, larger T read it
+inline int tb_for(int T) { return T <= 1 ? 1 : T <= 2 ? 2 : 4; }
+
+}  // namespace
+
+namespace lutmoe_host {
+
+bool decode_v2_supported(const lutmoe_moe_desc* d, int T, int k) {
+    const int E_tot = d->num_routed + d->num_shared;
+    const int P = T * (k + d->num_shared);
+    return d->w13.format == LUTMOE_FMT_BL4 && E_tot <= kMaxEtot && P <= kMaxP;
+}
+
+size_t decode_route_bytes() { return sizeof(RouteOut); }
+
+int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* topk_w,
+                     const int32_t* topk_ids, const float* logits, int T, int k, int renorm,
+                     float scaling, uint16_t* act, void* route_ws, void* out, int out_dtype,
+                     int stages, hipStream_t s) {
+    DecodeArgs A;
+    A.d = *d;
+    A.x = x;
+    A.topk_w = topk_w;
+    A.topk_ids = topk_ids;
+    A.logits = logits;
+    A.T = T;
+    A.k = k;
+    A.renorm = renorm;
+    A.scaling = scaling;
+    A.act = act;
+    A.out = out;
+    A.out_dtype = out_dtype;
+    A.route = (RouteOut*)route_ws;
+    const int E_tot = d->num_routed + d->num_shared;
+    const int P = T * (k + d->num_shared);
+    const int max_active = P < E_tot ? P : E_tot;
+    // Small grids recompute the routing in every CTA (no extra launch); larger
+    // ones route once into the workspace.
+    const bool pre = T > 2;
+    int rc;
+    if (pre && (stages & LUTMOE_STAGE_ROUTE)) {
+        hipLaunchKernelGGL(decode_route_kernel, dim3(1), dim3(256), 0, s, A);
+        if ((rc = check_launch())) return rc;
+    }
+#define LUTMOE_TB_SWITCH(KERNEL, GRID, LDS)                                                  \
+    switch (tb_for(T)) {                                                                    \
+        case 1: hipLaunchKernelGGL((KERNEL<1, false>), GRID, dim3(256), LDS, s, A); break;  \
+        case 2: hipLaunchKernelGGL((KERNEL<2, false>), GRID, dim3(256), LDS, s, A); break;  \
+        default: hipLaunchKernelGGL((KERNEL<4, true>), GRID, dim3(256), LDS, s, A); break;  \
+    }
+    if (stages & LUTMOE_STAGE_GATE_UP) {
+        const dim3 grid((d->inter + 15) / 16, max_active);
+        LUTMOE_TB_SWITCH(bl4_decode_gate_up, grid, 0)
+        if ((rc = check_launch())) return rc;
+    }
+    if (stages & LUTMOE_STAGE_DOWN) {
+        const dim3 grid((d->hidden + kRows - 1) / kRows);
+        const size_t lds = (size_t)P * kRows * sizeof(float);
+        LUTMOE_TB_SWITCH(bl4_decode_down, grid, lds)
+        return check_launch();
+    }
+#undef LUTMOE_TB_SWITCH
+    return LUTMOE_OK;
+}
+
+}  // namespace lutmoe_host

@@ -48,6 +48,14 @@ int launch_decode_down_combine(const lutmoe_moe_desc* d, const uint16_t* act,
                                const MoeRouting& r, void* out, int out_dtype,
                                int max_active, hipStream_t s);
 
+// decode.hip (BL4 decode layer, routing recomputed inside each CTA)
+bool decode_v2_supported(const lutmoe_moe_desc* d, int T, int k);
+size_t decode_route_bytes();
+int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* topk_w,
+                     const int32_t* topk_ids, const float* logits, int T, int k, int renorm,
+                     float scaling, uint16_t* act, void* route_ws, void* out, int out_dtype,
+                     int stages, hipStream_t s);
+
 // route.hip
 int launch_route_topk(const float* logits, int T, int E, int k, int renorm, float scaling,
                       float* w, int32_t* ids, hipStream_t s);

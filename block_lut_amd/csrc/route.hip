@@ -21,40 +21,50 @@ using namespace lutmoe;
 
 namespace {
 
-constexpr int kMaxTopK = 16;
-
+// One wave per token: lane l holds logits l, l+64, ...; softmax in fp32;
+// top-k by logit (softmax is monotone), ties to the lower expert id.
 __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict__ logits,
                                                          int T, int E, int k, int renorm,
                                                          float scaling, float* __restrict__ w,
                                                          int32_t* __restrict__ ids) {
-    const int t = blockIdx.x * 256 + threadIdx.x;
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= T) return;
     const float* l = logits + (int64_t)t * E;
-    float mx = l[0];
-    for (int e = 1; e < E; ++e) mx = fmaxf(mx, l[e]);
+    float mx = -INFINITY;
+    for (int e = lane; e < E; e += 64) mx = fmaxf(mx, l[e]);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
     float sum = 0.f;
-    for (int e = 0; e < E; ++e) sum += expf(l[e] - mx);
-    int sel[kMaxTopK];
-    float wsel[kMaxTopK];
-    float wsum = 0.f;
+    for (int e = lane; e < E; e += 64) sum += expf(l[e] - mx);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, kWave);
+    uint64_t taken = 0;
+    float wsel = 0.f, wsum = 0.f;
+    int isel = 0;
     for (int j = 0; j < k; ++j) {
-        int best = -1;
-        float bv = 0.f;
-        for (int e = 0; e < E; ++e) {
-            bool taken = false;
-            for (int q = 0; q < j; ++q) taken |= (sel[q] == e);
-            if (taken) continue;
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+        int q = 0;
+        for (int e = lane; e < E; e += 64, ++q) {
             const float v = l[e];
-            if (best < 0 || v > bv) { best = e; bv = v; }
+            if (!((taken >> q) & 1ull) && (v > bv || (v == bv && e < bi))) { bv = v; bi = e; }
         }
-        sel[j] = best;
-        wsel[j] = expf(bv - mx) / sum;
-        wsum += wsel[j];
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+            const float ov = __shfl_xor(bv, off, kWave);
+            const int oi = __shfl_xor(bi, off, kWave);
+            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+        }
+        if ((bi & 63) == lane) taken |= 1ull << (bi >> 6);
+        const float p = expf(bv - mx) / sum;
+        wsum += p;
+        if (lane == j) { wsel = p; isel = bi; }
     }
-    for (int j = 0; j < k; ++j) {
-        float v = renorm ? wsel[j] / wsum : wsel[j];
-        w[(int64_t)t * k + j] = v * scaling;
-        ids[(int64_t)t * k + j] = sel[j];
+    if (lane < k) {
+        const float v = renorm ? wsel / wsum : wsel;
+        w[(int64_t)t * k + lane] = v * scaling;
+        ids[(int64_t)t * k + lane] = isel;
     }
 }
 
@@ -159,7 +169,7 @@ namespace lutmoe_host {
 
 int launch_route_topk(const float* logits, int T, int E, int k, int renorm, float scaling,
                       float* w, int32_t* ids, hipStream_t s) {
-    hipLaunchKernelGGL(route_topk_kernel, dim3((T + 255) / 256), dim3(256), 0, s, logits, T, E,
+    hipLaunchKernelGGL(route_topk_kernel, dim3((T + 3) / 4), dim3(256), 0, s, logits, T, E,
                        k, renorm, scaling, w, ids);
     return check_launch();
 }

@@ -132,13 +132,18 @@ def ref_gemv(x: torch.Tensor, indices: torch.Tensor, codebook: torch.Tensor, abs
 # ---------------------------------------------------------------- routing
 
 def route_topk(logits: torch.Tensor, top_k: int, renormalize: bool = False,
-               scaling: float = 1.0) -> Tuple[torch.Tensor, torch.Tensor]:
+               scaling: float = 1.0, out_w: Optional[torch.Tensor] = None,
+               out_ids: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     """softmax(fp32) -> top-k (sorted, ties to the lower id); weights fp32 [T,k], ids int32."""
     lg = logits if logits.dtype == torch.float32 else logits.float()
     lg = _dev(lg.contiguous(), torch.float32, "logits")
     T, E = lg.shape
-    w = torch.empty((T, top_k), dtype=torch.float32, device=lg.device)
-    ids = torch.empty((T, top_k), dtype=torch.int32, device=lg.device)
+    w = torch.empty((T, top_k), dtype=torch.float32, device=lg.device) if out_w is None else \
+        _dev(out_w, torch.float32, "out_w")
+    ids = torch.empty((T, top_k), dtype=torch.int32, device=lg.device) if out_ids is None else \
+        _dev(out_ids, torch.int32, "out_ids")
+    if tuple(w.shape) != (T, top_k) or tuple(ids.shape) != (T, top_k):
+        raise ValueError("route_topk outputs must be [T, top_k]")
     N.check("lutmoe_route_topk",
             N.lib().lutmoe_route_topk(lg.data_ptr(), T, E, top_k, int(bool(renormalize)),
                                       float(scaling), w.data_ptr(), ids.data_ptr(), _stream()))
@@ -196,6 +201,37 @@ def moe_forward(moe: MoEWeights, x: torch.Tensor, topk_weights: torch.Tensor,
     N.check("lutmoe_moe_forward",
             N.lib().lutmoe_moe_forward_stages(ctypes.byref(d), x.data_ptr(), w.data_ptr(),
                                               ids.data_ptr(), T, k, out.data_ptr(),
+                                              _out_code(out_dtype), workspace.data_ptr(),
+                                              workspace.numel(), path, stages, _stream()))
+    return out
+
+
+def moe_forward_logits(moe: MoEWeights, x: torch.Tensor, logits: torch.Tensor, top_k: int,
+                       renormalize: bool = False, scaling: float = 1.0,
+                       out: Optional[torch.Tensor] = None, out_dtype: torch.dtype = torch.bfloat16,
+                       path: int = PATH_AUTO, workspace: Optional[torch.Tensor] = None,
+                       stages: int = N.STAGE_ALL) -> torch.Tensor:
+    """MoE block forward from router logits: softmax(fp32) -> top-k -> layer."""
+    _dev(x, torch.bfloat16, "x")
+    T, H = x.shape
+    if H != moe.hidden:
+        raise ValueError(f"x has {H} features, layer expects {moe.hidden}")
+    lg = logits if logits.dtype == torch.float32 else logits.float()
+    lg = _dev(lg.contiguous(), torch.float32, "logits")
+    if tuple(lg.shape) != (T, moe.num_routed):
+        raise ValueError(f"logits must be [T, {moe.num_routed}]")
+    if out is None:
+        out = torch.empty((T, H), dtype=out_dtype, device=x.device)
+    else:
+        _dev(out, out.dtype, "out")
+        out_dtype = out.dtype
+    need = moe_workspace_bytes(moe, T, top_k)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=x.device)
+    d = moe.desc()
+    N.check("lutmoe_moe_forward_logits",
+            N.lib().lutmoe_moe_forward_logits(ctypes.byref(d), x.data_ptr(), lg.data_ptr(), T, top_k,
+                                              int(bool(renormalize)), float(scaling), out.data_ptr(),
                                               _out_code(out_dtype), workspace.data_ptr(),
                                               workspace.numel(), path, stages, _stream()))
     return out

@@ -194,6 +194,16 @@ int lutmoe_moe_forward_stages(const lutmoe_moe_desc* d, const void* x_dev, const
                               int out_dtype, void* workspace_dev, size_t workspace_bytes,
                               int force_path, int stages, void* stream);
 
+/* The MoE block forward from router logits (DeepseekV2MoE_LUT.forward,
+ * vllm_lut/moe_layer.py:281-355): softmax(fp32 logits [T][E]) -> top-k
+ * (ties to the lower id) -> optional renormalisation -> x scaling -> the
+ * layer of lutmoe_moe_forward.  On the decode path the routing runs inside
+ * the two layer kernels (no extra launch). */
+int lutmoe_moe_forward_logits(const lutmoe_moe_desc* d, const void* x_dev, const float* logits_dev,
+                              int T, int k, int renormalize, float scaling, void* out_dev,
+                              int out_dtype, void* workspace_dev, size_t workspace_bytes,
+                              int force_path, int stages, void* stream);
+
 /* ---- encoders (format producers) ----------------------------------------- */
 
 /* BL4 per-64-block k-means encoder on the GPU: w fp32 [nblocks*64] ->

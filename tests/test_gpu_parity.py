@@ -274,6 +274,58 @@ def test_moe_layer(gpu, fmt, T, path):
     assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
 
 
+@pytest.mark.parametrize("T,path,renorm,E", [(1, 1, False, 12), (3, 1, True, 12), (32, 1, False, 12),
+                                             (40, 2, False, 12), (300, 2, True, 12),
+                                             (2, 1, True, 130), (5, 2, False, 130)])
+def test_moe_layer_from_logits(gpu, T, path, renorm, E):
+    """Block forward from router logits (routing inside the layer) vs oracle routing + layer;
+    E = 130 puts several logits on one lane of the in-kernel top-k."""
+    import torch
+    from block_lut_amd import ops
+    from block_lut_amd.formats import MoEWeights
+    S, k, H, I = 2, 3, 256, 192
+    w13, w2 = _moe_case("bl4", E, S, H, I, seed=70 + T)
+    moe = MoEWeights(w13.stack(gpu), w2.stack(gpu), H, I, E, S)
+    rng = np.random.default_rng(700 + T)
+    xb = _x(rng, T, H)
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    out = ops.moe_forward_logits(moe, to_dev_bf16(xb, gpu), torch.from_numpy(lg).to(gpu), k,
+                                 renormalize=renorm, scaling=1.0, out_dtype=torch.float32, path=path)
+    rw, rids = O.route(lg, k, renormalize=renorm)
+    ref = O.moe_layer(xb, rids, rw, w13.deq_f32, w2.deq_f32,
+                      shared=[(w13.deq_f32(E + s), w2.deq_f32(E + s)) for s in range(S)])
+    assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
+
+
+def test_moe_layer_qwen_decode_full_shape(gpu):
+    """Full Qwen1.5-MoE layer shape (H2048 I1408 E60 top-4), T=1 and T=8, BL4 weights from the
+    GPU encoder; oracle on the touched experts' GPU-dequantised weights (bit-exact separately)."""
+    import torch
+    from block_lut_amd import ops
+    from block_lut_amd.formats import BL4Stack, MoEWeights
+    H, I, E, k = 2048, 1408, 60, 4
+    g = torch.Generator(device="cpu").manual_seed(5)
+    w13 = (torch.randn((E, 2 * I, H), generator=g) * 0.02).to(gpu)
+    c13, t13 = ops.bl4_encode(w13, n_iter=4)
+    del w13
+    w2 = (torch.randn((E, H, I), generator=g) * 0.02).to(gpu)
+    c2, t2 = ops.bl4_encode(w2, n_iter=4)
+    del w2
+    moe = MoEWeights(BL4Stack.from_fp16(c13, t13), BL4Stack.from_fp16(c2, t2), H, I, E, 0)
+    for T in (1, 8):
+        rng = np.random.default_rng(T)
+        xb = _x(rng, T, H)
+        lg = rng.standard_normal((T, E)).astype(np.float32)
+        out = ops.moe_forward_logits(moe, to_dev_bf16(xb, gpu), torch.from_numpy(lg).to(gpu), k,
+                                     out_dtype=torch.float32).cpu().numpy()
+        rw, rids = O.route(lg, k)
+        used = sorted(set(rids.reshape(-1).tolist()))
+        d13 = {e: O.bf16_to_f32(bf16_bits(ops.dequant(moe.w13, e, 1)[0])) for e in used}
+        d2 = {e: O.bf16_to_f32(bf16_bits(ops.dequant(moe.w2, e, 1)[0])) for e in used}
+        ref = O.moe_layer(xb, rids, rw, d13.__getitem__, d2.__getitem__)
+        assert rel_maxabs(out, ref) <= TOL, T
+
+
 def test_moe_layer_paths_agree(gpu):
     """GEMV and MFMA paths on the same inputs (both fp32 accumulation)."""
     import torch
