@@ -5,7 +5,8 @@
 // applied per block: Lloyd iterations with argmin |x - c| (first minimum),
 // mean update leaving empty clusters unchanged, final sort, cast to the
 // storage dtype (fp16), codes re-assigned against the stored codebook
-// (quantize(), quantizer.py:292-296).  Initialisation is a binary-splitting
+// (quantize(), quantizer.py:292-296); in the final 16-means an empty cluster
+// is re-seeded at the farthest member instead of being left in place.  Initialisation is a binary-splitting
 // tree (4-means from the quantile start sorted[16i+8], then every cell split
 // by 2-means twice) instead of a random pick, so CPU and GPU agree exactly.
 // Cluster sums are the xor-butterfly over the 64 lanes (non-members add +0)
@@ -13,6 +14,7 @@
 // result is bit-identical to the CPU restatement run in the same order.
 #include "common.h"
 #include "kernels.h"
+#include "lut_core.h"
 
 using namespace lutmoe;
 
@@ -36,21 +38,48 @@ __device__ __forceinline__ int argmin_abs(float x, const float (&c)[K]) {
     return best;
 }
 
-// Lloyd on the member lanes; c[] is uniform across the wave.
 template <int K>
+__device__ __forceinline__ float pick(const float (&c)[K], int i) {
+    float v = c[0];
+#pragma unroll
+    for (int q = 1; q < K; ++q) v = (i == q) ? c[q] : v;
+    return v;
+}
+
+// Lloyd on the member lanes; c[] is uniform across the wave.  kReseed: after
+// each mean update every empty cluster (index order) moves to the member
+// farthest from its own centroid (lowest lane on ties, each lane once per
+// iteration) when that distance is > 0.
+template <int K, bool kReseed = false>
 __device__ void lloyd(float x, bool member, float (&c)[K], int n_iter, int& assign) {
+    const int lane = threadIdx.x & 63;
     assign = -1;
     for (int it = 0; it < n_iter; ++it) {
         const int a = member ? argmin_abs<K>(x, c) : -1;
         const bool changed = member && a != assign;
         assign = a;
         if (!__any(changed)) break;
+        uint32_t empty = 0;
 #pragma unroll
         for (int i = 0; i < K; ++i) {
             const bool in = member && assign == i;
             const float s = butterfly(in ? x : 0.0f);
             const int cnt = __popcll(__ballot(in));
             if (cnt) c[i] = s / (float)cnt;
+            else empty |= 1u << i;
+        }
+        if (kReseed && empty) {
+            bool taken = false;
+#pragma unroll
+            for (int i = 0; i < K; ++i) {
+                if (!((empty >> i) & 1u)) continue;
+                const float d = (member && !taken) ? fabsf(x - pick(c, assign)) : -1.0f;
+                const float mx = wave_reduce_max(d);
+                if (!(mx > 0.0f)) break;
+                const int j = (int)__builtin_ctzll(__ballot(d == mx));
+                c[i] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), j));
+                if (lane == j) taken = true;
+            }
         }
     }
 }
@@ -82,13 +111,6 @@ __device__ void split2(float x, bool member, float parent, int n_iter, float (&c
     if (ch[1] < ch[0]) { const float t = ch[0]; ch[0] = ch[1]; ch[1] = t; }
 }
 
-template <int K>
-__device__ __forceinline__ float pick(const float (&c)[K], int i) {
-    float v = c[0];
-#pragma unroll
-    for (int q = 1; q < K; ++q) v = (i == q) ? c[q] : v;
-    return v;
-}
 
 __global__ __launch_bounds__(256) void bl4_encode_kernel(const float* __restrict__ w,
                                                          int64_t nblocks, int n_iter,
@@ -153,7 +175,7 @@ __global__ __launch_bounds__(256) void bl4_encode_kernel(const float* __restrict
             c[k3 | 8] = ch[1];
         }
         int a16;
-        lloyd<16>(x, true, c, n_iter, a16);
+        lloyd<16, true>(x, true, c, n_iter, a16);
         sort_small<16>(c);
         float cf[16];
         uint32_t h_mine = 0;

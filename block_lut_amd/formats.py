@@ -67,9 +67,12 @@ class RefStack(WeightStack):
         self.block_size = int(block_size)
         if self.absmax.shape[0] != self.num_experts:
             raise ValueError("absmax must have one row per expert")
-        need = math.ceil(self.rows * self.cols / self.block_size)
-        if self.absmax.shape[1] < need:
-            raise ValueError(f"absmax has {self.absmax.shape[1]} blocks per expert, need {need}")
+        if self.absmax.shape[1] < 1:
+            raise ValueError("absmax needs at least one block per expert")
+        # fewer entries than ceil(M*K/block_size) is legal: block indices are
+        # clamped to the last entry, as decompress_blocklut does
+        # (vllm_lut/quantizer.py:473-474)
+        self.full_absmax = self.absmax.shape[1] >= math.ceil(self.rows * self.cols / self.block_size)
 
     def desc(self) -> N.lutmoe_weights:
         d = N.lutmoe_weights()

@@ -26,7 +26,10 @@
  *   - every cluster sum is the 64-lane xor-butterfly sum over the block
  *     (non-members contribute +0), which is the order a wave64 reduction uses;
  *   - iterations stop early once the assignment no longer changes (a fixed
- *     point, so the result equals running all n_iter iterations).
+ *     point, so the result equals running all n_iter iterations);
+ *   - in the final 16-means an empty cluster is re-seeded at the member
+ *     farthest from its centroid (the reference leaves empty clusters where
+ *     they are, which wastes codebook entries on blocks with repeated values).
  */
 #include <math.h>
 #include <stdint.h>
@@ -127,8 +130,13 @@ static inline int argmin_abs(float v, const float* c, int k) {
 
 /* Lloyd iterations on the members of one cell (mask) with k centroids.
  * assign[] holds the cluster of every member lane; non-members are ignored. */
-static void lloyd(const float* x, const uint8_t* member, int k, float* c,
-                  int n_iter, int* assign) {
+/* Lloyd iterations on the members of one cell (mask) with k centroids.
+ * assign[] holds the cluster of every member lane; non-members are ignored.
+ * reseed != 0: after each mean update, every cluster left empty (in index
+ * order) moves to the member farthest from its own centroid (lowest index on
+ * ties; each point used once per iteration), when that distance is > 0. */
+static void lloyd_ex(const float* x, const uint8_t* member, int k, float* c,
+                     int n_iter, int* assign, int reseed) {
     for (int j = 0; j < BL_BLOCK; ++j) assign[j] = -1;
     for (int it = 0; it < n_iter; ++it) {
         int changed = 0;
@@ -138,6 +146,7 @@ static void lloyd(const float* x, const uint8_t* member, int k, float* c,
             if (a != assign[j]) { changed = 1; assign[j] = a; }
         }
         if (!changed) break;
+        int empty[16], nempty = 0;
         for (int i = 0; i < k; ++i) {
             float v[BL_BLOCK];
             int cnt = 0;
@@ -147,8 +156,29 @@ static void lloyd(const float* x, const uint8_t* member, int k, float* c,
                 cnt += in;
             }
             if (cnt) c[i] = butterfly_sum64(v) / (float)cnt;
+            else if (nempty < 16) empty[nempty++] = i;
+        }
+        if (reseed && nempty) {
+            uint8_t taken[BL_BLOCK] = {0};
+            for (int q = 0; q < nempty; ++q) {
+                int best = -1;
+                float bd = 0.0f;
+                for (int j = 0; j < BL_BLOCK; ++j) {
+                    if (!member[j] || taken[j]) continue;
+                    float d = fabsf(x[j] - c[assign[j]]);
+                    if (d > bd) { bd = d; best = j; }
+                }
+                if (best < 0) break;
+                c[empty[q]] = x[best];
+                taken[best] = 1;
+            }
         }
     }
+}
+
+static void lloyd(const float* x, const uint8_t* member, int k, float* c,
+                  int n_iter, int* assign) {
+    lloyd_ex(x, member, k, c, n_iter, assign, 0);
 }
 
 static void sort_small(float* c, int k) {
@@ -227,7 +257,8 @@ static void tree_centroids(const float* x, int n_iter, float* c2s, float* c3, fl
 /* ---------------------------------------------------------------- BL4 */
 
 /* Encode nblocks blocks of 64 fp32 weights: tree init (16 leaves), then
- * n_iter Lloyd iterations with k = 16, sort, fp16, argmin codes.
+ * n_iter Lloyd iterations with k = 16 (empty clusters re-seeded at the
+ * farthest point), sort, fp16, argmin codes.
  * codes: one code (0..15) per weight, unpacked, [nblocks*64].
  * table: fp16 bits of the sorted 16-entry codebook, [nblocks*16]. */
 void oracle_bl4_encode(const float* w, int64_t nblocks, int n_iter,
@@ -239,7 +270,7 @@ void oracle_bl4_encode(const float* w, int64_t nblocks, int n_iter,
         int assign[BL_BLOCK];
         tree_centroids(x, n_iter, c2, c3, c);
         memset(member, 1, sizeof(member));
-        lloyd(x, member, 16, c, n_iter, assign);
+        lloyd_ex(x, member, 16, c, n_iter, assign, 1);
         sort_small(c, 16);
         for (int i = 0; i < 16; ++i) {
             table[b * 16 + i] = oracle_f32_to_f16(c[i]);

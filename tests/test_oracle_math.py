@@ -1,0 +1,257 @@
+"""The oracle pinned by what the mathematics fixes: independent library
+routines (torch casts and matmuls, scipy softmax, argsort), brute force on
+tiny inputs, closed forms and invariants.  CPU only."""
+import numpy as np
+import pytest
+
+import oracle as O
+
+
+# ----------------------------------------------------------------- rounding
+
+def test_f32_to_bf16_matches_torch_on_all_patterns_of_a_sweep():
+    import torch
+    rng = np.random.default_rng(0)
+    u = rng.integers(0, 2 ** 32, 2_000_000, dtype=np.uint64).astype(np.uint32)
+    x = u.view(np.float32)
+    x = x[~np.isnan(x)]
+    ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(O.f32_to_bf16(x), ref)
+    assert np.array_equal(O.c_f32_to_bf16(x), ref)
+
+
+def test_f32_to_f16_c_matches_numpy():
+    rng = np.random.default_rng(1)
+    x = np.concatenate([rng.standard_normal(300000).astype(np.float32) * s
+                        for s in (1e-9, 1e-7, 6e-5, 1e-3, 0.02, 1.0, 3e4, 7e4)])
+    x = np.concatenate([x, np.float32([0.0, -0.0, np.inf, -np.inf, 65504, 65520, 65519.99,
+                                       2 ** -24, 2 ** -25, 3 * 2 ** -26])])
+    with np.errstate(over="ignore"):
+        ref = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(O.c_f32_to_f16(x), ref)
+
+
+def test_f16_bf16_table_conversion_all_patterns():
+    import torch
+    h = np.arange(65536, dtype=np.uint16)
+    ok = ~np.isnan(h.view(np.float16))
+    ref = torch.from_numpy(h.view(np.float16)).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(O.bl4_tables_bf16(h)[ok], ref[ok])
+
+
+# ------------------------------------------------------------------- REF
+
+def test_ref_dequant_brute_force_vs_torch_bf16_mul():
+    """All 256 codes x a spread of absmax values; torch's bf16 multiply is the
+    independent reference (quantizer.py:349)."""
+    import torch
+    cb = O.f32_to_bf16(np.linspace(-1, 1, 256, dtype=np.float32))
+    scales = np.float32([0.0, 1e-40, 1e-10, 3e-3, 0.02, 0.5, 1.0, 3.0, 1e4, 3e38])
+    am = O.f32_to_bf16(scales)
+    idx = np.tile(np.arange(256, dtype=np.uint8), 10)
+    bs = 256
+    got = O.ref_dequant(idx, am, cb, bs)
+    tcb = torch.from_numpy(cb.view(np.int16)).view(torch.bfloat16)
+    tam = torch.from_numpy(am.view(np.int16)).view(torch.bfloat16)
+    ref = (tcb[torch.from_numpy(idx).long()] * tam[torch.arange(idx.size) // bs])
+    assert np.array_equal(got, ref.view(torch.int16).numpy().view(np.uint16))
+
+
+def test_ref_dequant_clamps_block_index():
+    cb = O.f32_to_bf16(np.linspace(-1, 1, 256, dtype=np.float32))
+    am = O.f32_to_bf16(np.float32([1.0, 2.0]))
+    idx = np.full(1000, 255, np.uint8)
+    out = O.bf16_to_f32(O.ref_dequant(idx, am, cb, 128))
+    assert np.all(out[:128] == 1.0) and np.all(out[128:] == 2.0)
+
+
+def test_ref_gemv_vs_torch_matmul():
+    import torch
+    rng = np.random.default_rng(2)
+    M, K = 70, 384
+    idx = rng.integers(0, 256, (M, K), dtype=np.uint8)
+    cb = O.f32_to_bf16(rng.standard_normal(256).astype(np.float32))
+    am = O.f32_to_bf16(np.abs(rng.standard_normal(M * K // 128)).astype(np.float32))
+    x = O.f32_to_bf16(rng.standard_normal(K).astype(np.float32))
+    W = torch.from_numpy(O.bf16_to_f32(cb)[idx].astype(np.float64)) * \
+        torch.from_numpy(np.repeat(O.bf16_to_f32(am).astype(np.float64), 128).reshape(M, K))
+    ref = (W @ torch.from_numpy(O.bf16_to_f32(x).astype(np.float64))).numpy()
+    got = O.ref_gemv(x, idx, cb, am)
+    assert np.abs(got - ref).max() <= 1e-6 * np.abs(ref).max()
+
+
+def test_bitplane_pack_roundtrip_all_codes():
+    codes = np.tile(np.arange(256, dtype=np.uint8), 4)
+    packed = O.bitplane_pack_ref(codes)
+    n = codes.size
+    assert packed.size == n // 2 + n // 4 + n // 4
+    assert np.array_equal(O.unpack_4bit_ref(packed, n), codes & 0x0F)
+    assert np.array_equal(O.unpack_6bit_ref(packed, n), codes & 0x3F)
+    # even element in the low nibble (model_offload.py:755)
+    assert packed[0] == (codes[0] & 15) | ((codes[1] & 15) << 4)
+
+
+# ------------------------------------------------------------------- BL4
+
+def _bl4(w, n_iter=30):
+    p, t = O.bl4_encode(w, n_iter=n_iter)
+    return O.bl4_unpack(p), O.f16_to_f32(t)
+
+
+def test_bl4_codes_are_argmin_of_stored_tables():
+    rng = np.random.default_rng(3)
+    w = (rng.standard_normal((32, 256)) * 0.02).astype(np.float32)
+    codes, tab = _bl4(w)
+    M, K = w.shape
+    t = tab.reshape(M, K // 64, 16)
+    for r in range(M):
+        for b in range(K // 64):
+            x = w[r, 64 * b: 64 * b + 64]
+            d = np.abs(x[:, None] - t[r, b][None, :])
+            assert np.array_equal(codes[r, 64 * b: 64 * b + 64], d.argmin(axis=1))
+
+
+def test_bl4_tables_sorted_and_fp16():
+    rng = np.random.default_rng(4)
+    w = (rng.standard_normal((16, 128)) * 0.02).astype(np.float32)
+    _, t = O.bl4_encode(w)
+    v = O.f16_to_f32(t)
+    assert np.all(np.diff(v, axis=-1) >= 0)
+
+
+def test_bl4_exact_when_block_has_at_most_16_values():
+    """Brute force: a block with <= 16 distinct values is reproduced to fp16."""
+    rng = np.random.default_rng(5)
+    for nvals in (1, 2, 5, 16):
+        vals = (rng.standard_normal(nvals) * 0.02).astype(np.float32)
+        w = rng.choice(vals, size=(1, 64)).astype(np.float32)
+        codes, tab = _bl4(w)
+        rec = tab.reshape(16)[codes[0]]
+        assert np.array_equal(rec, w[0].astype(np.float16).astype(np.float32)), nvals
+
+
+def test_bl4_quality_close_to_sklearn_kmeans():
+    from sklearn.cluster import KMeans
+    rng = np.random.default_rng(6)
+    w = (rng.standard_normal((4, 256)) * 0.02).astype(np.float32)
+    codes, tab = _bl4(w, 50)
+    rec = np.take_along_axis(tab.reshape(4, 4, 16), codes.reshape(4, 4, 64), axis=2).reshape(4, 256)
+    ours = ((rec - w) ** 2).sum()
+    sk = 0.0
+    for blk in w.reshape(-1, 64):
+        km = KMeans(16, n_init=4, random_state=0).fit(blk[:, None])
+        sk += ((km.cluster_centers_[km.labels_, 0] - blk) ** 2).sum()
+    assert ours <= 1.6 * sk
+
+
+def test_bl4_pack_roundtrip_and_dequant_closed_form():
+    rng = np.random.default_rng(7)
+    codes = rng.integers(0, 16, (3, 128), dtype=np.uint8)
+    assert np.array_equal(O.bl4_unpack(O.bl4_pack(codes)), codes)
+    tables = O.f32_to_f16(rng.standard_normal((3, 2, 16)).astype(np.float32))
+    deq = O.bl4_dequant(O.bl4_pack(codes), tables)
+    for r in range(3):
+        for c in range(128):
+            v = O.f16_to_f32(tables[r, c // 64, codes[r, c]])
+            assert deq[r, c] == O.f32_to_bf16(np.float32([v]))[0]
+
+
+# --------------------------------------------------------------- nested
+
+def test_nested_tiers_refine_and_use_low_bits():
+    rng = np.random.default_rng(8)
+    w = (rng.standard_normal((16, 256)) * 0.02).astype(np.float32)
+    codes, t2, t3, t4 = O.nested_encode(w, n_iter=30)
+    errs = []
+    for b, t in ((2, t2), (3, t3), (4, t4)):
+        rec = O.bf16_to_f32(O.nested_dequant(codes, t, b))
+        errs.append(((rec - w) ** 2).mean())
+        # tier-b reconstruction depends only on the low b bits
+        alt = codes ^ (np.uint8(0xF0) if b == 4 else np.uint8((0xF << b) & 0xF))
+        assert np.array_equal(O.nested_dequant(alt, t, b), O.nested_dequant(codes, t, b))
+    assert errs[0] > errs[1] > errs[2]
+    # descent: the level-2 cell is the argmin over T2
+    f2 = O.f16_to_f32(t2).reshape(16, 4, 4)
+    for r in range(4):
+        for blk in range(4):
+            x = w[r, 64 * blk: 64 * blk + 64]
+            assert np.array_equal(codes[r, 64 * blk: 64 * blk + 64] & 3,
+                                  np.abs(x[:, None] - f2[r, blk][None]).argmin(1))
+
+
+def test_nested_planes_roundtrip_and_prefix():
+    rng = np.random.default_rng(9)
+    codes = rng.integers(0, 16, (4, 128), dtype=np.uint8)
+    pl = O.nested_pack_planes(codes)
+    assert pl["p01"].shape == (4, 32) and pl["p2"].shape == (4, 16)
+    for b in (2, 3, 4):
+        assert np.array_equal(O.nested_unpack_planes(pl, b), codes & ((1 << b) - 1))
+
+
+def test_nested_exact_with_four_values_at_tier2():
+    rng = np.random.default_rng(10)
+    vals = (rng.standard_normal(4) * 0.02).astype(np.float32)
+    w = rng.choice(vals, size=(1, 64)).astype(np.float32)
+    codes, t2, _, _ = O.nested_encode(w, n_iter=20)
+    rec = O.f16_to_f32(t2).reshape(4)[codes[0] & 3]
+    assert np.array_equal(rec, w[0].astype(np.float16).astype(np.float32))
+
+
+# ---------------------------------------------------------- routing/permute
+
+def test_route_vs_scipy_softmax_and_argsort():
+    from scipy.special import softmax
+    rng = np.random.default_rng(11)
+    lg = rng.standard_normal((50, 60)).astype(np.float32)
+    lg[3, [5, 9, 40]] = 2.5           # ties: lower id first
+    w, ids = O.route(lg, 4)
+    p = softmax(lg.astype(np.float64), axis=1)
+    for t in range(50):
+        order = sorted(range(60), key=lambda e: (-lg[t, e], e))[:4]
+        assert list(ids[t]) == order
+        np.testing.assert_allclose(w[t], p[t, order], rtol=1e-6)
+    assert list(ids[3][:3]) == [5, 9, 40]
+    wr, _ = O.route(lg, 4, renormalize=True)
+    np.testing.assert_allclose(wr.sum(1), 1.0, rtol=1e-6)
+
+
+def test_permute_brute_force():
+    rng = np.random.default_rng(12)
+    T, k, E = 37, 3, 9
+    ids = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
+    off, perm, inv = O.permute(ids, E)
+    order = [t * k + s for e in range(E) for t in range(T) for s in range(k) if ids[t, s] == e]
+    assert list(perm) == order
+    assert np.array_equal(inv[perm], np.arange(T * k))
+    assert np.array_equal(np.diff(off), np.bincount(ids.reshape(-1), minlength=E))
+
+
+def test_moe_layer_loop_vs_dense_restatement():
+    rng = np.random.default_rng(13)
+    T, H, I, E, k = 9, 64, 32, 5, 2
+    x = O.f32_to_bf16(rng.standard_normal((T, H)).astype(np.float32))
+    W13 = [(rng.standard_normal((2 * I, H)) * 0.1).astype(np.float32) for _ in range(E)]
+    W2 = [(rng.standard_normal((H, I)) * 0.1).astype(np.float32) for _ in range(E)]
+    w, ids = O.route(rng.standard_normal((T, E)).astype(np.float32), k)
+    got = O.moe_layer(x, ids, w, W13.__getitem__, W2.__getitem__)
+    xf = O.bf16_to_f32(x).astype(np.float64)
+    dense = np.zeros((T, H))
+    for e in range(E):
+        gu = xf @ W13[e].astype(np.float64).T
+        g, u = gu[:, :I].astype(np.float32), gu[:, I:].astype(np.float32)
+        a = O.bf16_to_f32(O.f32_to_bf16(g / (1 + np.exp(-g)) * u)).astype(np.float64)
+        y = a @ W2[e].astype(np.float64).T
+        gate = (w * (ids == e)).sum(1)
+        dense += gate[:, None] * y
+    np.testing.assert_allclose(got, dense, rtol=1e-9, atol=1e-12)
+
+
+def test_cpu_baseline_dequant_matches_oracle():
+    import torch
+    from oracle.cpu_baseline import bl4_dequant_torch
+    rng = np.random.default_rng(14)
+    codes = rng.integers(0, 256, (8, 64), dtype=np.uint8)
+    tab16 = O.f32_to_f16(rng.standard_normal((8, 2, 16)).astype(np.float32))
+    tb = torch.from_numpy(O.bl4_tables_bf16(tab16).view(np.int16)).view(torch.bfloat16)
+    got = bl4_dequant_torch(torch.from_numpy(codes), tb).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, O.bl4_dequant(codes, tab16))
