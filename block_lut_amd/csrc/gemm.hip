@@ -1,40 +1,46 @@
 // Prefill grouped LUT-GEMM on MFMA (v_mfma_f32_32x32x16_bf16, gfx950).
 //
-// Positions (permuted (token, slot) pairs) of one expert are contiguous, so
-// the grouped GEMM walks tiles of 128 positions of one expert at a time
-// (tile -> expert found by a scan of the expert offsets; no host sync).
+// Positions (permuted (token, slot) pairs) of one expert are contiguous, so a
+// tile is up to 256 positions of one expert (tile -> expert found by a scan of
+// the expert offsets, heaviest experts -- the shared ones, stored last --
+// first; no host sync).
 //
-// CTA = 4 waves, tile = 128 positions x 256 weight rows, K step = 64 (one
-// BL4 codebook block per row).  Per K step:
-//   A (activations, bf16) 128 x 64 -> LDS (row stride padded to 144 B);
-//     stage 1 gathers the rows x[token(perm[p])] directly (fused permute).
+// CTA = 4 waves, tile = (up to) 256 positions x 256 weight rows, K step = 64
+// (one BL4 codebook block per row).  Wave w owns 64 weight rows (2 MFMA
+// n-tiles) and ALL m-tiles of 32 positions: up to 8 x 2 accumulators of 16
+// fp32 (256 per lane, held in AGPRs); m-tiles past the expert's position count
+// are skipped, so a tile costs what its positions need.  Per K step:
+//   A (activations, bf16) 256 x 64 -> LDS (144-byte padded rows), double
+//     buffered, one barrier per step; stage 1 gathers the rows
+//     x[token(perm[p])] directly (fused permute).
 //   B tables: the 256 rows' 32-byte bf16 tables of block kb -> LDS.
 //   B codes: each lane reads its own 16 bytes (32 codes) of its row straight
-//     from global memory into registers; the four 16-wide k-substeps of the
-//     MFMA take bytes 4ks..4ks+3, i.e. lane half h covers columns
-//     32h + 8ks .. +7 of the block.  A fragments use the same column map, so
-//     the contraction is unchanged (any consistent permutation of k is).
-//   The lookup (LDS table[row][code]) yields the bf16 dequantised weights
-//   (bit-exact rule) that form the MFMA B fragment.
-// Wave w owns 64 weight rows = 2 MFMA n-tiles and all 4 m-tiles of 32
-// positions: 8 accumulators of 16 fp32.
+//     from global memory; the four 16-wide k-substeps take bytes 4ks..4ks+3,
+//     i.e. lane half h covers columns 32h + 8ks .. +7 of the block, and the A
+//     fragments use the same column map (a consistent permutation of k leaves
+//     the contraction unchanged).  The lookup table[row][code] (one SDWA add
+//     and one ds_read_u16 per weight) gives the bf16 dequantised weights of
+//     the MFMA B fragment.
+//   The next step's A, tables and codes are loaded into registers while the
+//   current step's MFMAs run.
 //   stage 1 (gate_up): n-tile 0 = gate rows i0+32w.., n-tile 1 = up rows
-//     I+i0+32w..; epilogue act = bf16(silu(g) * u) written per position.
+//     I+i0+32w..; epilogue act = bf16(silu(g) * u) per position.
 //   stage 2 (down): n-tiles = rows h0+64w.., +32; epilogue y_pos[p][h] =
 //     acc * routing weight (fp32), summed per token by the combine kernel.
 // Restates the prefill branch of LUTFusedMoEMethod.apply
 // (vllm_lut/quant_method.py:261-277) and the per-expert GEMMs of the
-// llama.cpp mul_mat_id patch (llama-cpp-port/patches/0001:151-208), with the
+// llama.cpp mul_mat_id patch (llama-cpp-port/patches/0001:151-208), over the
 // routed tokens only instead of all T tokens.
 #include "common.h"
 #include "kernels.h"
+#include "lut_core.h"
 
 using namespace lutmoe;
 using lutmoe_host::MoeRouting;
 
 namespace {
 
-constexpr int kBM = 128;          // positions per tile
+constexpr int kBM = 256;          // positions per tile (max)
 constexpr int kBN = 256;          // weight rows per tile
 constexpr int kBK = 64;           // K step
 constexpr int kAStride = 72;      // bf16 per LDS A row (64 + 8 pad)
@@ -43,39 +49,45 @@ struct TileInfo {
     int e, m0, p0, n;
 };
 
-// blockIdx.y -> (expert, first position of the tile); e = -1 when past the end.
+// blockIdx.y -> (expert, first position of the tile); e = -1 past the end.
+// Experts are walked from the last id down so the always-on shared experts
+// (stored last, every token) are scheduled first.  Wave 0 does it 64 experts
+// at a time: per-expert tile counts, an inclusive wave scan, and a ballot for
+// the expert whose tile range holds j.
 __device__ __forceinline__ TileInfo find_tile(const MoeRouting& rt, int j) {
     __shared__ TileInfo s_tile;
-    if (threadIdx.x == 0) {
-        TileInfo ti{-1, 0, 0, 0};
-        int rem = j;
-        for (int e = 0; e < rt.num_experts_total; ++e) {
-            const int p0 = rt.offsets[e], n = rt.offsets[e + 1] - p0;
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        const int et = rt.num_experts_total;
+        int base = 0;   // tiles of the experts in earlier chunks
+        bool found = false;
+        for (int c0 = 0; c0 < et && !found; c0 += 64) {
+            const int e = et - 1 - (c0 + lane);
+            int p0 = 0, n = 0;
+            if (e >= 0) {
+                p0 = rt.offsets[e];
+                n = rt.offsets[e + 1] - p0;
+            }
             const int nt = (n + kBM - 1) / kBM;
-            if (rem < nt) { ti = TileInfo{e, rem * kBM, p0, n}; break; }
-            rem -= nt;
+            const int incl = wave_scan_incl(nt);
+            const int excl = incl - nt;
+            const bool hit = e >= 0 && j >= base + excl && j < base + incl;
+            if (hit) s_tile = TileInfo{e, (j - base - excl) * kBM, p0, n};
+            found = __ballot(hit) != 0;
+            base += __builtin_amdgcn_readlane(incl, 63);
         }
-        s_tile = ti;
+        if (!found && lane == 0) s_tile = TileInfo{-1, 0, 0, 0};
     }
     __syncthreads();
     return s_tile;
 }
 
-__device__ __forceinline__ bf16x8_t lookup8(uint32_t w, const uint16_t* tab) {
+// REF: 8 byte codes -> 8 bf16 weights bf16(cb[c] * absmax) (bit-exact dequant).
+__device__ __forceinline__ bf16x8_t lookup8_ref(uint32_t w0, uint32_t w1, const float* cb, float am) {
     uint32_t o[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const uint32_t b = (w >> (8 * j)) & 0xffu;
-        o[j] = (uint32_t)tab[b & 15u] | ((uint32_t)tab[b >> 4] << 16);
-    }
-    return __builtin_bit_cast(bf16x8_t, make_uint4(o[0], o[1], o[2], o[3]));
-}
-
-__device__ __forceinline__ bf16x8_t lookup8_ref(uint2 w, const float* cb, float am) {
-    uint32_t o[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t word = j < 2 ? w.x : w.y;
+        const uint32_t word = j < 2 ? w0 : w1;
         const uint32_t c0 = (word >> (16 * (j & 1))) & 0xffu;
         const uint32_t c1 = (word >> (16 * (j & 1) + 8)) & 0xffu;
         o[j] = f32_to_bf16(cb[c0] * am) | (f32_to_bf16(cb[c1] * am) << 16);
@@ -83,46 +95,68 @@ __device__ __forceinline__ bf16x8_t lookup8_ref(uint2 w, const float* cb, float 
     return __builtin_bit_cast(bf16x8_t, make_uint4(o[0], o[1], o[2], o[3]));
 }
 
-template <bool kGateUp, int kFmt>
-__global__ __launch_bounds__(256, 2) void prefill_kernel(lutmoe_moe_desc d,
-                                                         const uint16_t* __restrict__ src,
-                                                         MoeRouting rt, void* __restrict__ dst) {
-    __shared__ __attribute__((aligned(16))) uint16_t s_a[kBM * kAStride];
-    __shared__ __attribute__((aligned(16))) uint16_t s_t[kFmt == LUTMOE_FMT_BL4 ? kBN * 16 : 8];
-    __shared__ float s_cb[kFmt == LUTMOE_FMT_REF ? 256 : 1];
-    const TileInfo ti = find_tile(rt, blockIdx.y);
-    if (ti.e < 0) return;
-    const lutmoe_weights& w = kGateUp ? d.w13 : d.w2;
-    if (kFmt == LUTMOE_FMT_REF) {
-        const uint16_t* cb = (const uint16_t*)w.codebook;
-        s_cb[threadIdx.x] = bf16_to_f32(cb[threadIdx.x]);
+// One lane's B operand for one K step: its two weight rows (n-tiles), the
+// 32 columns 32h .. 32h+31 of the 64-column block kb.
+template <int kFmt>
+struct BStep;
+
+template <>
+struct BStep<LUTMOE_FMT_BL4> {
+    u32x4_t codes[2];     // 32 nibble codes per row
+    u32x4_t tab[2][2];    // the row's bf16[16] table of block kb
+    __device__ __forceinline__ void load(const uint8_t* codes_e, const uint8_t* tabs_e, const int (&row)[2],
+                                         int K, int kb, int bh) {
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            const int64_t off = (int64_t)row[nt] * (K / 2) + kb * 32;
+            codes[nt] = *reinterpret_cast<const u32x4_t*>(codes_e + off + 16 * bh);
+            tab[nt][0] = *reinterpret_cast<const u32x4_t*>(tabs_e + off);
+            tab[nt][1] = *reinterpret_cast<const u32x4_t*>(tabs_e + off + 16);
+        }
     }
+};
+
+template <>
+struct BStep<LUTMOE_FMT_REF> {
+    u32x4_t codes[2][2];  // 32 byte codes per row
+    float am[2];          // absmax of the row's 128-block holding these columns
+    __device__ __forceinline__ void load(const uint8_t* codes_e, const uint16_t* absmax_e, const int (&row)[2],
+                                         int K, int kb, int bh, int block_size, int64_t nabs) {
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            const int64_t flat = (int64_t)row[nt] * K + kb * kBK + 32 * bh;
+            codes[nt][0] = *reinterpret_cast<const u32x4_t*>(codes_e + flat);
+            codes[nt][1] = *reinterpret_cast<const u32x4_t*>(codes_e + flat + 16);
+            int64_t b = ((int64_t)row[nt] * K + kb * kBK) / block_size;
+            b = b < nabs ? b : nabs - 1;
+            am[nt] = bf16_to_f32(absmax_e[b]);
+        }
+    }
+};
+
+// One tile with NMT m-tiles of work (a compile-time count, so the K loop is
+// one basic block with no per-m-tile branches).
+template <bool kGateUp, int kFmt, int NMT>
+__device__ __forceinline__ void prefill_tile(const lutmoe_moe_desc& d, const uint16_t* __restrict__ src,
+                                             const MoeRouting& rt, void* __restrict__ dst,
+                                             const TileInfo ti, uint16_t (*s_a)[kBM * kAStride],
+                                             const float* s_cb) {
+    const lutmoe_weights& w = kGateUp ? d.w13 : d.w2;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int I = d.inter, H = d.hidden;
     const int K = kGateUp ? H : I;
     const int nkb = K / kBK;
     const int n0 = blockIdx.x * (kGateUp ? kBN / 2 : kBN);   // first intermediate idx / h row
-    const int nmax = kGateUp ? I : H;                        // bound on n0 + offset
+    const int nvalid = min(kBM, ti.n - ti.m0);               // positions in this tile
 
-    // ---- rows owned by this thread for A staging and table staging
-    const int a_row = tid >> 1, a_half = tid & 1;
-    int a_pos = ti.p0 + ti.m0 + a_row;
-    a_pos = min(a_pos, ti.p0 + ti.n - 1);
+    // ---- A staging: thread t owns tile row t (64 bf16 = 8 x 16 B per step);
+    // rows past the tile's positions repeat its last position (never read).
+    const int a_pos = ti.p0 + ti.m0 + min(tid, nvalid - 1);
     const uint16_t* a_src;
     if (kGateUp) a_src = src + (int64_t)(rt.perm[a_pos] / rt.k_eff) * H;
     else a_src = src + (int64_t)a_pos * I;
-    a_src += 32 * a_half;
 
-    auto wrow = [&](int local) -> int {   // weight row of local tile row 0..255
-        if (kGateUp) {
-            const int i = min(n0 + (local & 127), I - 1);
-            return local < 128 ? i : I + i;
-        }
-        return min(n0 + local, H - 1);
-    };
-    const int t_row = wrow(tid);
-
-    // ---- B rows of this lane: n-tile 0/1
+    // ---- B rows of this lane: n-tiles 0/1
     const int bn = lane & 31, bh = lane >> 5;
     int b_row[2];
     if (kGateUp) {
@@ -133,113 +167,131 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(lutmoe_moe_desc d,
         b_row[0] = min(n0 + 64 * wv + bn, H - 1);
         b_row[1] = min(n0 + 64 * wv + 32 + bn, H - 1);
     }
-    const int b_local[2] = {kGateUp ? 32 * wv + bn : 64 * wv + bn,
-                            kGateUp ? 128 + 32 * wv + bn : 64 * wv + 32 + bn};
-
     const uint8_t* codes;
-    const uint16_t* tables;
-    const uint16_t* absmax = nullptr;
+    const void* tabs;
     if (kFmt == LUTMOE_FMT_BL4) {
         const int64_t per = (int64_t)w.rows * (w.cols / 2);
         codes = (const uint8_t*)w.codes + ti.e * per;
-        tables = (const uint16_t*)((const uint8_t*)w.tables + ti.e * per);
+        tabs = (const uint8_t*)w.tables + ti.e * per;
     } else {
         codes = (const uint8_t*)w.codes + (int64_t)ti.e * w.rows * w.cols;
-        tables = nullptr;
-        absmax = (const uint16_t*)w.tables + (int64_t)ti.e * w.absmax_per_expert;
+        tabs = (const uint16_t*)w.tables + (int64_t)ti.e * w.absmax_per_expert;
     }
-
-    // ---- register staging for the next K step
-    uint4 ra[4];
-    uint4 rt2[2];
-    uint4 rc[2][2];   // BL4: [ntile][0] = 16 B codes; REF: [ntile][0..1] = 32 B codes
-    float ram[2];
-
-    auto load_step = [&](int kb) {
+    auto load_b = [&](BStep<kFmt>& b, int kb) __attribute__((always_inline)) {
+        if constexpr (kFmt == LUTMOE_FMT_BL4)
+            b.load(codes, (const uint8_t*)tabs, b_row, K, kb, bh);
+        else
+            b.load(codes, (const uint16_t*)tabs, b_row, K, kb, bh, w.block_size, w.absmax_per_expert);
+    };
+    u32x4_t ra[8];
+    auto load_a = [&](int kb) __attribute__((always_inline)) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) ra[q] = *reinterpret_cast<const uint4*>(a_src + kb * kBK + 8 * q);
-        if (kFmt == LUTMOE_FMT_BL4) {
-            const uint16_t* tp = tables + (int64_t)t_row * (K / 2 / 2) + kb * 16;
-            rt2[0] = *reinterpret_cast<const uint4*>(tp);
-            rt2[1] = *reinterpret_cast<const uint4*>(tp + 8);
+        for (int q = 0; q < 8; ++q) ra[q] = *reinterpret_cast<const u32x4_t*>(a_src + kb * kBK + 8 * q);
+    };
+    auto store_a = [&](int buf) __attribute__((always_inline)) {
+        uint16_t* ad = &s_a[buf][tid * kAStride];
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt)
-                rc[nt][0] = *reinterpret_cast<const uint4*>(codes + (int64_t)b_row[nt] * (K / 2) + kb * 32 + 16 * bh);
-        } else {
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
-                const int64_t flat = (int64_t)b_row[nt] * K + kb * kBK + 32 * bh;
-                rc[nt][0] = *reinterpret_cast<const uint4*>(codes + flat);
-                rc[nt][1] = *reinterpret_cast<const uint4*>(codes + flat + 16);
-                int64_t b = ((int64_t)b_row[nt] * K + kb * kBK) / w.block_size;
-                b = b < w.absmax_per_expert ? b : w.absmax_per_expert - 1;
-                ram[nt] = bf16_to_f32(absmax[b]);
-            }
-        }
+        for (int q = 0; q < 8; ++q) *reinterpret_cast<u32x4_t*>(ad + 8 * q) = ra[q];
     };
 
-    f32x16_t acc[4][2];
+    f32x16_t acc[NMT][2];
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
+    for (int mt = 0; mt < NMT; ++mt)
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[mt][nt][i] = 0.f;
 
-    load_step(0);
-    for (int kb = 0; kb < nkb; ++kb) {
-        // registers -> LDS
-        uint16_t* ad = s_a + a_row * kAStride + 32 * a_half;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) *reinterpret_cast<uint4*>(ad + 8 * q) = ra[q];
-        if (kFmt == LUTMOE_FMT_BL4) {
-            *reinterpret_cast<uint4*>(s_t + tid * 16) = rt2[0];
-            *reinterpret_cast<uint4*>(s_t + tid * 16 + 8) = rt2[1];
-        }
-        uint4 cc[2][2];
-        float cam[2];
+    auto frag_b = [&](const RegTable16 (&tb)[2], const BStep<kFmt>& b, int ks, bf16x8_t (&bf)[2])
+        __attribute__((always_inline)) {
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
-            cc[nt][0] = rc[nt][0];
-            cc[nt][1] = rc[nt][1];
-            cam[nt] = ram[nt];
+            if constexpr (kFmt == LUTMOE_FMT_BL4)
+                bf[nt] = __builtin_bit_cast(bf16x8_t, lookup8_reg(tb[nt], b.codes[nt][ks]));
+            else
+                bf[nt] = lookup8_ref(b.codes[nt][ks >> 1][2 * (ks & 1)], b.codes[nt][ks >> 1][2 * (ks & 1) + 1],
+                                     s_cb, b.am[nt]);
         }
-        __syncthreads();
-        if (kb + 1 < nkb) load_step(kb + 1);
+    };
+    auto split = [&](const BStep<kFmt>& b, RegTable16 (&tb)[2]) __attribute__((always_inline)) {
+        if constexpr (kFmt == LUTMOE_FMT_BL4) {
+            tb[0] = split_table16(b.tab[0][0], b.tab[0][1]);
+            tb[1] = split_table16(b.tab[1][0], b.tab[1][1]);
+        }
+    };
+    auto frag_a = [&](int buf, int ks, bf16x8_t (&af)[NMT]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int mt = 0; mt < NMT; ++mt)
+            af[mt] = *reinterpret_cast<const bf16x8_t*>(&s_a[buf][(mt * 32 + bn) * kAStride + 32 * bh + 8 * ks]);
+    };
+
+    // Software pipeline.  Entering step kb: A(kb) in LDS buffer kb&1 (visible
+    // after the last barrier), A(kb+1) in flight to registers `ra`, the B
+    // operand of step kb in `bcur` (tables already split into `tb`), of step
+    // kb+1 in flight to `bnext`, and the step-kb fragments of k-substep 0 in
+    // bf/af.  Each k-substep computes the next substep's fragments while its
+    // MFMAs issue; substep 3 prepares step kb+1's B side.
+    BStep<kFmt> bcur, bnext;
+    RegTable16 tb[2];
+    load_a(0);
+    load_b(bcur, 0);
+    store_a(0);
+    load_a(min(1, nkb - 1));
+    load_b(bnext, min(1, nkb - 1));
+    split(bcur, tb);
+    bf16x8_t bf[2], af[NMT];
+    frag_b(tb, bcur, 0, bf);
+    __syncthreads();
+    frag_a(0, 0, af);
+
+    for (int kb = 0; kb < nkb; ++kb) {
+        const int buf = kb & 1;
+        // A(kb+1) -> the other buffer (last read in step kb-1, before the
+        // previous barrier), then A(kb+2) -> registers.  Past the end these
+        // repeat the last step, harmlessly.
+        store_a(buf ^ 1);
+        load_a(min(kb + 2, nkb - 1));
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-            bf16x8_t bf[2];
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
-                if (kFmt == LUTMOE_FMT_BL4) {
-                    const uint32_t wd = ks == 0 ? cc[nt][0].x : ks == 1 ? cc[nt][0].y : ks == 2 ? cc[nt][0].z : cc[nt][0].w;
-                    bf[nt] = lookup8(wd, s_t + b_local[nt] * 16);
-                } else {
-                    const uint4 q4 = cc[nt][ks >> 1];
-                    const uint2 wd = (ks & 1) ? make_uint2(q4.z, q4.w) : make_uint2(q4.x, q4.y);
-                    bf[nt] = lookup8_ref(wd, s_cb, cam[nt]);
-                }
+            // the next substep's A fragments are read first, a whole substep
+            // of MFMAs ahead of their use (the fences keep the scheduler from
+            // sinking them next to their MFMAs)
+            bf16x8_t bf_n[2], af_n[NMT];
+            if (ks < 3) frag_a(buf, ks + 1, af_n);
+            __builtin_amdgcn_sched_barrier(0);
+            if (ks < 3) {
+                frag_b(tb, bcur, ks + 1, bf_n);
+            } else {
+                split(bnext, tb);
+                frag_b(tb, bnext, 0, bf_n);
             }
 #pragma unroll
-            for (int mt = 0; mt < 4; ++mt) {
-                const bf16x8_t af = *reinterpret_cast<const bf16x8_t*>(
-                    s_a + (mt * 32 + bn) * kAStride + 32 * bh + 8 * ks);
+            for (int mt = 0; mt < NMT; ++mt)
 #pragma unroll
                 for (int nt = 0; nt < 2; ++nt)
-                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bf[nt], acc[mt][nt], 0, 0, 0);
+                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mt], bf[nt], acc[mt][nt], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            bf[0] = bf_n[0];
+            bf[1] = bf_n[1];
+            if (ks < 3) {
+#pragma unroll
+                for (int mt = 0; mt < NMT; ++mt) af[mt] = af_n[mt];
             }
         }
+        bcur = bnext;
+        load_b(bnext, min(kb + 2, nkb - 1));
         __syncthreads();
+        frag_a(buf ^ 1, 0, af);
     }
 
     // ---- epilogue.  D layout: lane (n = lane%32, h = lane/32), element i ->
     // row m = 8*(i/4) + 4*h + (i%4), column n.
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
+    for (int mt = 0; mt < NMT; ++mt) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const int m = mt * 32 + 8 * (i >> 2) + 4 * bh + (i & 3);
-            if (ti.m0 + m >= ti.n) continue;
+            if (m >= nvalid) continue;
             const int p = ti.p0 + ti.m0 + m;
             if (kGateUp) {
                 const int ii = n0 + 32 * wv + bn;
@@ -258,29 +310,359 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(lutmoe_moe_desc d,
     }
 }
 
+// ---------------------------------------------------------------------------
+// BL4 tiles: operands staged global -> LDS by direct loads (global_load_lds,
+// no staging registers) through a ring of 3 stages of one K step each:
+//   A      [256 rows] x 128 B             (32 KB; 16-byte chunk c = columns
+//          8c..8c+7 of row r stored at chunk c ^ swz(r), so the 32 rows of a
+//          fragment read hit distinct LDS banks)
+//   codes  [256 rows] x 32 B             ( 8 KB; bytes 16h.. = columns 32h..32h+31)
+//   tables [256 rows] x 32 B             ( 8 KB; the rows' bf16[16] tables)
+// Each load instruction reads whole 128-byte lines (8 lanes per A row, 2 lanes
+// per 32-byte weight-row segment).  Every thread issues the same 12 loads per
+// stage, so `s_waitcnt vmcnt(12)` means "all but the newest stage have
+// landed".  Per step kb: k-substeps 0-2 run from slot kb%3; then a barrier
+// (stage kb+1 landed everywhere, slot kb%3 no longer read), the refill of slot
+// kb%3 with stage kb+3, and k-substep 3's MFMAs overlapped with reading and
+// looking up step kb+1's operands.
+constexpr int kSlotA = kBM * kBK * 2;              // 32 KB
+constexpr int kSlotB = kBN * 32;                   // 8 KB
+constexpr int kSlotBytes = kSlotA + 2 * kSlotB;    // 48 KB
+constexpr int kStages = 3;
+constexpr int kDmaPerStage = 12;
+
+// A-row chunk swizzle: distinct for any 8 consecutive rows, and (r&1, swz)
+// distinct for any 16 consecutive rows.
+__device__ __forceinline__ int a_swz(int r) { return ((r >> 1) ^ (r << 2)) & 7; }
+
+// 16 bytes per lane from sbase + voff into LDS at m0 + 16 * lane
+// (global_load_lds_dwordx4 with a scalar base, so per-step address updates
+// are scalar adds).  Issued as inline asm so the compiler does not track it:
+// the ring's explicit vmcnt waits and barriers order it, and no
+// compiler-visible global load is in flight between the first of these and
+// the final vmcnt(0).
+__device__ __forceinline__ void dma16(uint32_t voff, const void* sbase, uint32_t m0) {
+    asm volatile("global_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase), "{m0}"(m0) : "memory");
+}
+
+// Wait until at most `after` ring loads of this thread are in flight (the
+// stages issued after the one needed next), and all of its LDS reads are
+// done, then barrier.  Memory clobber: no LDS access moves across it.
+template <int kAfter>
+__device__ __forceinline__ void ring_wait_barrier_n() {
+    if constexpr (kAfter == 24)
+        asm volatile("s_waitcnt vmcnt(24) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else if constexpr (kAfter == 12)
+        asm volatile("s_waitcnt vmcnt(12) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+__device__ __forceinline__ void ring_wait_barrier(int stages_after) {
+    static_assert(kDmaPerStage == 12, "vmcnt immediates above");
+    if (stages_after >= 2) ring_wait_barrier_n<24>();
+    else if (stages_after == 1) ring_wait_barrier_n<12>();
+    else ring_wait_barrier_n<0>();
+}
+
+template <typename T>
+__device__ __forceinline__ const T* uniform_ptr(const T* p) {
+    const uint64_t v = (uint64_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (const T*)(((uint64_t)hi << 32) | lo);
+}
+
+template <bool kGateUp, int NMT>
+__device__ __forceinline__ void prefill_tile_bl4(const lutmoe_moe_desc& d, const uint16_t* __restrict__ src,
+                                                 const MoeRouting& rt, void* __restrict__ dst,
+                                                 const TileInfo ti, uint8_t* ring) {
+    const lutmoe_weights& w = d.w13;
+    const lutmoe_weights& w2 = d.w2;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int I = d.inter, H = d.hidden;
+    const int K = kGateUp ? H : I;
+    const int nkb = K / kBK;
+    const int n0 = blockIdx.x * (kGateUp ? kBN / 2 : kBN);
+    const int nvalid = min(kBM, ti.n - ti.m0);
+
+    // ---- loader side (all offsets 32-bit, from scalar bases; the host
+    // checks the sizes).  A load j of wave w covers tile rows 64w+8j .. +7:
+    // lane l reads the (l%8 ^ swz)-th 16 bytes of row 64w+8j+l/8.  Rows past
+    // the tile's positions repeat its last position (never read back).
+    const int wvu = __builtin_amdgcn_readfirstlane(wv);
+    uint32_t a_off[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int r = 64 * wv + 8 * j + (lane >> 3);
+        const int pos = ti.p0 + ti.m0 + min(r, nvalid - 1);
+        const uint32_t row = kGateUp ? (uint32_t)(rt.perm[pos] / rt.k_eff) * (uint32_t)H : (uint32_t)pos * (uint32_t)I;
+        a_off[j] = 2u * (row + 8u * (uint32_t)((lane & 7) ^ a_swz(r)));
+    }
+    // codes / tables: load h of wave w covers tile rows 64w+32h .. +31, two
+    // lanes per row (16 B each), so a row's 32 bytes land contiguous in LDS
+    const lutmoe_weights& ww = kGateUp ? w : w2;
+    const int64_t per = (int64_t)ww.rows * (ww.cols / 2);
+    const uint8_t* c_base = uniform_ptr((const uint8_t*)ww.codes + ti.e * per);
+    const uint8_t* t_base = uniform_ptr((const uint8_t*)ww.tables + ti.e * per);
+    uint32_t w_off[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int tr = 64 * wv + 32 * h + (lane >> 1);
+        int trow;
+        if (kGateUp) {
+            const int i = min(n0 + (tr & 127), I - 1);
+            trow = tr < 128 ? i : I + i;
+        } else {
+            trow = min(n0 + tr, H - 1);
+        }
+        w_off[h] = (uint32_t)trow * (uint32_t)(K / 2) + 16u * (uint32_t)(lane & 1);
+    }
+    const uint8_t* a_base = (const uint8_t*)src;
+
+    auto issue = [&](int kb, const uint8_t* sl) __attribute__((always_inline)) {
+        const uint32_t l0 = lds_addr(sl);
+        const uint8_t* ab = a_base + kb * (kBK * 2);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dma16(a_off[j], ab, l0 + (64 * wvu + 8 * j) * 128);
+        const uint8_t* cb = c_base + kb * 32;
+        const uint8_t* tbp = t_base + kb * 32;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            dma16(w_off[h], cb, l0 + kSlotA + wvu * 2048 + h * 1024);
+            dma16(w_off[h], tbp, l0 + kSlotA + kSlotB + wvu * 2048 + h * 1024);
+        }
+    };
+
+    // ---- compute side: lane (n = lane%32, h = lane/32), n-tiles 0/1
+    const int bn = lane & 31, bh = lane >> 5;
+    const int L0 = kGateUp ? 32 * wv + bn : 64 * wv + bn;
+    const int L1 = kGateUp ? 128 + 32 * wv + bn : 64 * wv + 32 + bn;
+
+    auto read_codes = [&](const uint8_t* sl, u32x4_t (&codes)[2]) __attribute__((always_inline)) {
+        const uint8_t* cb = sl + kSlotA + bh * 16;
+        codes[0] = *reinterpret_cast<const u32x4_t*>(cb + L0 * 32);
+        codes[1] = *reinterpret_cast<const u32x4_t*>(cb + L1 * 32);
+    };
+    const int sw = a_swz(bn);   // = a_swz(mt * 32 + bn) for every m-tile
+    auto frag_a = [&](const uint8_t* sl, int ks, bf16x8_t (&af)[NMT]) __attribute__((always_inline)) {
+        const uint8_t* p = sl + bn * 128 + 16 * ((4 * bh + ks) ^ sw);
+#pragma unroll
+        for (int mt = 0; mt < NMT; ++mt) af[mt] = *reinterpret_cast<const bf16x8_t*>(p + mt * 4096);
+    };
+    // B fragment of k-substep ks: the lane's 8 codes looked up in its rows'
+    // LDS tables of slot `sl` (reads issued here, combined later)
+    auto frag_b = [&](const uint8_t* sl, const u32x4_t (&codes)[2], int ks, Lookup8 (&lk)[2])
+        __attribute__((always_inline)) {
+        const uint32_t tbase = lds_addr(sl + kSlotA + kSlotB);
+        lk[0] = lookup8_issue(codes[0][ks], tbase + L0 * 32);
+        lk[1] = lookup8_issue(codes[1][ks], tbase + L1 * 32);
+    };
+
+    f32x16_t acc[NMT][2];
+#pragma unroll
+    for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[mt][nt][i] = 0.f;
+
+    // prologue: stages 0..2 in flight; wait for stage 0
+    const int npro = min(kStages, nkb);
+    for (int st = 0; st < npro; ++st) issue(st, ring + st * kSlotBytes);
+    ring_wait_barrier(npro - 1);
+    u32x4_t codes[2];
+    bf16x8_t bf[2], af[NMT];
+    read_codes(ring, codes);
+    frag_a(ring, 0, af);
+    {
+        Lookup8 lk[2];
+        frag_b(ring, codes, 0, lk);
+        bf[0] = __builtin_bit_cast(bf16x8_t, lookup8_combine(lk[0]));
+        bf[1] = __builtin_bit_cast(bf16x8_t, lookup8_combine(lk[1]));
+    }
+
+    int slot = 0;
+    for (int kb = 0; kb < nkb; ++kb) {
+        uint8_t* sl = ring + slot * kSlotBytes;
+        const int nslot = slot == kStages - 1 ? 0 : slot + 1;
+        const uint8_t* nsl = ring + nslot * kSlotBytes;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            // region 1: issue the LDS reads of the next k-substep's fragments
+            bf16x8_t af_n[NMT];
+            Lookup8 lk[2];
+            u32x4_t codes_n[2];
+            if (ks < 3) {
+                frag_a(sl, ks + 1, af_n);
+                frag_b(sl, codes, ks + 1, lk);
+            } else {
+                // stage kb+1 landed everywhere (only stage kb+2 may still be
+                // in flight) and no wave reads this slot any more -> refill
+                // it with stage kb+3
+                ring_wait_barrier(kb + 2 < nkb ? 1 : 0);
+                if (kb + 3 < nkb) issue(kb + 3, sl);
+                read_codes(nsl, codes_n);
+                frag_a(nsl, 0, af_n);
+                frag_b(nsl, codes_n, 0, lk);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            // region 2: this substep's MFMAs, with the next substep's
+            // combining ops slotted between them
+#pragma unroll
+            for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt)
+                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mt], bf[nt], acc[mt][nt], 0, 0, 0);
+            bf[0] = __builtin_bit_cast(bf16x8_t, lookup8_combine(lk[0]));
+            bf[1] = __builtin_bit_cast(bf16x8_t, lookup8_combine(lk[1]));
+#pragma unroll
+            for (int i = 0; i < 2 * NMT; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // 1 MFMA
+                if (i >= 2 * NMT - 8) __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);   // 1 VALU
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int mt = 0; mt < NMT; ++mt) af[mt] = af_n[mt];
+            if (ks == 3) {
+                codes[0] = codes_n[0];
+                codes[1] = codes_n[1];
+            }
+        }
+        slot = nslot;
+    }
+    // ---- epilogue through LDS, so global stores are whole lines.  D layout:
+    // lane (n = lane%32, h = lane/32), element i -> row m = 8*(i/4) + 4*h +
+    // (i%4), column n.  All loads landed (none may still write LDS) and all
+    // ring reads done -> the ring is free.
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if constexpr (kGateUp) {
+        // act tile [256 positions][128 intermediate columns] bf16
+        uint16_t* st = reinterpret_cast<uint16_t*>(ring);
+        const int col = 32 * wv + bn;
+#pragma unroll
+        for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int m = mt * 32 + 8 * (i >> 2) + 4 * bh + (i & 3);
+                st[m * 128 + col] = (uint16_t)f32_to_bf16(silu_mul(acc[mt][0][i], acc[mt][1][i]));
+            }
+        __syncthreads();
+        const int chunk = tid & 15;
+        if (n0 + 8 * chunk < I) {
+            uint16_t* out = (uint16_t*)dst + (int64_t)(ti.p0 + ti.m0) * I + n0 + 8 * chunk;
+            for (int r = tid >> 4; r < nvalid; r += 16)
+                *reinterpret_cast<u32x4_t*>(out + (int64_t)r * I) =
+                    *reinterpret_cast<const u32x4_t*>(&st[r * 128 + 8 * chunk]);
+        }
+    } else {
+        // y_pos tile [256 positions][256 h] fp32 times the routing weight, in
+        // two halves of 128 positions
+        float* st = reinterpret_cast<float*>(ring);
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            if (4 * hf < NMT) {
+                if (hf) __syncthreads();
+#pragma unroll
+                for (int mt = 4 * hf; mt < NMT && mt < 4 * hf + 4; ++mt)
+#pragma unroll
+                    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) {
+                            const int m = (mt - 4 * hf) * 32 + 8 * (i >> 2) + 4 * bh + (i & 3);
+                            st[m * 256 + 64 * wv + 32 * nt + bn] = acc[mt][nt][i];
+                        }
+                __syncthreads();
+                const int chunk = tid & 63;
+                if (n0 + 4 * chunk < H) {
+                    for (int r = tid >> 6; r < 128 && 128 * hf + r < nvalid; r += 4) {
+                        const int p = ti.p0 + ti.m0 + 128 * hf + r;
+                        const float pw = rt.pair_w[rt.perm[p]];
+                        float4 v = *reinterpret_cast<const float4*>(&st[r * 256 + 4 * chunk]);
+                        v.x *= pw;
+                        v.y *= pw;
+                        v.z *= pw;
+                        v.w *= pw;
+                        *reinterpret_cast<float4*>((float*)dst + (int64_t)p * H + n0 + 4 * chunk) = v;
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <bool kGateUp>
+__global__ __launch_bounds__(256, 1) void prefill_bl4_kernel(lutmoe_moe_desc d, const uint16_t* __restrict__ src,
+                                                             MoeRouting rt, void* __restrict__ dst) {
+    __shared__ __attribute__((aligned(16))) uint8_t ring[kStages * kSlotBytes];
+    const TileInfo ti = find_tile(rt, blockIdx.y);
+    if (ti.e < 0) return;
+    const int nmt = (min(kBM, ti.n - ti.m0) + 31) / 32;
+    switch (nmt) {
+#define LUTMOE_TILE_CASE(n) \
+    case n: prefill_tile_bl4<kGateUp, n>(d, src, rt, dst, ti, ring); break;
+        LUTMOE_TILE_CASE(1) LUTMOE_TILE_CASE(2) LUTMOE_TILE_CASE(3) LUTMOE_TILE_CASE(4)
+        LUTMOE_TILE_CASE(5) LUTMOE_TILE_CASE(6) LUTMOE_TILE_CASE(7) LUTMOE_TILE_CASE(8)
+#undef LUTMOE_TILE_CASE
+        default: break;
+    }
+}
+
+template <bool kGateUp, int kFmt>
+__global__ __launch_bounds__(256, 1) void prefill_kernel(lutmoe_moe_desc d,
+                                                         const uint16_t* __restrict__ src,
+                                                         MoeRouting rt, void* __restrict__ dst) {
+    __shared__ __attribute__((aligned(16))) uint16_t s_a[2][kBM * kAStride];
+    __shared__ float s_cb[kFmt == LUTMOE_FMT_REF ? 256 : 1];
+    const TileInfo ti = find_tile(rt, blockIdx.y);
+    if (ti.e < 0) return;
+    if (kFmt == LUTMOE_FMT_REF) {
+        const uint16_t* cb = (const uint16_t*)(kGateUp ? d.w13 : d.w2).codebook;
+        s_cb[threadIdx.x] = bf16_to_f32(cb[threadIdx.x]);
+    }
+    const int nmt = (min(kBM, ti.n - ti.m0) + 31) / 32;
+    switch (nmt) {
+#define LUTMOE_TILE_CASE(n) \
+    case n: prefill_tile<kGateUp, kFmt, n>(d, src, rt, dst, ti, s_a, s_cb); break;
+        LUTMOE_TILE_CASE(1) LUTMOE_TILE_CASE(2) LUTMOE_TILE_CASE(3) LUTMOE_TILE_CASE(4)
+        LUTMOE_TILE_CASE(5) LUTMOE_TILE_CASE(6) LUTMOE_TILE_CASE(7) LUTMOE_TILE_CASE(8)
+#undef LUTMOE_TILE_CASE
+        default: break;
+    }
+}
+
 inline int max_tiles(int P, int E_tot) { return (P + kBM - 1) / kBM + E_tot; }
 
 }  // namespace
 
 namespace lutmoe_host {
 
+// The BL4 kernel addresses activations and one expert's codes / tables with
+// 32-bit byte offsets from a scalar base.
+static bool bl4_offsets_fit(const lutmoe_moe_desc* d, const MoeRouting& r, int P) {
+    const int64_t lim = int64_t(1) << 32;
+    return (int64_t)r.T * d->hidden * 2 < lim && (int64_t)P * d->inter * 2 < lim &&
+           (int64_t)d->w13.rows * (d->w13.cols / 2) < lim && (int64_t)d->w2.rows * (d->w2.cols / 2) < lim;
+}
+
 int launch_prefill_gate_up(const lutmoe_moe_desc* d, const uint16_t* x, const MoeRouting& r,
                            uint16_t* act, int P, hipStream_t s) {
+    if (d->w13.format != LUTMOE_FMT_REF && !bl4_offsets_fit(d, r, P)) return LUTMOE_EUNSUPPORTED;
     const dim3 grid((d->inter + kBN / 2 - 1) / (kBN / 2), max_tiles(P, r.num_experts_total));
     if (d->w13.format == LUTMOE_FMT_REF)
         hipLaunchKernelGGL((prefill_kernel<true, LUTMOE_FMT_REF>), grid, dim3(256), 0, s, *d, x, r, (void*)act);
     else
-        hipLaunchKernelGGL((prefill_kernel<true, LUTMOE_FMT_BL4>), grid, dim3(256), 0, s, *d, x, r, (void*)act);
+        hipLaunchKernelGGL((prefill_bl4_kernel<true>), grid, dim3(256), 0, s, *d, x, r, (void*)act);
     return check_launch();
 }
 
 int launch_prefill_down(const lutmoe_moe_desc* d, const uint16_t* act, const MoeRouting& r,
                         float* y_pos, int P, hipStream_t s) {
+    if (d->w2.format != LUTMOE_FMT_REF && !bl4_offsets_fit(d, r, P)) return LUTMOE_EUNSUPPORTED;
     const dim3 grid((d->hidden + kBN - 1) / kBN, max_tiles(P, r.num_experts_total));
     if (d->w2.format == LUTMOE_FMT_REF)
         hipLaunchKernelGGL((prefill_kernel<false, LUTMOE_FMT_REF>), grid, dim3(256), 0, s, *d, act, r, (void*)y_pos);
     else
-        hipLaunchKernelGGL((prefill_kernel<false, LUTMOE_FMT_BL4>), grid, dim3(256), 0, s, *d, act, r, (void*)y_pos);
+        hipLaunchKernelGGL((prefill_bl4_kernel<false>), grid, dim3(256), 0, s, *d, act, r, (void*)y_pos);
     return check_launch();
 }
 
