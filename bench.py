@@ -103,8 +103,7 @@ def main():
             self.w = torch.empty((T, c["k"]), dtype=torch.float32, device=dev)
             self.ids = torch.empty((T, c["k"]), dtype=torch.int32, device=dev)
             self.out = torch.empty((T, c["H"]), dtype=torch.bfloat16, device=dev)
-            self.ws = torch.empty(ops.moe_workspace_bytes(layer, T, c["k"]), dtype=torch.uint8,
-                                  device=dev)
+            self.ws = ops.new_workspace(layer, T, c["k"], dev)
             ops.route_topk(self.logits, c["k"], out_w=self.w, out_ids=self.ids)
             torch.cuda.synchronize()
             ids = self.ids.cpu()

@@ -1,12 +1,14 @@
 // Decode-time fused MoE layer on BL4 weights: two kernels per layer.
 //
 //   bl4_decode_gate_up : routing + permutation (recomputed in every CTA from
-//                        top-k ids or router logits; T*k is small at decode)
+//                        top-k ids or router logits; T*k is small at decode;
+//                        the first CTA also stores it in the workspace)
 //                        -> grouped LUT-GEMV over W13 rows -> SwiGLU
 //                        -> act[position][I] (bf16)
-//   bl4_decode_down    : the same routing -> grouped LUT-GEMV over W2 rows
+//   bl4_decode_down    : the stored routing -> grouped LUT-GEMV over W2 rows
 //                        of every active expert -> per-position results meet
 //                        in LDS -> weighted sum per token in slot order -> out
+// For T > 2 decode_route_kernel routes once and both kernels read its copy.
 //
 // Reference behaviour: LUTFusedMoEMethod.apply, decode branch
 // (vllm_lut/quant_method.py:250-260), routing of moe_layer._routing
@@ -17,8 +19,10 @@
 // chunk lane l = 8g + q reads the code dword q of block g of every row and
 // the same-offset dword of that block's bf16 table (codes and tables are both
 // K/2 bytes per row), stages the tables in its LDS slot and looks each
-// nibble up there.  All chunk loads of a chunk group are issued before any is
-// consumed so a wave keeps up to 16 KB in flight.
+// nibble up there.  All chunk loads of a chunk group are issued (activations
+// first, then the weights chunk by chunk, without branches) before any is
+// consumed, so a wave keeps up to 16 KB in flight and starts on chunk 0 while
+// the later chunks are still arriving.
 #include <utility>
 
 #include "common.h"
@@ -29,9 +33,9 @@ using namespace lutmoe;
 
 namespace {
 
-constexpr int kChunk = 512;
+constexpr int kWChunk = 2048;            // columns per lane pass (64 lanes x 32)
 constexpr int kRows = 8;
-constexpr int kSlot = kRows * 256;
+constexpr int kSlot = kRows * 1024;      // LDS bytes per wave: 8 rows' tables of a chunk
 constexpr int kMaxEtot = 320;
 constexpr int kMaxP = 512;
 
@@ -53,6 +57,13 @@ struct RouteScratch {
     int pid[kMaxP];                     // expert of each pair (-1: dropped)
     int rin[kMaxP];                     // rank among same-expert pairs of its 64-pair chunk
     int ccnt[kMaxP / 64][kMaxEtot];     // per chunk, per expert count -> exclusive prefix
+};
+
+// Routing scratch is dead once the routing is in RouteOut (every routing
+// path ends with a CTA barrier), so it shares LDS with the GEMV table slots.
+union RouteOrSlots {
+    RouteScratch X;
+    __attribute__((aligned(16))) uint8_t slot[4 * kSlot];
 };
 
 struct DecodeArgs {
@@ -339,10 +350,9 @@ __device__ __forceinline__ void get_route(const DecodeArgs& A, RouteOut& R, Rout
     }
 }
 
-__global__ __launch_bounds__(256) void decode_route_kernel(DecodeArgs A) {
-    __shared__ RouteOut R;
-    __shared__ RouteScratch X;
-    cta_route(A, R, X);
+// The routing result in LDS -> its global copy (read by later kernels of the
+// same layer through get_route<true>).
+__device__ __forceinline__ void put_route(const DecodeArgs& A, const RouteOut& R) {
     const int E_tot = A.d.num_routed + A.d.num_shared;
     const int P = A.T * (A.k + A.d.num_shared);
     RouteOut* g = A.route;
@@ -359,53 +369,107 @@ __global__ __launch_bounds__(256) void decode_route_kernel(DecodeArgs A) {
     if (threadIdx.x == 0) g->nact = R.nact;
 }
 
-// One wave, 8 rows, chunks [c0, c0+CG) of K: loads first, then per chunk
-// stage tables in the wave's LDS slot and accumulate.
-template <int TB, int CG>
-__device__ __forceinline__ void bl4_rows8(const uint8_t* __restrict__ codes,
-                                          const uint8_t* __restrict__ tabs, const int (&rows)[kRows],
-                                          int K, int c0, int nch, int lane, uint8_t* slot,
-                                          const uint16_t* const (&xrow)[TB], int nt,
-                                          float (&acc)[kRows][TB]) {
-    const int nblk = K / kBlockBL;
-    uint32_t cw[CG][kRows], tw[CG][kRows];
-    uint32_t xs[CG][TB][4];
+__global__ __launch_bounds__(256) void decode_route_kernel(DecodeArgs A) {
+    __shared__ RouteOut R;
+    __shared__ RouteScratch X;
+    cta_route(A, R, X);
+    put_route(A, R);
+}
+
+// One wave, 8 rows, one 2048-column chunk cc of K: lane l covers columns
+// [2048cc + 32l, +32), i.e. 16 bytes of every row's codes and the matching 16
+// bytes of its tables (half of the block's bf16[16]); codes and tables are
+// both K/2 bytes per row.  Two 16-byte loads per row per chunk, issued
+// without branches (lanes past K read the row start and drop the values).
+struct Rows8 {
+    u32x4_t cw[kRows], tw[kRows];
+};
+
+__device__ __forceinline__ void load_rows8(const uint8_t* __restrict__ codes, const uint8_t* __restrict__ tabs,
+                                           const int (&rows)[kRows], int K, int cc, int lane, Rows8& b) {
+    const bool ok = cc * kWChunk + 32 * lane < K;
 #pragma unroll
-    for (int c = 0; c < CG; ++c) {
-        const int cc = c0 + c;
-        const bool ok = cc < nch && (cc * 8 + (lane >> 3)) < nblk;
+    for (int r = 0; r < kRows; ++r) {
+        const int64_t off = (int64_t)rows[r] * (K / 2) + (ok ? cc * (kWChunk / 2) + 16 * lane : 0);
+        b.cw[r] = *reinterpret_cast<const u32x4_t*>(codes + off);
+        b.tw[r] = *reinterpret_cast<const u32x4_t*>(tabs + off);
+    }
+}
+
+// The lane's 32 activations of up to TB vectors (dword 4j+i = columns 8j+2i,
+// 8j+2i+1 of its 32).  Lanes past K (and vectors past nt) read valid
+// activations that meet zero tables (past K) or are dropped (past nt).
+template <int TB>
+__device__ __forceinline__ void load_x8(const uint16_t* const (&xrow)[TB], int K, int cc, int lane, int nt,
+                                        uint32_t (&xs)[TB][16]) {
+    const bool ok = cc * kWChunk + 32 * lane < K;
 #pragma unroll
-        for (int r = 0; r < kRows; ++r) {
-            const int64_t off = (int64_t)rows[r] * (K / 2) + cc * 256 + 4 * lane;
-            cw[c][r] = ok ? *reinterpret_cast<const uint32_t*>(codes + off) : 0u;
-            tw[c][r] = ok ? *reinterpret_cast<const uint32_t*>(tabs + off) : 0u;
-        }
+    for (int t = 0; t < TB; ++t) {
+        const uint16_t* p = xrow[t] + (ok ? cc * kWChunk + 32 * lane : 0);
 #pragma unroll
-        for (int t = 0; t < TB; ++t) {
-            uint4 q = make_uint4(0u, 0u, 0u, 0u);
-            if (ok && t < nt) q = *reinterpret_cast<const uint4*>(xrow[t] + cc * kChunk + 8 * lane);
-            xs[c][t][0] = q.x; xs[c][t][1] = q.y; xs[c][t][2] = q.z; xs[c][t][3] = q.w;
+        for (int q = 0; q < 4; ++q) {
+            const uint4 v = *reinterpret_cast<const uint4*>(p + 8 * q);
+            xs[t][4 * q + 0] = v.x;
+            xs[t][4 * q + 1] = v.y;
+            xs[t][4 * q + 2] = v.z;
+            xs[t][4 * q + 3] = v.w;
         }
     }
-    const uint32_t gbase = lds_addr(slot) + ((lane >> 3) << 5);
+}
+
+// Row by row: stage row r's tables of the chunk in its 1 KB of the wave's LDS
+// slot (block g at r*1024 + 32g), then look its codes up there and
+// accumulate; row r only waits for its own loads, so the first rows are done
+// while the later ones are still arriving.
+template <int TB>
+__device__ __forceinline__ void compute_rows8(const Rows8& b, const uint32_t (&xs)[TB][16], bool ok, int lane,
+                                              uint8_t* slot, int nt, float (&acc)[kRows][TB]) {
+    const uint32_t tab = lds_addr(slot) + ((lane >> 1) << 5);
+    const u32x4_t z = {0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int c = 0; c < CG; ++c) {
-        if (c0 + c >= nch) break;
-#pragma unroll
-        for (int r = 0; r < kRows; ++r) *reinterpret_cast<uint32_t*>(slot + r * 256 + 4 * lane) = tw[c][r];
+    for (int r = 0; r < kRows; ++r) {
+        // lanes past K stage zero tables (their loads read the row start)
+        *reinterpret_cast<u32x4_t*>(slot + r * 1024 + 16 * lane) = ok ? b.tw[r] : z;
         wave_lds_sync();
 #pragma unroll
-        for (int r = 0; r < kRows; ++r) bl4_dot8<TB>(cw[c][r], gbase + r * 256, xs[c], nt, acc[r]);
-        wave_lds_sync();
+        for (int j = 0; j < 4; ++j) {
+            uint32_t xj[TB][4];
+#pragma unroll
+            for (int t = 0; t < TB; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) xj[t][i] = xs[t][4 * j + i];
+            bl4_dot8<TB>(b.cw[r][j], tab + r * 1024, xj, nt, acc[r]);
+        }
+    }
+    wave_lds_sync();
+}
+
+// All of K, chunk by chunk: activations first (small), then the weights.
+template <int TB>
+__device__ __forceinline__ void bl4_rows8(const uint8_t* __restrict__ codes, const uint8_t* __restrict__ tabs,
+                                          const int (&rows)[kRows], int K, int lane, uint8_t* slot,
+                                          const uint16_t* const (&xrow)[TB], int nt, float (&acc)[kRows][TB]) {
+    const int nch = (K + kWChunk - 1) / kWChunk;
+    for (int cc = 0; cc < nch; ++cc) {
+        Rows8 b;
+        uint32_t xs[TB][16];
+        load_x8<TB>(xrow, K, cc, lane, nt, xs);
+        __builtin_amdgcn_sched_barrier(0);
+        load_rows8(codes, tabs, rows, K, cc, lane, b);
+        // every load in flight before the first row is consumed
+        __builtin_amdgcn_sched_barrier(0);
+        compute_rows8<TB>(b, xs, cc * kWChunk + 32 * lane < K, lane, slot, nt, acc);
     }
 }
 
 template <int TB, bool kPre>
-__global__ __launch_bounds__(256) void bl4_decode_gate_up(DecodeArgs A) {
+__global__ __launch_bounds__(256, TB <= 2 ? 3 : 2) void bl4_decode_gate_up(DecodeArgs A) {
     __shared__ RouteOut R;
-    __shared__ RouteScratch X;
-    __shared__ __attribute__((aligned(16))) uint8_t s_slot[4 * kSlot];
-    get_route<kPre>(A, R, X);
+    __shared__ RouteOrSlots U;
+    uint8_t* s_slot = U.slot;
+    get_route<kPre>(A, R, U.X);
+    // the first CTA publishes the routing it computed for the down kernel
+    if (!kPre && blockIdx.x == 0 && blockIdx.y == 0) put_route(A, R);
     const int a = blockIdx.y;
     if (a >= R.nact) return;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -424,8 +488,6 @@ __global__ __launch_bounds__(256) void bl4_decode_gate_up(DecodeArgs A) {
     const int64_t per = (int64_t)A.d.w13.rows * (H / 2);
     const uint8_t* codes = (const uint8_t*)A.d.w13.codes + e * per;
     const uint8_t* tabs = (const uint8_t*)A.d.w13.tables + e * per;
-    const int nch = (H + kChunk - 1) / kChunk;
-    constexpr int CG = TB <= 2 ? 4 : 2;
     uint8_t* slot = s_slot + wv * kSlot;
     for (int tb = 0; tb < n; tb += TB) {
         const int nt = min(TB, n - tb);
@@ -437,8 +499,7 @@ __global__ __launch_bounds__(256) void bl4_decode_gate_up(DecodeArgs A) {
         for (int r = 0; r < kRows; ++r)
 #pragma unroll
             for (int t = 0; t < TB; ++t) acc[r][t] = 0.f;
-        for (int c0 = 0; c0 < nch; c0 += CG)
-            bl4_rows8<TB, CG>(codes, tabs, rows, H, c0, nch, lane, slot, xrow, nt, acc);
+        bl4_rows8<TB>(codes, tabs, rows, H, lane, slot, xrow, nt, acc);
         float g[4][TB], u[4][TB];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -457,12 +518,12 @@ __global__ __launch_bounds__(256) void bl4_decode_gate_up(DecodeArgs A) {
 }
 
 template <int TB, bool kPre>
-__global__ __launch_bounds__(256) void bl4_decode_down(DecodeArgs A) {
+__global__ __launch_bounds__(256, TB <= 2 ? 3 : 2) void bl4_decode_down(DecodeArgs A) {
     __shared__ RouteOut R;
-    __shared__ RouteScratch X;
-    __shared__ __attribute__((aligned(16))) uint8_t s_slot[4 * kSlot];
+    __shared__ RouteOrSlots U;
+    uint8_t* s_slot = U.slot;
     extern __shared__ float s_y[];   // [P][8]
-    get_route<kPre>(A, R, X);
+    get_route<kPre>(A, R, U.X);
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int I = A.d.inter, H = A.d.hidden, ke = A.k + A.d.num_shared;
     const int h0 = blockIdx.x * kRows;
@@ -470,8 +531,6 @@ __global__ __launch_bounds__(256) void bl4_decode_down(DecodeArgs A) {
 #pragma unroll
     for (int r = 0; r < kRows; ++r) rows[r] = min(h0 + r, H - 1);
     const int64_t per = (int64_t)A.d.w2.rows * (I / 2);
-    const int nch = (I + kChunk - 1) / kChunk;
-    constexpr int CG = TB <= 2 ? 4 : 2;
     uint8_t* slot = s_slot + wv * kSlot;
     for (int a = wv; a < R.nact; a += 4) {
         const int e = R.act[a];
@@ -488,8 +547,7 @@ __global__ __launch_bounds__(256) void bl4_decode_down(DecodeArgs A) {
             for (int r = 0; r < kRows; ++r)
 #pragma unroll
                 for (int t = 0; t < TB; ++t) acc[r][t] = 0.f;
-            for (int c0 = 0; c0 < nch; c0 += CG)
-                bl4_rows8<TB, CG>(codes, tabs, rows, I, c0, nch, lane, slot, xrow, nt, acc);
+            bl4_rows8<TB>(codes, tabs, rows, I, lane, slot, xrow, nt, acc);
 #pragma unroll
             for (int t = 0; t < TB; ++t) {
                 const int p = p0 + tb + min(t, nt - 1);
@@ -518,6 +576,207 @@ __global__ __launch_bounds__(256) void bl4_decode_down(DecodeArgs A) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// One persistent kernel for the whole layer.  Every CTA routes, then takes
+// work items from a queue in the workspace: first the gate_up items (one per
+// active expert and 16 intermediate indices, as bl4_decode_gate_up's CTAs),
+// then the down items (8 output rows of every active expert, as
+// bl4_decode_down's CTAs).  A down item issues its W2 loads, then waits until
+// every gate_up item has published its act slice, so W13 and W2 stream from
+// HBM together and the layer costs one launch.  Items are taken in queue
+// order, so every gate_up item a down item waits for is already held by a
+// running CTA: no CTA waits on one that may not be resident.  Waits are
+// bounded (20 ms; a CTA that hits the bound sets DecodeSync::err and carries
+// on), and
+// the last CTA to finish puts the counters back to zero for the next call.
+struct DecodeSync {
+    int queue;      // next work item
+    int gu_done;    // gate_up items whose act slice is published
+    int cta_done;   // CTAs finished
+    int err;        // sticky: a wait hit its bound
+};
+constexpr uint64_t kWaitTicks = 2000000;   // 20 ms of the 100 MHz real-time counter
+
+// The persistent kernel is switched off: its first GPU runs did not complete
+// (cause not yet found; the per-stage kernels below run instead).
+constexpr bool kFusedDecodeEnabled = false;
+
+__device__ __forceinline__ int atomic_add_agent(int* p, int v) {
+    return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int TB>
+__device__ __forceinline__ void fused_gate_up_item(const DecodeArgs& A, const RouteOut& R, int a, int slice,
+                                                   uint8_t* slot) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int I = A.d.inter, H = A.d.hidden, ke = A.k + A.d.num_shared;
+    const int i0 = (slice * 4 + wv) * 4;
+    if (i0 >= I) return;
+    const int e = R.act[a];
+    const int p0 = R.aoff[a], n = R.an[a];
+    int rows[kRows];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int i = min(i0 + j, I - 1);
+        rows[j] = i;
+        rows[4 + j] = I + i;
+    }
+    const int64_t per = (int64_t)A.d.w13.rows * (H / 2);
+    const uint8_t* codes = (const uint8_t*)A.d.w13.codes + e * per;
+    const uint8_t* tabs = (const uint8_t*)A.d.w13.tables + e * per;
+    for (int tb = 0; tb < n; tb += TB) {
+        const int nt = min(TB, n - tb);
+        const uint16_t* xrow[TB];
+#pragma unroll
+        for (int t = 0; t < TB; ++t) xrow[t] = A.x + (int64_t)(R.perm[p0 + tb + min(t, nt - 1)] / ke) * H;
+        float acc[kRows][TB];
+#pragma unroll
+        for (int r = 0; r < kRows; ++r)
+#pragma unroll
+            for (int t = 0; t < TB; ++t) acc[r][t] = 0.f;
+        bl4_rows8<TB>(codes, tabs, rows, H, lane, slot, xrow, nt, acc);
+        float g[4][TB], u[4][TB];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int t = 0; t < TB; ++t) {
+                g[j][t] = wave_reduce(acc[j][t]);
+                u[j][t] = wave_reduce(acc[4 + j][t]);
+            }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int t = 0; t < TB; ++t)
+                if (lane == j * TB + t && t < nt && i0 + j < I)
+                    A.act[(int64_t)(p0 + tb + t) * I + i0 + j] = (uint16_t)f32_to_bf16(silu_mul(g[j][t], u[j][t]));
+    }
+}
+
+template <int TB>
+__device__ __forceinline__ void fused_down_item(const DecodeArgs& A, const RouteOut& R, int hs, int n_gu,
+                                                DecodeSync* sync, uint8_t* slot, float* s_y) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int I = A.d.inter, H = A.d.hidden, ke = A.k + A.d.num_shared;
+    const int h0 = hs * kRows;
+    int rows[kRows];
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) rows[r] = min(h0 + r, H - 1);
+    const int64_t per = (int64_t)A.d.w2.rows * (I / 2);
+    const int nch = (I + kWChunk - 1) / kWChunk;
+    // W2 rows of this wave's first expert (first chunk): issued before the wait
+    Rows8 pre;
+    if (wv < R.nact) {
+        const int e = R.act[wv];
+        load_rows8((const uint8_t*)A.d.w2.codes + e * per, (const uint8_t*)A.d.w2.tables + e * per, rows, I, 0,
+                   lane, pre);
+    }
+    // Wait for every act slice: poll with relaxed loads (no cache
+    // invalidation per poll), bounded in wall time, then one acquire fence
+    // (invalidates this CU's caches, so the act loads below see the slices).
+    if (threadIdx.x == 0) {
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        while (__hip_atomic_load(&sync->gu_done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < n_gu) {
+            if (__builtin_amdgcn_s_memrealtime() - t0 > kWaitTicks) {
+                __hip_atomic_store(&sync->err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(8);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    }
+    __syncthreads();
+    for (int a = wv; a < R.nact; a += 4) {
+        const int e = R.act[a];
+        const int p0 = R.aoff[a], n = R.an[a];
+        const uint8_t* codes = (const uint8_t*)A.d.w2.codes + e * per;
+        const uint8_t* tabs = (const uint8_t*)A.d.w2.tables + e * per;
+        for (int tb = 0; tb < n; tb += TB) {
+            const int nt = min(TB, n - tb);
+            const uint16_t* xrow[TB];
+#pragma unroll
+            for (int t = 0; t < TB; ++t) xrow[t] = A.act + (int64_t)(p0 + tb + min(t, nt - 1)) * I;
+            float acc[kRows][TB];
+#pragma unroll
+            for (int r = 0; r < kRows; ++r)
+#pragma unroll
+                for (int t = 0; t < TB; ++t) acc[r][t] = 0.f;
+            for (int cc = 0; cc < nch; ++cc) {
+                // the first pass uses the prefetched rows, later ones reload
+                if (!(a == wv && tb == 0 && cc == 0)) load_rows8(codes, tabs, rows, I, cc, lane, pre);
+                uint32_t xs[TB][16];
+                load_x8<TB>(xrow, I, cc, lane, nt, xs);
+                compute_rows8<TB>(pre, xs, cc * kWChunk + 32 * lane < I, lane, slot, nt, acc);
+            }
+#pragma unroll
+            for (int t = 0; t < TB; ++t) {
+                const int p = p0 + tb + min(t, nt - 1);
+                const float pw = R.pw[R.perm[p]];
+#pragma unroll
+                for (int r = 0; r < kRows; ++r) {
+                    const float v = wave_reduce(acc[r][t]);
+                    if (lane == r && t < nt) s_y[p * kRows + r] = v * pw;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    const int T = A.T;
+    for (int idx = threadIdx.x; idx < T * kRows; idx += 256) {
+        const int t = idx / kRows, r = idx % kRows;
+        if (h0 + r >= H) continue;
+        float sum = 0.f;
+        for (int q = 0; q < ke; ++q) {
+            const int pos = R.inv[t * ke + q];
+            if (pos >= 0) sum += s_y[pos * kRows + r];
+        }
+        const int64_t o = (int64_t)t * H + h0 + r;
+        if (A.out_dtype == LUTMOE_DTYPE_F32) ((float*)A.out)[o] = sum;
+        else ((uint16_t*)A.out)[o] = (uint16_t)f32_to_bf16(sum);
+    }
+    __syncthreads();   // s_y is reused by the next item
+}
+
+template <int TB, bool kPre>
+__global__ __launch_bounds__(256) void bl4_decode_fused(DecodeArgs A, DecodeSync* sync) {
+    __shared__ RouteOut R;
+    __shared__ RouteScratch X;
+    __shared__ __attribute__((aligned(16))) uint8_t s_slot[4 * kSlot];
+    __shared__ int s_item;
+    extern __shared__ float s_y[];   // [P][8]
+    get_route<kPre>(A, R, X);
+    const int I = A.d.inter, H = A.d.hidden;
+    const int nsl = (I + 15) / 16;
+    const int n_gu = R.nact * nsl;
+    const int n_all = n_gu + (H + kRows - 1) / kRows;
+    uint8_t* slot = s_slot + (threadIdx.x >> 6) * kSlot;
+    for (;;) {
+        if (threadIdx.x == 0) s_item = atomic_add_agent(&sync->queue, 1);
+        __syncthreads();
+        const int item = s_item;
+        __syncthreads();
+        if (item >= n_all) break;
+        if (item < n_gu) {
+            fused_gate_up_item<TB>(A, R, item / nsl, item % nsl, slot);
+            // publish: every wave's act stores complete in L2, then one
+            // release fence (writes the L2 back) and the count
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            if (threadIdx.x == 0) {
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+                atomic_add_agent(&sync->gu_done, 1);
+            }
+        } else {
+            fused_down_item<TB>(A, R, item - n_gu, n_gu, sync, slot, s_y);
+        }
+    }
+    if (threadIdx.x == 0 &&
+        __hip_atomic_fetch_add(&sync->cta_done, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == (int)gridDim.x - 1) {
+        __hip_atomic_store(&sync->queue, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&sync->gu_done, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&sync->cta_done, 0, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 // tokens per pass: T=1 and T=2 recompute routing per CTA, larger T read it
 inline int tb_for(int T) { return T <= 1 ? 1 : T <= 2 ? 2 : 4; }
 
@@ -532,11 +791,12 @@ bool decode_v2_supported(const lutmoe_moe_desc* d, int T, int k) {
 }
 
 size_t decode_route_bytes() { return sizeof(RouteOut); }
+size_t decode_sync_bytes() { return sizeof(DecodeSync); }
 
 int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* topk_w,
                      const int32_t* topk_ids, const float* logits, int T, int k, int renorm,
-                     float scaling, uint16_t* act, void* route_ws, void* out, int out_dtype,
-                     int stages, hipStream_t s) {
+                     float scaling, uint16_t* act, void* route_ws, void* sync_ws, void* out,
+                     int out_dtype, int stages, hipStream_t s) {
     DecodeArgs A;
     A.d = *d;
     A.x = x;
@@ -568,15 +828,33 @@ int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* t
         case 2: hipLaunchKernelGGL((KERNEL<2, false>), GRID, dim3(256), LDS, s, A); break;  \
         default: hipLaunchKernelGGL((KERNEL<4, true>), GRID, dim3(256), LDS, s, A); break;  \
     }
+    if (kFusedDecodeEnabled && stages == LUTMOE_STAGE_ALL && sync_ws) {
+        // one persistent launch: enough CTAs for one item each
+        const int items = max_active * ((d->inter + 15) / 16) + (d->hidden + kRows - 1) / kRows;
+        const size_t lds = (size_t)P * kRows * sizeof(float);
+        DecodeSync* sy = (DecodeSync*)sync_ws;
+        switch (tb_for(T)) {
+            case 1: hipLaunchKernelGGL((bl4_decode_fused<1, false>), dim3(items), dim3(256), lds, s, A, sy); break;
+            case 2: hipLaunchKernelGGL((bl4_decode_fused<2, false>), dim3(items), dim3(256), lds, s, A, sy); break;
+            default: hipLaunchKernelGGL((bl4_decode_fused<4, true>), dim3(items), dim3(256), lds, s, A, sy); break;
+        }
+        return check_launch();
+    }
     if (stages & LUTMOE_STAGE_GATE_UP) {
         const dim3 grid((d->inter + 15) / 16, max_active);
         LUTMOE_TB_SWITCH(bl4_decode_gate_up, grid, 0)
         if ((rc = check_launch())) return rc;
     }
     if (stages & LUTMOE_STAGE_DOWN) {
+        // the routing comes from the global copy written by the gate_up
+        // kernel (T <= 2) or by decode_route_kernel
         const dim3 grid((d->hidden + kRows - 1) / kRows);
         const size_t lds = (size_t)P * kRows * sizeof(float);
-        LUTMOE_TB_SWITCH(bl4_decode_down, grid, lds)
+        switch (tb_for(T)) {
+            case 1: hipLaunchKernelGGL((bl4_decode_down<1, true>), grid, dim3(256), lds, s, A); break;
+            case 2: hipLaunchKernelGGL((bl4_decode_down<2, true>), grid, dim3(256), lds, s, A); break;
+            default: hipLaunchKernelGGL((bl4_decode_down<4, true>), grid, dim3(256), lds, s, A); break;
+        }
         return check_launch();
     }
 #undef LUTMOE_TB_SWITCH

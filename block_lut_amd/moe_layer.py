@@ -73,7 +73,7 @@ class LUTMoELayer(nn.Module):
         logits = F.linear(xb.float(), self.gate.float())
         need = ops.moe_workspace_bytes(self.moe, xb.shape[0], self.top_k)
         if self._ws is None or self._ws.numel() < need or self._ws.device != xb.device:
-            self._ws = torch.empty(need, dtype=torch.uint8, device=xb.device)
+            self._ws = ops.new_workspace(self.moe, xb.shape[0], self.top_k, xb.device)
         out = ops.moe_forward_logits(self.moe, xb.contiguous(), logits, self.top_k,
                                      renormalize=self.renormalize,
                                      scaling=self.routed_scaling_factor, workspace=self._ws)

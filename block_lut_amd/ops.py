@@ -175,6 +175,14 @@ def moe_workspace_bytes(moe: MoEWeights, T: int, k: int) -> int:
     return int(N.lib().lutmoe_moe_workspace_size(ctypes.byref(d), T, k))
 
 
+def new_workspace(moe: MoEWeights, T: int, k: int, device) -> torch.Tensor:
+    """A zero-filled workspace for the MoE layer at up to T tokens (the
+    decode kernel's counters at its start must be zero before first use; each
+    call leaves them zero).  Reuse it across calls; do not share it between
+    calls that overlap in time."""
+    return torch.zeros(max(moe_workspace_bytes(moe, T, k), 256), dtype=torch.uint8, device=device)
+
+
 def moe_forward(moe: MoEWeights, x: torch.Tensor, topk_weights: torch.Tensor,
                 topk_ids: torch.Tensor, out: Optional[torch.Tensor] = None,
                 out_dtype: torch.dtype = torch.bfloat16, path: int = PATH_AUTO,
@@ -196,7 +204,7 @@ def moe_forward(moe: MoEWeights, x: torch.Tensor, topk_weights: torch.Tensor,
         out_dtype = out.dtype
     need = moe_workspace_bytes(moe, T, k)
     if workspace is None or workspace.numel() < need:
-        workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=x.device)
+        workspace = new_workspace(moe, T, k, x.device)
     d = moe.desc()
     N.check("lutmoe_moe_forward",
             N.lib().lutmoe_moe_forward_stages(ctypes.byref(d), x.data_ptr(), w.data_ptr(),
@@ -227,7 +235,7 @@ def moe_forward_logits(moe: MoEWeights, x: torch.Tensor, logits: torch.Tensor, t
         out_dtype = out.dtype
     need = moe_workspace_bytes(moe, T, top_k)
     if workspace is None or workspace.numel() < need:
-        workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=x.device)
+        workspace = new_workspace(moe, T, top_k, x.device)
     d = moe.desc()
     N.check("lutmoe_moe_forward_logits",
             N.lib().lutmoe_moe_forward_logits(ctypes.byref(d), x.data_ptr(), lg.data_ptr(), T, top_k,

@@ -202,8 +202,12 @@ class LUTFusedMoEMethod:
         if getattr(layer, "_lut_moe", None) is None:
             self.process_weights_after_loading(layer)
         x2 = x if x.dtype == torch.bfloat16 else x.to(torch.bfloat16)
+        T, k = x2.shape[0], topk_ids.shape[1]
+        ws = getattr(layer, "_lut_ws", None)
+        if ws is None or ws.device != x2.device or ws.numel() < ops.moe_workspace_bytes(layer._lut_moe, T, k):
+            ws = layer._lut_ws = ops.new_workspace(layer._lut_moe, T, k, x2.device)
         out = ops.moe_forward(layer._lut_moe, x2.contiguous(), topk_weights, topk_ids,
-                              out_dtype=torch.bfloat16)
+                              out_dtype=torch.bfloat16, workspace=ws)
         return out if x.dtype == torch.bfloat16 else out.to(x.dtype)
 
     def __repr__(self) -> str:

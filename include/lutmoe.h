@@ -166,7 +166,12 @@ int lutmoe_permute(const int32_t* topk_ids_dev, int T, int k, int E, int32_t* of
 
 /* ---- fused MoE layer ------------------------------------------------------ */
 
-/* Workspace bytes lutmoe_moe_forward needs for T tokens and top-k. */
+/* Workspace bytes lutmoe_moe_forward needs for T tokens and top-k.
+ * The workspace is device memory, 256-byte aligned, owned by the caller.
+ * Its first 256 bytes hold the decode kernel's cross-CTA counters: zero-fill
+ * the workspace (or at least those bytes) once before its first use; every
+ * call leaves them zero again.  Calls that overlap in time must not share a
+ * workspace. */
 size_t lutmoe_moe_workspace_size(const lutmoe_moe_desc* d, int T, int k);
 
 /* out[T][H] (out_dtype) = sum_k topk_w[t][k] * FFN_{ids[t][k]}(x[t])
@@ -198,7 +203,7 @@ int lutmoe_moe_forward_stages(const lutmoe_moe_desc* d, const void* x_dev, const
  * vllm_lut/moe_layer.py:281-355): softmax(fp32 logits [T][E]) -> top-k
  * (ties to the lower id) -> optional renormalisation -> x scaling -> the
  * layer of lutmoe_moe_forward.  On the decode path the routing runs inside
- * the two layer kernels (no extra launch). */
+ * decode layer kernel (one launch per layer at T <= 2). */
 int lutmoe_moe_forward_logits(const lutmoe_moe_desc* d, const void* x_dev, const float* logits_dev,
                               int T, int k, int renormalize, float scaling, void* out_dev,
                               int out_dtype, void* workspace_dev, size_t workspace_bytes,

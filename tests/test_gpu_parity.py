@@ -297,6 +297,30 @@ def test_moe_layer_from_logits(gpu, T, path, renorm, E):
     assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
 
 
+@pytest.mark.skip(reason="the one-launch persistent decode kernel (bl4_decode_fused) did not complete "
+                         "on its first GPU runs (E=8, S=1, k=2, H=512, I=320, T=1); it is switched off "
+                         "(kFusedDecodeEnabled) until the cause is found on the CPU")
+def test_moe_layer_fused_decode(gpu):
+    """Layer through the persistent decode kernel: must match the per-stage
+    kernels bit for bit (same GEMV arithmetic, same combine order)."""
+    import torch
+    from block_lut_amd import ops
+    from block_lut_amd.formats import MoEWeights
+    E, S, k, H, I, T = 8, 1, 2, 512, 320, 1
+    w13, w2 = _moe_case("bl4", E, S, H, I, seed=21)
+    moe = MoEWeights(w13.stack(gpu), w2.stack(gpu), H, I, E, S)
+    rng = np.random.default_rng(T)
+    xb = _x(rng, T, H)
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    rw, rids = O.route(lg, k)
+    args = (moe, to_dev_bf16(xb, gpu), torch.from_numpy(rw).to(gpu), torch.from_numpy(rids).to(gpu))
+    ws = ops.new_workspace(moe, T, k, gpu)
+    fused = ops.moe_forward(*args, out_dtype=torch.float32, path=1, workspace=ws)
+    staged = ops.moe_forward(*args, out_dtype=torch.float32, path=1, workspace=ws,
+                             stages=7)
+    assert torch.equal(fused, staged)
+
+
 def test_moe_layer_qwen_decode_full_shape(gpu):
     """Full Qwen1.5-MoE layer shape (H2048 I1408 E60 top-4), T=1 and T=8, BL4 weights from the
     GPU encoder; oracle on the touched experts' GPU-dequantised weights (bit-exact separately)."""
