@@ -102,7 +102,6 @@ int validate_moe(const lutmoe_moe_desc* d) {
     const int E_tot = d->num_routed + d->num_shared;
     if (d->w13.num_experts < E_tot || d->w2.num_experts < E_tot) return LUTMOE_EINVAL;
     if (d->w13.format != d->w2.format) return LUTMOE_EUNSUPPORTED;
-    if (d->w13.format == LUTMOE_FMT_NESTED) return LUTMOE_EUNSUPPORTED;
     if (H % 64 || I % 64) return LUTMOE_EUNSUPPORTED;
     if (d->w13.format == LUTMOE_FMT_REF) {
         if ((rc = validate_ref_vector(&d->w13)) || (rc = validate_ref_vector(&d->w2))) return rc;
@@ -316,8 +315,14 @@ int moe_forward_impl(const lutmoe_moe_desc* d, const void* x, const float* topk_
     const int64_t P = (int64_t)T * ke;
     if (P >= (1ll << 31) / (d->hidden > d->inter ? d->hidden : d->inter)) return LUTMOE_EUNSUPPORTED;
     const bool lds_ok = P * 8 * 4 <= 48 * 1024;
-    const bool gemv = force_path == 1 || (force_path == 0 && T <= 32 && lds_ok);
+    bool gemv = force_path == 1 || (force_path == 0 && T <= 32 && lds_ok);
     if (gemv && !lds_ok) return LUTMOE_EUNSUPPORTED;
+    // NestedLUT decodes only through the decode-layer kernels; otherwise the
+    // grouped MFMA path
+    if (d->w13.format == LUTMOE_FMT_NESTED && gemv && !decode_v2_supported(d, T, k)) {
+        if (force_path == 1) return LUTMOE_EUNSUPPORTED;
+        gemv = false;
+    }
 
     char* ws = (char*)workspace;
     uint16_t* act = (uint16_t*)(ws + L.act);

@@ -462,7 +462,92 @@ __device__ __forceinline__ void bl4_rows8(const uint8_t* __restrict__ codes, con
     }
 }
 
-template <int TB, bool kPre>
+// ---- NestedLUT experts (NestedView, lut_core.h).
+// The lane's 32 columns [2048cc + 32l, +32) of 8 rows: 8 bytes of p01, 4 of
+// p2, 4 of p3 per row, and 16 bytes of the row's tables starting at this
+// lane's share of its block's table (2^b bytes: entries 2^(b-1)*(l%2) ..).
+struct Rows8N {
+    uint32_t f01[kRows][2], f2[kRows], f3[kRows];
+    u32x4_t tw[kRows];
+};
+
+__device__ __forceinline__ void load_rows8n(const NestedView& v, const int (&rows)[kRows], int K, int cc,
+                                            int lane, Rows8N& b) {
+    const bool ok = cc * kWChunk + 32 * lane < K;
+    const uint32_t c0 = ok ? cc * kWChunk + 32 * lane : 0;
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+        const uint32_t i0 = (uint32_t)rows[r] * (uint32_t)K + c0;
+        const auto q = __builtin_amdgcn_raw_buffer_load_b64(v.planes, (int)(i0 / 4), 0, 0);
+        b.f01[r][0] = q[0];
+        b.f01[r][1] = q[1];
+        b.f2[r] = __builtin_amdgcn_raw_buffer_load_b32(v.planes, (int)(v.p2_off + i0 / 8), 0, 0);
+        b.f3[r] = __builtin_amdgcn_raw_buffer_load_b32(v.planes, (int)(v.p3_off + i0 / 8), 0, 0);
+        const uint32_t tofs = ((i0 >> 6) << (v.bits + 1)) + ((uint32_t)(lane & 1) << v.bits);
+        b.tw[r] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(v.table, (int)tofs, 0, 0));
+    }
+}
+
+// Row by row: the 16 table bytes go to the block's 32-byte LDS slot at this
+// lane's share (for b < 4 the two lanes of a block write overlapping bytes
+// with the same values, and a lookup only reads the first 2^(b+1) bytes);
+// codes are rebuilt as BL4 nibbles and looked up as for BL4.
+template <int TB>
+__device__ __forceinline__ void compute_rows8n(const Rows8N& b, const uint32_t (&xs)[TB][16], bool ok, int bits,
+                                               int lane, uint8_t* slot, int nt, float (&acc)[kRows][TB]) {
+    const uint32_t tab = lds_addr(slot) + ((lane >> 1) << 5);
+    const int woff = ((lane >> 1) << 5) + ((lane & 1) << bits);
+    const u32x4_t z = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+        *reinterpret_cast<u32x4_t*>(slot + r * 1024 + woff) = ok ? b.tw[r] : z;
+        wave_lds_sync();
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t f01 = b.f01[r][j >> 1] >> (16 * (j & 1));
+            const uint32_t w = nested_nibbles8(f01, b.f2[r] >> (8 * j), b.f3[r] >> (8 * j));
+            uint32_t xj[TB][4];
+#pragma unroll
+            for (int t = 0; t < TB; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) xj[t][i] = xs[t][4 * j + i];
+            bl4_dot8<TB>(w, tab + r * 1024, xj, nt, acc[r]);
+        }
+    }
+    wave_lds_sync();
+}
+
+template <int TB>
+__device__ __forceinline__ void nested_rows8(const NestedView& v, const int (&rows)[kRows], int K, int lane,
+                                             uint8_t* slot, const uint16_t* const (&xrow)[TB], int nt,
+                                             float (&acc)[kRows][TB]) {
+    const int nch = (K + kWChunk - 1) / kWChunk;
+    for (int cc = 0; cc < nch; ++cc) {
+        Rows8N b;
+        uint32_t xs[TB][16];
+        load_x8<TB>(xrow, K, cc, lane, nt, xs);
+        __builtin_amdgcn_sched_barrier(0);
+        load_rows8n(v, rows, K, cc, lane, b);
+        __builtin_amdgcn_sched_barrier(0);
+        compute_rows8n<TB>(b, xs, cc * kWChunk + 32 * lane < K, v.bits, lane, slot, nt, acc);
+    }
+}
+
+// Rows of expert e of a stack in either decode format.
+template <int kFmt, int TB>
+__device__ __forceinline__ void expert_rows8(const lutmoe_weights& w, int e, const int (&rows)[kRows], int K,
+                                             int lane, uint8_t* slot, const uint16_t* const (&xrow)[TB], int nt,
+                                             float (&acc)[kRows][TB]) {
+    if constexpr (kFmt == LUTMOE_FMT_NESTED) {
+        nested_rows8<TB>(nested_view(w, e), rows, K, lane, slot, xrow, nt, acc);
+    } else {
+        const int64_t per = (int64_t)w.rows * (K / 2);
+        bl4_rows8<TB>((const uint8_t*)w.codes + e * per, (const uint8_t*)w.tables + e * per, rows, K, lane, slot,
+                      xrow, nt, acc);
+    }
+}
+
+template <int TB, bool kPre, int kFmt>
 __global__ __launch_bounds__(256, TB <= 2 ? 3 : 2) void bl4_decode_gate_up(DecodeArgs A) {
     __shared__ RouteOut R;
     __shared__ RouteOrSlots U;
@@ -485,9 +570,6 @@ __global__ __launch_bounds__(256, TB <= 2 ? 3 : 2) void bl4_decode_gate_up(Decod
         rows[j] = i;
         rows[4 + j] = I + i;
     }
-    const int64_t per = (int64_t)A.d.w13.rows * (H / 2);
-    const uint8_t* codes = (const uint8_t*)A.d.w13.codes + e * per;
-    const uint8_t* tabs = (const uint8_t*)A.d.w13.tables + e * per;
     uint8_t* slot = s_slot + wv * kSlot;
     for (int tb = 0; tb < n; tb += TB) {
         const int nt = min(TB, n - tb);
@@ -499,7 +581,7 @@ __global__ __launch_bounds__(256, TB <= 2 ? 3 : 2) void bl4_decode_gate_up(Decod
         for (int r = 0; r < kRows; ++r)
 #pragma unroll
             for (int t = 0; t < TB; ++t) acc[r][t] = 0.f;
-        bl4_rows8<TB>(codes, tabs, rows, H, lane, slot, xrow, nt, acc);
+        expert_rows8<kFmt, TB>(A.d.w13, e, rows, H, lane, slot, xrow, nt, acc);
         float g[4][TB], u[4][TB];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -517,7 +599,7 @@ __global__ __launch_bounds__(256, TB <= 2 ? 3 : 2) void bl4_decode_gate_up(Decod
     }
 }
 
-template <int TB, bool kPre>
+template <int TB, bool kPre, int kFmt>
 __global__ __launch_bounds__(256, TB <= 2 ? 3 : 2) void bl4_decode_down(DecodeArgs A) {
     __shared__ RouteOut R;
     __shared__ RouteOrSlots U;
@@ -530,13 +612,10 @@ __global__ __launch_bounds__(256, TB <= 2 ? 3 : 2) void bl4_decode_down(DecodeAr
     int rows[kRows];
 #pragma unroll
     for (int r = 0; r < kRows; ++r) rows[r] = min(h0 + r, H - 1);
-    const int64_t per = (int64_t)A.d.w2.rows * (I / 2);
     uint8_t* slot = s_slot + wv * kSlot;
     for (int a = wv; a < R.nact; a += 4) {
         const int e = R.act[a];
         const int p0 = R.aoff[a], n = R.an[a];
-        const uint8_t* codes = (const uint8_t*)A.d.w2.codes + e * per;
-        const uint8_t* tabs = (const uint8_t*)A.d.w2.tables + e * per;
         for (int tb = 0; tb < n; tb += TB) {
             const int nt = min(TB, n - tb);
             const uint16_t* xrow[TB];
@@ -547,7 +626,7 @@ __global__ __launch_bounds__(256, TB <= 2 ? 3 : 2) void bl4_decode_down(DecodeAr
             for (int r = 0; r < kRows; ++r)
 #pragma unroll
                 for (int t = 0; t < TB; ++t) acc[r][t] = 0.f;
-            bl4_rows8<TB>(codes, tabs, rows, I, lane, slot, xrow, nt, acc);
+            expert_rows8<kFmt, TB>(A.d.w2, e, rows, I, lane, slot, xrow, nt, acc);
 #pragma unroll
             for (int t = 0; t < TB; ++t) {
                 const int p = p0 + tb + min(t, nt - 1);
@@ -777,6 +856,46 @@ __global__ __launch_bounds__(256) void bl4_decode_fused(DecodeArgs A, DecodeSync
     }
 }
 
+// Single-matrix NestedLUT GEMV (lutmoe_gemv): y[t][m] = sum_k x[t][k] W_e[m][k]
+// for T vectors, TB at a time; a wave owns 8 rows, a CTA 32.
+template <int TB>
+__global__ __launch_bounds__(256, 2) void nested_gemv_kernel(lutmoe_weights w, int e, const uint16_t* __restrict__ x,
+                                                             int T, void* __restrict__ y, int y_dtype) {
+    __shared__ __attribute__((aligned(16))) uint8_t s_slot[4 * kSlot];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int M = w.rows, K = w.cols;
+    const int m0 = (blockIdx.x * 4 + wv) * kRows;
+    if (m0 >= M) return;
+    int rows[kRows];
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) rows[r] = min(m0 + r, M - 1);
+    const NestedView v = nested_view(w, e);
+    uint8_t* slot = s_slot + wv * kSlot;
+    for (int t0 = 0; t0 < T; t0 += TB) {
+        const int nt = min(TB, T - t0);
+        const uint16_t* xrow[TB];
+#pragma unroll
+        for (int t = 0; t < TB; ++t) xrow[t] = x + (int64_t)(t0 + min(t, nt - 1)) * K;
+        float acc[kRows][TB];
+#pragma unroll
+        for (int r = 0; r < kRows; ++r)
+#pragma unroll
+            for (int t = 0; t < TB; ++t) acc[r][t] = 0.f;
+        nested_rows8<TB>(v, rows, K, lane, slot, xrow, nt, acc);
+#pragma unroll
+        for (int r = 0; r < kRows; ++r)
+#pragma unroll
+            for (int t = 0; t < TB; ++t) {
+                const float s = wave_reduce(acc[r][t]);
+                if (lane == r * TB + t && t < nt && m0 + r < M) {
+                    const int64_t o = (int64_t)(t0 + t) * M + m0 + r;
+                    if (y_dtype == LUTMOE_DTYPE_F32) ((float*)y)[o] = s;
+                    else ((uint16_t*)y)[o] = (uint16_t)f32_to_bf16(s);
+                }
+            }
+    }
+}
+
 // tokens per pass: T=1 and T=2 recompute routing per CTA, larger T read it
 inline int tb_for(int T) { return T <= 1 ? 1 : T <= 2 ? 2 : 4; }
 
@@ -787,7 +906,25 @@ namespace lutmoe_host {
 bool decode_v2_supported(const lutmoe_moe_desc* d, int T, int k) {
     const int E_tot = d->num_routed + d->num_shared;
     const int P = T * (k + d->num_shared);
-    return d->w13.format == LUTMOE_FMT_BL4 && E_tot <= kMaxEtot && P <= kMaxP;
+    if (d->w13.format == LUTMOE_FMT_NESTED &&
+        ((int64_t)d->w13.rows * d->w13.cols >= (int64_t(1) << 32) ||
+         (int64_t)d->w2.rows * d->w2.cols >= (int64_t(1) << 32)))
+        return false;
+    return (d->w13.format == LUTMOE_FMT_BL4 || d->w13.format == LUTMOE_FMT_NESTED) && E_tot <= kMaxEtot &&
+           P <= kMaxP;
+}
+
+int launch_nested_gemv(const lutmoe_weights* w, int expert, const uint16_t* x, int T, void* y, int y_dtype,
+                       hipStream_t s) {
+    if ((int64_t)w->rows * w->cols >= (int64_t(1) << 32)) return LUTMOE_EUNSUPPORTED;
+    const dim3 grid((w->rows + 4 * kRows - 1) / (4 * kRows));
+    if (T <= 1)
+        hipLaunchKernelGGL((nested_gemv_kernel<1>), grid, dim3(256), 0, s, *w, expert, x, T, y, y_dtype);
+    else if (T == 2)
+        hipLaunchKernelGGL((nested_gemv_kernel<2>), grid, dim3(256), 0, s, *w, expert, x, T, y, y_dtype);
+    else
+        hipLaunchKernelGGL((nested_gemv_kernel<4>), grid, dim3(256), 0, s, *w, expert, x, T, y, y_dtype);
+    return check_launch();
 }
 
 size_t decode_route_bytes() { return sizeof(RouteOut); }
@@ -822,13 +959,8 @@ int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* t
         hipLaunchKernelGGL(decode_route_kernel, dim3(1), dim3(256), 0, s, A);
         if ((rc = check_launch())) return rc;
     }
-#define LUTMOE_TB_SWITCH(KERNEL, GRID, LDS)                                                  \
-    switch (tb_for(T)) {                                                                    \
-        case 1: hipLaunchKernelGGL((KERNEL<1, false>), GRID, dim3(256), LDS, s, A); break;  \
-        case 2: hipLaunchKernelGGL((KERNEL<2, false>), GRID, dim3(256), LDS, s, A); break;  \
-        default: hipLaunchKernelGGL((KERNEL<4, true>), GRID, dim3(256), LDS, s, A); break;  \
-    }
-    if (kFusedDecodeEnabled && stages == LUTMOE_STAGE_ALL && sync_ws) {
+    const bool nested = d->w13.format == LUTMOE_FMT_NESTED;
+    if (kFusedDecodeEnabled && !nested && stages == LUTMOE_STAGE_ALL && sync_ws) {
         // one persistent launch: enough CTAs for one item each
         const int items = max_active * ((d->inter + 15) / 16) + (d->hidden + kRows - 1) / kRows;
         const size_t lds = (size_t)P * kRows * sizeof(float);
@@ -840,9 +972,18 @@ int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* t
         }
         return check_launch();
     }
+#define LUTMOE_DECODE_LAUNCH(KERNEL, PRE12, GRID, LDS)                                                    \
+    switch (tb_for(T) * 4 + (nested ? 1 : 0)) {                                                           \
+        case 4: hipLaunchKernelGGL((KERNEL<1, PRE12, LUTMOE_FMT_BL4>), GRID, dim3(256), LDS, s, A); break;    \
+        case 5: hipLaunchKernelGGL((KERNEL<1, PRE12, LUTMOE_FMT_NESTED>), GRID, dim3(256), LDS, s, A); break; \
+        case 8: hipLaunchKernelGGL((KERNEL<2, PRE12, LUTMOE_FMT_BL4>), GRID, dim3(256), LDS, s, A); break;    \
+        case 9: hipLaunchKernelGGL((KERNEL<2, PRE12, LUTMOE_FMT_NESTED>), GRID, dim3(256), LDS, s, A); break; \
+        case 17: hipLaunchKernelGGL((KERNEL<4, true, LUTMOE_FMT_NESTED>), GRID, dim3(256), LDS, s, A); break; \
+        default: hipLaunchKernelGGL((KERNEL<4, true, LUTMOE_FMT_BL4>), GRID, dim3(256), LDS, s, A); break;    \
+    }
     if (stages & LUTMOE_STAGE_GATE_UP) {
         const dim3 grid((d->inter + 15) / 16, max_active);
-        LUTMOE_TB_SWITCH(bl4_decode_gate_up, grid, 0)
+        LUTMOE_DECODE_LAUNCH(bl4_decode_gate_up, false, grid, 0)
         if ((rc = check_launch())) return rc;
     }
     if (stages & LUTMOE_STAGE_DOWN) {
@@ -850,14 +991,10 @@ int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* t
         // kernel (T <= 2) or by decode_route_kernel
         const dim3 grid((d->hidden + kRows - 1) / kRows);
         const size_t lds = (size_t)P * kRows * sizeof(float);
-        switch (tb_for(T)) {
-            case 1: hipLaunchKernelGGL((bl4_decode_down<1, true>), grid, dim3(256), lds, s, A); break;
-            case 2: hipLaunchKernelGGL((bl4_decode_down<2, true>), grid, dim3(256), lds, s, A); break;
-            default: hipLaunchKernelGGL((bl4_decode_down<4, true>), grid, dim3(256), lds, s, A); break;
-        }
+        LUTMOE_DECODE_LAUNCH(bl4_decode_down, true, grid, lds)
         return check_launch();
     }
-#undef LUTMOE_TB_SWITCH
+#undef LUTMOE_DECODE_LAUNCH
     return LUTMOE_OK;
 }
 

@@ -134,6 +134,31 @@ struct BStep<LUTMOE_FMT_REF> {
     }
 };
 
+// NestedLUT: the lane's 32 columns of each row from the bit planes, and the
+// first 32 bytes of the row's block-kb table (the first 2^(b+1) are the
+// tier's entries; codes never reach the rest).
+template <>
+struct BStep<LUTMOE_FMT_NESTED> {
+    uint32_t f01[2][2], f2[2], f3[2];
+    u32x4_t tab[2][2];
+    __device__ __forceinline__ void load(const NestedView& v, const int (&row)[2], int K, int kb, int bh) {
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            const uint32_t blk0 = (uint32_t)row[nt] * (uint32_t)K + (uint32_t)kb * kBK;
+            const uint32_t i0 = blk0 + 32u * bh;
+            const auto q = __builtin_amdgcn_raw_buffer_load_b64(v.planes, (int)(i0 / 4), 0, 0);
+            f01[nt][0] = q[0];
+            f01[nt][1] = q[1];
+            f2[nt] = __builtin_amdgcn_raw_buffer_load_b32(v.planes, (int)(v.p2_off + i0 / 8), 0, 0);
+            f3[nt] = __builtin_amdgcn_raw_buffer_load_b32(v.planes, (int)(v.p3_off + i0 / 8), 0, 0);
+            const uint32_t tofs = (blk0 >> 6) << (v.bits + 1);
+            tab[nt][0] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(v.table, (int)tofs, 0, 0));
+            tab[nt][1] =
+                __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(v.table, (int)tofs + 16, 0, 0));
+        }
+    }
+};
+
 // One tile with NMT m-tiles of work (a compile-time count, so the K loop is
 // one basic block with no per-m-tile branches).
 template <bool kGateUp, int kFmt, int NMT>
@@ -167,9 +192,12 @@ __device__ __forceinline__ void prefill_tile(const lutmoe_moe_desc& d, const uin
         b_row[0] = min(n0 + 64 * wv + bn, H - 1);
         b_row[1] = min(n0 + 64 * wv + 32 + bn, H - 1);
     }
-    const uint8_t* codes;
-    const void* tabs;
-    if (kFmt == LUTMOE_FMT_BL4) {
+    const uint8_t* codes = nullptr;
+    const void* tabs = nullptr;
+    NestedView nv;
+    if constexpr (kFmt == LUTMOE_FMT_NESTED) {
+        nv = nested_view(w, ti.e);
+    } else if constexpr (kFmt == LUTMOE_FMT_BL4) {
         const int64_t per = (int64_t)w.rows * (w.cols / 2);
         codes = (const uint8_t*)w.codes + ti.e * per;
         tabs = (const uint8_t*)w.tables + ti.e * per;
@@ -178,7 +206,9 @@ __device__ __forceinline__ void prefill_tile(const lutmoe_moe_desc& d, const uin
         tabs = (const uint16_t*)w.tables + (int64_t)ti.e * w.absmax_per_expert;
     }
     auto load_b = [&](BStep<kFmt>& b, int kb) __attribute__((always_inline)) {
-        if constexpr (kFmt == LUTMOE_FMT_BL4)
+        if constexpr (kFmt == LUTMOE_FMT_NESTED)
+            b.load(nv, b_row, K, kb, bh);
+        else if constexpr (kFmt == LUTMOE_FMT_BL4)
             b.load(codes, (const uint8_t*)tabs, b_row, K, kb, bh);
         else
             b.load(codes, (const uint16_t*)tabs, b_row, K, kb, bh, w.block_size, w.absmax_per_expert);
@@ -206,15 +236,20 @@ __device__ __forceinline__ void prefill_tile(const lutmoe_moe_desc& d, const uin
         __attribute__((always_inline)) {
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
-            if constexpr (kFmt == LUTMOE_FMT_BL4)
+            if constexpr (kFmt == LUTMOE_FMT_NESTED) {
+                const uint32_t wd = nested_nibbles8(b.f01[nt][ks >> 1] >> (16 * (ks & 1)), b.f2[nt] >> (8 * ks),
+                                                    b.f3[nt] >> (8 * ks));
+                bf[nt] = __builtin_bit_cast(bf16x8_t, lookup8_reg(tb[nt], wd));
+            } else if constexpr (kFmt == LUTMOE_FMT_BL4) {
                 bf[nt] = __builtin_bit_cast(bf16x8_t, lookup8_reg(tb[nt], b.codes[nt][ks]));
-            else
+            } else {
                 bf[nt] = lookup8_ref(b.codes[nt][ks >> 1][2 * (ks & 1)], b.codes[nt][ks >> 1][2 * (ks & 1) + 1],
                                      s_cb, b.am[nt]);
+            }
         }
     };
     auto split = [&](const BStep<kFmt>& b, RegTable16 (&tb)[2]) __attribute__((always_inline)) {
-        if constexpr (kFmt == LUTMOE_FMT_BL4) {
+        if constexpr (kFmt != LUTMOE_FMT_REF) {
             tb[0] = split_table16(b.tab[0][0], b.tab[0][1]);
             tb[1] = split_table16(b.tab[1][0], b.tab[1][1]);
         }
@@ -646,10 +681,14 @@ static bool bl4_offsets_fit(const lutmoe_moe_desc* d, const MoeRouting& r, int P
 
 int launch_prefill_gate_up(const lutmoe_moe_desc* d, const uint16_t* x, const MoeRouting& r,
                            uint16_t* act, int P, hipStream_t s) {
-    if (d->w13.format != LUTMOE_FMT_REF && !bl4_offsets_fit(d, r, P)) return LUTMOE_EUNSUPPORTED;
+    if (d->w13.format == LUTMOE_FMT_BL4 && !bl4_offsets_fit(d, r, P)) return LUTMOE_EUNSUPPORTED;
+    if (d->w13.format == LUTMOE_FMT_NESTED && (int64_t)d->w13.rows * d->w13.cols >= (int64_t(1) << 32))
+        return LUTMOE_EUNSUPPORTED;
     const dim3 grid((d->inter + kBN / 2 - 1) / (kBN / 2), max_tiles(P, r.num_experts_total));
     if (d->w13.format == LUTMOE_FMT_REF)
         hipLaunchKernelGGL((prefill_kernel<true, LUTMOE_FMT_REF>), grid, dim3(256), 0, s, *d, x, r, (void*)act);
+    else if (d->w13.format == LUTMOE_FMT_NESTED)
+        hipLaunchKernelGGL((prefill_kernel<true, LUTMOE_FMT_NESTED>), grid, dim3(256), 0, s, *d, x, r, (void*)act);
     else
         hipLaunchKernelGGL((prefill_bl4_kernel<true>), grid, dim3(256), 0, s, *d, x, r, (void*)act);
     return check_launch();
@@ -657,10 +696,14 @@ int launch_prefill_gate_up(const lutmoe_moe_desc* d, const uint16_t* x, const Mo
 
 int launch_prefill_down(const lutmoe_moe_desc* d, const uint16_t* act, const MoeRouting& r,
                         float* y_pos, int P, hipStream_t s) {
-    if (d->w2.format != LUTMOE_FMT_REF && !bl4_offsets_fit(d, r, P)) return LUTMOE_EUNSUPPORTED;
+    if (d->w2.format == LUTMOE_FMT_BL4 && !bl4_offsets_fit(d, r, P)) return LUTMOE_EUNSUPPORTED;
+    if (d->w2.format == LUTMOE_FMT_NESTED && (int64_t)d->w2.rows * d->w2.cols >= (int64_t(1) << 32))
+        return LUTMOE_EUNSUPPORTED;
     const dim3 grid((d->hidden + kBN - 1) / kBN, max_tiles(P, r.num_experts_total));
     if (d->w2.format == LUTMOE_FMT_REF)
         hipLaunchKernelGGL((prefill_kernel<false, LUTMOE_FMT_REF>), grid, dim3(256), 0, s, *d, act, r, (void*)y_pos);
+    else if (d->w2.format == LUTMOE_FMT_NESTED)
+        hipLaunchKernelGGL((prefill_kernel<false, LUTMOE_FMT_NESTED>), grid, dim3(256), 0, s, *d, act, r, (void*)y_pos);
     else
         hipLaunchKernelGGL((prefill_bl4_kernel<false>), grid, dim3(256), 0, s, *d, act, r, (void*)y_pos);
     return check_launch();

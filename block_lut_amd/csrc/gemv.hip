@@ -495,9 +495,6 @@ int launch_bl4_gemv(const lutmoe_weights* w, int expert, const uint16_t* x, int 
     return gemv_dispatch<Bl4Dec>(w, expert, x, T, y, y_dtype, s);
 }
 
-int launch_nested_gemv(const lutmoe_weights*, int, const uint16_t*, int, void*, int, hipStream_t) {
-    return LUTMOE_EUNSUPPORTED;
-}
 
 template <class Dec>
 static int gate_up_dispatch(const lutmoe_moe_desc* d, const uint16_t* x, const MoeRouting& r,

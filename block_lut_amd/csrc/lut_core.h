@@ -89,6 +89,53 @@ __device__ __forceinline__ u32x4_t lookup8_lds(uint32_t w, uint32_t tab) {
     return lookup8_combine(lookup8_issue(w, tab));
 }
 
+// A NestedLUT expert: bit-plane sections [p01 n/4 | p2 n/8 | p3 n/8] (p2
+// from tier 3 on, p3 from tier 4 on; n = rows*K) and bf16 tables
+// [rows][K/64][2^b], read through bounds-checked buffer descriptors: a tier's
+// missing plane sections and any table bytes past the end read as zero.
+constexpr int kBufWord3 = 0x00020000;   // raw buffer, dword format (gfx9)
+
+struct NestedView {
+    __amdgpu_buffer_rsrc_t planes, table;
+    uint32_t p2_off, p3_off;   // byte offsets of the p2 / p3 sections
+    int bits;
+};
+
+__device__ __forceinline__ NestedView nested_view(const lutmoe_weights& w, int e) {
+    const uint8_t* pl = ((const uint8_t* const*)w.codes)[e];
+    const uint16_t* tb = ((const uint16_t* const*)w.tables)[e];
+    const int b = w.tier_bits[e];
+    const uint32_t n = (uint32_t)w.rows * (uint32_t)w.cols;   // < 2^32 (checked on the host)
+    NestedView v;
+    v.planes = __builtin_amdgcn_make_buffer_rsrc((void*)pl, 0, (int)(n / 4 + (b >= 3 ? n / 8 : 0) + (b >= 4 ? n / 8 : 0)),
+                                                 kBufWord3);
+    v.table = __builtin_amdgcn_make_buffer_rsrc((void*)tb, 0, (int)(((n / 64) << b) * 2), kBufWord3);
+    v.p2_off = n / 4;
+    v.p3_off = n / 4 + n / 8;
+    v.bits = b;
+    return v;
+}
+
+// NestedLUT bit-plane sections -> BL4 code dword (nibble j = code of column
+// j) for 8 consecutive columns: f01 = their 2-bit fields (column j at bits
+// 2j..2j+1), f2 / f3 = their bit-2 / bit-3 planes (column j at bit j; zero
+// for lower tiers).  Fields are spread to nibbles by shift-or-mask steps.
+__device__ __forceinline__ uint32_t nested_nibbles8(uint32_t f01, uint32_t f2, uint32_t f3) {
+    uint32_t x = f01 & 0xffffu;
+    x = (x | (x << 8)) & 0x00ff00ffu;   // 4 fields per byte in bytes 0, 2
+    x = (x | (x << 4)) & 0x0f0f0f0fu;   // 2 fields per byte
+    x = (x | (x << 2)) & 0x33333333u;   // field j in the low 2 bits of nibble j
+    uint32_t y = f2 & 0xffu;            // bit j -> bit 4j
+    y = (y | (y << 12)) & 0x000f000fu;
+    y = (y | (y << 6)) & 0x03030303u;
+    y = (y | (y << 3)) & 0x11111111u;
+    uint32_t z = f3 & 0xffu;
+    z = (z | (z << 12)) & 0x000f000fu;
+    z = (z | (z << 6)) & 0x03030303u;
+    z = (z | (z << 3)) & 0x11111111u;
+    return x | (y << 2) | (z << 3);
+}
+
 // A 16-entry bf16 table held in registers as byte planes: lo[q] = low bytes
 // of entries 4q..4q+3, hi[q] = their high bytes.  Lookups are v_perm_b32 byte
 // selects (bytes 0-3 of the 8-byte source come from the second operand),

@@ -94,3 +94,47 @@ class RefExpertset:
         from block_lut_amd.formats import RefStack
         return RefStack(torch.from_numpy(self.codes).to(device), to_dev_bf16(self.absmax, device),
                         to_dev_bf16(self.cb, device), self.bs)
+
+
+class NestedExpertset:
+    """E NestedLUT matrices [M, K] built by the CPU oracle's nested encoder from
+    seeded N(0, std) weights; expert e is kept at tier bits[e] (2, 3 or 4):
+    bit-plane sections [p01 | p2 | p3] of its low bits[e] code bits and the
+    tier's bf16 tables [M, K/64, 2^b]."""
+
+    def __init__(self, bits, M, K, seed, std=0.02, n_iter=20):
+        rng = np.random.default_rng(seed)
+        self.bits = list(bits)
+        self.E, self.M, self.K = len(self.bits), M, K
+        self.codes, self.tables = [], []
+        for b in self.bits:
+            w = (rng.standard_normal((M, K)) * std).astype(np.float32)
+            codes, t2, t3, t4 = O.nested_encode(w, n_iter=n_iter)
+            self.codes.append(codes & ((1 << b) - 1))
+            self.tables.append({2: t2, 3: t3, 4: t4}[b])
+
+    def planes(self, e) -> np.ndarray:
+        pl = O.nested_pack_planes(self.codes[e])
+        parts = [pl["p01"].reshape(-1)]
+        if self.bits[e] >= 3:
+            parts.append(pl["p2"].reshape(-1))
+        if self.bits[e] >= 4:
+            parts.append(pl["p3"].reshape(-1))
+        return np.concatenate(parts)
+
+    def table_bf16(self, e) -> np.ndarray:
+        return O.f32_to_bf16(O.f16_to_f32(self.tables[e]))
+
+    def deq_bits(self, e) -> np.ndarray:
+        return O.nested_dequant(self.codes[e], self.tables[e], self.bits[e])
+
+    def deq_f32(self, e) -> np.ndarray:
+        return O.bf16_to_f32(self.deq_bits(e))
+
+    def stack(self, device):
+        import torch
+        from block_lut_amd.formats import NestedExpert, NestedStack
+        ex = [NestedExpert(b, torch.from_numpy(self.planes(e)).to(device),
+                           to_dev_bf16(self.table_bf16(e), device))
+              for e, b in enumerate(self.bits)]
+        return NestedStack(ex, self.M, self.K)

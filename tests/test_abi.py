@@ -123,10 +123,14 @@ def test_moe_validation(lib):
     assert lib.lutmoe_moe_forward(*args(d, out_dtype=3)) == N.LUTMOE_EINVAL
     assert lib.lutmoe_moe_forward(*args(d, path=3)) == N.LUTMOE_EINVAL
     assert lib.lutmoe_moe_forward(*args(d, wsb=16)) == N.LUTMOE_EWORKSPACE
-    d = _desc(N, fmt=N.FMT_NESTED)
+    d = _desc(N, fmt=N.FMT_NESTED)                            # nested without tier bits
+    assert lib.lutmoe_moe_forward(*args(d)) == N.LUTMOE_EINVAL
     d.w13.tier_bits = 1
     d.w2.tier_bits = 1
+    d.w2.format = N.FMT_BL4                                   # mixed formats
     assert lib.lutmoe_moe_forward(*args(d)) == N.LUTMOE_EUNSUPPORTED
+    d.w2.format = N.FMT_NESTED                                # nested, GEMV forced past its limits
+    assert lib.lutmoe_moe_forward(*args(d, T=300, path=1)) == N.LUTMOE_EUNSUPPORTED
     d = _desc(N)
     d.w2.num_experts = 3                                      # fewer than routed + shared
     assert lib.lutmoe_moe_forward(*args(d)) == N.LUTMOE_EINVAL

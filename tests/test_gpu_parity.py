@@ -9,8 +9,8 @@ import numpy as np
 import pytest
 
 import oracle as O
-from lutmoe_testutil import (BL4Expertset, RefExpertset, bf16_bits, golden_codebook, rel_maxabs,
-                             to_dev_bf16, to_dev_f16)
+from lutmoe_testutil import (BL4Expertset, NestedExpertset, RefExpertset, bf16_bits, golden_codebook,
+                             rel_maxabs, to_dev_bf16, to_dev_f16)
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-3
@@ -149,6 +149,56 @@ def test_bl4_gemv_c1_shape(gpu, T):
     y = ops.gemv(st, to_dev_bf16(xb, gpu), 0, out_dtype=torch.float32).cpu().numpy()
     ref = O.bf16_to_f32(xb).astype(np.float64) @ es.deq_f32(0).astype(np.float64).T
     assert rel_maxabs(y, ref) <= TOL
+
+
+# ------------------------------------------------------------ NestedLUT
+
+def test_nested_dequant_bitexact(gpu):
+    """Tier-b dequant of the bit-plane sections, experts at tiers 2, 3, 4."""
+    from block_lut_amd import ops
+    es = NestedExpertset([2, 3, 4], 96, 640, seed=3)
+    got = ops.dequant(es.stack(gpu))
+    for e in range(es.E):
+        assert np.array_equal(bf16_bits(got[e]), es.deq_bits(e)), f"expert {e} (tier {es.bits[e]})"
+
+
+@pytest.mark.parametrize("bits,M,K,T", [(2, 2816, 2048, 1), (3, 2048, 1408, 1), (4, 2048, 1408, 2),
+                                        (3, 300, 640, 5), (2, 40, 4160, 3)])
+def test_nested_gemv(gpu, bits, M, K, T):
+    """Single-matrix GEMV (lutmoe_gemv) on a tier-b expert, including K past
+    one 2048-column pass and a row count that is not a multiple of 32."""
+    import torch
+    from block_lut_amd import ops
+    es = NestedExpertset([4, bits], M, K, seed=M + K, n_iter=8)
+    rng = np.random.default_rng(bits)
+    xb = _x(rng, T, K)
+    y = ops.gemv(es.stack(gpu), to_dev_bf16(xb, gpu), 1, out_dtype=torch.float32).cpu().numpy()
+    ref = O.bf16_to_f32(xb).astype(np.float64) @ es.deq_f32(1).astype(np.float64).T
+    assert rel_maxabs(y, ref) <= TOL
+
+
+@pytest.mark.parametrize("T,path", [(1, 1), (4, 1), (9, 1), (150, 2), (5, 2)])
+def test_moe_layer_nested_tiers(gpu, T, path):
+    """MoE layer over NestedLUT experts of mixed tiers (decode GEMV and the
+    grouped MFMA path): routed experts at tiers 2/3/4 and a tier-4 shared
+    expert, against the dense restatement of the tier-b weights."""
+    import torch
+    from block_lut_amd import ops
+    from block_lut_amd.formats import MoEWeights
+    E, S, k, H, I = 6, 1, 2, 512, 320
+    bits = [2, 3, 4, 2, 3, 4, 4]
+    w13 = NestedExpertset(bits, 2 * I, H, seed=40 + T, n_iter=8)
+    w2 = NestedExpertset(bits, H, I, seed=41 + T, n_iter=8)
+    moe = MoEWeights(w13.stack(gpu), w2.stack(gpu), H, I, E, S)
+    rng = np.random.default_rng(T)
+    xb = _x(rng, T, H)
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    rw, rids = O.route(lg, k)
+    out = ops.moe_forward(moe, to_dev_bf16(xb, gpu), torch.from_numpy(rw).to(gpu),
+                          torch.from_numpy(rids).to(gpu), out_dtype=torch.float32, path=path)
+    ref = O.moe_layer(xb, rids, rw, w13.deq_f32, w2.deq_f32,
+                      shared=[(w13.deq_f32(E + s), w2.deq_f32(E + s)) for s in range(S)])
+    assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
 
 
 @pytest.mark.parametrize("M,K,T", [(2816, 2048, 1), (2048, 1408, 1), (300, 640, 3)])
