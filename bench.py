@@ -6,9 +6,10 @@ Default workload (one step = one MoE layer decode step):
   routed experts, top-4 softmax routing of N(0,1) logits, SwiGLU gate/up/down
   all BL4 4-bit (64-weight blocks, 16-entry codebooks), T = 1 token of bf16
   N(0,1) activations.  Each step is one call of the MoE block forward from
-  router logits: two kernels, each recomputing the softmax/top-k routing and
-  the token permutation in-CTA, the first running the grouped LUT-GEMV gate/up
-  + SwiGLU, the second the down projection + weighted combine.  Steps rotate over 16 distinct layer weight copies (8.3 GB,
+  router logits: two kernels, the first computing the softmax/top-k routing
+  and the token permutation in every CTA (its first CTA stores them for the
+  second) and running the grouped LUT-GEMV gate/up + SwiGLU, the second the
+  down projection + weighted combine.  Steps rotate over 16 distinct layer weight copies (8.3 GB,
   each step with its own routing) so the touched bytes per rotation exceed
   the 256 MB Infinity Cache: the figure is cold-HBM, not MALL.
 
@@ -22,7 +23,10 @@ cpu_baseline = the reference's CPU dequant + matmul path restated with torch
              on the host (oracle/cpu_baseline.py), on a bounded sample of the
              same steps.
 extra      = the other configurations (decode T=8/32, DeepSeek-V2-Lite prefill
-             grouped GEMM TFLOP/s, switch-base-8 single linear, hot-cache decode).
+             grouped GEMM TFLOP/s, switch-base-8 single linear, hot-cache decode,
+             and the NestedLUT tier workload: Qwen shape, 20 experts each at 2, 3
+             and 4 bits, Zipf(1.1) expert popularity with Gumbel-top-4 routing,
+             decode T=16 and prefill T=1024).
 
 Weights are synthetic BL4 data of the configured shapes (uniform random 4-bit
 codes, sorted N(0, 0.02) codebook entries): throughput does not depend on the
@@ -51,6 +55,20 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
+def measured_traffic(name="decode_gate_up_traffic.md"):
+    """HBM bytes per launch of the dominant kernel from the committed counter
+    summary (FETCH_SIZE and WRITE_SIZE passes, each scaled by what it reads
+    for a copy of known size); None when the summary is absent."""
+    path = os.path.join(ROOT, "profiles", name)
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
+
+
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
@@ -61,6 +79,9 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-extra", action="store_true", help="skip the other configurations")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--pmc-sample", action="store_true",
+                   help="run only a 256 MiB device copy and the decode gate/up kernel of the "
+                        "default workload (for rocprofv3 --pmc passes), then exit")
     return p.parse_args()
 
 
@@ -73,7 +94,7 @@ def main():
     import torch
     from block_lut_amd import ops
     from block_lut_amd import _native as N
-    from block_lut_amd.formats import BL4Stack, MoEWeights
+    from block_lut_amd.formats import BL4Stack, MoEWeights, NestedExpert, NestedStack
 
     dev = torch.device("cuda:0")
     torch.manual_seed(0)
@@ -143,6 +164,24 @@ def main():
     # ------------------------------------------------------------ main leg
     c = QWEN
     T = a.tokens
+    if a.pmc_sample:
+        # calibration: a plain copy of known size (256 MiB read + 256 MiB written)
+        src = torch.empty(1 << 28, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        layers = [rand_layer(c) for _ in range(a.layers)]
+        steps = [Step(L, c, T) for L in layers]
+        for s in steps:
+            s.run(stages=N.STAGE_GATE_UP)
+        for s in steps:
+            s.run(stages=N.STAGE_GATE_UP)
+        torch.cuda.synchronize()
+        log(f"[bench] pmc sample: gate/up algorithmic bytes per launch "
+            f"{sum(s.bytes_gate_up for s in steps) / len(steps):.0f}")
+        return
     log(f"[bench] building {a.layers} Qwen-shaped BL4 layers ({a.layers * c['E'] * expert_bytes(c) / 1e9:.1f} GB)")
     layers = [rand_layer(c) for _ in range(a.layers)]
     steps = [Step(L, c, T) for L in layers]
@@ -199,7 +238,7 @@ def main():
         "tokens_per_s": round(T / (ms_per_step / 1e3), 1),
         "roofline": {"bound": "hbm", "kernel": "bl4_decode_gate_up<1>",
                      "achieved": round(ach_gu, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(ach_gu / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(ach_gu / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "avg_launch_us": round(dur_gu * 1e6, 3),
                      "algorithmic_bytes_per_launch": int(bytes_gu)},
         "kernels": {"decode_down_combine_us": round(dur_dn * 1e6, 3),
@@ -240,6 +279,8 @@ def main():
         extra["prefill_dsv2_T2048_TFLOPs"] = round(flops / sec / 1e12, 1)
         extra["prefill_dsv2_T2048_frac_bf16_peak"] = round(flops / sec / 1e12 / BF16_PEAK_TFLOPS, 4)
         log(f"[bench] prefill DeepSeek T=2048: {sec * 1e6:.0f} us, {flops / sec / 1e12:.1f} TFLOP/s")
+        extra.update(nested_tiers(a, ops, N, torch, dev, NestedExpert, NestedStack, MoEWeights,
+                                  graph_of, time_graph))
         # switch-base-8 single BL4 linear 768 -> 3072, one token
         st1 = rand_stack(1, 3072, 768)
         x1 = torch.randn((1, 768), device=dev).to(torch.bfloat16)
@@ -258,6 +299,71 @@ def main():
         result["cpu_baseline"] = cpu_baseline(a, c, T)
 
     print(json.dumps(result), flush=True)
+
+
+def nested_tiers(a, ops, N, torch, dev, NestedExpert, NestedStack, MoEWeights, graph_of,
+                 time_graph):
+    """NestedLUT tier workload: Qwen1.5-MoE shape (H2048, I1408, E60, top-4),
+    experts at 2/3/4 bits (20 each, seeded permutation), expert popularity
+    p_e ~ rank^-1.1 (seeded rank permutation) and Gumbel-top-4 routing: the
+    router logits are log p_e + Gumbel noise, so the kernels' own softmax /
+    top-k performs the Gumbel-top-k selection.  Decode T=16 (HBM bytes of the
+    touched experts at their tiers) and prefill T=1024 (MFMA flops)."""
+    import numpy as np
+    H, I, E, k = 2048, 1408, 60, 4
+    rng = np.random.default_rng(2024)
+    bits = np.array([2] * 20 + [3] * 20 + [4] * 20)[rng.permutation(E)]
+    rank = rng.permutation(E) + 1
+    logp = np.log(rank.astype(np.float64) ** -1.1 / np.sum(rank.astype(np.float64) ** -1.1))
+
+    def stack(M, K):
+        ex = []
+        n = M * K
+        for b in bits:
+            b = int(b)
+            size = n // 4 + (n // 8 if b >= 3 else 0) + (n // 8 if b >= 4 else 0)
+            planes = torch.randint(0, 256, (size,), dtype=torch.uint8, device=dev)
+            tab = torch.sort(torch.randn((M, K // 64, 1 << b), device=dev) * 0.02, dim=-1).values
+            ex.append(NestedExpert(b, planes, tab.to(torch.bfloat16)))
+        return NestedStack(ex, M, K)
+
+    def exp_bytes(b):
+        w = 3 * H * I
+        return w * b / 8 + (w / 64) * (1 << b) * 2
+
+    nl = 4   # 4 layer copies: about 1.4 GB, past the Infinity Cache
+    layers = [MoEWeights(stack(2 * I, H), stack(H, I), H, I, E, 0) for _ in range(nl)]
+    out = {}
+    for T, path, label in ((16, ops.PATH_GEMV, "decode"), (1024, ops.PATH_MFMA, "prefill")):
+        steps = []
+        for L in layers:
+            g = rng.gumbel(size=(T, E))
+            lg = torch.from_numpy((logp[None, :] + g).astype(np.float32)).to(dev)
+            ids = np.argsort(-(logp[None, :] + g), axis=1, kind="stable")[:, :k]
+            uniq = np.unique(ids)
+            x = torch.randn((T, H), device=dev).to(torch.bfloat16)
+            o = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
+            ws = ops.new_workspace(L, T, k, dev)
+            steps.append((L, lg, x, o, ws, sum(exp_bytes(int(bits[e])) for e in uniq)))
+        fns = [(lambda s=s: ops.moe_forward_logits(s[0], s[2], s[1], k, out=s[3], workspace=s[4],
+                                                   path=path)) for s in steps]
+        g = graph_of(fns)
+        time_graph(g, 2)
+        sec = time_graph(g, 8) / (8 * len(steps))
+        if label == "decode":
+            b = sum(s[5] for s in steps) / len(steps) + 2 * T * H * 2
+            out["nested_tiers_decode_T16_us_per_layer"] = round(sec * 1e6, 2)
+            out["nested_tiers_decode_T16_TBs"] = round(b / sec / 1e12, 3)
+            log(f"[bench] nested tiers decode T=16: {sec * 1e6:.1f} us/layer, {b / sec / 1e12:.3f} TB/s")
+        else:
+            fl = 6 * H * I * T * k
+            out["nested_tiers_prefill_T1024_us"] = round(sec * 1e6, 1)
+            out["nested_tiers_prefill_T1024_TFLOPs"] = round(fl / sec / 1e12, 1)
+            log(f"[bench] nested tiers prefill T=1024: {sec * 1e6:.0f} us, {fl / sec / 1e12:.1f} TFLOP/s")
+        del g
+    del layers
+    torch.cuda.empty_cache()
+    return out
 
 
 def cpu_baseline(a, c, T):
