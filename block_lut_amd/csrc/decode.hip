@@ -1,14 +1,16 @@
-// Decode-time fused MoE layer on BL4 weights: two kernels per layer.
+// Decode-time fused MoE layer on BL4 / NestedLUT weights: two kernels per layer.
 //
-//   bl4_decode_gate_up : routing + permutation (recomputed in every CTA from
-//                        top-k ids or router logits; T*k is small at decode;
-//                        the first CTA also stores it in the workspace)
-//                        -> grouped LUT-GEMV over W13 rows -> SwiGLU
-//                        -> act[position][I] (bf16)
-//   bl4_decode_down    : the stored routing -> grouped LUT-GEMV over W2 rows
-//                        of every active expert -> per-position results meet
-//                        in LDS -> weighted sum per token in slot order -> out
-// For T > 2 decode_route_kernel routes once and both kernels read its copy.
+//   bl4_decode_gate_up : routing -> grouped LUT-GEMV over W13 rows of every
+//                        active expert -> SwiGLU -> act[position][I] (bf16)
+//   bl4_decode_down    : routing -> grouped LUT-GEMV over W2 rows of every
+//                        active expert -> per-position results meet in LDS
+//                        -> weighted sum per token in slot order -> out
+// When the T*(k+S) pairs fit one wave (and top-k from logits has E <= 64)
+// every wave of the gate/up kernel computes the routing itself in registers
+// (a few hundred instructions, no LDS, no barrier) and its first CTA writes
+// it, with the pair weights, to the workspace; otherwise decode_route_kernel
+// routes once into the workspace.  The down kernel copies the workspace
+// routing into LDS.
 //
 // Reference behaviour: LUTFusedMoEMethod.apply, decode branch
 // (vllm_lut/quant_method.py:250-260), routing of moe_layer._routing
@@ -57,13 +59,6 @@ struct RouteScratch {
     int pid[kMaxP];                     // expert of each pair (-1: dropped)
     int rin[kMaxP];                     // rank among same-expert pairs of its 64-pair chunk
     int ccnt[kMaxP / 64][kMaxEtot];     // per chunk, per expert count -> exclusive prefix
-};
-
-// Routing scratch is dead once the routing is in RouteOut (every routing
-// path ends with a CTA barrier), so it shares LDS with the GEMV table slots.
-union RouteOrSlots {
-    RouteScratch X;
-    __attribute__((aligned(16))) uint8_t slot[4 * kSlot];
 };
 
 struct DecodeArgs {
@@ -250,12 +245,57 @@ __device__ void cta_route(const DecodeArgs& A, RouteOut& R, RouteScratch& X) {
     __syncthreads();
 }
 
-// Single-wave routing for P = T*(k+S) <= 64 pairs (the decode case): lane p
-// holds pair p.  Top-k from logits needs E <= 64 (lane = expert): k rounds of
-// a DPP wave max, the lowest lane holding it wins (ties -> lower id).
-// Positions and the active list come from runtime-bounded readlane loops over
-// the P pairs.  Only wave 0 works; the others wait at the CTA barrier.
-__device__ void wave_route_small(const DecodeArgs& A, RouteOut& R) {
+// Routing of P = T*(k+S) <= 64 pairs in one wave's registers (the decode
+// case).  Lane p holds pair p = t*(k+S) + s: its expert (-1 when dropped or
+// p >= P), its weight, and its position in the expert-major order (experts
+// ascending, pairs in pair order inside an expert).  Top-k from logits needs
+// E <= 64 (lane = expert): k rounds of a DPP wave max, the lowest lane
+// holding it wins (ties -> lower id).  Positions come from runtime-bounded
+// readlane loops over the P pairs.  Every wave that needs the routing
+// computes it itself: no LDS copy, no CTA barrier.
+struct WaveRoute {
+    int e;        // this lane's pair: expert, -1 if dropped
+    float w;      // its weight
+    int pos;      // its position, -1 if dropped
+    int cnt;      // pairs routed to its expert
+    int arank;    // rank of its expert among the active experts
+    bool first;   // first pair of its expert
+    int nact;     // active experts (wave-uniform)
+};
+
+__device__ __forceinline__ bool wave_route_fits(const DecodeArgs& A) {
+    const int P = A.T * (A.k + A.d.num_shared);
+    return P <= 64 && (A.topk_ids != nullptr || A.d.num_routed <= 64);
+}
+
+// Order-preserving int key of a float: larger float -> larger key, -0 and +0
+// equal (v + 0 turns -0 into +0), NaN -> INT_MIN (never selected, as a float
+// comparison never selects it).
+__device__ __forceinline__ int float_key(float v) {
+    const int b = __builtin_bit_cast(int, v + 0.0f);
+    return v != v ? INT_MIN : b ^ ((b >> 31) & 0x7fffffff);
+}
+
+template <int CTRL, int RMASK>
+__device__ __forceinline__ int dpp_max_i32(int v) {
+    return max(v, __builtin_amdgcn_update_dpp(INT_MIN, v, CTRL, RMASK, 0xf, false));
+}
+
+// Wave maximum of an int (every lane gets it).
+__device__ __forceinline__ int wave_max_i32(int v) {
+    v = dpp_max_i32<0xb1, 0xf>(v);    // quad_perm [1,0,3,2]
+    v = dpp_max_i32<0x4e, 0xf>(v);    // quad_perm [2,3,0,1]
+    v = dpp_max_i32<0x141, 0xf>(v);   // row_half_mirror
+    v = dpp_max_i32<0x140, 0xf>(v);   // row_mirror
+    v = dpp_max_i32<0x142, 0xa>(v);   // row_bcast:15
+    v = dpp_max_i32<0x143, 0xc>(v);   // row_bcast:31
+    return __builtin_amdgcn_readlane(v, 63);
+}
+
+// kWeights = false: expert ids and positions only (the gate/up CTAs that do
+// not publish the routing skip the softmax).
+template <bool kWeights>
+__device__ __forceinline__ WaveRoute wave_pairs(const DecodeArgs& A) {
     const int lane = threadIdx.x & 63;
     const int E = A.d.num_routed, S = A.d.num_shared;
     const int k = A.k, ke = k + S, T = A.T, P = T * ke;
@@ -266,7 +306,7 @@ __device__ void wave_route_small(const DecodeArgs& A, RouteOut& R) {
             const int t = lane / ke, sl = lane - t * ke;
             if (sl < k) {
                 e = A.topk_ids[t * k + sl];
-                w = A.topk_w[t * k + sl];
+                if (kWeights) w = A.topk_w[t * k + sl];
                 if (e < 0 || e >= E) e = -1;
             } else {
                 e = E + sl - k;
@@ -275,20 +315,29 @@ __device__ void wave_route_small(const DecodeArgs& A, RouteOut& R) {
         }
     } else {
         for (int t = 0; t < T; ++t) {
-            float v = lane < E ? A.logits[(int64_t)t * E + lane] : -INFINITY;
-            const float mx = wave_reduce_max(v);
-            const float sum = wave_reduce(lane < E ? expf(v - mx) : 0.f);
+            const float v = lane < E ? A.logits[(int64_t)t * E + lane] : -INFINITY;
+            int key = lane < E ? float_key(v) : INT_MIN;
+            float mx = 0.f, sum = 1.f;
+            if (kWeights) {
+                mx = wave_reduce_max(v);
+                sum = wave_reduce(lane < E ? expf(v - mx) : 0.f);
+            }
             float wsum = 0.f;
             for (int j = 0; j < k; ++j) {
-                const float m = wave_reduce_max(v);
-                const uint64_t b = __ballot(lane < E && v == m);
-                const int sel = (int)__builtin_ctzll(b);
-                const float pj = expf(m - mx) / sum;
-                wsum += pj;
-                if (lane == t * ke + j) { e = sel; w = pj; }
-                if (lane == sel) v = -INFINITY;
+                const int m = wave_max_i32(key);
+                const uint64_t b = __ballot(lane < E && key == m && m != INT_MIN);
+                const int sel = b ? (int)__builtin_ctzll(b) : -1;   // none: NaN logits
+                if (lane == t * ke + j) e = sel;
+                if (kWeights) {
+                    const float vm = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                                   __builtin_bit_cast(int, v), sel < 0 ? 0 : sel));
+                    const float pj = expf(vm - mx) / sum;
+                    wsum += pj;
+                    if (lane == t * ke + j) w = pj;
+                }
+                if (lane == sel) key = INT_MIN;
             }
-            if (lane >= t * ke && lane < t * ke + k) w = (A.renorm ? w / wsum : w) * A.scaling;
+            if (kWeights && lane >= t * ke && lane < t * ke + k) w = (A.renorm ? w / wsum : w) * A.scaling;
             if (lane >= t * ke + k && lane < (t + 1) * ke) { e = E + lane - t * ke - k; w = 1.0f; }
         }
     }
@@ -300,49 +349,128 @@ __device__ void wave_route_small(const DecodeArgs& A, RouteOut& R) {
         cnt += (u == e);
     }
     const bool valid = lane < P && e >= 0;
-    const uint64_t first = __ballot(valid && before == 0);
+    const uint64_t fm = __ballot(valid && before == 0);
     int arank = 0;
     for (int q = 0; q < P; ++q) {
         const int u = __builtin_amdgcn_readlane(e, q);
-        arank += (int)((first >> q) & 1ull) & (u < e);
+        arank += (int)((fm >> q) & 1ull) & (u < e);
     }
-    if (valid && before == 0) {
-        R.act[arank] = e;
-        R.aoff[arank] = less;
-        R.an[arank] = cnt;
+    WaveRoute r;
+    r.e = valid ? e : -1;
+    r.w = w;
+    r.pos = valid ? less + before : -1;
+    r.cnt = cnt;
+    r.arank = arank;
+    r.first = valid && before == 0;
+    r.nact = __popcll(fm);
+    return r;
+}
+
+// Active slot a of a routing: expert, first position, number of positions.
+struct SlotRef {
+    int e, p0, n;
+};
+
+// Read access to a routing result, either in this wave's registers
+// (WaveRoute) or in LDS (RouteOut), with the same calls.
+struct WaveRouteView {
+    WaveRoute r;
+    __device__ int nact() const { return r.nact; }
+    __device__ SlotRef slot(int a) const {
+        const uint64_t b = __ballot(r.first && r.arank == a);
+        if (!b) return {-1, 0, 0};
+        const int L = (int)__builtin_ctzll(b);
+        return {__builtin_amdgcn_readlane(r.e, L), __builtin_amdgcn_readlane(r.pos, L),
+                __builtin_amdgcn_readlane(r.cnt, L)};
+    }
+    // pair at position p (wave-uniform p)
+    __device__ int pair_at(int p) const {
+        const uint64_t b = __ballot(r.pos == p);
+        return b ? (int)__builtin_ctzll(b) : 0;
+    }
+    __device__ float weight_at(int p) const {
+        return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, r.w), pair_at(p)));
+    }
+    // position of pair q (lane-varying q; whole wave must call)
+    __device__ int pos_of(int q) const { return __shfl(r.pos, q, 64); }
+};
+
+struct LdsRouteView {
+    const RouteOut* R;
+    __device__ int nact() const { return R->nact; }
+    __device__ SlotRef slot(int a) const {
+        if (a >= R->nact) return {-1, 0, 0};
+        return {R->act[a], R->aoff[a], R->an[a]};
+    }
+    __device__ int pair_at(int p) const { return R->perm[p]; }
+    __device__ float weight_at(int p) const { return R->pw[R->perm[p]]; }
+    __device__ int pos_of(int q) const { return R->inv[q]; }
+};
+
+// The wave routing -> the LDS layout (wave 0 writes; callers then barrier).
+__device__ __forceinline__ void wave_route_to_lds(const DecodeArgs& A, RouteOut& R) {
+    const int lane = threadIdx.x & 63;
+    const int P = A.T * (A.k + A.d.num_shared);
+    const WaveRoute r = wave_pairs<true>(A);
+    if (r.first) {
+        R.act[r.arank] = r.e;
+        R.aoff[r.arank] = r.pos;
+        R.an[r.arank] = r.cnt;
     }
     if (lane < P) {
-        const int pos = valid ? less + before : -1;
-        R.inv[lane] = pos;
-        R.pw[lane] = w;
-        if (valid) R.perm[pos] = lane;
+        R.inv[lane] = r.pos;
+        R.pw[lane] = r.w;
+        if (r.pos >= 0) R.perm[r.pos] = lane;
     }
-    if (lane == 0) R.nact = __popcll(first);
+    if (lane == 0) R.nact = r.nact;
+}
+
+// One wave's register routing -> the global copy (the layout
+// decode_route_kernel writes), for the down kernel of the same layer.
+__device__ __forceinline__ void wave_route_publish(const DecodeArgs& A, const WaveRoute& r) {
+    const int lane = threadIdx.x & 63;
+    const int P = A.T * (A.k + A.d.num_shared);
+    RouteOut* g = A.route;
+    if (r.first) {
+        g->act[r.arank] = r.e;
+        g->aoff[r.arank] = r.pos;
+        g->an[r.arank] = r.cnt;
+    }
+    if (lane < P) {
+        g->inv[lane] = r.pos;
+        g->pw[lane] = r.w;
+        if (r.pos >= 0) g->perm[r.pos] = lane;
+    }
+    if (lane == 0) g->nact = r.nact;
+}
+
+// The precomputed routing (decode_route_kernel's global copy) -> LDS.
+__device__ __forceinline__ void load_route(const DecodeArgs& A, RouteOut& R) {
+    const int E_tot = A.d.num_routed + A.d.num_shared;
+    const int P = A.T * (A.k + A.d.num_shared);
+    const RouteOut* g = A.route;
+    for (int i = threadIdx.x; i < E_tot; i += 256) {
+        R.act[i] = g->act[i];
+        R.aoff[i] = g->aoff[i];
+        R.an[i] = g->an[i];
+    }
+    for (int i = threadIdx.x; i < P; i += 256) {
+        R.perm[i] = g->perm[i];
+        R.inv[i] = g->inv[i];
+        R.pw[i] = g->pw[i];
+    }
+    if (threadIdx.x == 0) R.nact = g->nact;
+    __syncthreads();
 }
 
 // Routing into LDS: computed here, or copied from the precomputed global copy.
 template <bool kPre>
 __device__ __forceinline__ void get_route(const DecodeArgs& A, RouteOut& R, RouteScratch& X) {
     if constexpr (kPre) {
-        const int E_tot = A.d.num_routed + A.d.num_shared;
-        const int P = A.T * (A.k + A.d.num_shared);
-        const RouteOut* g = A.route;
-        for (int i = threadIdx.x; i < E_tot; i += 256) {
-            R.act[i] = g->act[i];
-            R.aoff[i] = g->aoff[i];
-            R.an[i] = g->an[i];
-        }
-        for (int i = threadIdx.x; i < P; i += 256) {
-            R.perm[i] = g->perm[i];
-            R.inv[i] = g->inv[i];
-            R.pw[i] = g->pw[i];
-        }
-        if (threadIdx.x == 0) R.nact = g->nact;
-        __syncthreads();
+        load_route(A, R);
     } else {
-        const int P = A.T * (A.k + A.d.num_shared);
-        if (P <= 64 && (A.topk_ids || A.d.num_routed <= 64)) {
-            if (threadIdx.x < 64) wave_route_small(A, R);
+        if (wave_route_fits(A)) {
+            if (threadIdx.x < 64) wave_route_to_lds(A, R);
             __syncthreads();
         } else {
             cta_route(A, R, X);
@@ -547,22 +675,17 @@ __device__ __forceinline__ void expert_rows8(const lutmoe_weights& w, int e, con
     }
 }
 
-template <int TB, bool kPre, int kFmt>
-__global__ __launch_bounds__(256, TB <= 2 ? 3 : 2) void bl4_decode_gate_up(DecodeArgs A) {
-    __shared__ RouteOut R;
-    __shared__ RouteOrSlots U;
-    uint8_t* s_slot = U.slot;
-    get_route<kPre>(A, R, U.X);
-    // the first CTA publishes the routing it computed for the down kernel
-    if (!kPre && blockIdx.x == 0 && blockIdx.y == 0) put_route(A, R);
-    const int a = blockIdx.y;
-    if (a >= R.nact) return;
+// Gate/up for one routing view: CTA (x, y) covers 16 intermediate indices of
+// active slot y, wave wv 4 of them (4 gate rows + 4 up rows); SwiGLU of the
+// two projections -> act (bf16).
+template <int TB, int kFmt, class RV>
+__device__ __forceinline__ void gate_up_body(const DecodeArgs& A, const RV& rv, uint8_t* s_slot) {
+    const SlotRef sl = rv.slot(blockIdx.y);
+    if (sl.e < 0) return;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int I = A.d.inter, H = A.d.hidden, ke = A.k + A.d.num_shared;
     const int i0 = (blockIdx.x * 4 + wv) * 4;
     if (i0 >= I) return;
-    const int e = R.act[a];
-    const int p0 = R.aoff[a], n = R.an[a];
     int rows[kRows];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -571,41 +694,54 @@ __global__ __launch_bounds__(256, TB <= 2 ? 3 : 2) void bl4_decode_gate_up(Decod
         rows[4 + j] = I + i;
     }
     uint8_t* slot = s_slot + wv * kSlot;
-    for (int tb = 0; tb < n; tb += TB) {
-        const int nt = min(TB, n - tb);
+    for (int tb = 0; tb < sl.n; tb += TB) {
+        const int nt = min(TB, sl.n - tb);
         const uint16_t* xrow[TB];
 #pragma unroll
-        for (int t = 0; t < TB; ++t) xrow[t] = A.x + (int64_t)(R.perm[p0 + tb + min(t, nt - 1)] / ke) * H;
+        for (int t = 0; t < TB; ++t) xrow[t] = A.x + (int64_t)(rv.pair_at(sl.p0 + tb + min(t, nt - 1)) / ke) * H;
         float acc[kRows][TB];
 #pragma unroll
         for (int r = 0; r < kRows; ++r)
 #pragma unroll
             for (int t = 0; t < TB; ++t) acc[r][t] = 0.f;
-        expert_rows8<kFmt, TB>(A.d.w13, e, rows, H, lane, slot, xrow, nt, acc);
-        float g[4][TB], u[4][TB];
+        expert_rows8<kFmt, TB>(A.d.w13, sl.e, rows, H, lane, slot, xrow, nt, acc);
+        const int j = lane >> 3;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int t = 0; t < TB; ++t) {
+            float v[kRows];
 #pragma unroll
-            for (int t = 0; t < TB; ++t) {
-                g[j][t] = wave_reduce(acc[j][t]);
-                u[j][t] = wave_reduce(acc[4 + j][t]);
-            }
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int t = 0; t < TB; ++t)
-                if (lane == j * TB + t && t < nt && i0 + j < I)
-                    A.act[(int64_t)(p0 + tb + t) * I + i0 + j] = (uint16_t)f32_to_bf16(silu_mul(g[j][t], u[j][t]));
+            for (int r = 0; r < kRows; ++r) v[r] = acc[r][t];
+            const float g = wave_reduce8(v);       // lane l: row l >> 3 (gate j for l < 32)
+            const float u = from_upper_half(g);    // up row j
+            if (lane < 32 && (lane & 7) == 0 && t < nt && i0 + j < I)
+                A.act[(int64_t)(sl.p0 + tb + t) * I + i0 + j] = (uint16_t)f32_to_bf16(silu_mul(g, u));
+        }
     }
 }
 
 template <int TB, bool kPre, int kFmt>
-__global__ __launch_bounds__(256, TB <= 2 ? 3 : 2) void bl4_decode_down(DecodeArgs A) {
-    __shared__ RouteOut R;
-    __shared__ RouteOrSlots U;
-    uint8_t* s_slot = U.slot;
-    extern __shared__ float s_y[];   // [P][8]
-    get_route<kPre>(A, R, U.X);
+__global__ __launch_bounds__(256, TB <= 2 ? 3 : 2) void bl4_decode_gate_up(DecodeArgs A) {
+    __shared__ __attribute__((aligned(16))) uint8_t s_slot[4 * kSlot];
+    if constexpr (kPre) {
+        __shared__ RouteOut R;
+        load_route(A, R);
+        gate_up_body<TB, kFmt>(A, LdsRouteView{&R}, s_slot);
+    } else if (blockIdx.x == 0 && blockIdx.y == 0) {
+        // this CTA also publishes the routing (with the pair weights) for the
+        // down kernel
+        const WaveRoute r = wave_pairs<true>(A);
+        if (threadIdx.x < 64) wave_route_publish(A, r);
+        gate_up_body<TB, kFmt>(A, WaveRouteView{r}, s_slot);
+    } else {
+        gate_up_body<TB, kFmt>(A, WaveRouteView{wave_pairs<false>(A)}, s_slot);
+    }
+}
+
+// Down for one routing view: CTA x covers 8 output rows; wave wv runs the
+// active slots wv, wv+4, ..; per-position results (times the pair weight)
+// meet in LDS and are summed per token in slot order.
+template <int TB, int kFmt, class RV>
+__device__ __forceinline__ void down_body(const DecodeArgs& A, const RV& rv, uint8_t* s_slot, float* s_y) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int I = A.d.inter, H = A.d.hidden, ke = A.k + A.d.num_shared;
     const int h0 = blockIdx.x * kRows;
@@ -613,45 +749,61 @@ __global__ __launch_bounds__(256, TB <= 2 ? 3 : 2) void bl4_decode_down(DecodeAr
 #pragma unroll
     for (int r = 0; r < kRows; ++r) rows[r] = min(h0 + r, H - 1);
     uint8_t* slot = s_slot + wv * kSlot;
-    for (int a = wv; a < R.nact; a += 4) {
-        const int e = R.act[a];
-        const int p0 = R.aoff[a], n = R.an[a];
-        for (int tb = 0; tb < n; tb += TB) {
-            const int nt = min(TB, n - tb);
+    const int nact = rv.nact();
+    for (int a = wv; a < nact; a += 4) {
+        const SlotRef sl = rv.slot(a);
+        for (int tb = 0; tb < sl.n; tb += TB) {
+            const int nt = min(TB, sl.n - tb);
             const uint16_t* xrow[TB];
 #pragma unroll
-            for (int t = 0; t < TB; ++t) xrow[t] = A.act + (int64_t)(p0 + tb + min(t, nt - 1)) * I;
+            for (int t = 0; t < TB; ++t) xrow[t] = A.act + (int64_t)(sl.p0 + tb + min(t, nt - 1)) * I;
             float acc[kRows][TB];
 #pragma unroll
             for (int r = 0; r < kRows; ++r)
 #pragma unroll
                 for (int t = 0; t < TB; ++t) acc[r][t] = 0.f;
-            expert_rows8<kFmt, TB>(A.d.w2, e, rows, I, lane, slot, xrow, nt, acc);
+            expert_rows8<kFmt, TB>(A.d.w2, sl.e, rows, I, lane, slot, xrow, nt, acc);
 #pragma unroll
             for (int t = 0; t < TB; ++t) {
-                const int p = p0 + tb + min(t, nt - 1);
-                const float pw = R.pw[R.perm[p]];
+                const int p = sl.p0 + tb + min(t, nt - 1);
+                const float pw = rv.weight_at(p);
+                float v[kRows];
 #pragma unroll
-                for (int r = 0; r < kRows; ++r) {
-                    const float v = wave_reduce(acc[r][t]);
-                    if (lane == r && t < nt) s_y[p * kRows + r] = v * pw;
-                }
+                for (int r = 0; r < kRows; ++r) v[r] = acc[r][t];
+                const float y = wave_reduce8(v);   // lane l: row l >> 3
+                if ((lane & 7) == 0 && t < nt) s_y[p * kRows + (lane >> 3)] = y * pw;
             }
         }
     }
     __syncthreads();
     const int T = A.T;
-    for (int idx = threadIdx.x; idx < T * kRows; idx += 256) {
-        const int t = idx / kRows, r = idx % kRows;
-        if (h0 + r >= H) continue;
-        float s = 0.f;
+    // every thread runs the same trip counts (pos_of may be a wave operation)
+    for (int base = 0; base < T * kRows; base += 256) {
+        const int idx = base + threadIdx.x;
+        const int t = min(idx / kRows, T - 1), r = idx % kRows;
+        float sum = 0.f;
         for (int q = 0; q < ke; ++q) {
-            const int pos = R.inv[t * ke + q];
-            if (pos >= 0) s += s_y[pos * kRows + r];
+            const int pos = rv.pos_of(t * ke + q);
+            if (pos >= 0) sum += s_y[pos * kRows + r];
         }
-        const int64_t o = (int64_t)t * H + h0 + r;
-        if (A.out_dtype == LUTMOE_DTYPE_F32) ((float*)A.out)[o] = s;
-        else ((uint16_t*)A.out)[o] = (uint16_t)f32_to_bf16(s);
+        if (idx < T * kRows && h0 + r < H) {
+            const int64_t o = (int64_t)t * H + h0 + r;
+            if (A.out_dtype == LUTMOE_DTYPE_F32) ((float*)A.out)[o] = sum;
+            else ((uint16_t*)A.out)[o] = (uint16_t)f32_to_bf16(sum);
+        }
+    }
+}
+
+template <int TB, bool kPre, int kFmt>
+__global__ __launch_bounds__(256, TB <= 2 ? 3 : 2) void bl4_decode_down(DecodeArgs A) {
+    __shared__ __attribute__((aligned(16))) uint8_t s_slot[4 * kSlot];
+    extern __shared__ float s_y[];   // [P][8]
+    if constexpr (kPre) {
+        __shared__ RouteOut R;
+        load_route(A, R);
+        down_body<TB, kFmt>(A, LdsRouteView{&R}, s_slot, s_y);
+    } else {
+        down_body<TB, kFmt>(A, WaveRouteView{wave_pairs<true>(A)}, s_slot, s_y);
     }
 }
 
@@ -951,9 +1103,9 @@ int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* t
     const int E_tot = d->num_routed + d->num_shared;
     const int P = T * (k + d->num_shared);
     const int max_active = P < E_tot ? P : E_tot;
-    // Small grids recompute the routing in every CTA (no extra launch); larger
-    // ones route once into the workspace.
-    const bool pre = T > 2;
+    // T <= 2 with the pairs in one wave: both kernels route in registers; else
+    // one routing kernel writes the workspace copy both kernels read.
+    const bool pre = T > 2 || !(P <= 64 && (topk_ids != nullptr || d->num_routed <= 64));
     int rc;
     if (pre && (stages & LUTMOE_STAGE_ROUTE)) {
         hipLaunchKernelGGL(decode_route_kernel, dim3(1), dim3(256), 0, s, A);
@@ -972,28 +1124,36 @@ int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* t
         }
         return check_launch();
     }
-#define LUTMOE_DECODE_LAUNCH(KERNEL, PRE12, GRID, LDS)                                                    \
-    switch (tb_for(T) * 4 + (nested ? 1 : 0)) {                                                           \
-        case 4: hipLaunchKernelGGL((KERNEL<1, PRE12, LUTMOE_FMT_BL4>), GRID, dim3(256), LDS, s, A); break;    \
-        case 5: hipLaunchKernelGGL((KERNEL<1, PRE12, LUTMOE_FMT_NESTED>), GRID, dim3(256), LDS, s, A); break; \
-        case 8: hipLaunchKernelGGL((KERNEL<2, PRE12, LUTMOE_FMT_BL4>), GRID, dim3(256), LDS, s, A); break;    \
-        case 9: hipLaunchKernelGGL((KERNEL<2, PRE12, LUTMOE_FMT_NESTED>), GRID, dim3(256), LDS, s, A); break; \
-        case 17: hipLaunchKernelGGL((KERNEL<4, true, LUTMOE_FMT_NESTED>), GRID, dim3(256), LDS, s, A); break; \
-        default: hipLaunchKernelGGL((KERNEL<4, true, LUTMOE_FMT_BL4>), GRID, dim3(256), LDS, s, A); break;    \
+#define LUTMOE_DECODE_CASE(N, TB, PRE, FMT, KERNEL, GRID, LDS) \
+    case N: hipLaunchKernelGGL((KERNEL<TB, PRE, FMT>), GRID, dim3(256), LDS, s, A); break;
+#define LUTMOE_DECODE_LAUNCH(KERNEL, PRE, GRID, LDS)                                \
+    switch (tb_for(T) * 4 + ((PRE) ? 2 : 0) + (nested ? 1 : 0)) {                   \
+        LUTMOE_DECODE_CASE(4, 1, false, LUTMOE_FMT_BL4, KERNEL, GRID, LDS)          \
+        LUTMOE_DECODE_CASE(5, 1, false, LUTMOE_FMT_NESTED, KERNEL, GRID, LDS)       \
+        LUTMOE_DECODE_CASE(6, 1, true, LUTMOE_FMT_BL4, KERNEL, GRID, LDS)           \
+        LUTMOE_DECODE_CASE(7, 1, true, LUTMOE_FMT_NESTED, KERNEL, GRID, LDS)        \
+        LUTMOE_DECODE_CASE(8, 2, false, LUTMOE_FMT_BL4, KERNEL, GRID, LDS)          \
+        LUTMOE_DECODE_CASE(9, 2, false, LUTMOE_FMT_NESTED, KERNEL, GRID, LDS)       \
+        LUTMOE_DECODE_CASE(10, 2, true, LUTMOE_FMT_BL4, KERNEL, GRID, LDS)          \
+        LUTMOE_DECODE_CASE(11, 2, true, LUTMOE_FMT_NESTED, KERNEL, GRID, LDS)       \
+        LUTMOE_DECODE_CASE(18, 4, true, LUTMOE_FMT_BL4, KERNEL, GRID, LDS)          \
+        LUTMOE_DECODE_CASE(19, 4, true, LUTMOE_FMT_NESTED, KERNEL, GRID, LDS)       \
+        default: return LUTMOE_EINVAL;                                               \
     }
     if (stages & LUTMOE_STAGE_GATE_UP) {
         const dim3 grid((d->inter + 15) / 16, max_active);
-        LUTMOE_DECODE_LAUNCH(bl4_decode_gate_up, false, grid, 0)
+        LUTMOE_DECODE_LAUNCH(bl4_decode_gate_up, pre, grid, 0)
         if ((rc = check_launch())) return rc;
     }
     if (stages & LUTMOE_STAGE_DOWN) {
-        // the routing comes from the global copy written by the gate_up
-        // kernel (T <= 2) or by decode_route_kernel
         const dim3 grid((d->hidden + kRows - 1) / kRows);
         const size_t lds = (size_t)P * kRows * sizeof(float);
+        // the routing comes from the copy in the workspace (written by the
+        // gate/up kernel's first CTA, or by decode_route_kernel)
         LUTMOE_DECODE_LAUNCH(bl4_decode_down, true, grid, lds)
         return check_launch();
     }
+#undef LUTMOE_DECODE_CASE
 #undef LUTMOE_DECODE_LAUNCH
     return LUTMOE_OK;
 }

@@ -225,6 +225,55 @@ __device__ __forceinline__ float wave_reduce_max(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
+// The two results of a swap are copied out by value: a bit cast of a
+// vector element lvalue reads element 0 with this compiler.
+__device__ __forceinline__ float swap_sum32(float a, float b) {
+    const auto s = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
+                                                    false, false);
+    const uint32_t s0 = s[0], s1 = s[1];
+    return __uint_as_float(s0) + __uint_as_float(s1);
+}
+__device__ __forceinline__ float swap_sum16(float a, float b) {
+    const auto s = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
+                                                    false, false);
+    const uint32_t s0 = s[0], s1 = s[1];
+    return __uint_as_float(s0) + __uint_as_float(s1);
+}
+
+// Reduce-scatter of 8 per-lane partial sums over the wave: lane l returns the
+// wave total of v[l >> 3].  Halves of the wave trade values 4..7 for 0..3
+// (permlane32 swap: lane l of the upper half gets the lower half's lane l,
+// and the other way round, so swapped + kept is the pair sum), then 16-lane
+// rows trade 2 of their 4 (permlane16 swap), then the two 8-lane halves of a
+// row trade 1 of 2 (row mirror), and each 8-lane group sums its value (two
+// quad permutes and a half-row mirror).  19 cross-lane/add steps instead of
+// eight full reductions.
+__device__ __forceinline__ float wave_reduce8(const float (&v)[8]) {
+    const int lane = threadIdx.x & 63;
+    float a[4], b[2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a[i] = swap_sum32(v[i], v[i + 4]);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) b[i] = swap_sum16(a[i], a[i + 2]);
+    const bool hi = (lane >> 3) & 1;
+    const float send = hi ? b[0] : b[1];
+    float c = (hi ? b[1] : b[0]) +
+              __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, send), 0x140, 0xf, 0xf,
+                                                                    false));   // row_mirror
+    c += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, c), 0xb1, 0xf, 0xf, false));
+    c += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, c), 0x4e, 0xf, 0xf, false));
+    c += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, c), 0x141, 0xf, 0xf, false));
+    return c;
+}
+
+// The value of lane l + 32 in lanes l < 32 (permlane32 swap).
+__device__ __forceinline__ float from_upper_half(float v) {
+    const auto s = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
+                                                    false, false);
+    const uint32_t s1 = s[1];
+    return __uint_as_float(s1);
+}
+
 // Inclusive prefix sum over the 64 lanes (row shifts within 16-lane rows,
 // then row broadcasts across rows).
 __device__ __forceinline__ int wave_scan_incl(int v) {

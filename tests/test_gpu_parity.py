@@ -347,6 +347,33 @@ def test_moe_layer_from_logits(gpu, T, path, renorm, E):
     assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
 
 
+@pytest.mark.parametrize("T,E,renorm", [(1, 12, False), (2, 12, True), (1, 60, False), (2, 60, False)])
+def test_moe_layer_from_logits_ties(gpu, T, E, renorm):
+    """Decode routing on logits with many exact ties, -0.0 next to +0.0 and a -inf:
+    the in-kernel top-k must pick the lower expert id on every tie, as the oracle
+    (and torch.topk on the reference's softmax) does, so any other choice changes
+    the experts and the output."""
+    import torch
+    from block_lut_amd import ops
+    from block_lut_amd.formats import MoEWeights
+    S, k, H, I = 1, 4, 256, 192
+    w13, w2 = _moe_case("bl4", E, S, H, I, seed=90 + T + E)
+    moe = MoEWeights(w13.stack(gpu), w2.stack(gpu), H, I, E, S)
+    rng = np.random.default_rng(900 + T + E)
+    xb = _x(rng, T, H)
+    lg = (np.round(rng.standard_normal((T, E)) * 1.5) / 2).astype(np.float32)   # few distinct values
+    lg[0, 1] = -0.0
+    lg[0, 2] = 0.0
+    lg[0, 3] = np.float32(lg.max())          # a tie at the top
+    lg[-1, 0] = -np.inf
+    out = ops.moe_forward_logits(moe, to_dev_bf16(xb, gpu), torch.from_numpy(lg).to(gpu), k,
+                                 renormalize=renorm, scaling=1.0, out_dtype=torch.float32, path=1)
+    rw, rids = O.route(lg, k, renormalize=renorm)
+    ref = O.moe_layer(xb, rids, rw, w13.deq_f32, w2.deq_f32,
+                      shared=[(w13.deq_f32(E + s), w2.deq_f32(E + s)) for s in range(S)])
+    assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
+
+
 @pytest.mark.skip(reason="the one-launch persistent decode kernel (bl4_decode_fused) did not complete "
                          "on its first GPU runs (E=8, S=1, k=2, H=512, I=320, T=1); it is switched off "
                          "(kFusedDecodeEnabled) until the cause is found on the CPU")
