@@ -39,6 +39,7 @@ constexpr int kWChunk = 2048;            // columns per lane pass (64 lanes x 32
 constexpr int kRows = 8;
 constexpr int kSlot = kRows * 1024;      // LDS bytes per wave: 8 rows' tables of a chunk
 constexpr int kMaxEtot = 320;
+constexpr int kGuWaves = 1;              // waves per gate/up CTA (4 intermediate indices each)
 constexpr int kMaxP = 512;
 
 // Routing result: active experts (ascending), per-expert position offsets,
@@ -116,9 +117,9 @@ __device__ void cta_route(const DecodeArgs& A, RouteOut& R, RouteScratch& X) {
     const int E = A.d.num_routed, S = A.d.num_shared, E_tot = E + S;
     const int k = A.k, ke = k + S, T = A.T, P = T * ke;
     const int nchunk = (P + 63) / 64;
-    for (int i = tid; i < nchunk * E_tot; i += 256) X.ccnt[i / E_tot][i % E_tot] = 0;
+    for (int i = tid; i < nchunk * E_tot; i += blockDim.x) X.ccnt[i / E_tot][i % E_tot] = 0;
     if (A.topk_ids) {
-        for (int p = tid; p < P; p += 256) {
+        for (int p = tid; p < P; p += blockDim.x) {
             const int t = p / ke, s = p - t * ke;
             int e;
             float w;
@@ -136,7 +137,7 @@ __device__ void cta_route(const DecodeArgs& A, RouteOut& R, RouteScratch& X) {
     } else {
         // logits mode, wave per token: softmax in fp32; top-k by logit (softmax
         // is monotone): rank(e) = #{e' : l[e'] > l[e] or (l[e'] == l[e], e' < e)}.
-        for (int t = wv; t < T; t += 4) {
+        for (int t = wv; t < T; t += (int)(blockDim.x >> 6)) {
             const float* src = A.logits + (int64_t)t * E;
             float mx = -INFINITY;
             for (int e = lane; e < E; e += 64) mx = fmaxf(mx, src[e]);
@@ -189,7 +190,7 @@ __device__ void cta_route(const DecodeArgs& A, RouteOut& R, RouteScratch& X) {
     }
     __syncthreads();
     // stable ranks inside 64-pair chunks + per-chunk expert counts
-    for (int c = wv; c < nchunk; c += 4) {
+    for (int c = wv; c < nchunk; c += (int)(blockDim.x >> 6)) {
         const int p = c * 64 + lane;
         const int e = p < P ? X.pid[p] : -1;
         int before = 0, after = 0;
@@ -230,12 +231,12 @@ __device__ void cta_route(const DecodeArgs& A, RouteOut& R, RouteScratch& X) {
         if (lane == 63) { R.off[E_tot] = ic; R.nact = ia; }
     }
     __syncthreads();
-    for (int a = tid; a < R.nact; a += 256) {
+    for (int a = tid; a < R.nact; a += blockDim.x) {
         const int e = R.act[a];
         R.aoff[a] = R.off[e];
         R.an[a] = R.off[e + 1] - R.off[e];
     }
-    for (int p = tid; p < P; p += 256) {
+    for (int p = tid; p < P; p += blockDim.x) {
         const int e = X.pid[p];
         if (e < 0) { R.inv[p] = -1; continue; }
         const int pos = R.off[e] + X.ccnt[p >> 6][e] + X.rin[p];
@@ -449,12 +450,12 @@ __device__ __forceinline__ void load_route(const DecodeArgs& A, RouteOut& R) {
     const int E_tot = A.d.num_routed + A.d.num_shared;
     const int P = A.T * (A.k + A.d.num_shared);
     const RouteOut* g = A.route;
-    for (int i = threadIdx.x; i < E_tot; i += 256) {
+    for (int i = threadIdx.x; i < E_tot; i += blockDim.x) {
         R.act[i] = g->act[i];
         R.aoff[i] = g->aoff[i];
         R.an[i] = g->an[i];
     }
-    for (int i = threadIdx.x; i < P; i += 256) {
+    for (int i = threadIdx.x; i < P; i += blockDim.x) {
         R.perm[i] = g->perm[i];
         R.inv[i] = g->inv[i];
         R.pw[i] = g->pw[i];
@@ -484,12 +485,12 @@ __device__ __forceinline__ void put_route(const DecodeArgs& A, const RouteOut& R
     const int E_tot = A.d.num_routed + A.d.num_shared;
     const int P = A.T * (A.k + A.d.num_shared);
     RouteOut* g = A.route;
-    for (int i = threadIdx.x; i < E_tot; i += 256) {
+    for (int i = threadIdx.x; i < E_tot; i += blockDim.x) {
         g->act[i] = R.act[i];
         g->aoff[i] = R.aoff[i];
         g->an[i] = R.an[i];
     }
-    for (int i = threadIdx.x; i < P; i += 256) {
+    for (int i = threadIdx.x; i < P; i += blockDim.x) {
         g->perm[i] = R.perm[i];
         g->inv[i] = R.inv[i];
         g->pw[i] = R.pw[i];
@@ -675,16 +676,18 @@ __device__ __forceinline__ void expert_rows8(const lutmoe_weights& w, int e, con
     }
 }
 
-// Gate/up for one routing view: CTA (x, y) covers 16 intermediate indices of
-// active slot y, wave wv 4 of them (4 gate rows + 4 up rows); SwiGLU of the
-// two projections -> act (bf16).
+// Gate/up for one routing view: CTA (x, y) covers 4*kGuWaves intermediate
+// indices of active slot y, wave wv 4 of them (4 gate rows + 4 up rows);
+// SwiGLU of the two projections -> act (bf16).  One-wave CTAs (16 KB of
+// weights each) spread a layer's work evenly over the CUs: a CU streams at
+// most ~40 GB/s, so a CU holding a CTA more than the others sets the tail.
 template <int TB, int kFmt, class RV>
 __device__ __forceinline__ void gate_up_body(const DecodeArgs& A, const RV& rv, uint8_t* s_slot) {
     const SlotRef sl = rv.slot(blockIdx.y);
     if (sl.e < 0) return;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int I = A.d.inter, H = A.d.hidden, ke = A.k + A.d.num_shared;
-    const int i0 = (blockIdx.x * 4 + wv) * 4;
+    const int i0 = (blockIdx.x * kGuWaves + wv) * 4;
     if (i0 >= I) return;
     int rows[kRows];
 #pragma unroll
@@ -698,7 +701,10 @@ __device__ __forceinline__ void gate_up_body(const DecodeArgs& A, const RV& rv, 
         const int nt = min(TB, sl.n - tb);
         const uint16_t* xrow[TB];
 #pragma unroll
-        for (int t = 0; t < TB; ++t) xrow[t] = A.x + (int64_t)(rv.pair_at(sl.p0 + tb + min(t, nt - 1)) / ke) * H;
+        for (int t = 0; t < TB; ++t) {
+            const int tok = rv.pair_at(sl.p0 + tb + min(t, nt - 1)) / ke;
+            xrow[t] = A.x + (int64_t)min(max(tok, 0), A.T - 1) * H;   // in bounds whatever the routing holds
+        }
         float acc[kRows][TB];
 #pragma unroll
         for (int r = 0; r < kRows; ++r)
@@ -720,8 +726,8 @@ __device__ __forceinline__ void gate_up_body(const DecodeArgs& A, const RV& rv, 
 }
 
 template <int TB, bool kPre, int kFmt>
-__global__ __launch_bounds__(256, TB <= 2 ? 3 : 2) void bl4_decode_gate_up(DecodeArgs A) {
-    __shared__ __attribute__((aligned(16))) uint8_t s_slot[4 * kSlot];
+__global__ __launch_bounds__(64 * kGuWaves, TB <= 2 ? 3 : 2) void bl4_decode_gate_up(DecodeArgs A) {
+    __shared__ __attribute__((aligned(16))) uint8_t s_slot[kGuWaves * kSlot];
     if constexpr (kPre) {
         __shared__ RouteOut R;
         load_route(A, R);
@@ -750,7 +756,7 @@ __device__ __forceinline__ void down_body(const DecodeArgs& A, const RV& rv, uin
     for (int r = 0; r < kRows; ++r) rows[r] = min(h0 + r, H - 1);
     uint8_t* slot = s_slot + wv * kSlot;
     const int nact = rv.nact();
-    for (int a = wv; a < nact; a += 4) {
+    for (int a = wv; a < nact; a += (int)(blockDim.x >> 6)) {
         const SlotRef sl = rv.slot(a);
         for (int tb = 0; tb < sl.n; tb += TB) {
             const int nt = min(TB, sl.n - tb);
@@ -778,7 +784,7 @@ __device__ __forceinline__ void down_body(const DecodeArgs& A, const RV& rv, uin
     __syncthreads();
     const int T = A.T;
     // every thread runs the same trip counts (pos_of may be a wave operation)
-    for (int base = 0; base < T * kRows; base += 256) {
+    for (int base = 0; base < T * kRows; base += blockDim.x) {
         const int idx = base + threadIdx.x;
         const int t = min(idx / kRows, T - 1), r = idx % kRows;
         float sum = 0.f;
@@ -952,7 +958,7 @@ __device__ __forceinline__ void fused_down_item(const DecodeArgs& A, const Route
     }
     __syncthreads();
     const int T = A.T;
-    for (int idx = threadIdx.x; idx < T * kRows; idx += 256) {
+    for (int idx = threadIdx.x; idx < T * kRows; idx += blockDim.x) {
         const int t = idx / kRows, r = idx % kRows;
         if (h0 + r >= H) continue;
         float sum = 0.f;
@@ -1124,25 +1130,25 @@ int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* t
         }
         return check_launch();
     }
-#define LUTMOE_DECODE_CASE(N, TB, PRE, FMT, KERNEL, GRID, LDS) \
-    case N: hipLaunchKernelGGL((KERNEL<TB, PRE, FMT>), GRID, dim3(256), LDS, s, A); break;
-#define LUTMOE_DECODE_LAUNCH(KERNEL, PRE, GRID, LDS)                                \
-    switch (tb_for(T) * 4 + ((PRE) ? 2 : 0) + (nested ? 1 : 0)) {                   \
-        LUTMOE_DECODE_CASE(4, 1, false, LUTMOE_FMT_BL4, KERNEL, GRID, LDS)          \
-        LUTMOE_DECODE_CASE(5, 1, false, LUTMOE_FMT_NESTED, KERNEL, GRID, LDS)       \
-        LUTMOE_DECODE_CASE(6, 1, true, LUTMOE_FMT_BL4, KERNEL, GRID, LDS)           \
-        LUTMOE_DECODE_CASE(7, 1, true, LUTMOE_FMT_NESTED, KERNEL, GRID, LDS)        \
-        LUTMOE_DECODE_CASE(8, 2, false, LUTMOE_FMT_BL4, KERNEL, GRID, LDS)          \
-        LUTMOE_DECODE_CASE(9, 2, false, LUTMOE_FMT_NESTED, KERNEL, GRID, LDS)       \
-        LUTMOE_DECODE_CASE(10, 2, true, LUTMOE_FMT_BL4, KERNEL, GRID, LDS)          \
-        LUTMOE_DECODE_CASE(11, 2, true, LUTMOE_FMT_NESTED, KERNEL, GRID, LDS)       \
-        LUTMOE_DECODE_CASE(18, 4, true, LUTMOE_FMT_BL4, KERNEL, GRID, LDS)          \
-        LUTMOE_DECODE_CASE(19, 4, true, LUTMOE_FMT_NESTED, KERNEL, GRID, LDS)       \
-        default: return LUTMOE_EINVAL;                                               \
+#define LUTMOE_DECODE_CASE(N, TB, PRE, FMT, KERNEL, GRID, BLOCK, LDS) \
+    case N: hipLaunchKernelGGL((KERNEL<TB, PRE, FMT>), GRID, BLOCK, LDS, s, A); break;
+#define LUTMOE_DECODE_LAUNCH(KERNEL, PRE, GRID, BLOCK, LDS)                                \
+    switch (tb_for(T) * 4 + ((PRE) ? 2 : 0) + (nested ? 1 : 0)) {                          \
+        LUTMOE_DECODE_CASE(4, 1, false, LUTMOE_FMT_BL4, KERNEL, GRID, BLOCK, LDS)          \
+        LUTMOE_DECODE_CASE(5, 1, false, LUTMOE_FMT_NESTED, KERNEL, GRID, BLOCK, LDS)       \
+        LUTMOE_DECODE_CASE(6, 1, true, LUTMOE_FMT_BL4, KERNEL, GRID, BLOCK, LDS)           \
+        LUTMOE_DECODE_CASE(7, 1, true, LUTMOE_FMT_NESTED, KERNEL, GRID, BLOCK, LDS)        \
+        LUTMOE_DECODE_CASE(8, 2, false, LUTMOE_FMT_BL4, KERNEL, GRID, BLOCK, LDS)          \
+        LUTMOE_DECODE_CASE(9, 2, false, LUTMOE_FMT_NESTED, KERNEL, GRID, BLOCK, LDS)       \
+        LUTMOE_DECODE_CASE(10, 2, true, LUTMOE_FMT_BL4, KERNEL, GRID, BLOCK, LDS)          \
+        LUTMOE_DECODE_CASE(11, 2, true, LUTMOE_FMT_NESTED, KERNEL, GRID, BLOCK, LDS)       \
+        LUTMOE_DECODE_CASE(18, 4, true, LUTMOE_FMT_BL4, KERNEL, GRID, BLOCK, LDS)          \
+        LUTMOE_DECODE_CASE(19, 4, true, LUTMOE_FMT_NESTED, KERNEL, GRID, BLOCK, LDS)       \
+        default: return LUTMOE_EINVAL;                                                      \
     }
     if (stages & LUTMOE_STAGE_GATE_UP) {
-        const dim3 grid((d->inter + 15) / 16, max_active);
-        LUTMOE_DECODE_LAUNCH(bl4_decode_gate_up, pre, grid, 0)
+        const dim3 grid((d->inter + 4 * kGuWaves - 1) / (4 * kGuWaves), max_active);
+        LUTMOE_DECODE_LAUNCH(bl4_decode_gate_up, pre, grid, dim3(64 * kGuWaves), 0)
         if ((rc = check_launch())) return rc;
     }
     if (stages & LUTMOE_STAGE_DOWN) {
@@ -1150,7 +1156,7 @@ int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* t
         const size_t lds = (size_t)P * kRows * sizeof(float);
         // the routing comes from the copy in the workspace (written by the
         // gate/up kernel's first CTA, or by decode_route_kernel)
-        LUTMOE_DECODE_LAUNCH(bl4_decode_down, true, grid, lds)
+        LUTMOE_DECODE_LAUNCH(bl4_decode_down, true, grid, dim3(256), lds)
         return check_launch();
     }
 #undef LUTMOE_DECODE_CASE
