@@ -26,7 +26,8 @@ extra      = the other configurations (decode T=8/32, DeepSeek-V2-Lite prefill
              grouped GEMM TFLOP/s, switch-base-8 single linear, hot-cache decode,
              and the NestedLUT tier workload: Qwen shape, 20 experts each at 2, 3
              and 4 bits, Zipf(1.1) expert popularity with Gumbel-top-4 routing,
-             decode T=16 and prefill T=1024).
+             decode T=16 and prefill T=1024; the Mixtral-8x7B-shaped stack of
+             32 resident layers: decode B=1/64 and prefill 4096 tokens).
 
 Weights are synthetic BL4 data of the configured shapes (uniform random 4-bit
 codes, sorted N(0, 0.02) codebook entries): throughput does not depend on the
@@ -281,6 +282,10 @@ def main():
         log(f"[bench] prefill DeepSeek T=2048: {sec * 1e6:.0f} us, {flops / sec / 1e12:.1f} TFLOP/s")
         extra.update(nested_tiers(a, ops, N, torch, dev, NestedExpert, NestedStack, MoEWeights,
                                   graph_of, time_graph))
+        del lay, sp, g
+        torch.cuda.empty_cache()
+        extra.update(mixtral_stack(ops, torch, dev, rand_stack, MoEWeights, graph_of, time_graph))
+        torch.cuda.empty_cache()
         # switch-base-8 single BL4 linear 768 -> 3072, one token
         st1 = rand_stack(1, 3072, 768)
         x1 = torch.randn((1, 768), device=dev).to(torch.bfloat16)
@@ -299,6 +304,57 @@ def main():
         result["cpu_baseline"] = cpu_baseline(a, c, T)
 
     print(json.dumps(result), flush=True)
+
+
+def mixtral_stack(ops, torch, dev, rand_stack, MoEWeights, graph_of, time_graph):
+    """Mixtral-8x7B-shaped stack of 32 MoE layers resident in HBM (H4096,
+    I14336, 8 experts, top-2 softmax with renormalisation, SwiGLU BL4: 1.41 GB
+    per layer, 45 GB in all).  Decode B=1 and B=64: one step = the batch
+    through all 32 layers (each layer its own router logits); bytes = the
+    distinct routed experts of every layer at 1.0 B/weight + activations.
+    Prefill: 4096 tokens through all 32 layers on the grouped MFMA path;
+    flops = 32 * 6*H*I*T*k."""
+    H, I, E, k, L = 4096, 14336, 8, 2, 32
+    log(f"[bench] Mixtral stack: building {L} layers ({L * 3 * H * I * E / 1e9:.1f} GB)")
+    layers = [MoEWeights(rand_stack(E, 2 * I, H), rand_stack(E, H, I), H, I, E, 0) for _ in range(L)]
+    gen = torch.Generator(device="cpu").manual_seed(8)
+    res = {}
+    for B in (1, 64):
+        xs = [torch.randn((B, H), generator=gen).to(torch.bfloat16).to(dev) for _ in range(L)]
+        lgs = [torch.randn((B, E), generator=gen).to(dev) for _ in range(L)]
+        outs = [torch.empty((B, H), dtype=torch.bfloat16, device=dev) for _ in range(L)]
+        ws = ops.new_workspace(layers[0], B, k, dev)
+        U = sum(int(torch.unique(torch.topk(lg, k, dim=1).indices).numel()) for lg in lgs)
+        calls = [lambda l=l, x=x, lg=lg, o=o: ops.moe_forward_logits(l, x, lg, k, renormalize=True, out=o,
+                                                                     workspace=ws)
+                 for l, x, lg, o in zip(layers, xs, lgs, outs)]
+        g = graph_of(calls)
+        time_graph(g, 2)
+        sec = time_graph(g, 6) / 6
+        by = U * 3 * H * I * BYTES_PER_WEIGHT + L * 2 * B * H * 2
+        res[f"mixtral_decode_B{B}_ms_per_step"] = round(sec * 1e3, 4)
+        res[f"mixtral_decode_B{B}_us_per_layer"] = round(sec * 1e6 / L, 2)
+        res[f"mixtral_decode_B{B}_TBs"] = round(by / sec / 1e12, 3)
+        log(f"[bench] Mixtral decode B={B}: {sec * 1e3:.3f} ms per step of {L} layers "
+            f"({sec * 1e6 / L:.1f} us/layer), {by / sec / 1e12:.3f} TB/s")
+        del xs, lgs, outs, ws, calls, g
+    T = 4096
+    x = torch.randn((T, H), generator=gen).to(torch.bfloat16).to(dev)
+    lgs = [torch.randn((T, E), generator=gen).to(dev) for _ in range(L)]
+    out = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
+    ws = ops.new_workspace(layers[0], T, k, dev)
+    calls = [lambda l=l, lg=lg: ops.moe_forward_logits(l, x, lg, k, renormalize=True, out=out, workspace=ws,
+                                                       path=ops.PATH_MFMA)
+             for l, lg in zip(layers, lgs)]
+    g = graph_of(calls)
+    time_graph(g, 1)
+    sec = time_graph(g, 3) / 3
+    flops = L * 6 * H * I * T * k
+    res["mixtral_prefill_T4096_ms_per_stack"] = round(sec * 1e3, 3)
+    res["mixtral_prefill_T4096_TFLOPs"] = round(flops / sec / 1e12, 1)
+    log(f"[bench] Mixtral prefill T=4096: {sec * 1e3:.2f} ms per {L} layers, {flops / sec / 1e12:.1f} TFLOP/s")
+    del layers, x, lgs, out, ws, calls, g
+    return res
 
 
 def nested_tiers(a, ops, N, torch, dev, NestedExpert, NestedStack, MoEWeights, graph_of,

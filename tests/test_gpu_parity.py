@@ -427,6 +427,51 @@ def test_moe_layer_qwen_decode_full_shape(gpu):
         assert rel_maxabs(out, ref) <= TOL, T
 
 
+def test_moe_layer_mixtral_shape(gpu):
+    """Mixtral-8x7B layer shape (H4096 I14336, 8 experts top-2 with renormalisation): K spans
+    two (W13) and seven (W2) 2048-column decode chunks, and the MFMA path runs 112 n-tiles per
+    expert.  Decode T=1 and T=3 from logits, prefill T=64 from ids on 3 experts; oracle on the
+    touched experts' GPU-dequantised weights (dequantisation is bit-exact separately)."""
+    import torch
+    from block_lut_amd import ops
+    from block_lut_amd.formats import BL4Stack, MoEWeights
+    H, I, E, k = 4096, 14336, 8, 2
+    g = torch.Generator(device=gpu).manual_seed(14)
+
+    def rand_stack(M, K):
+        codes = torch.randint(0, 256, (E, M, K // 2), dtype=torch.uint8, generator=g, device=gpu)
+        tabs = torch.sort(torch.randn((E, M, K // 64, 16), generator=g, device=gpu) * 0.02, dim=-1).values
+        return BL4Stack(codes, tabs.to(torch.bfloat16))
+
+    moe = MoEWeights(rand_stack(2 * I, H), rand_stack(H, I), H, I, E, 0)
+    cache = {}
+
+    def deq(w, e):
+        key = (id(w), e)
+        if key not in cache:
+            cache[key] = O.bf16_to_f32(bf16_bits(ops.dequant(w, e, 1)[0]))
+        return cache[key]
+
+    for T in (1, 3):
+        rng = np.random.default_rng(140 + T)
+        xb = _x(rng, T, H)
+        lg = rng.standard_normal((T, E)).astype(np.float32)
+        out = ops.moe_forward_logits(moe, to_dev_bf16(xb, gpu), torch.from_numpy(lg).to(gpu), k,
+                                     renormalize=True, out_dtype=torch.float32, path=1).cpu().numpy()
+        rw, rids = O.route(lg, k, renormalize=True)
+        ref = O.moe_layer(xb, rids, rw, lambda e: deq(moe.w13, e), lambda e: deq(moe.w2, e))
+        assert rel_maxabs(out, ref) <= TOL, T
+    T = 64
+    rng = np.random.default_rng(164)
+    xb = _x(rng, T, H)
+    rids = np.stack([rng.choice([0, 3, 5], size=k, replace=False) for _ in range(T)]).astype(np.int32)
+    rw = rng.dirichlet(np.ones(k), size=T).astype(np.float32)
+    out = ops.moe_forward(moe, to_dev_bf16(xb, gpu), torch.from_numpy(rw).to(gpu),
+                          torch.from_numpy(rids).to(gpu), out_dtype=torch.float32, path=2).cpu().numpy()
+    ref = O.moe_layer(xb, rids, rw, lambda e: deq(moe.w13, e), lambda e: deq(moe.w2, e))
+    assert rel_maxabs(out, ref) <= TOL
+
+
 def test_moe_layer_paths_agree(gpu):
     """GEMV and MFMA paths on the same inputs (both fp32 accumulation)."""
     import torch
