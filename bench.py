@@ -83,6 +83,9 @@ def parse():
     p.add_argument("--pmc-sample", action="store_true",
                    help="run only a 256 MiB device copy and the decode gate/up kernel of the "
                         "default workload (for rocprofv3 --pmc passes), then exit")
+    p.add_argument("--prefill-sample", action="store_true",
+                   help="run only the DeepSeek-V2-Lite T=2048 prefill (graph-captured, 10 replays, "
+                        "for rocprofv3 kernel traces), then exit")
     return p.parse_args()
 
 
@@ -182,6 +185,16 @@ def main():
         torch.cuda.synchronize()
         log(f"[bench] pmc sample: gate/up algorithmic bytes per launch "
             f"{sum(s.bytes_gate_up for s in steps) / len(steps):.0f}")
+        return
+    if a.prefill_sample:
+        d = DSV2
+        sp = Step(rand_layer(d), d, 2048)
+        g = graph_of([lambda: sp.run(path=ops.PATH_MFMA)])
+        time_graph(g, 2)
+        sec = time_graph(g, 10) / 10
+        flops = 6 * d["H"] * d["I"] * 2048 * (d["k"] + d["S"])
+        log(f"[bench] prefill sample: DeepSeek T=2048 {sec * 1e6:.1f} us, {flops / sec / 1e12:.1f} TFLOP/s "
+            f"({flops} flops per layer)")
         return
     log(f"[bench] building {a.layers} Qwen-shaped BL4 layers ({a.layers * c['E'] * expert_bytes(c) / 1e9:.1f} GB)")
     layers = [rand_layer(c) for _ in range(a.layers)]

@@ -352,9 +352,8 @@ int moe_forward_impl(const lutmoe_moe_desc* d, const void* x, const float* topk_
             topk_w = tw;
             topk_ids = ti;
         }
-        if ((rc = launch_build_pairs(topk_ids, topk_w, T, k, E, S, pair_ids, pair_w, s))) return rc;
-        if ((rc = launch_permute(pair_ids, T, ke, E_tot, (int32_t*)r.offsets, (int32_t*)r.perm,
-                                 (int32_t*)r.inv, (int32_t*)r.active, s)))
+        if ((rc = launch_route_pairs(topk_ids, topk_w, T, k, E, S, (int32_t*)r.offsets, (int32_t*)r.perm,
+                                     (int32_t*)r.inv, (int32_t*)r.active, pair_ids, pair_w, s)))
             return rc;
     }
     const int max_active = (int)(P < E_tot ? P : E_tot);

@@ -67,6 +67,11 @@ int launch_build_pairs(const int32_t* topk_ids, const float* topk_w, int T, int 
                        int E, int S, int32_t* pair_ids, float* pair_w, hipStream_t s);
 int launch_permute(const int32_t* pair_ids, int T, int k_eff, int E_tot, int32_t* offsets,
                    int32_t* perm, int32_t* inv, int32_t* active, hipStream_t s);
+// pairs built from top-k ids (+ S shared slots per token), permuted, and
+// their ids / weights written to pair_ids / pair_w
+int launch_route_pairs(const int32_t* topk_ids, const float* topk_w, int T, int k, int E, int S,
+                       int32_t* offsets, int32_t* perm, int32_t* inv, int32_t* active, int32_t* pair_ids,
+                       float* pair_w, hipStream_t s);
 int launch_combine(const float* y_pos, const int32_t* inv, int T, int k_eff, int H,
                    void* out, int out_dtype, hipStream_t s);
 

@@ -8,14 +8,16 @@
 //  permute      : expert-major, pair-ascending stable order, the order the
 //                 llama.cpp mul_mat_id patch builds on the host
 //                 (llama-cpp-port/patches/0001:96-110), plus its inverse and
-//                 the active-expert list.  One CTA per expert, no atomics on
-//                 global memory, deterministic.  Pairs whose expert id is out
-//                 of range are dropped (inv = -1) and contribute nothing.
+//                 the active-expert list.  One CTA per 1024 pairs (E_tot <=
+//                 512; one CTA per expert above that), no atomics on global
+//                 memory, deterministic.  Pairs whose expert id is out of
+//                 range are dropped (inv = -1) and contribute nothing.
 //  combine      : out[t] = sum over slots of y[pos(t, slot)] in slot order
 //                 (the un-permute scatter of patches/0001:210-219 plus the
 //                 weighted sum of quant_method.py:257-277).
 #include "common.h"
 #include "kernels.h"
+#include "lut_core.h"
 
 using namespace lutmoe;
 
@@ -140,6 +142,147 @@ __global__ __launch_bounds__(256) void permute_kernel(const int32_t* __restrict_
     }
 }
 
+// Lanes of this wave holding the same id as this lane (ids < 2^nbits;
+// invalid lanes match nobody and get 0): one ballot per id bit.
+__device__ __forceinline__ uint64_t match_lanes(int id, bool ok, int nbits) {
+    uint64_t m = __ballot(ok);
+    for (int b = 0; b < nbits; ++b) {
+        const bool bit = (id >> b) & 1;
+        const uint64_t bal = __ballot(ok && bit);
+        m &= bit ? bal : ~bal;
+    }
+    return ok ? m : 0ull;
+}
+
+// The same permutation as permute_kernel, built from the top-k ids directly:
+// pair i = (token i / ke, slot i % ke) is routed expert topk_ids[t][s] for
+// s < k and shared expert E + s - k after that.  One CTA of 16 waves per
+// 1024 consecutive pairs, no global scratch and no waiting between CTAs.
+// Each CTA
+//   (a) histograms all P pairs and the pairs before its chunk: every wave
+//       loads 16 blocks of 64 ids before it uses any (one memory round trip
+//       for P <= 16K), groups equal ids with match_lanes, and the lowest lane
+//       of a group adds the group size (one LDS atomic per distinct id per 64),
+//   (b) wave w counts sub-chunk w (64 pairs) per expert and ranks each pair
+//       among the equal ids before it (stable),
+//   (c) offsets = exclusive scan of the totals; per expert, an exclusive scan
+//       over the 16 sub-chunks starting at offset + pairs before the chunk,
+//   (d) pos = that base + rank -> perm, inv; and writes its pairs' ids and
+//       weights (pair_ids / pair_w, when given) for the kernels that follow.
+// CTA 0 also writes offsets and the active-expert list.  Requires E_tot <= 512.
+constexpr int kPermChunk = 1024;
+constexpr int kPermSub = kPermChunk / 64;   // = waves per CTA
+constexpr int kPermLoads = 16;              // id blocks in flight per wave in (a)
+
+struct PairSrc {
+    const int32_t* topk_ids;   // [T][k]
+    const float* topk_w;       // [T][k] (nullable)
+    int T, k, ke, E;           // ke = k + S; shared expert s has id E + s
+};
+
+__device__ __forceinline__ int pair_expert(const PairSrc& ps, int i) {
+    const int t = i / ps.ke, s = i - t * ps.ke;
+    return s < ps.k ? ps.topk_ids[(int64_t)t * ps.k + s] : ps.E + (s - ps.k);
+}
+
+__global__ __launch_bounds__(1024) void permute_chunk_kernel(PairSrc ps, int P, int E_tot, int nbits,
+                                                             int32_t* __restrict__ offsets,
+                                                             int32_t* __restrict__ perm, int32_t* __restrict__ inv,
+                                                             int32_t* __restrict__ active,
+                                                             int32_t* __restrict__ pair_ids,
+                                                             float* __restrict__ pair_w) {
+    extern __shared__ int32_t sm[];   // h_all[E_tot] | h_bef[E_tot] | off[E_tot+1] | sub[kPermSub][E_tot]
+    int32_t* h_all = sm;
+    int32_t* h_bef = sm + E_tot;
+    int32_t* off = sm + 2 * E_tot;
+    int32_t* sub = sm + 3 * E_tot + 1;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int c0 = blockIdx.x * kPermChunk;
+    const uint64_t lt = (1ull << lane) - 1ull;
+    for (int i = tid; i < (3 + kPermSub) * E_tot + 1; i += blockDim.x) sm[i] = 0;
+    __syncthreads();
+    // (a) id blocks wv, wv + 16, ... of 64; block index * 64 is a multiple of
+    // 64 and c0 of 1024, so a block is wholly before the chunk or not
+    for (int b0 = wv; b0 * 64 < P; b0 += kPermSub * kPermLoads) {
+        int idv[kPermLoads];
+#pragma unroll
+        for (int u = 0; u < kPermLoads; ++u) {
+            const int i = (b0 + u * kPermSub) * 64 + lane;
+            idv[u] = i < P ? pair_expert(ps, i) : -1;
+        }
+#pragma unroll
+        for (int u = 0; u < kPermLoads; ++u) {
+            const int blk = b0 + u * kPermSub;
+            if (blk * 64 >= P) break;
+            const int id = idv[u];
+            const bool ok = id >= 0 && id < E_tot;
+            const uint64_t m = match_lanes(id, ok, nbits);
+            if (ok && (m & lt) == 0) {
+                atomicAdd(&h_all[id], __popcll(m));
+                if (blk * 64 < c0) atomicAdd(&h_bef[id], __popcll(m));
+            }
+        }
+    }
+    // (b) wave wv: sub-chunk wv
+    const int i = c0 + wv * 64 + lane;
+    const int id = i < P ? pair_expert(ps, i) : -1;
+    const bool ok = id >= 0 && id < E_tot;
+    const uint64_t m = match_lanes(id, ok, nbits);
+    const int rk = __popcll(m & lt);
+    if (ok && rk == 0) sub[wv * E_tot + id] = __popcll(m);
+    if (i < P) {
+        if (!ok) inv[i] = -1;                  // out-of-range id: the pair is dropped
+        if (pair_ids) {
+            const int t = i / ps.ke, s = i - t * ps.ke;
+            pair_ids[i] = id;
+            pair_w[i] = s < ps.k ? ps.topk_w[(int64_t)t * ps.k + s] : 1.0f;
+        }
+    }
+    __syncthreads();
+    // (c) offsets (wave 0: lane l owns experts [l*per, l*per+per)), active list
+    if (wv == 0) {
+        const int per = (E_tot + 63) / 64;
+        int c = 0, a = 0;
+        for (int q = 0; q < per; ++q) {
+            const int e = lane * per + q;
+            if (e < E_tot) { c += h_all[e]; a += h_all[e] > 0; }
+        }
+        int oc = wave_scan_incl(c) - c, oa = wave_scan_incl(a) - a;
+        for (int q = 0; q < per; ++q) {
+            const int e = lane * per + q;
+            if (e < E_tot) {
+                off[e] = oc;
+                if (blockIdx.x == 0) {
+                    offsets[e] = oc;
+                    if (h_all[e] > 0) active[1 + oa] = e;
+                }
+                oc += h_all[e];
+                oa += h_all[e] > 0;
+            }
+        }
+        if (lane == 63) {
+            off[E_tot] = oc;
+            if (blockIdx.x == 0) { offsets[E_tot] = oc; active[0] = oa; }
+        }
+    }
+    __syncthreads();
+    for (int e = tid; e < E_tot; e += blockDim.x) {
+        int run = off[e] + h_bef[e];
+        for (int sc = 0; sc < kPermSub; ++sc) {
+            const int v = sub[sc * E_tot + e];
+            sub[sc * E_tot + e] = run;
+            run += v;
+        }
+    }
+    __syncthreads();
+    // (d)
+    if (ok) {
+        const int pos = sub[wv * E_tot + id] + rk;
+        perm[pos] = i;
+        inv[i] = pos;
+    }
+}
+
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ y, const int32_t* __restrict__ inv,
                                                       int T, int ke, int H, void* __restrict__ out,
                                                       int out_dtype) {
@@ -184,9 +327,34 @@ int launch_build_pairs(const int32_t* topk_ids, const float* topk_w, int T, int 
 
 int launch_permute(const int32_t* pair_ids, int T, int k_eff, int E_tot, int32_t* offsets,
                    int32_t* perm, int32_t* inv, int32_t* active, hipStream_t s) {
-    const int P = T * k_eff;
+    // pairs = the given ids (k_eff per token, no shared slots)
+    return launch_route_pairs(pair_ids, nullptr, T, k_eff, E_tot, 0, offsets, perm, inv, active, nullptr,
+                              nullptr, s);
+}
+
+int launch_route_pairs(const int32_t* topk_ids, const float* topk_w, int T, int k, int E, int S,
+                       int32_t* offsets, int32_t* perm, int32_t* inv, int32_t* active, int32_t* pair_ids,
+                       float* pair_w, hipStream_t s) {
+    const int ke = k + S, E_tot = E + S;
+    const int P = T * ke;
+    if (E_tot <= 512) {
+        int nbits = 1;
+        while ((1 << nbits) < E_tot) ++nbits;
+        const int nchunk = P > 0 ? (P + kPermChunk - 1) / kPermChunk : 1;
+        const size_t lds = ((size_t)(3 + kPermSub) * E_tot + 1) * sizeof(int32_t);
+        const PairSrc ps{topk_ids, topk_w, T, k, ke, E};
+        hipLaunchKernelGGL(permute_chunk_kernel, dim3(nchunk), dim3(64 * kPermSub), lds, s, ps, P, E_tot, nbits,
+                           offsets, perm, inv, active, pair_ids, pair_w);
+        return check_launch();
+    }
+    int rc;
+    if (pair_ids) {
+        if ((rc = launch_build_pairs(topk_ids, topk_w, T, k, E, S, pair_ids, pair_w, s))) return rc;
+    } else if (S != 0) {
+        return LUTMOE_EINVAL;
+    }
     hipLaunchKernelGGL(permute_kernel, dim3(E_tot), dim3(256), E_tot * sizeof(int32_t), s,
-                       pair_ids, P, E_tot, offsets, perm, inv, active);
+                       pair_ids ? pair_ids : topk_ids, P, E_tot, offsets, perm, inv, active);
     return check_launch();
 }
 

@@ -276,7 +276,8 @@ def test_route_topk(gpu, T, E, k, renorm):
     np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=2e-6, atol=1e-7)
 
 
-@pytest.mark.parametrize("T,k,E", [(1, 4, 60), (32, 4, 60), (2048, 8, 66), (300, 2, 8)])
+@pytest.mark.parametrize("T,k,E", [(1, 4, 60), (32, 4, 60), (2048, 8, 66), (300, 2, 8), (1000, 3, 300),
+                                   (10, 2, 600)])
 def test_permute(gpu, T, k, E):
     import torch
     from block_lut_amd import ops
@@ -289,6 +290,25 @@ def test_permute(gpu, T, k, E):
     assert np.array_equal(inv, rinv)
     nz = np.nonzero(np.diff(roff))[0]
     assert act[0] == nz.size and np.array_equal(act[1:1 + nz.size], nz)
+
+
+def test_permute_drops_out_of_range(gpu):
+    """Pairs whose expert id is outside [0, E) get inv = -1 and no position; the others keep
+    the expert-major, pair-ascending order among themselves."""
+    import torch
+    from block_lut_amd import ops
+    rng = np.random.default_rng(77)
+    T, k, E = 700, 3, 10
+    ids = rng.integers(-2, E + 2, size=(T, k)).astype(np.int32)
+    off, perm, inv, act = [t.cpu().numpy() for t in ops.permute(torch.from_numpy(ids).to(gpu), E)]
+    flat = ids.reshape(-1)
+    valid = (flat >= 0) & (flat < E)
+    assert np.all(inv[~valid] == -1)
+    vi = np.nonzero(valid)[0]
+    order = vi[np.argsort(flat[vi], kind="stable")]
+    assert np.array_equal(perm[:order.size], order)
+    assert np.array_equal(inv[order], np.arange(order.size))
+    assert np.array_equal(off, np.concatenate([[0], np.cumsum(np.bincount(flat[vi], minlength=E))]))
 
 
 # --------------------------------------------------------------- MoE layer
