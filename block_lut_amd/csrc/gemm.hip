@@ -354,9 +354,10 @@ __device__ __forceinline__ void prefill_tile(const lutmoe_moe_desc& d, const uin
 //   codes  [256 rows] x 32 B             ( 8 KB; bytes 16h.. = columns 32h..32h+31)
 //   tables [256 rows] x 32 B             ( 8 KB; the rows' bf16[16] tables)
 // Each load instruction reads whole 128-byte lines (8 lanes per A row, 2 lanes
-// per 32-byte weight-row segment).  Every thread issues the same 12 loads per
-// stage, so `s_waitcnt vmcnt(12)` means "all but the newest stage have
-// landed".  Per step kb: k-substeps 0-2 run from slot kb%3; then a barrier
+// per 32-byte weight-row segment; NestedLUT rows take 8 lanes of 4 bytes).
+// Only the tile's NMT*32 activation rows are loaded.  Every thread issues the
+// same kDma loads per stage (NMT + 4 for BL4, NMT + 16 for NestedLUT), so
+// `s_waitcnt vmcnt(kDma)` means "all but the newest stage have landed".  Per step kb: k-substeps 0-2 run from slot kb%3; then a barrier
 // (stage kb+1 landed everywhere, slot kb%3 no longer read), the refill of slot
 // kb%3 with stage kb+3, and k-substep 3's MFMAs overlapped with reading and
 // looking up step kb+1's operands.
@@ -364,7 +365,6 @@ constexpr int kSlotA = kBM * kBK * 2;              // 32 KB
 constexpr int kSlotB = kBN * 32;                   // 8 KB
 constexpr int kSlotBytes = kSlotA + 2 * kSlotB;    // 48 KB
 constexpr int kStages = 3;
-constexpr int kDmaPerStage = 12;
 
 // A-row chunk swizzle: distinct for any 8 consecutive rows, and (r&1, swz)
 // distinct for any 16 consecutive rows.
@@ -385,18 +385,20 @@ __device__ __forceinline__ void dma16(uint32_t voff, const void* sbase, uint32_t
 // done, then barrier.  Memory clobber: no LDS access moves across it.
 template <int kAfter>
 __device__ __forceinline__ void ring_wait_barrier_n() {
-    if constexpr (kAfter == 24)
-        asm volatile("s_waitcnt vmcnt(24) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    else if constexpr (kAfter == 12)
-        asm volatile("s_waitcnt vmcnt(12) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    else
-        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    static_assert(kAfter >= 0 && kAfter <= 63, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(kAfter) : "memory");
 }
+// kDma = ring loads per stage per thread (A loads + weight loads)
+template <int kDma>
 __device__ __forceinline__ void ring_wait_barrier(int stages_after) {
-    static_assert(kDmaPerStage == 12, "vmcnt immediates above");
-    if (stages_after >= 2) ring_wait_barrier_n<24>();
-    else if (stages_after == 1) ring_wait_barrier_n<12>();
+    if (stages_after >= 2) ring_wait_barrier_n<2 * kDma>();
+    else if (stages_after == 1) ring_wait_barrier_n<kDma>();
     else ring_wait_barrier_n<0>();
+}
+
+// 4 bytes per lane from sbase + voff into LDS at m0 + 4 * lane.
+__device__ __forceinline__ void dma4(uint32_t voff, const void* sbase, uint32_t m0) {
+    asm volatile("global_load_lds_dword %0, %1" : : "v"(voff), "s"(sbase), "{m0}"(m0) : "memory");
 }
 
 template <typename T>
@@ -407,10 +409,13 @@ __device__ __forceinline__ const T* uniform_ptr(const T* p) {
     return (const T*)(((uint64_t)hi << 32) | lo);
 }
 
-template <bool kGateUp, int NMT>
-__device__ __forceinline__ void prefill_tile_bl4(const lutmoe_moe_desc& d, const uint16_t* __restrict__ src,
-                                                 const MoeRouting& rt, void* __restrict__ dst,
-                                                 const TileInfo ti, uint8_t* ring) {
+template <bool kGateUp, int kFmt, int NMT>
+__device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, const uint16_t* __restrict__ src,
+                                                  const MoeRouting& rt, void* __restrict__ dst,
+                                                  const TileInfo ti, uint8_t* ring) {
+    constexpr bool kNested = kFmt == LUTMOE_FMT_NESTED;
+    // A loads per thread per stage: only the tile's NMT*32 rows are loaded
+    constexpr int kDma = NMT + (kNested ? 16 : 4);
     const lutmoe_weights& w = d.w13;
     const lutmoe_weights& w2 = d.w2;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -421,50 +426,91 @@ __device__ __forceinline__ void prefill_tile_bl4(const lutmoe_moe_desc& d, const
     const int nvalid = min(kBM, ti.n - ti.m0);
 
     // ---- loader side (all offsets 32-bit, from scalar bases; the host
-    // checks the sizes).  A load j of wave w covers tile rows 64w+8j .. +7:
-    // lane l reads the (l%8 ^ swz)-th 16 bytes of row 64w+8j+l/8.  Rows past
-    // the tile's positions repeat its last position (never read back).
+    // checks the sizes).  The tile's first NMT*32 activation rows are
+    // loaded: load j of wave w covers rows 8*NMT*w + 8j .. +7, lane l reads
+    // the (l%8 ^ swz)-th 16 bytes of row 8*NMT*w + 8j + l/8.  Rows past the
+    // tile's positions repeat its last position (never read back).
     const int wvu = __builtin_amdgcn_readfirstlane(wv);
-    uint32_t a_off[8];
+    uint32_t a_off[NMT];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int r = 64 * wv + 8 * j + (lane >> 3);
+    for (int j = 0; j < NMT; ++j) {
+        const int r = 8 * NMT * wv + 8 * j + (lane >> 3);
         const int pos = ti.p0 + ti.m0 + min(r, nvalid - 1);
         const uint32_t row = kGateUp ? (uint32_t)(rt.perm[pos] / rt.k_eff) * (uint32_t)H : (uint32_t)pos * (uint32_t)I;
         a_off[j] = 2u * (row + 8u * (uint32_t)((lane & 7) ^ a_swz(r)));
     }
-    // codes / tables: load h of wave w covers tile rows 64w+32h .. +31, two
-    // lanes per row (16 B each), so a row's 32 bytes land contiguous in LDS
-    const lutmoe_weights& ww = kGateUp ? w : w2;
-    const int64_t per = (int64_t)ww.rows * (ww.cols / 2);
-    const uint8_t* c_base = uniform_ptr((const uint8_t*)ww.codes + ti.e * per);
-    const uint8_t* t_base = uniform_ptr((const uint8_t*)ww.tables + ti.e * per);
-    uint32_t w_off[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int tr = 64 * wv + 32 * h + (lane >> 1);
-        int trow;
+    // weight row of tile row tr (gate/up: rows 0..127 gate, 128..255 up)
+    auto tile_row = [&](int tr) __attribute__((always_inline)) {
         if (kGateUp) {
             const int i = min(n0 + (tr & 127), I - 1);
-            trow = tr < 128 ? i : I + i;
-        } else {
-            trow = min(n0 + tr, H - 1);
+            return tr < 128 ? i : I + i;
         }
-        w_off[h] = (uint32_t)trow * (uint32_t)(K / 2) + 16u * (uint32_t)(lane & 1);
-    }
+        return min(n0 + tr, H - 1);
+    };
+    const lutmoe_weights& ww = kGateUp ? w : w2;
     const uint8_t* a_base = (const uint8_t*)src;
+    // BL4 codes / tables: load h of wave w covers tile rows 64w+32h .. +31,
+    // two lanes per row (16 B each), so a row's 32 bytes land contiguous in
+    // LDS.  NestedLUT: load j of wave w covers tile rows 64w+8j .. +7, eight
+    // lanes (4 B each) per row: codes region = [p01 16 B | p2 8 B | p3 8 B],
+    // tables region = the tier's 2^b entries (repeated up to 32 B).  Lanes of
+    // a plane the tier does not have re-read p01 bytes (masked off when the
+    // codes are rebuilt).
+    const uint8_t* c_base;
+    const uint8_t* t_base;
+    uint32_t w_off[kNested ? 16 : 2];
+    uint32_t c_step = 32, t_step = 32;
+    int bits = 4;
+    if constexpr (kNested) {
+        c_base = uniform_ptr(((const uint8_t* const*)ww.codes)[ti.e]);
+        t_base = uniform_ptr((const uint8_t*)((const uint16_t* const*)ww.tables)[ti.e]);
+        bits = __builtin_amdgcn_readfirstlane((int)ww.tier_bits[ti.e]);
+        const uint32_t n = (uint32_t)ww.rows * (uint32_t)ww.cols;
+        const int q = lane & 7;
+        const bool has_p = q < 4 || (q < 6 ? bits >= 3 : bits >= 4);
+        c_step = has_p && q >= 4 ? 8u : 16u;
+        t_step = 2u << bits;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t fb = (uint32_t)tile_row(64 * wv + 8 * j + (lane >> 3)) * (uint32_t)K;
+            uint32_t co;
+            if (!has_p) co = fb / 4 + 4u * (uint32_t)(q & 3);
+            else if (q < 4) co = fb / 4 + 4u * (uint32_t)q;
+            else if (q < 6) co = n / 4 + fb / 8 + 4u * (uint32_t)(q - 4);
+            else co = n / 4 + n / 8 + fb / 8 + 4u * (uint32_t)(q - 6);
+            w_off[j] = co;
+            w_off[8 + j] = (fb / 64) * t_step + 4u * (uint32_t)(q & ((1 << (bits - 1)) - 1));
+        }
+    } else {
+        const int64_t per = (int64_t)ww.rows * (ww.cols / 2);
+        c_base = uniform_ptr((const uint8_t*)ww.codes + ti.e * per);
+        t_base = uniform_ptr((const uint8_t*)ww.tables + ti.e * per);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            w_off[h] = (uint32_t)tile_row(64 * wv + 32 * h + (lane >> 1)) * (uint32_t)(K / 2) +
+                       16u * (uint32_t)(lane & 1);
+    }
 
     auto issue = [&](int kb, const uint8_t* sl) __attribute__((always_inline)) {
         const uint32_t l0 = lds_addr(sl);
         const uint8_t* ab = a_base + kb * (kBK * 2);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) dma16(a_off[j], ab, l0 + (64 * wvu + 8 * j) * 128);
-        const uint8_t* cb = c_base + kb * 32;
-        const uint8_t* tbp = t_base + kb * 32;
+        for (int j = 0; j < NMT; ++j) dma16(a_off[j], ab, l0 + (8 * NMT * wvu + 8 * j) * 128);
+        if constexpr (kNested) {
+            const uint32_t cs = (uint32_t)kb * c_step, ts = (uint32_t)kb * t_step;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            dma16(w_off[h], cb, l0 + kSlotA + wvu * 2048 + h * 1024);
-            dma16(w_off[h], tbp, l0 + kSlotA + kSlotB + wvu * 2048 + h * 1024);
+            for (int j = 0; j < 8; ++j) {
+                dma4(w_off[j] + cs, c_base, l0 + kSlotA + (64 * wvu + 8 * j) * 32);
+                dma4(w_off[8 + j] + ts, t_base, l0 + kSlotA + kSlotB + (64 * wvu + 8 * j) * 32);
+            }
+        } else {
+            const uint8_t* cb = c_base + kb * 32;
+            const uint8_t* tbp = t_base + kb * 32;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                dma16(w_off[h], cb, l0 + kSlotA + wvu * 2048 + h * 1024);
+                dma16(w_off[h], tbp, l0 + kSlotA + kSlotB + wvu * 2048 + h * 1024);
+            }
         }
     };
 
@@ -473,10 +519,32 @@ __device__ __forceinline__ void prefill_tile_bl4(const lutmoe_moe_desc& d, const
     const int L0 = kGateUp ? 32 * wv + bn : 64 * wv + bn;
     const int L1 = kGateUp ? 128 + 32 * wv + bn : 64 * wv + 32 + bn;
 
+    // BL4: codes[nt] = the lane's 16 code bytes of row Lnt.  NestedLUT:
+    // codes[nt] = dword bh of p01 (as .x) and of p01's second half (.y), p2 and
+    // p3 bytes of this lane half (.z, .w): see nested_code below.
     auto read_codes = [&](const uint8_t* sl, u32x4_t (&codes)[2]) __attribute__((always_inline)) {
-        const uint8_t* cb = sl + kSlotA + bh * 16;
-        codes[0] = *reinterpret_cast<const u32x4_t*>(cb + L0 * 32);
-        codes[1] = *reinterpret_cast<const u32x4_t*>(cb + L1 * 32);
+        if constexpr (kNested) {
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                const uint8_t* rb = sl + kSlotA + (nt ? L1 : L0) * 32;
+                const uint2 f = *reinterpret_cast<const uint2*>(rb + 8 * bh);        // p01 bytes 8bh..
+                const uint32_t f2 = *reinterpret_cast<const uint32_t*>(rb + 16 + 4 * bh);
+                const uint32_t f3 = *reinterpret_cast<const uint32_t*>(rb + 24 + 4 * bh);
+                codes[nt] = u32x4_t{f.x, f.y, bits >= 3 ? f2 : 0u, bits >= 4 ? f3 : 0u};
+            }
+        } else {
+            const uint8_t* cb = sl + kSlotA + bh * 16;
+            codes[0] = *reinterpret_cast<const u32x4_t*>(cb + L0 * 32);
+            codes[1] = *reinterpret_cast<const u32x4_t*>(cb + L1 * 32);
+        }
+    };
+    // the 8 codes of k-substep ks (columns 32bh + 8ks .. +7 of the block) as
+    // BL4 nibbles
+    auto nested_code = [&](const u32x4_t& c, int ks) __attribute__((always_inline)) {
+        if constexpr (kNested)
+            return nested_nibbles8(c[ks >> 1] >> (16 * (ks & 1)), c[2] >> (8 * ks), c[3] >> (8 * ks));
+        else
+            return c[ks];
     };
     const int sw = a_swz(bn);   // = a_swz(mt * 32 + bn) for every m-tile
     auto frag_a = [&](const uint8_t* sl, int ks, bf16x8_t (&af)[NMT]) __attribute__((always_inline)) {
@@ -489,8 +557,8 @@ __device__ __forceinline__ void prefill_tile_bl4(const lutmoe_moe_desc& d, const
     auto frag_b = [&](const uint8_t* sl, const u32x4_t (&codes)[2], int ks, Lookup8 (&lk)[2])
         __attribute__((always_inline)) {
         const uint32_t tbase = lds_addr(sl + kSlotA + kSlotB);
-        lk[0] = lookup8_issue(codes[0][ks], tbase + L0 * 32);
-        lk[1] = lookup8_issue(codes[1][ks], tbase + L1 * 32);
+        lk[0] = lookup8_issue(nested_code(codes[0], ks), tbase + L0 * 32);
+        lk[1] = lookup8_issue(nested_code(codes[1], ks), tbase + L1 * 32);
     };
 
     f32x16_t acc[NMT][2];
@@ -504,7 +572,7 @@ __device__ __forceinline__ void prefill_tile_bl4(const lutmoe_moe_desc& d, const
     // prologue: stages 0..2 in flight; wait for stage 0
     const int npro = min(kStages, nkb);
     for (int st = 0; st < npro; ++st) issue(st, ring + st * kSlotBytes);
-    ring_wait_barrier(npro - 1);
+    ring_wait_barrier<kDma>(npro - 1);
     u32x4_t codes[2];
     bf16x8_t bf[2], af[NMT];
     read_codes(ring, codes);
@@ -534,7 +602,7 @@ __device__ __forceinline__ void prefill_tile_bl4(const lutmoe_moe_desc& d, const
                 // stage kb+1 landed everywhere (only stage kb+2 may still be
                 // in flight) and no wave reads this slot any more -> refill
                 // it with stage kb+3
-                ring_wait_barrier(kb + 2 < nkb ? 1 : 0);
+                ring_wait_barrier<kDma>(kb + 2 < nkb ? 1 : 0);
                 if (kb + 3 < nkb) issue(kb + 3, sl);
                 read_codes(nsl, codes_n);
                 frag_a(nsl, 0, af_n);
@@ -625,16 +693,16 @@ __device__ __forceinline__ void prefill_tile_bl4(const lutmoe_moe_desc& d, const
     }
 }
 
-template <bool kGateUp>
-__global__ __launch_bounds__(256, 1) void prefill_bl4_kernel(lutmoe_moe_desc d, const uint16_t* __restrict__ src,
-                                                             MoeRouting rt, void* __restrict__ dst) {
+template <bool kGateUp, int kFmt>
+__global__ __launch_bounds__(256, 1) void prefill_ring_kernel(lutmoe_moe_desc d, const uint16_t* __restrict__ src,
+                                                              MoeRouting rt, void* __restrict__ dst) {
     __shared__ __attribute__((aligned(16))) uint8_t ring[kStages * kSlotBytes];
     const TileInfo ti = find_tile(rt, blockIdx.y);
     if (ti.e < 0) return;
     const int nmt = (min(kBM, ti.n - ti.m0) + 31) / 32;
     switch (nmt) {
 #define LUTMOE_TILE_CASE(n) \
-    case n: prefill_tile_bl4<kGateUp, n>(d, src, rt, dst, ti, ring); break;
+    case n: prefill_tile_ring<kGateUp, kFmt, n>(d, src, rt, dst, ti, ring); break;
         LUTMOE_TILE_CASE(1) LUTMOE_TILE_CASE(2) LUTMOE_TILE_CASE(3) LUTMOE_TILE_CASE(4)
         LUTMOE_TILE_CASE(5) LUTMOE_TILE_CASE(6) LUTMOE_TILE_CASE(7) LUTMOE_TILE_CASE(8)
 #undef LUTMOE_TILE_CASE
@@ -671,41 +739,42 @@ inline int max_tiles(int P, int E_tot) { return (P + kBM - 1) / kBM + E_tot; }
 
 namespace lutmoe_host {
 
-// The BL4 kernel addresses activations and one expert's codes / tables with
-// 32-bit byte offsets from a scalar base.
-static bool bl4_offsets_fit(const lutmoe_moe_desc* d, const MoeRouting& r, int P) {
+// The ring kernels address activations and one expert's codes / tables (or
+// NestedLUT planes / tables) with 32-bit byte offsets from a scalar base.
+static bool ring_offsets_fit(const lutmoe_moe_desc* d, const MoeRouting& r, int P) {
     const int64_t lim = int64_t(1) << 32;
-    return (int64_t)r.T * d->hidden * 2 < lim && (int64_t)P * d->inter * 2 < lim &&
-           (int64_t)d->w13.rows * (d->w13.cols / 2) < lim && (int64_t)d->w2.rows * (d->w2.cols / 2) < lim;
+    if ((int64_t)r.T * d->hidden * 2 >= lim || (int64_t)P * d->inter * 2 >= lim) return false;
+    if (d->w13.format == LUTMOE_FMT_NESTED)
+        return (int64_t)d->w13.rows * d->w13.cols < lim && (int64_t)d->w2.rows * d->w2.cols < lim;
+    return (int64_t)d->w13.rows * (d->w13.cols / 2) < lim && (int64_t)d->w2.rows * (d->w2.cols / 2) < lim;
 }
 
 int launch_prefill_gate_up(const lutmoe_moe_desc* d, const uint16_t* x, const MoeRouting& r,
                            uint16_t* act, int P, hipStream_t s) {
-    if (d->w13.format == LUTMOE_FMT_BL4 && !bl4_offsets_fit(d, r, P)) return LUTMOE_EUNSUPPORTED;
-    if (d->w13.format == LUTMOE_FMT_NESTED && (int64_t)d->w13.rows * d->w13.cols >= (int64_t(1) << 32))
-        return LUTMOE_EUNSUPPORTED;
+    if (d->w13.format != LUTMOE_FMT_REF && !ring_offsets_fit(d, r, P)) return LUTMOE_EUNSUPPORTED;
     const dim3 grid((d->inter + kBN / 2 - 1) / (kBN / 2), max_tiles(P, r.num_experts_total));
     if (d->w13.format == LUTMOE_FMT_REF)
         hipLaunchKernelGGL((prefill_kernel<true, LUTMOE_FMT_REF>), grid, dim3(256), 0, s, *d, x, r, (void*)act);
     else if (d->w13.format == LUTMOE_FMT_NESTED)
-        hipLaunchKernelGGL((prefill_kernel<true, LUTMOE_FMT_NESTED>), grid, dim3(256), 0, s, *d, x, r, (void*)act);
+        hipLaunchKernelGGL((prefill_ring_kernel<true, LUTMOE_FMT_NESTED>), grid, dim3(256), 0, s, *d, x, r,
+                           (void*)act);
     else
-        hipLaunchKernelGGL((prefill_bl4_kernel<true>), grid, dim3(256), 0, s, *d, x, r, (void*)act);
+        hipLaunchKernelGGL((prefill_ring_kernel<true, LUTMOE_FMT_BL4>), grid, dim3(256), 0, s, *d, x, r, (void*)act);
     return check_launch();
 }
 
 int launch_prefill_down(const lutmoe_moe_desc* d, const uint16_t* act, const MoeRouting& r,
                         float* y_pos, int P, hipStream_t s) {
-    if (d->w2.format == LUTMOE_FMT_BL4 && !bl4_offsets_fit(d, r, P)) return LUTMOE_EUNSUPPORTED;
-    if (d->w2.format == LUTMOE_FMT_NESTED && (int64_t)d->w2.rows * d->w2.cols >= (int64_t(1) << 32))
-        return LUTMOE_EUNSUPPORTED;
+    if (d->w2.format != LUTMOE_FMT_REF && !ring_offsets_fit(d, r, P)) return LUTMOE_EUNSUPPORTED;
     const dim3 grid((d->hidden + kBN - 1) / kBN, max_tiles(P, r.num_experts_total));
     if (d->w2.format == LUTMOE_FMT_REF)
         hipLaunchKernelGGL((prefill_kernel<false, LUTMOE_FMT_REF>), grid, dim3(256), 0, s, *d, act, r, (void*)y_pos);
     else if (d->w2.format == LUTMOE_FMT_NESTED)
-        hipLaunchKernelGGL((prefill_kernel<false, LUTMOE_FMT_NESTED>), grid, dim3(256), 0, s, *d, act, r, (void*)y_pos);
+        hipLaunchKernelGGL((prefill_ring_kernel<false, LUTMOE_FMT_NESTED>), grid, dim3(256), 0, s, *d, act, r,
+                           (void*)y_pos);
     else
-        hipLaunchKernelGGL((prefill_bl4_kernel<false>), grid, dim3(256), 0, s, *d, act, r, (void*)y_pos);
+        hipLaunchKernelGGL((prefill_ring_kernel<false, LUTMOE_FMT_BL4>), grid, dim3(256), 0, s, *d, act, r,
+                           (void*)y_pos);
     return check_launch();
 }
 
