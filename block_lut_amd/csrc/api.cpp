@@ -330,7 +330,7 @@ int moe_forward_impl(const lutmoe_moe_desc* d, const void* x, const float* topk_
     if (gemv && decode_v2_supported(d, T, k)) {
         // routing + permutation happen inside both decode kernels
         return launch_decode_v2(d, (const uint16_t*)x, topk_w, topk_ids, logits, T, k, renorm,
-                                scaling, act, ws + L.route, ws + L.sync, out, out_dtype, stages, s);
+                                scaling, act, ws + L.route, ws + L.sync, (float*)(ws + L.y), out, out_dtype, stages, s);
     }
     int32_t* pair_ids = (int32_t*)(ws + L.pair_ids);
     float* pair_w = (float*)(ws + L.pair_w);

@@ -25,8 +25,6 @@
 // first, then the weights chunk by chunk, without branches) before any is
 // consumed, so a wave keeps up to 16 KB in flight and starts on chunk 0 while
 // the later chunks are still arriving.
-#include <utility>
-
 #include "common.h"
 #include "kernels.h"
 #include "lut_core.h"
@@ -76,39 +74,6 @@ struct DecodeArgs {
     RouteOut* route;           // global copy (precomputed-routing mode)
 };
 
-template <int Q>
-__device__ __forceinline__ int rdl(int v) { return __builtin_amdgcn_readlane(v, Q); }
-template <int Q>
-__device__ __forceinline__ float rdlf(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), Q));
-}
-
-// r += #{lanes q : (v_q > v) or (v_q == v and q < lane)} over the wave; the
-// other lanes' values are read back with readlane (no LDS).
-template <int Q>
-__device__ __forceinline__ void rank_step(float v, int lane, int& r) {
-    const float uq = rdlf<Q>(v);
-    r += (uq > v) || (uq == v && Q < lane);
-}
-template <int... Q>
-__device__ __forceinline__ void rank_all(float v, int lane, int& r, std::integer_sequence<int, Q...>) {
-    (rank_step<Q>(v, lane, r), ...);
-}
-
-// in-chunk stable rank of each lane's expert id, and whether it is the last
-// lane of that expert in the chunk.
-template <int Q>
-__device__ __forceinline__ void match_step(int e, int lane, int& before, int& after) {
-    const int u = rdl<Q>(e);
-    before += (Q < lane) & (u == e);
-    after += (Q > lane) & (u == e);
-}
-template <int... Q>
-__device__ __forceinline__ void match_all(int e, int lane, int& before, int& after,
-                                          std::integer_sequence<int, Q...>) {
-    (match_step<Q>(e, lane, before, after), ...);
-}
-
 // Routing + permutation of all T*(k+S) pairs into LDS; identical in every CTA
 // that runs it.  Cross-lane work is readlane/DPP only (no LDS round trips in
 // the rank loops).
@@ -147,16 +112,28 @@ __device__ void cta_route(const DecodeArgs& A, RouteOut& R, RouteScratch& X) {
             const float sum = wave_reduce(ps);
             float wsum = 0.f;
             if (E <= 64) {
-                // one logit per lane; ranks from readlane (no LDS round trips)
+                // one logit per lane; k rounds of a DPP max over int keys
+                // (ties -> lowest lane = lower expert id; NaN never selected)
                 const float v = lane < E ? src[lane] : -INFINITY;
-                int r = 0;
-                rank_all(v, lane, r, std::make_integer_sequence<int, 64>{});
-                const bool sel = lane < E && r < k;
-                const float pj = sel ? expf(v - mx) / sum : 0.f;
-                wsum = wave_reduce(pj);
-                if (sel) {
-                    X.pid[t * ke + r] = lane;
-                    R.pw[t * ke + r] = (A.renorm ? pj / wsum : pj) * A.scaling;
+                int key = lane < E ? float_key(v) : INT_MIN;
+                for (int j = 0; j < k; ++j) {
+                    const int m = wave_max_i32(key);
+                    const uint64_t b = __ballot(lane < E && key == m && m != INT_MIN);
+                    const int sel = b ? (int)__builtin_ctzll(b) : -1;
+                    const float vm = __builtin_bit_cast(
+                        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), sel < 0 ? 0 : sel));
+                    const float pj = sel < 0 ? 0.f : expf(vm - mx) / sum;
+                    wsum += pj;
+                    if (lane == 0) {
+                        X.pid[t * ke + j] = sel;
+                        R.pw[t * ke + j] = pj;
+                    }
+                    if (lane == sel) key = INT_MIN;
+                }
+                wave_lds_sync();
+                if (lane < k) {
+                    const float pj = R.pw[t * ke + lane];
+                    R.pw[t * ke + lane] = (A.renorm ? pj / wsum : pj) * A.scaling;
                 }
             } else {
                 float lsum = 0.f;
@@ -189,12 +166,16 @@ __device__ void cta_route(const DecodeArgs& A, RouteOut& R, RouteScratch& X) {
         }
     }
     __syncthreads();
-    // stable ranks inside 64-pair chunks + per-chunk expert counts
+    // stable ranks inside 64-pair chunks + per-chunk expert counts (equal ids
+    // grouped with one ballot per id bit)
+    int nbits = 1;
+    while ((1 << nbits) < E_tot) ++nbits;
+    const uint64_t lt = (1ull << lane) - 1ull;
     for (int c = wv; c < nchunk; c += (int)(blockDim.x >> 6)) {
         const int p = c * 64 + lane;
         const int e = p < P ? X.pid[p] : -1;
-        int before = 0, after = 0;
-        match_all(e, lane, before, after, std::make_integer_sequence<int, 64>{});
+        const uint64_t m = match_lanes(e, e >= 0, nbits);
+        const int before = __popcll(m & lt), after = __popcll(m & ~lt) - 1;
         if (p < P) X.rin[p] = before;
         if (e >= 0 && after == 0) X.ccnt[c][e] = before + 1;
     }
@@ -267,30 +248,6 @@ struct WaveRoute {
 __device__ __forceinline__ bool wave_route_fits(const DecodeArgs& A) {
     const int P = A.T * (A.k + A.d.num_shared);
     return P <= 64 && (A.topk_ids != nullptr || A.d.num_routed <= 64);
-}
-
-// Order-preserving int key of a float: larger float -> larger key, -0 and +0
-// equal (v + 0 turns -0 into +0), NaN -> INT_MIN (never selected, as a float
-// comparison never selects it).
-__device__ __forceinline__ int float_key(float v) {
-    const int b = __builtin_bit_cast(int, v + 0.0f);
-    return v != v ? INT_MIN : b ^ ((b >> 31) & 0x7fffffff);
-}
-
-template <int CTRL, int RMASK>
-__device__ __forceinline__ int dpp_max_i32(int v) {
-    return max(v, __builtin_amdgcn_update_dpp(INT_MIN, v, CTRL, RMASK, 0xf, false));
-}
-
-// Wave maximum of an int (every lane gets it).
-__device__ __forceinline__ int wave_max_i32(int v) {
-    v = dpp_max_i32<0xb1, 0xf>(v);    // quad_perm [1,0,3,2]
-    v = dpp_max_i32<0x4e, 0xf>(v);    // quad_perm [2,3,0,1]
-    v = dpp_max_i32<0x141, 0xf>(v);   // row_half_mirror
-    v = dpp_max_i32<0x140, 0xf>(v);   // row_mirror
-    v = dpp_max_i32<0x142, 0xa>(v);   // row_bcast:15
-    v = dpp_max_i32<0x143, 0xc>(v);   // row_bcast:31
-    return __builtin_amdgcn_readlane(v, 63);
 }
 
 // kWeights = false: expert ids and positions only (the gate/up CTAs that do
@@ -397,6 +354,21 @@ struct WaveRouteView {
 };
 
 struct LdsRouteView {
+    const RouteOut* R;
+    __device__ int nact() const { return R->nact; }
+    __device__ SlotRef slot(int a) const {
+        if (a >= R->nact) return {-1, 0, 0};
+        return {R->act[a], R->aoff[a], R->an[a]};
+    }
+    __device__ int pair_at(int p) const { return R->perm[p]; }
+    __device__ float weight_at(int p) const { return R->pw[R->perm[p]]; }
+    __device__ int pos_of(int q) const { return R->inv[q]; }
+};
+
+// The routing copy in global memory read in place: a wave reads only its
+// slot's expert / first position / count and its positions' pairs and
+// weights (wave-uniform indices), with no LDS copy and no CTA barrier.
+struct GlobalRouteView {
     const RouteOut* R;
     __device__ int nact() const { return R->nact; }
     __device__ SlotRef slot(int a) const {
@@ -729,9 +701,7 @@ template <int TB, bool kPre, int kFmt>
 __global__ __launch_bounds__(64 * kGuWaves, TB <= 2 ? 3 : 2) void bl4_decode_gate_up(DecodeArgs A) {
     __shared__ __attribute__((aligned(16))) uint8_t s_slot[kGuWaves * kSlot];
     if constexpr (kPre) {
-        __shared__ RouteOut R;
-        load_route(A, R);
-        gate_up_body<TB, kFmt>(A, LdsRouteView{&R}, s_slot);
+        gate_up_body<TB, kFmt>(A, GlobalRouteView{A.route}, s_slot);
     } else if (blockIdx.x == 0 && blockIdx.y == 0) {
         // this CTA also publishes the routing (with the pair weights) for the
         // down kernel
@@ -810,6 +780,50 @@ __global__ __launch_bounds__(256, TB <= 2 ? 3 : 2) void bl4_decode_down(DecodeAr
         down_body<TB, kFmt>(A, LdsRouteView{&R}, s_slot, s_y);
     } else {
         down_body<TB, kFmt>(A, WaveRouteView{wave_pairs<true>(A)}, s_slot, s_y);
+    }
+}
+
+// Down projection when many experts are active (more than 8 slots would be
+// walked one after another by the 4 waves of bl4_decode_down): CTA (x, g)
+// covers output rows 8x..8x+7 of active slots 4g..4g+3, one slot per wave;
+// each position's result times its pair weight goes to y[pos][h] (fp32) and
+// combine_kernel sums each token's slots in slot order.
+template <int TB, int kFmt>
+__global__ __launch_bounds__(256, TB <= 2 ? 3 : 2) void bl4_decode_down_y(DecodeArgs A, float* __restrict__ y) {
+    __shared__ __attribute__((aligned(16))) uint8_t s_slot[4 * kSlot];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int a = blockIdx.y * 4 + wv;
+    const GlobalRouteView rv{A.route};
+    const SlotRef sl = rv.slot(a);
+    if (sl.e < 0) return;
+    const int I = A.d.inter, H = A.d.hidden;
+    const int h0 = blockIdx.x * kRows;
+    int rows[kRows];
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) rows[r] = min(h0 + r, H - 1);
+    uint8_t* slot = s_slot + wv * kSlot;
+    for (int tb = 0; tb < sl.n; tb += TB) {
+        const int nt = min(TB, sl.n - tb);
+        const uint16_t* xrow[TB];
+#pragma unroll
+        for (int t = 0; t < TB; ++t) xrow[t] = A.act + (int64_t)(sl.p0 + tb + min(t, nt - 1)) * I;
+        float acc[kRows][TB];
+#pragma unroll
+        for (int r = 0; r < kRows; ++r)
+#pragma unroll
+            for (int t = 0; t < TB; ++t) acc[r][t] = 0.f;
+        expert_rows8<kFmt, TB>(A.d.w2, sl.e, rows, I, lane, slot, xrow, nt, acc);
+#pragma unroll
+        for (int t = 0; t < TB; ++t) {
+            const int p = sl.p0 + tb + min(t, nt - 1);
+            const float pw = rv.weight_at(p);
+            float v[kRows];
+#pragma unroll
+            for (int r = 0; r < kRows; ++r) v[r] = acc[r][t];
+            const float yv = wave_reduce8(v);   // lane l: row l >> 3
+            const int r = lane >> 3;
+            if ((lane & 7) == 0 && t < nt && h0 + r < H) y[(int64_t)p * H + h0 + r] = yv * pw;
+        }
     }
 }
 
@@ -1090,7 +1104,7 @@ size_t decode_sync_bytes() { return sizeof(DecodeSync); }
 
 int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* topk_w,
                      const int32_t* topk_ids, const float* logits, int T, int k, int renorm,
-                     float scaling, uint16_t* act, void* route_ws, void* sync_ws, void* out,
+                     float scaling, uint16_t* act, void* route_ws, void* sync_ws, float* y_ws, void* out,
                      int out_dtype, int stages, hipStream_t s) {
     DecodeArgs A;
     A.d = *d;
@@ -1156,6 +1170,23 @@ int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* t
         const size_t lds = (size_t)P * kRows * sizeof(float);
         // the routing comes from the copy in the workspace (written by the
         // gate/up kernel's first CTA, or by decode_route_kernel)
+        if (max_active > 8) {
+            // many experts: y + combine, every slot in parallel
+            const dim3 gy((d->hidden + kRows - 1) / kRows, (max_active + 3) / 4);
+            const int tb = tb_for(T);
+            if (nested) {
+                if (tb == 1) hipLaunchKernelGGL((bl4_decode_down_y<1, LUTMOE_FMT_NESTED>), gy, dim3(256), 0, s, A, y_ws);
+                else if (tb == 2) hipLaunchKernelGGL((bl4_decode_down_y<2, LUTMOE_FMT_NESTED>), gy, dim3(256), 0, s, A, y_ws);
+                else hipLaunchKernelGGL((bl4_decode_down_y<4, LUTMOE_FMT_NESTED>), gy, dim3(256), 0, s, A, y_ws);
+            } else {
+                if (tb == 1) hipLaunchKernelGGL((bl4_decode_down_y<1, LUTMOE_FMT_BL4>), gy, dim3(256), 0, s, A, y_ws);
+                else if (tb == 2) hipLaunchKernelGGL((bl4_decode_down_y<2, LUTMOE_FMT_BL4>), gy, dim3(256), 0, s, A, y_ws);
+                else hipLaunchKernelGGL((bl4_decode_down_y<4, LUTMOE_FMT_BL4>), gy, dim3(256), 0, s, A, y_ws);
+            }
+            if ((rc = check_launch())) return rc;
+            const int32_t* inv = ((const RouteOut*)route_ws)->inv;
+            return launch_combine(y_ws, inv, T, k + d->num_shared, d->hidden, out, out_dtype, s);
+        }
         LUTMOE_DECODE_LAUNCH(bl4_decode_down, true, grid, dim3(256), lds)
         return check_launch();
     }

@@ -57,7 +57,7 @@ size_t decode_sync_bytes();
 // launch, otherwise the per-stage kernels run.
 int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* topk_w,
                      const int32_t* topk_ids, const float* logits, int T, int k, int renorm,
-                     float scaling, uint16_t* act, void* route_ws, void* sync_ws, void* out,
+                     float scaling, uint16_t* act, void* route_ws, void* sync_ws, float* y_ws, void* out,
                      int out_dtype, int stages, hipStream_t s);
 
 // route.hip

@@ -274,6 +274,42 @@ __device__ __forceinline__ float from_upper_half(float v) {
     return __uint_as_float(s1);
 }
 
+// Lanes of this wave holding the same id as this lane (ids < 2^nbits;
+// invalid lanes match nobody and get 0): one ballot per id bit.
+__device__ __forceinline__ uint64_t match_lanes(int id, bool ok, int nbits) {
+    uint64_t m = __ballot(ok);
+    for (int b = 0; b < nbits; ++b) {
+        const bool bit = (id >> b) & 1;
+        const uint64_t bal = __ballot(ok && bit);
+        m &= bit ? bal : ~bal;
+    }
+    return ok ? m : 0ull;
+}
+
+// Order-preserving int key of a float: larger float -> larger key, -0 and +0
+// equal (v + 0 turns -0 into +0), NaN -> INT_MIN (never selected, as a float
+// comparison never selects it).
+__device__ __forceinline__ int float_key(float v) {
+    const int b = __builtin_bit_cast(int, v + 0.0f);
+    return v != v ? INT_MIN : b ^ ((b >> 31) & 0x7fffffff);
+}
+
+template <int CTRL, int RMASK>
+__device__ __forceinline__ int dpp_max_i32(int v) {
+    return max(v, __builtin_amdgcn_update_dpp(INT_MIN, v, CTRL, RMASK, 0xf, false));
+}
+
+// Wave maximum of an int (every lane gets it).
+__device__ __forceinline__ int wave_max_i32(int v) {
+    v = dpp_max_i32<0xb1, 0xf>(v);    // quad_perm [1,0,3,2]
+    v = dpp_max_i32<0x4e, 0xf>(v);    // quad_perm [2,3,0,1]
+    v = dpp_max_i32<0x141, 0xf>(v);   // row_half_mirror
+    v = dpp_max_i32<0x140, 0xf>(v);   // row_mirror
+    v = dpp_max_i32<0x142, 0xa>(v);   // row_bcast:15
+    v = dpp_max_i32<0x143, 0xc>(v);   // row_bcast:31
+    return __builtin_amdgcn_readlane(v, 63);
+}
+
 // Inclusive prefix sum over the 64 lanes (row shifts within 16-lane rows,
 // then row broadcasts across rows).
 __device__ __forceinline__ int wave_scan_incl(int v) {

@@ -142,18 +142,6 @@ __global__ __launch_bounds__(256) void permute_kernel(const int32_t* __restrict_
     }
 }
 
-// Lanes of this wave holding the same id as this lane (ids < 2^nbits;
-// invalid lanes match nobody and get 0): one ballot per id bit.
-__device__ __forceinline__ uint64_t match_lanes(int id, bool ok, int nbits) {
-    uint64_t m = __ballot(ok);
-    for (int b = 0; b < nbits; ++b) {
-        const bool bit = (id >> b) & 1;
-        const uint64_t bal = __ballot(ok && bit);
-        m &= bit ? bal : ~bal;
-    }
-    return ok ? m : 0ull;
-}
-
 // The same permutation as permute_kernel, built from the top-k ids directly:
 // pair i = (token i / ke, slot i % ke) is routed expert topk_ids[t][s] for
 // s < k and shared expert E + s - k after that.  One CTA of 16 waves per
