@@ -470,7 +470,8 @@ __device__ __forceinline__ void put_route(const DecodeArgs& A, const RouteOut& R
     if (threadIdx.x == 0) g->nact = R.nact;
 }
 
-__global__ __launch_bounds__(256) void decode_route_kernel(DecodeArgs A) {
+// One CTA of 16 waves (one token per wave in the top-k loop for T <= 16).
+__global__ __launch_bounds__(1024) void decode_route_kernel(DecodeArgs A) {
     __shared__ RouteOut R;
     __shared__ RouteScratch X;
     cta_route(A, R, X);
@@ -1128,7 +1129,7 @@ int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* t
     const bool pre = T > 2 || !(P <= 64 && (topk_ids != nullptr || d->num_routed <= 64));
     int rc;
     if (pre && (stages & LUTMOE_STAGE_ROUTE)) {
-        hipLaunchKernelGGL(decode_route_kernel, dim3(1), dim3(256), 0, s, A);
+        hipLaunchKernelGGL(decode_route_kernel, dim3(1), dim3(1024), 0, s, A);
         if ((rc = check_launch())) return rc;
     }
     const bool nested = d->w13.format == LUTMOE_FMT_NESTED;
