@@ -635,13 +635,81 @@ __device__ __forceinline__ void nested_rows8(const NestedView& v, const int (&ro
     }
 }
 
-// Rows of expert e of a stack in either decode format.
+// ---- REF experts (the reference's uint8 codes, bf16 absmax per block_size
+// flat elements, one bf16[256] codebook).  The lane's 32 columns
+// [2048cc + 32l, +32) of 8 rows: 32 code bytes and the absmax of their block
+// (block_size % 32 == 0, so 32 aligned columns share one block; block
+// indices are clamped to the last entry as the reference's dequant does).
+// Per row the lane sums x * cb over its 32 columns and scales the sum by the
+// absmax: the reference GEMV's fp32 (x * cb) * absmax, factored per 32
+// columns.  The codebook sits in the first 512 bytes of the wave's LDS slot.
+struct Rows8R {
+    u32x4_t cw[kRows][2];
+    uint32_t am[kRows];
+};
+
+__device__ __forceinline__ void load_rows8r(const uint8_t* __restrict__ codes, const uint16_t* __restrict__ am,
+                                            int64_t nb, int bs, const int (&rows)[kRows], int K, int cc, int lane,
+                                            Rows8R& b) {
+    const bool ok = cc * kWChunk + 32 * lane < K;
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+        const int64_t off = (int64_t)rows[r] * K + (ok ? cc * kWChunk + 32 * lane : 0);
+        b.cw[r][0] = *reinterpret_cast<const u32x4_t*>(codes + off);
+        b.cw[r][1] = *reinterpret_cast<const u32x4_t*>(codes + off + 16);
+        int64_t blk = off / bs;
+        blk = blk < nb ? blk : nb - 1;
+        b.am[r] = am[blk];
+    }
+}
+
+template <int TB>
+__device__ __forceinline__ void ref_rows8(const lutmoe_weights& w, int e, const int (&rows)[kRows], int K, int lane,
+                                          uint8_t* slot, const uint16_t* const (&xrow)[TB], int nt,
+                                          float (&acc)[kRows][TB]) {
+    const uint8_t* codes = (const uint8_t*)w.codes + (int64_t)e * w.rows * w.cols;
+    const uint16_t* am = (const uint16_t*)w.tables + (int64_t)e * w.absmax_per_expert;
+    const int64_t nb = w.absmax_per_expert;
+    const int bs = w.block_size;
+    // codebook -> the slot (8 bytes per lane), issued with the first chunk's loads
+    const uint2 cbv = reinterpret_cast<const uint2*>(w.codebook)[lane];
+    const uint32_t cbase = lds_addr(slot);
+    const int nch = (K + kWChunk - 1) / kWChunk;
+    for (int cc = 0; cc < nch; ++cc) {
+        Rows8R b;
+        uint32_t xs[TB][16];
+        load_x8<TB>(xrow, K, cc, lane, nt, xs);
+        __builtin_amdgcn_sched_barrier(0);
+        load_rows8r(codes, am, nb, bs, rows, K, cc, lane, b);
+        __builtin_amdgcn_sched_barrier(0);
+        if (cc == 0) {
+            *reinterpret_cast<uint2*>(slot + 8 * lane) = cbv;
+            wave_lds_sync();
+        }
+        const bool ok = cc * kWChunk + 32 * lane < K;
+#pragma unroll
+        for (int r = 0; r < kRows; ++r) {
+            float g[TB];
+#pragma unroll
+            for (int t = 0; t < TB; ++t) g[t] = 0.f;
+            ref_dot32<TB>(b.cw[r], cbase, xs, nt, g);
+            const float a = ok ? bf16_to_f32(b.am[r]) : 0.f;   // lanes past K contribute nothing
+#pragma unroll
+            for (int t = 0; t < TB; ++t) acc[r][t] = fmaf(a, g[t], acc[r][t]);
+        }
+    }
+    wave_lds_sync();
+}
+
+// Rows of expert e of a stack in any decode format.
 template <int kFmt, int TB>
 __device__ __forceinline__ void expert_rows8(const lutmoe_weights& w, int e, const int (&rows)[kRows], int K,
                                              int lane, uint8_t* slot, const uint16_t* const (&xrow)[TB], int nt,
                                              float (&acc)[kRows][TB]) {
     if constexpr (kFmt == LUTMOE_FMT_NESTED) {
         nested_rows8<TB>(nested_view(w, e), rows, K, lane, slot, xrow, nt, acc);
+    } else if constexpr (kFmt == LUTMOE_FMT_REF) {
+        ref_rows8<TB>(w, e, rows, K, lane, slot, xrow, nt, acc);
     } else {
         const int64_t per = (int64_t)w.rows * (K / 2);
         bl4_rows8<TB>((const uint8_t*)w.codes + e * per, (const uint8_t*)w.tables + e * per, rows, K, lane, slot,
@@ -1083,8 +1151,10 @@ bool decode_v2_supported(const lutmoe_moe_desc* d, int T, int k) {
         ((int64_t)d->w13.rows * d->w13.cols >= (int64_t(1) << 32) ||
          (int64_t)d->w2.rows * d->w2.cols >= (int64_t(1) << 32)))
         return false;
-    return (d->w13.format == LUTMOE_FMT_BL4 || d->w13.format == LUTMOE_FMT_NESTED) && E_tot <= kMaxEtot &&
-           P <= kMaxP;
+    if (d->w13.format == LUTMOE_FMT_REF &&
+        (d->w13.block_size <= 0 || d->w13.block_size % 32 || d->w2.block_size <= 0 || d->w2.block_size % 32))
+        return false;
+    return E_tot <= kMaxEtot && P <= kMaxP;
 }
 
 int launch_nested_gemv(const lutmoe_weights* w, int expert, const uint16_t* x, int T, void* y, int y_dtype,
@@ -1133,7 +1203,8 @@ int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* t
         if ((rc = check_launch())) return rc;
     }
     const bool nested = d->w13.format == LUTMOE_FMT_NESTED;
-    if (kFusedDecodeEnabled && !nested && stages == LUTMOE_STAGE_ALL && sync_ws) {
+    const int fmt_idx = nested ? 1 : d->w13.format == LUTMOE_FMT_REF ? 2 : 0;
+    if (kFusedDecodeEnabled && fmt_idx == 0 && stages == LUTMOE_STAGE_ALL && sync_ws) {
         // one persistent launch: enough CTAs for one item each
         const int items = max_active * ((d->inter + 15) / 16) + (d->hidden + kRows - 1) / kRows;
         const size_t lds = (size_t)P * kRows * sizeof(float);
@@ -1147,19 +1218,18 @@ int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* t
     }
 #define LUTMOE_DECODE_CASE(N, TB, PRE, FMT, KERNEL, GRID, BLOCK, LDS) \
     case N: hipLaunchKernelGGL((KERNEL<TB, PRE, FMT>), GRID, BLOCK, LDS, s, A); break;
-#define LUTMOE_DECODE_LAUNCH(KERNEL, PRE, GRID, BLOCK, LDS)                                \
-    switch (tb_for(T) * 4 + ((PRE) ? 2 : 0) + (nested ? 1 : 0)) {                          \
-        LUTMOE_DECODE_CASE(4, 1, false, LUTMOE_FMT_BL4, KERNEL, GRID, BLOCK, LDS)          \
-        LUTMOE_DECODE_CASE(5, 1, false, LUTMOE_FMT_NESTED, KERNEL, GRID, BLOCK, LDS)       \
-        LUTMOE_DECODE_CASE(6, 1, true, LUTMOE_FMT_BL4, KERNEL, GRID, BLOCK, LDS)           \
-        LUTMOE_DECODE_CASE(7, 1, true, LUTMOE_FMT_NESTED, KERNEL, GRID, BLOCK, LDS)        \
-        LUTMOE_DECODE_CASE(8, 2, false, LUTMOE_FMT_BL4, KERNEL, GRID, BLOCK, LDS)          \
-        LUTMOE_DECODE_CASE(9, 2, false, LUTMOE_FMT_NESTED, KERNEL, GRID, BLOCK, LDS)       \
-        LUTMOE_DECODE_CASE(10, 2, true, LUTMOE_FMT_BL4, KERNEL, GRID, BLOCK, LDS)          \
-        LUTMOE_DECODE_CASE(11, 2, true, LUTMOE_FMT_NESTED, KERNEL, GRID, BLOCK, LDS)       \
-        LUTMOE_DECODE_CASE(18, 4, true, LUTMOE_FMT_BL4, KERNEL, GRID, BLOCK, LDS)          \
-        LUTMOE_DECODE_CASE(19, 4, true, LUTMOE_FMT_NESTED, KERNEL, GRID, BLOCK, LDS)       \
-        default: return LUTMOE_EINVAL;                                                      \
+#define LUTMOE_DECODE_FMTS(N, TB, PRE, KERNEL, GRID, BLOCK, LDS)                    \
+    LUTMOE_DECODE_CASE(N, TB, PRE, LUTMOE_FMT_BL4, KERNEL, GRID, BLOCK, LDS)        \
+    LUTMOE_DECODE_CASE(N + 1, TB, PRE, LUTMOE_FMT_NESTED, KERNEL, GRID, BLOCK, LDS) \
+    LUTMOE_DECODE_CASE(N + 2, TB, PRE, LUTMOE_FMT_REF, KERNEL, GRID, BLOCK, LDS)
+#define LUTMOE_DECODE_LAUNCH(KERNEL, PRE, GRID, BLOCK, LDS)                 \
+    switch (tb_for(T) * 8 + ((PRE) ? 4 : 0) + fmt_idx) {                    \
+        LUTMOE_DECODE_FMTS(8, 1, false, KERNEL, GRID, BLOCK, LDS)           \
+        LUTMOE_DECODE_FMTS(12, 1, true, KERNEL, GRID, BLOCK, LDS)           \
+        LUTMOE_DECODE_FMTS(16, 2, false, KERNEL, GRID, BLOCK, LDS)          \
+        LUTMOE_DECODE_FMTS(20, 2, true, KERNEL, GRID, BLOCK, LDS)           \
+        LUTMOE_DECODE_FMTS(36, 4, true, KERNEL, GRID, BLOCK, LDS)           \
+        default: return LUTMOE_EINVAL;                                      \
     }
     if (stages & LUTMOE_STAGE_GATE_UP) {
         const dim3 grid((d->inter + 4 * kGuWaves - 1) / (4 * kGuWaves), max_active);
@@ -1174,16 +1244,20 @@ int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* t
         if (max_active > 8) {
             // many experts: y + combine, every slot in parallel
             const dim3 gy((d->hidden + kRows - 1) / kRows, (max_active + 3) / 4);
-            const int tb = tb_for(T);
-            if (nested) {
-                if (tb == 1) hipLaunchKernelGGL((bl4_decode_down_y<1, LUTMOE_FMT_NESTED>), gy, dim3(256), 0, s, A, y_ws);
-                else if (tb == 2) hipLaunchKernelGGL((bl4_decode_down_y<2, LUTMOE_FMT_NESTED>), gy, dim3(256), 0, s, A, y_ws);
-                else hipLaunchKernelGGL((bl4_decode_down_y<4, LUTMOE_FMT_NESTED>), gy, dim3(256), 0, s, A, y_ws);
-            } else {
-                if (tb == 1) hipLaunchKernelGGL((bl4_decode_down_y<1, LUTMOE_FMT_BL4>), gy, dim3(256), 0, s, A, y_ws);
-                else if (tb == 2) hipLaunchKernelGGL((bl4_decode_down_y<2, LUTMOE_FMT_BL4>), gy, dim3(256), 0, s, A, y_ws);
-                else hipLaunchKernelGGL((bl4_decode_down_y<4, LUTMOE_FMT_BL4>), gy, dim3(256), 0, s, A, y_ws);
+#define LUTMOE_DOWN_Y(TB, FMT) hipLaunchKernelGGL((bl4_decode_down_y<TB, FMT>), gy, dim3(256), 0, s, A, y_ws)
+            switch (tb_for(T) * 4 + fmt_idx) {
+                case 4: LUTMOE_DOWN_Y(1, LUTMOE_FMT_BL4); break;
+                case 5: LUTMOE_DOWN_Y(1, LUTMOE_FMT_NESTED); break;
+                case 6: LUTMOE_DOWN_Y(1, LUTMOE_FMT_REF); break;
+                case 8: LUTMOE_DOWN_Y(2, LUTMOE_FMT_BL4); break;
+                case 9: LUTMOE_DOWN_Y(2, LUTMOE_FMT_NESTED); break;
+                case 10: LUTMOE_DOWN_Y(2, LUTMOE_FMT_REF); break;
+                case 16: LUTMOE_DOWN_Y(4, LUTMOE_FMT_BL4); break;
+                case 17: LUTMOE_DOWN_Y(4, LUTMOE_FMT_NESTED); break;
+                case 18: LUTMOE_DOWN_Y(4, LUTMOE_FMT_REF); break;
+                default: return LUTMOE_EINVAL;
             }
+#undef LUTMOE_DOWN_Y
             if ((rc = check_launch())) return rc;
             const int32_t* inv = ((const RouteOut*)route_ws)->inv;
             return launch_combine(y_ws, inv, T, k + d->num_shared, d->hidden, out, out_dtype, s);
@@ -1192,6 +1266,7 @@ int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* t
         return check_launch();
     }
 #undef LUTMOE_DECODE_CASE
+#undef LUTMOE_DECODE_FMTS
 #undef LUTMOE_DECODE_LAUNCH
     return LUTMOE_OK;
 }

@@ -24,6 +24,19 @@ __device__ __forceinline__ uint32_t add_byte(uint32_t base, uint32_t w) {
     return r;
 }
 
+// base + 16-bit field j of w (SDWA word select on src1).
+template <int J>
+__device__ __forceinline__ uint32_t add_word(uint32_t base, uint32_t w) {
+    uint32_t r;
+    if constexpr (J == 0)
+        asm("v_add_u32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:WORD_0"
+            : "=v"(r) : "v"(base), "v"(w));
+    else
+        asm("v_add_u32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:WORD_1"
+            : "=v"(r) : "v"(base), "v"(w));
+    return r;
+}
+
 typedef __attribute__((address_space(3))) const uint16_t lds_u16_t;
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
@@ -31,6 +44,30 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 }
 
 __device__ __forceinline__ uint32_t lds_ld16(uint32_t a) { return *(lds_u16_t*)a; }
+
+// 32 REF byte codes (8 dwords, code j of the lane's 32 columns in byte j%4 of
+// dword j/4) against the bf16[256] codebook at LDS byte address `cbase`:
+// g[t] += sum_j x_t[j] * cb[code j], products exact in fp32 (bf16 x bf16),
+// two per v_dot2_f32_bf16.  x dword i holds columns 2i, 2i+1.
+template <int TB>
+__device__ __forceinline__ void ref_dot32(const u32x4_t (&cw)[2], uint32_t cbase, const uint32_t (&x)[TB][16],
+                                          int nt, float (&g)[TB]) {
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+        const uint32_t w = cw[d >> 2][d & 3];
+        const uint32_t we = (w & 0x00ff00ffu) << 1;   // 2*code of columns 4d, 4d+2 (16-bit fields)
+        const uint32_t wo = (w >> 7) & 0x01fe01feu;   // 2*code of columns 4d+1, 4d+3
+        const uint32_t p0 = lds_ld16(add_word<0>(cbase, we)) | (lds_ld16(add_word<0>(cbase, wo)) << 16);
+        const uint32_t p1 = lds_ld16(add_word<1>(cbase, we)) | (lds_ld16(add_word<1>(cbase, wo)) << 16);
+#pragma unroll
+        for (int t = 0; t < TB; ++t) {
+            if (t < nt) {
+                g[t] = dot2_bf16(p0, x[t][2 * d], g[t]);
+                g[t] = dot2_bf16(p1, x[t][2 * d + 1], g[t]);
+            }
+        }
+    }
+}
 
 // One BL4 code dword (8 nibbles = 8 consecutive weights of one row) against
 // its block's bf16 table at LDS byte address `tab`:

@@ -322,7 +322,8 @@ def _moe_case(fmt, E, S, H, I, seed):
 
 @pytest.mark.parametrize("fmt,T,path", [("bl4", 1, 1), ("bl4", 4, 1), ("bl4", 9, 1),
                                         ("bl4", 200, 2), ("bl4", 5, 2),
-                                        ("ref", 1, 1), ("ref", 3, 1), ("ref", 150, 2)])
+                                        ("ref", 1, 1), ("ref", 2, 1), ("ref", 3, 1), ("ref", 9, 1),
+                                        ("ref", 150, 2)])
 def test_moe_layer(gpu, fmt, T, path):
     import torch
     from block_lut_amd import ops
@@ -341,6 +342,28 @@ def test_moe_layer(gpu, fmt, T, path):
     # bf16 table entries on both paths.
     f13, f2 = (w13.gemv_f32, w2.gemv_f32) if (fmt == "ref" and path == 1) else (w13.deq_f32, w2.deq_f32)
     ref = O.moe_layer(xb, rids, rw, f13, f2, shared=[(f13(E + s), f2(E + s)) for s in range(S)])
+    assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
+
+
+@pytest.mark.parametrize("block_size,T", [(64, 1), (64, 9), (256, 1), (256, 9)])
+def test_moe_layer_ref_block_sizes(gpu, block_size, T):
+    """REF decode with absmax blocks of 64 and 256 (a lane's 32 aligned columns share one
+    block), following the reference GEMV's (x * cb) * absmax products; T=9 runs the down
+    projection of every active expert in parallel (y + combine)."""
+    import torch
+    from block_lut_amd import ops
+    from block_lut_amd.formats import MoEWeights
+    E, S, k, H, I = 8, 1, 2, 256, 192
+    w13 = RefExpertset(E + S, 2 * I, H, seed=30 + block_size, block_size=block_size)
+    w2 = RefExpertset(E + S, H, I, seed=31 + block_size, block_size=block_size)
+    moe = MoEWeights(w13.stack(gpu), w2.stack(gpu), H, I, E, S)
+    rng = np.random.default_rng(block_size + T)
+    xb = _x(rng, T, H)
+    rw, rids = O.route(rng.standard_normal((T, E)).astype(np.float32), k)
+    out = ops.moe_forward(moe, to_dev_bf16(xb, gpu), torch.from_numpy(rw).to(gpu),
+                          torch.from_numpy(rids).to(gpu), out_dtype=torch.float32, path=1)
+    ref = O.moe_layer(xb, rids, rw, w13.gemv_f32, w2.gemv_f32,
+                      shared=[(w13.gemv_f32(E + s), w2.gemv_f32(E + s)) for s in range(S)])
     assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
 
 
