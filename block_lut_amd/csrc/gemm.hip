@@ -569,21 +569,23 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[mt][nt][i] = 0.f;
 
-    // prologue: stages 0..2 in flight; wait for stage 0
+    // prologue: stages 0..2 in flight; wait for stage 0, then issue the LDS
+    // reads of k-substep 0's fragments
     const int npro = min(kStages, nkb);
     for (int st = 0; st < npro; ++st) issue(st, ring + st * kSlotBytes);
     ring_wait_barrier<kDma>(npro - 1);
     u32x4_t codes[2];
     bf16x8_t bf[2], af[NMT];
+    Lookup8 lk[2];
     read_codes(ring, codes);
     frag_a(ring, 0, af);
-    {
-        Lookup8 lk[2];
-        frag_b(ring, codes, 0, lk);
-        bf[0] = __builtin_bit_cast(bf16x8_t, lookup8_combine(lk[0]));
-        bf[1] = __builtin_bit_cast(bf16x8_t, lookup8_combine(lk[1]));
-    }
+    frag_b(ring, codes, 0, lk);
 
+    // Software pipeline, per k-substep: (1) combine this substep's looked-up
+    // entries (their LDS reads were issued one substep earlier, so they had
+    // a whole substep of MFMAs to land) into B fragments; (2) issue the LDS
+    // reads of the next substep's A fragments and lookups, interleaved with
+    // (3) this substep's MFMAs, so the LDS latency hides behind the MFMAs.
     int slot = 0;
     for (int kb = 0; kb < nkb; ++kb) {
         uint8_t* sl = ring + slot * kSlotBytes;
@@ -591,12 +593,16 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
         const uint8_t* nsl = ring + nslot * kSlotBytes;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-            // region 1: issue the LDS reads of the next k-substep's fragments
+            bf[0] = __builtin_bit_cast(bf16x8_t, lookup8_combine(lk[0]));
+            bf[1] = __builtin_bit_cast(bf16x8_t, lookup8_combine(lk[1]));
+            __builtin_amdgcn_sched_barrier(0);
             bf16x8_t af_n[NMT];
-            Lookup8 lk[2];
             u32x4_t codes_n[2];
+            // the next substep's lookups, interleaved with this substep's
+            // n-tile 0 MFMAs; then its A fragment reads, with the n-tile 1
+            // MFMAs (the lookups are combined at the start of the next
+            // substep, the A fragments used only at its first MFMA)
             if (ks < 3) {
-                frag_a(sl, ks + 1, af_n);
                 frag_b(sl, codes, ks + 1, lk);
             } else {
                 // stage kb+1 landed everywhere (only stage kb+2 may still be
@@ -605,23 +611,26 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
                 ring_wait_barrier<kDma>(kb + 2 < nkb ? 1 : 0);
                 if (kb + 3 < nkb) issue(kb + 3, sl);
                 read_codes(nsl, codes_n);
-                frag_a(nsl, 0, af_n);
                 frag_b(nsl, codes_n, 0, lk);
             }
-            __builtin_amdgcn_sched_barrier(0);
-            // region 2: this substep's MFMAs, with the next substep's
-            // combining ops slotted between them
 #pragma unroll
             for (int mt = 0; mt < NMT; ++mt)
+                acc[mt][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mt], bf[0], acc[mt][0], 0, 0, 0);
 #pragma unroll
-                for (int nt = 0; nt < 2; ++nt)
-                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mt], bf[nt], acc[mt][nt], 0, 0, 0);
-            bf[0] = __builtin_bit_cast(bf16x8_t, lookup8_combine(lk[0]));
-            bf[1] = __builtin_bit_cast(bf16x8_t, lookup8_combine(lk[1]));
+            for (int i = 0; i < NMT; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                     // 1 MFMA
+                if (!kNested) __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);      // VALU
+                __builtin_amdgcn_sched_group_barrier(0x100, (16 + NMT - 1) / NMT, 0);  // lookups
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            frag_a(ks < 3 ? sl : nsl, (ks + 1) & 3, af_n);
 #pragma unroll
-            for (int i = 0; i < 2 * NMT; ++i) {
+            for (int mt = 0; mt < NMT; ++mt)
+                acc[mt][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mt], bf[1], acc[mt][1], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < NMT; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // 1 MFMA
-                if (i >= 2 * NMT - 8) __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);   // 1 VALU
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // A fragment read
             }
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
