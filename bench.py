@@ -293,9 +293,16 @@ def main():
         extra["prefill_dsv2_T2048_TFLOPs"] = round(flops / sec / 1e12, 1)
         extra["prefill_dsv2_T2048_frac_bf16_peak"] = round(flops / sec / 1e12 / BF16_PEAK_TFLOPS, 4)
         log(f"[bench] prefill DeepSeek T=2048: {sec * 1e6:.0f} us, {flops / sec / 1e12:.1f} TFLOP/s")
+        del lay, sp, g
+        torch.cuda.empty_cache()
+        ceil = measured_ceilings(torch, dev, d)
+        extra.update(ceil)
+        extra["prefill_dsv2_T2048_frac_hipblaslt_ceiling"] = round(
+            flops / sec / 1e12 / ceil["ceiling_hipblaslt_bf16_TFLOPs"], 4)
+        extra["decode_T1_frac_device_copy_ceiling"] = round(
+            result["value"] * 1e3 / ceil["ceiling_device_copy_GBs"], 4)
         extra.update(nested_tiers(a, ops, N, torch, dev, NestedExpert, NestedStack, MoEWeights,
                                   graph_of, time_graph))
-        del lay, sp, g
         torch.cuda.empty_cache()
         extra.update(mixtral_stack(ops, torch, dev, rand_stack, MoEWeights, graph_of, time_graph))
         torch.cuda.empty_cache()
@@ -317,6 +324,45 @@ def main():
         result["cpu_baseline"] = cpu_baseline(a, c, T)
 
     print(json.dumps(result), flush=True)
+
+
+def measured_ceilings(torch, dev, d, T=2048):
+    """Measured ceilings beside the published peaks: a 1 GiB device-to-device copy (read +
+    write bytes per second), and torch's bf16 GEMM (hipBLASLt) on the dense-equivalent shapes
+    of the DeepSeek T=2048 prefill: [T*(k+S), H] x [H, 2I] and [T*(k+S), I] x [I, H]."""
+    def timed(fn, reps):
+        fn()
+        torch.cuda.synchronize()
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(reps):
+            fn()
+        t1.record()
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) / reps * 1e-3
+
+    out = {}
+    src = torch.empty(1 << 29, dtype=torch.bfloat16, device=dev).normal_()
+    dst = torch.empty_like(src)
+    sec = timed(lambda: dst.copy_(src), 10)
+    out["ceiling_device_copy_GBs"] = round(2 * src.numel() * 2 / sec / 1e9, 1)
+    del src, dst
+    torch.cuda.empty_cache()
+    P = T * (d["k"] + d["S"])
+    fl = tsum = 0.0
+    for K, Nn in ((d["H"], 2 * d["I"]), (d["I"], d["H"])):
+        a_ = torch.randn(P, K, device=dev).to(torch.bfloat16)
+        b_ = torch.randn(K, Nn, device=dev).to(torch.bfloat16)
+        o_ = torch.empty(P, Nn, dtype=torch.bfloat16, device=dev)
+        tsum += timed(lambda: torch.mm(a_, b_, out=o_), 20)
+        fl += 2.0 * P * K * Nn
+        del a_, b_, o_
+    out["ceiling_hipblaslt_bf16_TFLOPs"] = round(fl / tsum / 1e12, 1)
+    out["ceiling_blas_library"] = str(torch.backends.cuda.preferred_blas_library())
+    log(f"[bench] ceilings: device copy {out['ceiling_device_copy_GBs']:.0f} GB/s, "
+        f"bf16 GEMM {out['ceiling_hipblaslt_bf16_TFLOPs']:.0f} TFLOP/s")
+    return out
 
 
 def mixtral_stack(ops, torch, dev, rand_stack, MoEWeights, graph_of, time_graph):

@@ -31,6 +31,8 @@
 // (vllm_lut/quant_method.py:261-277) and the per-expert GEMMs of the
 // llama.cpp mul_mat_id patch (llama-cpp-port/patches/0001:151-208), over the
 // routed tokens only instead of all T tokens.
+#include <atomic>
+
 #include "common.h"
 #include "kernels.h"
 #include "lut_core.h"
@@ -46,22 +48,53 @@ constexpr int kBK = 64;           // K step
 constexpr int kAStride = 72;      // bf16 per LDS A row (64 + 8 pad)
 
 struct TileInfo {
-    int e, m0, p0, n;
+    int e, m0, p0, n;   // tile = positions [p0 + m0, p0 + min(n, m0 + 256)) of expert e
 };
 
-// blockIdx.y -> (expert, first position of the tile); e = -1 past the end.
-// Experts are walked from the last id down so the always-on shared experts
-// (stored last, every token) are scheduled first.  Wave 0 does it 64 experts
-// at a time: per-expert tile counts, an inclusive wave scan, and a ballot for
-// the expert whose tile range holds j.
-__device__ __forceinline__ TileInfo find_tile(const MoeRouting& rt, int j) {
+// blockIdx.y -> tile; e = -1 past the end.  Experts are walked from the last
+// id down so the always-on shared experts (stored last, every token) are
+// scheduled first; an expert of n positions has ceil(n / 256) tile rows, and
+// every tile row runs as gridDim.x CTAs (one per weight-row block).
+//
+// Tail split: CTAs start in blockIdx order as CUs free up, one per CU, so the
+// last (Ttot * gridDim.x) mod ncu CTAs form a partial final round.  When that
+// round's tile rows, cut in two 128-position halves, still fit the CUs, they
+// are cut: the final round then runs half-height tiles (same weight work,
+// half the activation work) and ends sooner.  The host sizes the grid for the
+// extra rows (tail_rows_max).
+//
+// Wave 0 does it 64 experts at a time: per-expert tile counts, an inclusive
+// wave scan, and a ballot for the expert whose tile range holds the row.
+__device__ __forceinline__ int tail_split_rows(int ttot, int nx, int ncu) {
+    if (ncu <= 0) return 0;
+    const int rem = (int)(((int64_t)ttot * nx) % ncu);
+    if (rem == 0) return 0;
+    const int r = (rem + nx - 1) / nx;
+    return 2 * r * nx <= ncu ? r : 0;
+}
+
+__device__ __forceinline__ TileInfo find_tile(const MoeRouting& rt, int j, int ncu) {
     __shared__ TileInfo s_tile;
     if (threadIdx.x < 64) {
         const int lane = threadIdx.x;
         const int et = rt.num_experts_total;
+        // total tile rows
+        int ttot = 0;
+        for (int c0 = 0; c0 < et; c0 += 64) {
+            const int e = c0 + lane;
+            const int n = e < et ? rt.offsets[e + 1] - rt.offsets[e] : 0;
+            ttot += __builtin_amdgcn_readlane(wave_scan_incl((n + kBM - 1) / kBM), 63);
+        }
+        const int split = tail_split_rows(ttot, (int)gridDim.x, ncu);
+        const int s0 = ttot - split;   // first split row
+        int row = j, half = -1;
+        if (j >= s0) {
+            row = s0 + (j - s0) / 2;
+            half = (j - s0) & 1;
+        }
         int base = 0;   // tiles of the experts in earlier chunks
         bool found = false;
-        for (int c0 = 0; c0 < et && !found; c0 += 64) {
+        for (int c0 = 0; c0 < et && !found && row < ttot; c0 += 64) {
             const int e = et - 1 - (c0 + lane);
             int p0 = 0, n = 0;
             if (e >= 0) {
@@ -71,8 +104,15 @@ __device__ __forceinline__ TileInfo find_tile(const MoeRouting& rt, int j) {
             const int nt = (n + kBM - 1) / kBM;
             const int incl = wave_scan_incl(nt);
             const int excl = incl - nt;
-            const bool hit = e >= 0 && j >= base + excl && j < base + incl;
-            if (hit) s_tile = TileInfo{e, (j - base - excl) * kBM, p0, n};
+            const bool hit = e >= 0 && row >= base + excl && row < base + incl;
+            if (hit) {
+                int m0 = (row - base - excl) * kBM, nn = n;
+                if (half >= 0) {
+                    m0 += half * (kBM / 2);
+                    nn = min(n, m0 + kBM / 2);
+                }
+                s_tile = m0 < nn ? TileInfo{e, m0, p0, nn} : TileInfo{-1, 0, 0, 0};
+            }
             found = __ballot(hit) != 0;
             base += __builtin_amdgcn_readlane(incl, 63);
         }
@@ -704,9 +744,9 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
 
 template <bool kGateUp, int kFmt>
 __global__ __launch_bounds__(256, 1) void prefill_ring_kernel(lutmoe_moe_desc d, const uint16_t* __restrict__ src,
-                                                              MoeRouting rt, void* __restrict__ dst) {
+                                                              MoeRouting rt, void* __restrict__ dst, int ncu) {
     __shared__ __attribute__((aligned(16))) uint8_t ring[kStages * kSlotBytes];
-    const TileInfo ti = find_tile(rt, blockIdx.y);
+    const TileInfo ti = find_tile(rt, blockIdx.y, ncu);
     if (ti.e < 0) return;
     const int nmt = (min(kBM, ti.n - ti.m0) + 31) / 32;
     switch (nmt) {
@@ -722,10 +762,10 @@ __global__ __launch_bounds__(256, 1) void prefill_ring_kernel(lutmoe_moe_desc d,
 template <bool kGateUp, int kFmt>
 __global__ __launch_bounds__(256, 1) void prefill_kernel(lutmoe_moe_desc d,
                                                          const uint16_t* __restrict__ src,
-                                                         MoeRouting rt, void* __restrict__ dst) {
+                                                         MoeRouting rt, void* __restrict__ dst, int ncu) {
     __shared__ __attribute__((aligned(16))) uint16_t s_a[2][kBM * kAStride];
     __shared__ float s_cb[kFmt == LUTMOE_FMT_REF ? 256 : 1];
-    const TileInfo ti = find_tile(rt, blockIdx.y);
+    const TileInfo ti = find_tile(rt, blockIdx.y, ncu);
     if (ti.e < 0) return;
     if (kFmt == LUTMOE_FMT_REF) {
         const uint16_t* cb = (const uint16_t*)(kGateUp ? d.w13 : d.w2).codebook;
@@ -743,10 +783,24 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(lutmoe_moe_desc d,
 }
 
 inline int max_tiles(int P, int E_tot) { return (P + kBM - 1) / kBM + E_tot; }
+// extra grid rows for the tail split (find_tile cuts at most ncu / (2 nx) rows)
+inline int tail_rows_max(int nx, int ncu) { return ncu / (2 * nx) + 1; }
 
 }  // namespace
 
 namespace lutmoe_host {
+
+// Compute units of the current device (a per-device property cache).
+static int cu_count() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    int v = cache[dev].load(std::memory_order_relaxed);
+    if (v > 0) return v;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) return 0;
+    cache[dev].store(v, std::memory_order_relaxed);
+    return v;
+}
 
 // The ring kernels address activations and one expert's codes / tables (or
 // NestedLUT planes / tables) with 32-bit byte offsets from a scalar base.
@@ -761,29 +815,33 @@ static bool ring_offsets_fit(const lutmoe_moe_desc* d, const MoeRouting& r, int 
 int launch_prefill_gate_up(const lutmoe_moe_desc* d, const uint16_t* x, const MoeRouting& r,
                            uint16_t* act, int P, hipStream_t s) {
     if (d->w13.format != LUTMOE_FMT_REF && !ring_offsets_fit(d, r, P)) return LUTMOE_EUNSUPPORTED;
-    const dim3 grid((d->inter + kBN / 2 - 1) / (kBN / 2), max_tiles(P, r.num_experts_total));
+    const int nx = (d->inter + kBN / 2 - 1) / (kBN / 2), ncu = cu_count();
+    const dim3 grid(nx, max_tiles(P, r.num_experts_total) + tail_rows_max(nx, ncu));
     if (d->w13.format == LUTMOE_FMT_REF)
-        hipLaunchKernelGGL((prefill_kernel<true, LUTMOE_FMT_REF>), grid, dim3(256), 0, s, *d, x, r, (void*)act);
+        hipLaunchKernelGGL((prefill_kernel<true, LUTMOE_FMT_REF>), grid, dim3(256), 0, s, *d, x, r, (void*)act, ncu);
     else if (d->w13.format == LUTMOE_FMT_NESTED)
         hipLaunchKernelGGL((prefill_ring_kernel<true, LUTMOE_FMT_NESTED>), grid, dim3(256), 0, s, *d, x, r,
-                           (void*)act);
+                           (void*)act, ncu);
     else
-        hipLaunchKernelGGL((prefill_ring_kernel<true, LUTMOE_FMT_BL4>), grid, dim3(256), 0, s, *d, x, r, (void*)act);
+        hipLaunchKernelGGL((prefill_ring_kernel<true, LUTMOE_FMT_BL4>), grid, dim3(256), 0, s, *d, x, r, (void*)act,
+                           ncu);
     return check_launch();
 }
 
 int launch_prefill_down(const lutmoe_moe_desc* d, const uint16_t* act, const MoeRouting& r,
                         float* y_pos, int P, hipStream_t s) {
     if (d->w2.format != LUTMOE_FMT_REF && !ring_offsets_fit(d, r, P)) return LUTMOE_EUNSUPPORTED;
-    const dim3 grid((d->hidden + kBN - 1) / kBN, max_tiles(P, r.num_experts_total));
+    const int nx = (d->hidden + kBN - 1) / kBN, ncu = cu_count();
+    const dim3 grid(nx, max_tiles(P, r.num_experts_total) + tail_rows_max(nx, ncu));
     if (d->w2.format == LUTMOE_FMT_REF)
-        hipLaunchKernelGGL((prefill_kernel<false, LUTMOE_FMT_REF>), grid, dim3(256), 0, s, *d, act, r, (void*)y_pos);
+        hipLaunchKernelGGL((prefill_kernel<false, LUTMOE_FMT_REF>), grid, dim3(256), 0, s, *d, act, r, (void*)y_pos,
+                           ncu);
     else if (d->w2.format == LUTMOE_FMT_NESTED)
         hipLaunchKernelGGL((prefill_ring_kernel<false, LUTMOE_FMT_NESTED>), grid, dim3(256), 0, s, *d, act, r,
-                           (void*)y_pos);
+                           (void*)y_pos, ncu);
     else
         hipLaunchKernelGGL((prefill_ring_kernel<false, LUTMOE_FMT_BL4>), grid, dim3(256), 0, s, *d, act, r,
-                           (void*)y_pos);
+                           (void*)y_pos, ncu);
     return check_launch();
 }
 
