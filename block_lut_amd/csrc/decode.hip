@@ -25,6 +25,8 @@
 // first, then the weights chunk by chunk, without branches) before any is
 // consumed, so a wave keeps up to 16 KB in flight and starts on chunk 0 while
 // the later chunks are still arriving.
+#include <algorithm>
+
 #include "common.h"
 #include "kernels.h"
 #include "lut_core.h"
@@ -52,6 +54,19 @@ struct RouteOut {
     int perm[kMaxP];
     int inv[kMaxP];
     float pw[kMaxP];
+};
+
+// Work items of the precomputed-routing kernels (gate/up CTA rows, down_y
+// waves): an active slot's positions cut into chunks of at most C, so one
+// heavily routed expert does not hold the layer up behind many passes of
+// TB tokens.  C = TB * round(mean positions per active slot / TB), at least
+// TB: routing where every expert gets about as many positions keeps one chunk
+// per slot.  Stored in the workspace right after the RouteOut copy.
+struct RouteChunks {
+    int nchunk;
+    int ce[kMaxP];                      // expert of chunk c
+    int cp0[kMaxP];                     // its first position
+    int cn[kMaxP];                      // its positions
 };
 
 struct RouteScratch {
@@ -341,6 +356,7 @@ struct WaveRouteView {
         return {__builtin_amdgcn_readlane(r.e, L), __builtin_amdgcn_readlane(r.pos, L),
                 __builtin_amdgcn_readlane(r.cnt, L)};
     }
+    __device__ SlotRef work(int a) const { return slot(a); }
     // pair at position p (wave-uniform p)
     __device__ int pair_at(int p) const {
         const uint64_t b = __ballot(r.pos == p);
@@ -360,6 +376,7 @@ struct LdsRouteView {
         if (a >= R->nact) return {-1, 0, 0};
         return {R->act[a], R->aoff[a], R->an[a]};
     }
+    __device__ SlotRef work(int a) const { return slot(a); }
     __device__ int pair_at(int p) const { return R->perm[p]; }
     __device__ float weight_at(int p) const { return R->pw[R->perm[p]]; }
     __device__ int pos_of(int q) const { return R->inv[q]; }
@@ -374,6 +391,12 @@ struct GlobalRouteView {
     __device__ SlotRef slot(int a) const {
         if (a >= R->nact) return {-1, 0, 0};
         return {R->act[a], R->aoff[a], R->an[a]};
+    }
+    // work item c (a chunk of an active slot's positions)
+    __device__ SlotRef work(int c) const {
+        const RouteChunks* C = reinterpret_cast<const RouteChunks*>(R + 1);
+        if (c >= C->nchunk) return {-1, 0, 0};
+        return {C->ce[c], C->cp0[c], C->cn[c]};
     }
     __device__ int pair_at(int p) const { return R->perm[p]; }
     __device__ float weight_at(int p) const { return R->pw[R->perm[p]]; }
@@ -415,6 +438,14 @@ __device__ __forceinline__ void wave_route_publish(const DecodeArgs& A, const Wa
         if (r.pos >= 0) g->perm[r.pos] = lane;
     }
     if (lane == 0) g->nact = r.nact;
+    // one work item per slot
+    RouteChunks* c = reinterpret_cast<RouteChunks*>(g + 1);
+    if (r.first) {
+        c->ce[r.arank] = r.e;
+        c->cp0[r.arank] = r.pos;
+        c->cn[r.arank] = r.cnt;
+    }
+    if (lane == 0) c->nchunk = r.nact;
 }
 
 // The precomputed routing (decode_route_kernel's global copy) -> LDS.
@@ -470,12 +501,41 @@ __device__ __forceinline__ void put_route(const DecodeArgs& A, const RouteOut& R
     if (threadIdx.x == 0) g->nact = R.nact;
 }
 
+// The slots of R (LDS, complete) -> chunk work items in the global copy.
+// Thread a < nact takes slot a (nact <= kMaxEtot <= blockDim.x); chunk
+// indices are a block-wide exclusive scan of the per-slot chunk counts.
+__device__ __forceinline__ void put_chunks(const DecodeArgs& A, const RouteOut& R) {
+    __shared__ int s_wsum[32];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int nact = R.nact;
+    const int TB = A.T <= 1 ? 1 : A.T <= 2 ? 2 : 4;   // tokens per pass (the host's tb_for)
+    const int pv = nact > 0 ? R.aoff[nact - 1] + R.an[nact - 1] : 0;
+    const int navg = nact > 0 ? (pv + nact - 1) / nact : 1;
+    const int C = TB * max(1, (navg + TB / 2) / TB);
+    const int n = tid < nact ? R.an[tid] : 0;
+    const int nc = (n + C - 1) / C;
+    const int incl = wave_scan_incl(nc);
+    if (lane == 63) s_wsum[wv] = incl;
+    __syncthreads();
+    int base = 0;
+    for (int w = 0; w < wv; ++w) base += s_wsum[w];
+    RouteChunks* g = reinterpret_cast<RouteChunks*>(A.route + 1);
+    const int first = base + incl - nc;
+    for (int j = 0; j < nc; ++j) {
+        g->ce[first + j] = R.act[tid];
+        g->cp0[first + j] = R.aoff[tid] + j * C;
+        g->cn[first + j] = min(C, n - j * C);
+    }
+    if (tid == (int)blockDim.x - 1) g->nchunk = base + incl;
+}
+
 // One CTA of 16 waves (one token per wave in the top-k loop for T <= 16).
 __global__ __launch_bounds__(1024) void decode_route_kernel(DecodeArgs A) {
     __shared__ RouteOut R;
     __shared__ RouteScratch X;
     cta_route(A, R, X);
     put_route(A, R);
+    put_chunks(A, R);
 }
 
 // One wave, 8 rows, one 2048-column chunk cc of K: lane l covers columns
@@ -724,7 +784,7 @@ __device__ __forceinline__ void expert_rows8(const lutmoe_weights& w, int e, con
 // most ~40 GB/s, so a CU holding a CTA more than the others sets the tail.
 template <int TB, int kFmt, class RV>
 __device__ __forceinline__ void gate_up_body(const DecodeArgs& A, const RV& rv, uint8_t* s_slot) {
-    const SlotRef sl = rv.slot(blockIdx.y);
+    const SlotRef sl = rv.work(blockIdx.y);
     if (sl.e < 0) return;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int I = A.d.inter, H = A.d.hidden, ke = A.k + A.d.num_shared;
@@ -863,7 +923,7 @@ __global__ __launch_bounds__(256, TB <= 2 ? 3 : 2) void bl4_decode_down_y(Decode
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int a = blockIdx.y * 4 + wv;
     const GlobalRouteView rv{A.route};
-    const SlotRef sl = rv.slot(a);
+    const SlotRef sl = rv.work(a);
     if (sl.e < 0) return;
     const int I = A.d.inter, H = A.d.hidden;
     const int h0 = blockIdx.x * kRows;
@@ -1170,7 +1230,7 @@ int launch_nested_gemv(const lutmoe_weights* w, int expert, const uint16_t* x, i
     return check_launch();
 }
 
-size_t decode_route_bytes() { return sizeof(RouteOut); }
+size_t decode_route_bytes() { return sizeof(RouteOut) + sizeof(RouteChunks); }
 size_t decode_sync_bytes() { return sizeof(DecodeSync); }
 
 int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* topk_w,
@@ -1231,8 +1291,11 @@ int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* t
         LUTMOE_DECODE_FMTS(36, 4, true, KERNEL, GRID, BLOCK, LDS)           \
         default: return LUTMOE_EINVAL;                                      \
     }
+    // work items: the active slots, cut into chunks by decode_route_kernel
+    // (at most P, and at most one more per slot than ceil(P / TB))
+    const int max_work = pre ? std::min(P, max_active + (P + tb_for(T) - 1) / tb_for(T)) : max_active;
     if (stages & LUTMOE_STAGE_GATE_UP) {
-        const dim3 grid((d->inter + 4 * kGuWaves - 1) / (4 * kGuWaves), max_active);
+        const dim3 grid((d->inter + 4 * kGuWaves - 1) / (4 * kGuWaves), max_work);
         LUTMOE_DECODE_LAUNCH(bl4_decode_gate_up, pre, grid, dim3(64 * kGuWaves), 0)
         if ((rc = check_launch())) return rc;
     }
@@ -1243,7 +1306,7 @@ int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* t
         // gate/up kernel's first CTA, or by decode_route_kernel)
         if (max_active > 8) {
             // many experts: y + combine, every slot in parallel
-            const dim3 gy((d->hidden + kRows - 1) / kRows, (max_active + 3) / 4);
+            const dim3 gy((d->hidden + kRows - 1) / kRows, (max_work + 3) / 4);
 #define LUTMOE_DOWN_Y(TB, FMT) hipLaunchKernelGGL((bl4_decode_down_y<TB, FMT>), gy, dim3(256), 0, s, A, y_ws)
             switch (tb_for(T) * 4 + fmt_idx) {
                 case 4: LUTMOE_DOWN_Y(1, LUTMOE_FMT_BL4); break;
