@@ -345,6 +345,35 @@ def test_moe_layer(gpu, fmt, T, path):
     assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
 
 
+@pytest.mark.parametrize("fmt,T", [("bl4", 16), ("bl4", 40), ("ref", 16), ("nested", 16)])
+def test_moe_layer_skewed_routing(gpu, fmt, T):
+    """Decode with one heavily routed expert: every token picks expert 0 plus k-1 others, so
+    expert 0 holds T positions while the mean slot holds about 3, and the routing kernel
+    cuts its slot into several work chunks (gate/up CTA rows, down y waves)."""
+    import torch
+    from block_lut_amd import ops
+    from block_lut_amd.formats import MoEWeights
+    E, S, k, H, I = 24, 0, 4, 256, 192
+    if fmt == "nested":
+        bits = [2, 3, 4] * (E // 3)
+        w13 = NestedExpertset(bits, 2 * I, H, seed=90 + T, n_iter=8)
+        w2 = NestedExpertset(bits, H, I, seed=91 + T, n_iter=8)
+        f13, f2 = w13.deq_f32, w2.deq_f32
+    else:
+        w13, w2 = _moe_case(fmt, E, S, H, I, seed=90 + T)
+        f13, f2 = (w13.gemv_f32, w2.gemv_f32) if fmt == "ref" else (w13.deq_f32, w2.deq_f32)
+    moe = MoEWeights(w13.stack(gpu), w2.stack(gpu), H, I, E, S)
+    rng = np.random.default_rng(900 + T)
+    xb = _x(rng, T, H)
+    rids = np.stack([np.concatenate([[0], 1 + rng.permutation(E - 1)[:k - 1]]) for _ in range(T)])
+    rids = rids.astype(np.int64)
+    rw = rng.random((T, k)).astype(np.float32)
+    out = ops.moe_forward(moe, to_dev_bf16(xb, gpu), torch.from_numpy(rw).to(gpu),
+                          torch.from_numpy(rids).to(gpu), out_dtype=torch.float32, path=1)
+    ref = O.moe_layer(xb, rids, rw, f13, f2, shared=[])
+    assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
+
+
 @pytest.mark.parametrize("block_size,T", [(64, 1), (64, 9), (256, 1), (256, 9)])
 def test_moe_layer_ref_block_sizes(gpu, block_size, T):
     """REF decode with absmax blocks of 64 and 256 (a lane's 32 aligned columns share one
