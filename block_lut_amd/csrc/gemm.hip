@@ -587,18 +587,19 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
             return c[ks];
     };
     const int sw = a_swz(bn);   // = a_swz(mt * 32 + bn) for every m-tile
-    auto frag_a = [&](const uint8_t* sl, int ks, bf16x8_t (&af)[NMT]) __attribute__((always_inline)) {
+    // A fragments of m-tiles [mt0, mt1) of k-substep ks
+    auto frag_a = [&](const uint8_t* sl, int ks, bf16x8_t (&af)[NMT], int mt0, int mt1) __attribute__((always_inline)) {
         const uint8_t* p = sl + bn * 128 + 16 * ((4 * bh + ks) ^ sw);
 #pragma unroll
-        for (int mt = 0; mt < NMT; ++mt) af[mt] = *reinterpret_cast<const bf16x8_t*>(p + mt * 4096);
+        for (int mt = 0; mt < NMT; ++mt)
+            if (mt >= mt0 && mt < mt1) af[mt] = *reinterpret_cast<const bf16x8_t*>(p + mt * 4096);
     };
     // B fragment of k-substep ks: the lane's 8 codes looked up in its rows'
     // LDS tables of slot `sl` (reads issued here, combined later)
-    auto frag_b = [&](const uint8_t* sl, const u32x4_t (&codes)[2], int ks, Lookup8 (&lk)[2])
-        __attribute__((always_inline)) {
+    // B lookups of n-tile nt, k-substep ks (reads issued here, combined later)
+    auto frag_b = [&](const uint8_t* sl, const u32x4_t (&codes)[2], int ks, int nt) __attribute__((always_inline)) {
         const uint32_t tbase = lds_addr(sl + kSlotA + kSlotB);
-        lk[0] = lookup8_issue(nested_code(codes[0], ks), tbase + L0 * 32);
-        lk[1] = lookup8_issue(nested_code(codes[1], ks), tbase + L1 * 32);
+        return lookup8_issue(nested_code(codes[nt], ks), tbase + (nt ? L1 : L0) * 32);
     };
 
     f32x16_t acc[NMT][2];
@@ -616,16 +617,17 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
     ring_wait_barrier<kDma>(npro - 1);
     u32x4_t codes[2];
     bf16x8_t bf[2], af[NMT];
-    Lookup8 lk[2];
     read_codes(ring, codes);
-    frag_a(ring, 0, af);
-    frag_b(ring, codes, 0, lk);
+    Lookup8 lk0 = frag_b(ring, codes, 0, 0), lk1 = frag_b(ring, codes, 0, 1);
+    frag_a(ring, 0, af, 0, NMT);
 
-    // Software pipeline, per k-substep: (1) combine this substep's looked-up
-    // entries (their LDS reads were issued one substep earlier, so they had
-    // a whole substep of MFMAs to land) into B fragments; (2) issue the LDS
-    // reads of the next substep's A fragments and lookups, interleaved with
-    // (3) this substep's MFMAs, so the LDS latency hides behind the MFMAs.
+    // Software pipeline, per k-substep and n-tile nt: combine the n-tile's
+    // looked-up entries (issued one half-substep earlier) into its B
+    // fragment, then its NMT MFMAs interleaved with the next substep's LDS
+    // reads: that substep's n-tile-nt lookups and half of its A fragments,
+    // one or two reads per MFMA, so the LDS queue drains while the MFMAs
+    // run and every read has a half-substep of MFMAs to land.
+    constexpr int kHalfA = (NMT + 1) / 2;
     int slot = 0;
     for (int kb = 0; kb < nkb; ++kb) {
         uint8_t* sl = ring + slot * kSlotBytes;
@@ -633,44 +635,49 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
         const uint8_t* nsl = ring + nslot * kSlotBytes;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-            bf[0] = __builtin_bit_cast(bf16x8_t, lookup8_combine(lk[0]));
-            bf[1] = __builtin_bit_cast(bf16x8_t, lookup8_combine(lk[1]));
-            __builtin_amdgcn_sched_barrier(0);
             bf16x8_t af_n[NMT];
             u32x4_t codes_n[2];
-            // the next substep's lookups, interleaved with this substep's
-            // n-tile 0 MFMAs; then its A fragment reads, with the n-tile 1
-            // MFMAs (the lookups are combined at the start of the next
-            // substep, the A fragments used only at its first MFMA)
-            if (ks < 3) {
-                frag_b(sl, codes, ks + 1, lk);
-            } else {
+            const uint8_t* rs = ks < 3 ? sl : nsl;      // slot of the next substep's operands
+            const int ksn = (ks + 1) & 3;
+            // ---- n-tile 0
+            bf[0] = __builtin_bit_cast(bf16x8_t, lookup8_combine(lk0));
+            __builtin_amdgcn_sched_barrier(0);
+            if (ks == 3) {
                 // stage kb+1 landed everywhere (only stage kb+2 may still be
-                // in flight) and no wave reads this slot any more -> refill
-                // it with stage kb+3
+                // in flight) and every read of this slot is done (its values
+                // are in registers) -> refill it with stage kb+3
                 ring_wait_barrier<kDma>(kb + 2 < nkb ? 1 : 0);
                 if (kb + 3 < nkb) issue(kb + 3, sl);
                 read_codes(nsl, codes_n);
-                frag_b(nsl, codes_n, 0, lk);
+                frag_a(nsl, 0, af_n, 0, kHalfA);
+                lk0 = frag_b(nsl, codes_n, 0, 0);
+            } else {
+                lk0 = frag_b(sl, codes, ksn, 0);
+                frag_a(sl, ksn, af_n, 0, kHalfA);
             }
 #pragma unroll
             for (int mt = 0; mt < NMT; ++mt)
                 acc[mt][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mt], bf[0], acc[mt][0], 0, 0, 0);
 #pragma unroll
             for (int i = 0; i < NMT; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                     // 1 MFMA
-                if (!kNested) __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);      // VALU
-                __builtin_amdgcn_sched_group_barrier(0x100, (16 + NMT - 1) / NMT, 0);  // lookups
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                            // 1 MFMA
+                if (!kNested) __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);             // VALU
+                __builtin_amdgcn_sched_group_barrier(0x100, (8 + kHalfA + 2 + NMT - 1) / NMT, 0);   // LDS reads
             }
             __builtin_amdgcn_sched_barrier(0);
-            frag_a(ks < 3 ? sl : nsl, (ks + 1) & 3, af_n);
+            // ---- n-tile 1
+            bf[1] = __builtin_bit_cast(bf16x8_t, lookup8_combine(lk1));
+            __builtin_amdgcn_sched_barrier(0);
+            lk1 = frag_b(rs, ks == 3 ? codes_n : codes, ksn, 1);
+            frag_a(rs, ksn, af_n, kHalfA, NMT);
 #pragma unroll
             for (int mt = 0; mt < NMT; ++mt)
                 acc[mt][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mt], bf[1], acc[mt][1], 0, 0, 0);
 #pragma unroll
             for (int i = 0; i < NMT; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // 1 MFMA
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // A fragment read
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                if (!kNested) __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, (8 + NMT - kHalfA + NMT - 1) / NMT, 0);
             }
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
