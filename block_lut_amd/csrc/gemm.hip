@@ -449,13 +449,61 @@ __device__ __forceinline__ const T* uniform_ptr(const T* p) {
     return (const T*)(((uint64_t)hi << 32) | lo);
 }
 
+// Ring slot geometry per format: A, then codes, then tables.  REF: codes
+// 256 rows x 64 B (one byte per weight) and one absmax dword per row.
+template <int kFmt>
+struct RingSlot {
+    static constexpr int kCodes = kFmt == LUTMOE_FMT_REF ? kBN * 64 : kSlotB;
+    static constexpr int kTabs = kFmt == LUTMOE_FMT_REF ? kBN * 4 : kSlotB;
+    static constexpr int kBytes = kSlotA + kCodes + kTabs;
+    // LDS of a ring kernel: the stages, and REF's fp32 codebook after them
+    static constexpr int kLds = kStages * kBytes + (kFmt == LUTMOE_FMT_REF ? 1024 : 0);
+};
+
+// REF lookups: 8 byte codes (two dwords, code j in byte j%4 of dword j/4)
+// against the fp32[256] codebook at LDS byte address cbase; entries of
+// columns 2j / 2j+1 in e[j] / o[j], as lookup8_issue.
+__device__ __forceinline__ Lookup8 lookup8_ref_issue(uint32_t w0, uint32_t w1, uint32_t cbase) {
+    Lookup8 r;
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+        const uint32_t w = d ? w1 : w0;
+        const uint32_t we = (w << 2) & 0x03fc03fcu;   // 4 * codes 0, 2 (16-bit fields)
+        const uint32_t wo = (w >> 6) & 0x03fc03fcu;   // 4 * codes 1, 3
+        r.e[2 * d] = lds_ld32(add_word<0>(cbase, we));
+        r.e[2 * d + 1] = lds_ld32(add_word<1>(cbase, we));
+        r.o[2 * d] = lds_ld32(add_word<0>(cbase, wo));
+        r.o[2 * d + 1] = lds_ld32(add_word<1>(cbase, wo));
+    }
+    return r;
+}
+
+// bf16(cb[c] * absmax) for the 8 looked-up entries: the product of two bf16
+// values is exact in fp32; v_cvt_pk_bf16_f32 rounds to nearest even (as the
+// reference's dequantisation; finite values and infinities round alike).
+__device__ __forceinline__ u32x4_t lookup8_ref_combine(const Lookup8& l, float am) {
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    u32x4_t r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const f32x2_t p = {__uint_as_float(l.e[j]) * am, __uint_as_float(l.o[j]) * am};
+        r[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(p, bf16x2_t));
+    }
+    return r;
+}
+
 template <bool kGateUp, int kFmt, int NMT>
 __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, const uint16_t* __restrict__ src,
                                                   const MoeRouting& rt, void* __restrict__ dst,
                                                   const TileInfo ti, uint8_t* ring) {
     constexpr bool kNested = kFmt == LUTMOE_FMT_NESTED;
-    // A loads per thread per stage: only the tile's NMT*32 rows are loaded
-    constexpr int kDma = NMT + (kNested ? 16 : 4);
+    constexpr bool kRef = kFmt == LUTMOE_FMT_REF;
+    constexpr int kCodesB = RingSlot<kFmt>::kCodes, kSlot = RingSlot<kFmt>::kBytes;
+    constexpr int kNC = kRef ? 4 : 2;   // code registers (u32x4) per lane per K step
+    // ring loads per thread per stage: the tile's NMT activation loads (only
+    // its NMT*32 rows are loaded) and the weight loads
+    constexpr int kDma = NMT + (kNested ? 16 : kRef ? 5 : 4);
     const lutmoe_weights& w = d.w13;
     const lutmoe_weights& w2 = d.w2;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -498,10 +546,26 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
     // codes are rebuilt).
     const uint8_t* c_base;
     const uint8_t* t_base;
-    uint32_t w_off[kNested ? 16 : 2];
+    uint32_t w_off[kNested ? 16 : kRef ? 4 : 2];
     uint32_t c_step = 32, t_step = 32;
     int bits = 4;
-    if constexpr (kNested) {
+    // REF: absmax block of K step kb of weight row r = min((r*K/64 + kb) / q, nb - 1)
+    // with q = block_size / 64 (whole 64-column steps per block, checked on the host)
+    const uint32_t q = kRef ? (uint32_t)(ww.block_size / 64) : 1u;
+    const uint32_t nb = kRef ? (uint32_t)ww.absmax_per_expert : 1u;
+    uint32_t am_row64 = 0;   // the absmax DMA lane's weight row * K/64
+    if constexpr (kRef) {
+        c_base = uniform_ptr((const uint8_t*)ww.codes + (int64_t)ti.e * ww.rows * ww.cols);
+        t_base = uniform_ptr((const uint8_t*)((const uint16_t*)ww.tables + (int64_t)ti.e * ww.absmax_per_expert));
+        // codes: load h of wave w covers tile rows 64w+16h .. +15, four lanes
+        // (16 B each) per row, so a row's 64 bytes land contiguous in LDS;
+        // absmax: lane l of wave w fetches the aligned dword holding row
+        // 64w+l's entry
+#pragma unroll
+        for (int h = 0; h < 4; ++h)
+            w_off[h] = (uint32_t)tile_row(64 * wv + 16 * h + (lane >> 2)) * (uint32_t)K + 16u * (uint32_t)(lane & 3);
+        am_row64 = (uint32_t)tile_row(64 * wv + lane) * (uint32_t)(K / 64);
+    } else if constexpr (kNested) {
         c_base = uniform_ptr(((const uint8_t* const*)ww.codes)[ti.e]);
         t_base = uniform_ptr((const uint8_t*)((const uint16_t* const*)ww.tables)[ti.e]);
         bits = __builtin_amdgcn_readfirstlane((int)ww.tier_bits[ti.e]);
@@ -536,12 +600,18 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
         const uint8_t* ab = a_base + kb * (kBK * 2);
 #pragma unroll
         for (int j = 0; j < NMT; ++j) dma16(a_off[j], ab, l0 + (8 * NMT * wvu + 8 * j) * 128);
-        if constexpr (kNested) {
+        if constexpr (kRef) {
+            const uint8_t* cb = c_base + kb * 64;
+#pragma unroll
+            for (int h = 0; h < 4; ++h) dma16(w_off[h], cb, l0 + kSlotA + (64 * wvu + 16 * h) * 64);
+            const uint32_t idx = min((am_row64 + (uint32_t)kb) / q, nb - 1u);
+            dma4((idx & ~1u) * 2u, t_base, l0 + kSlotA + kCodesB + 256 * wvu);
+        } else if constexpr (kNested) {
             const uint32_t cs = (uint32_t)kb * c_step, ts = (uint32_t)kb * t_step;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 dma4(w_off[j] + cs, c_base, l0 + kSlotA + (64 * wvu + 8 * j) * 32);
-                dma4(w_off[8 + j] + ts, t_base, l0 + kSlotA + kSlotB + (64 * wvu + 8 * j) * 32);
+                dma4(w_off[8 + j] + ts, t_base, l0 + kSlotA + kCodesB + (64 * wvu + 8 * j) * 32);
             }
         } else {
             const uint8_t* cb = c_base + kb * 32;
@@ -549,7 +619,7 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 dma16(w_off[h], cb, l0 + kSlotA + wvu * 2048 + h * 1024);
-                dma16(w_off[h], tbp, l0 + kSlotA + kSlotB + wvu * 2048 + h * 1024);
+                dma16(w_off[h], tbp, l0 + kSlotA + kCodesB + wvu * 2048 + h * 1024);
             }
         }
     };
@@ -562,8 +632,33 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
     // BL4: codes[nt] = the lane's 16 code bytes of row Lnt.  NestedLUT:
     // codes[nt] = dword bh of p01 (as .x) and of p01's second half (.y), p2 and
     // p3 bytes of this lane half (.z, .w): see nested_code below.
-    auto read_codes = [&](const uint8_t* sl, u32x4_t (&codes)[2]) __attribute__((always_inline)) {
-        if constexpr (kNested) {
+    // REF: codes[2nt], codes[2nt+1] = the lane's 32 code bytes of row Lnt; am[nt]
+    // = that row's absmax for K step kb (the aligned dword holds it in the
+    // half its index parity selects)
+    uint32_t row64[2] = {0u, 0u};
+    if constexpr (kRef) {
+        row64[0] = (uint32_t)tile_row(L0) * (uint32_t)(K / 64);
+        row64[1] = (uint32_t)tile_row(L1) * (uint32_t)(K / 64);
+    }
+    auto read_am = [&](const uint8_t* sl, int kb, float (&am)[2]) __attribute__((always_inline)) {
+        if constexpr (kRef) {
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                const uint32_t idx = min((row64[nt] + (uint32_t)kb) / q, nb - 1u);
+                const uint32_t wd = *reinterpret_cast<const uint32_t*>(sl + kSlotA + kCodesB + 4 * (nt ? L1 : L0));
+                am[nt] = bf16_to_f32((wd >> (16 * (idx & 1u))) & 0xffffu);
+            }
+        }
+    };
+    auto read_codes = [&](const uint8_t* sl, u32x4_t (&codes)[kNC]) __attribute__((always_inline)) {
+        if constexpr (kRef) {
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                const uint8_t* rb = sl + kSlotA + (nt ? L1 : L0) * 64 + 32 * bh;
+                codes[2 * nt] = *reinterpret_cast<const u32x4_t*>(rb);
+                codes[2 * nt + 1] = *reinterpret_cast<const u32x4_t*>(rb + 16);
+            }
+        } else if constexpr (kNested) {
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) {
                 const uint8_t* rb = sl + kSlotA + (nt ? L1 : L0) * 32;
@@ -597,9 +692,21 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
     // B fragment of k-substep ks: the lane's 8 codes looked up in its rows'
     // LDS tables of slot `sl` (reads issued here, combined later)
     // B lookups of n-tile nt, k-substep ks (reads issued here, combined later)
-    auto frag_b = [&](const uint8_t* sl, const u32x4_t (&codes)[2], int ks, int nt) __attribute__((always_inline)) {
-        const uint32_t tbase = lds_addr(sl + kSlotA + kSlotB);
-        return lookup8_issue(nested_code(codes[nt], ks), tbase + (nt ? L1 : L0) * 32);
+    auto frag_b = [&](const uint8_t* sl, const u32x4_t (&codes)[kNC], int ks, int nt) __attribute__((always_inline)) {
+        if constexpr (kRef) {
+            // the 8 codes (bytes 8ks .. of the lane's 32) looked up in the fp32 codebook
+            const u32x4_t& c = codes[2 * nt + (ks >> 1)];
+            return lookup8_ref_issue(c[2 * (ks & 1)], c[2 * (ks & 1) + 1], lds_addr(ring + kStages * kSlot));
+        } else {
+            const uint32_t tbase = lds_addr(sl + kSlotA + kCodesB);
+            return lookup8_issue(nested_code(codes[nt], ks), tbase + (nt ? L1 : L0) * 32);
+        }
+    };
+    // looked-up entries -> bf16x8 B fragment (REF: times the row's absmax,
+    // rounded to bf16: the reference's dequantised weight)
+    auto combine = [&](const Lookup8& lk, float am) __attribute__((always_inline)) {
+        if constexpr (kRef) return __builtin_bit_cast(bf16x8_t, lookup8_ref_combine(lk, am));
+        else return __builtin_bit_cast(bf16x8_t, lookup8_combine(lk));
     };
 
     f32x16_t acc[NMT][2];
@@ -613,11 +720,13 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
     // prologue: stages 0..2 in flight; wait for stage 0, then issue the LDS
     // reads of k-substep 0's fragments
     const int npro = min(kStages, nkb);
-    for (int st = 0; st < npro; ++st) issue(st, ring + st * kSlotBytes);
+    for (int st = 0; st < npro; ++st) issue(st, ring + st * kSlot);
     ring_wait_barrier<kDma>(npro - 1);
-    u32x4_t codes[2];
+    u32x4_t codes[kNC];
+    float am[2] = {0.f, 0.f};
     bf16x8_t bf[2], af[NMT];
     read_codes(ring, codes);
+    read_am(ring, 0, am);
     Lookup8 lk0 = frag_b(ring, codes, 0, 0), lk1 = frag_b(ring, codes, 0, 1);
     frag_a(ring, 0, af, 0, NMT);
 
@@ -630,17 +739,18 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
     constexpr int kHalfA = (NMT + 1) / 2;
     int slot = 0;
     for (int kb = 0; kb < nkb; ++kb) {
-        uint8_t* sl = ring + slot * kSlotBytes;
+        uint8_t* sl = ring + slot * kSlot;
         const int nslot = slot == kStages - 1 ? 0 : slot + 1;
-        const uint8_t* nsl = ring + nslot * kSlotBytes;
+        const uint8_t* nsl = ring + nslot * kSlot;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             bf16x8_t af_n[NMT];
-            u32x4_t codes_n[2];
+            u32x4_t codes_n[kNC];
+            float am_n[2] = {0.f, 0.f};
             const uint8_t* rs = ks < 3 ? sl : nsl;      // slot of the next substep's operands
             const int ksn = (ks + 1) & 3;
             // ---- n-tile 0
-            bf[0] = __builtin_bit_cast(bf16x8_t, lookup8_combine(lk0));
+            bf[0] = combine(lk0, am[0]);
             __builtin_amdgcn_sched_barrier(0);
             if (ks == 3) {
                 // stage kb+1 landed everywhere (only stage kb+2 may still be
@@ -649,6 +759,7 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
                 ring_wait_barrier<kDma>(kb + 2 < nkb ? 1 : 0);
                 if (kb + 3 < nkb) issue(kb + 3, sl);
                 read_codes(nsl, codes_n);
+                read_am(nsl, kb + 1, am_n);
                 frag_a(nsl, 0, af_n, 0, kHalfA);
                 lk0 = frag_b(nsl, codes_n, 0, 0);
             } else {
@@ -666,7 +777,7 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
             }
             __builtin_amdgcn_sched_barrier(0);
             // ---- n-tile 1
-            bf[1] = __builtin_bit_cast(bf16x8_t, lookup8_combine(lk1));
+            bf[1] = combine(lk1, am[1]);
             __builtin_amdgcn_sched_barrier(0);
             lk1 = frag_b(rs, ks == 3 ? codes_n : codes, ksn, 1);
             frag_a(rs, ksn, af_n, kHalfA, NMT);
@@ -683,8 +794,10 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
 #pragma unroll
             for (int mt = 0; mt < NMT; ++mt) af[mt] = af_n[mt];
             if (ks == 3) {
-                codes[0] = codes_n[0];
-                codes[1] = codes_n[1];
+#pragma unroll
+                for (int c = 0; c < kNC; ++c) codes[c] = codes_n[c];
+                am[0] = am_n[0];
+                am[1] = am_n[1];
             }
         }
         slot = nslot;
@@ -752,9 +865,15 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
 template <bool kGateUp, int kFmt>
 __global__ __launch_bounds__(256, 1) void prefill_ring_kernel(lutmoe_moe_desc d, const uint16_t* __restrict__ src,
                                                               MoeRouting rt, void* __restrict__ dst, int ncu) {
-    __shared__ __attribute__((aligned(16))) uint8_t ring[kStages * kSlotBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t ring[RingSlot<kFmt>::kLds];
     const TileInfo ti = find_tile(rt, blockIdx.y, ncu);
     if (ti.e < 0) return;
+    if constexpr (kFmt == LUTMOE_FMT_REF) {
+        // fp32 codebook after the stages (ordered before its first read by
+        // the prologue's barrier)
+        const uint16_t* cb = (const uint16_t*)(kGateUp ? d.w13 : d.w2).codebook;
+        reinterpret_cast<float*>(ring + kStages * RingSlot<kFmt>::kBytes)[threadIdx.x] = bf16_to_f32(cb[threadIdx.x]);
+    }
     const int nmt = (min(kBM, ti.n - ti.m0) + 31) / 32;
     switch (nmt) {
 #define LUTMOE_TILE_CASE(n) \
@@ -814,6 +933,16 @@ static int cu_count() {
 static bool ring_offsets_fit(const lutmoe_moe_desc* d, const MoeRouting& r, int P) {
     const int64_t lim = int64_t(1) << 32;
     if ((int64_t)r.T * d->hidden * 2 >= lim || (int64_t)P * d->inter * 2 >= lim) return false;
+    if (d->w13.format == LUTMOE_FMT_REF) {
+        // one expert's codes and absmax by 32-bit offsets; absmax read as
+        // aligned dwords (an even count per expert keeps them inside it)
+        for (const lutmoe_weights* w : {&d->w13, &d->w2}) {
+            if ((int64_t)w->rows * w->cols >= lim || w->absmax_per_expert % 2 || (uintptr_t)w->tables % 4)
+                return false;
+            if (w->block_size % 64 || w->cols % 64) return false;
+        }
+        return true;
+    }
     if (d->w13.format == LUTMOE_FMT_NESTED)
         return (int64_t)d->w13.rows * d->w13.cols < lim && (int64_t)d->w2.rows * d->w2.cols < lim;
     return (int64_t)d->w13.rows * (d->w13.cols / 2) < lim && (int64_t)d->w2.rows * (d->w2.cols / 2) < lim;
@@ -821,10 +950,14 @@ static bool ring_offsets_fit(const lutmoe_moe_desc* d, const MoeRouting& r, int 
 
 int launch_prefill_gate_up(const lutmoe_moe_desc* d, const uint16_t* x, const MoeRouting& r,
                            uint16_t* act, int P, hipStream_t s) {
-    if (d->w13.format != LUTMOE_FMT_REF && !ring_offsets_fit(d, r, P)) return LUTMOE_EUNSUPPORTED;
+    const bool ring = ring_offsets_fit(d, r, P);
+    if (d->w13.format != LUTMOE_FMT_REF && !ring) return LUTMOE_EUNSUPPORTED;
     const int nx = (d->inter + kBN / 2 - 1) / (kBN / 2), ncu = cu_count();
     const dim3 grid(nx, max_tiles(P, r.num_experts_total) + tail_rows_max(nx, ncu));
-    if (d->w13.format == LUTMOE_FMT_REF)
+    if (d->w13.format == LUTMOE_FMT_REF && ring)
+        hipLaunchKernelGGL((prefill_ring_kernel<true, LUTMOE_FMT_REF>), grid, dim3(256), 0, s, *d, x, r, (void*)act,
+                           ncu);
+    else if (d->w13.format == LUTMOE_FMT_REF)
         hipLaunchKernelGGL((prefill_kernel<true, LUTMOE_FMT_REF>), grid, dim3(256), 0, s, *d, x, r, (void*)act, ncu);
     else if (d->w13.format == LUTMOE_FMT_NESTED)
         hipLaunchKernelGGL((prefill_ring_kernel<true, LUTMOE_FMT_NESTED>), grid, dim3(256), 0, s, *d, x, r,
@@ -837,10 +970,14 @@ int launch_prefill_gate_up(const lutmoe_moe_desc* d, const uint16_t* x, const Mo
 
 int launch_prefill_down(const lutmoe_moe_desc* d, const uint16_t* act, const MoeRouting& r,
                         float* y_pos, int P, hipStream_t s) {
-    if (d->w2.format != LUTMOE_FMT_REF && !ring_offsets_fit(d, r, P)) return LUTMOE_EUNSUPPORTED;
+    const bool ring = ring_offsets_fit(d, r, P);
+    if (d->w2.format != LUTMOE_FMT_REF && !ring) return LUTMOE_EUNSUPPORTED;
     const int nx = (d->hidden + kBN - 1) / kBN, ncu = cu_count();
     const dim3 grid(nx, max_tiles(P, r.num_experts_total) + tail_rows_max(nx, ncu));
-    if (d->w2.format == LUTMOE_FMT_REF)
+    if (d->w2.format == LUTMOE_FMT_REF && ring)
+        hipLaunchKernelGGL((prefill_ring_kernel<false, LUTMOE_FMT_REF>), grid, dim3(256), 0, s, *d, act, r,
+                           (void*)y_pos, ncu);
+    else if (d->w2.format == LUTMOE_FMT_REF)
         hipLaunchKernelGGL((prefill_kernel<false, LUTMOE_FMT_REF>), grid, dim3(256), 0, s, *d, act, r, (void*)y_pos,
                            ncu);
     else if (d->w2.format == LUTMOE_FMT_NESTED)

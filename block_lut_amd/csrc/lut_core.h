@@ -45,6 +45,9 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 
 __device__ __forceinline__ uint32_t lds_ld16(uint32_t a) { return *(lds_u16_t*)a; }
 
+typedef __attribute__((address_space(3))) const uint32_t lds_u32_t;
+__device__ __forceinline__ uint32_t lds_ld32(uint32_t a) { return *(lds_u32_t*)a; }
+
 // 32 REF byte codes (8 dwords, code j of the lane's 32 columns in byte j%4 of
 // dword j/4) against the bf16[256] codebook at LDS byte address `cbase`:
 // g[t] += sum_j x_t[j] * cb[code j], products exact in fp32 (bf16 x bf16),

@@ -374,11 +374,14 @@ def test_moe_layer_skewed_routing(gpu, fmt, T):
     assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
 
 
-@pytest.mark.parametrize("block_size,T", [(64, 1), (64, 9), (256, 1), (256, 9)])
-def test_moe_layer_ref_block_sizes(gpu, block_size, T):
-    """REF decode with absmax blocks of 64 and 256 (a lane's 32 aligned columns share one
-    block), following the reference GEMV's (x * cb) * absmax products; T=9 runs the down
-    projection of every active expert in parallel (y + combine)."""
+@pytest.mark.parametrize("block_size,T,path", [(64, 1, 1), (64, 9, 1), (256, 1, 1), (256, 9, 1),
+                                               (64, 40, 2), (192, 40, 2), (256, 300, 2)])
+def test_moe_layer_ref_block_sizes(gpu, block_size, T, path):
+    """REF with absmax blocks of 64, 192 and 256 columns.  Decode (path 1) follows the
+    reference GEMV's (x * cb) * absmax products (a lane's 32 aligned columns share one block;
+    T=9 runs the down projection of every active expert in parallel, y + combine); prefill
+    (path 2) the reference's dequantise-then-GEMM branch, bf16(cb * absmax) weights, with the
+    absmax block of each 64-column K step picked per weight row."""
     import torch
     from block_lut_amd import ops
     from block_lut_amd.formats import MoEWeights
@@ -390,9 +393,9 @@ def test_moe_layer_ref_block_sizes(gpu, block_size, T):
     xb = _x(rng, T, H)
     rw, rids = O.route(rng.standard_normal((T, E)).astype(np.float32), k)
     out = ops.moe_forward(moe, to_dev_bf16(xb, gpu), torch.from_numpy(rw).to(gpu),
-                          torch.from_numpy(rids).to(gpu), out_dtype=torch.float32, path=1)
-    ref = O.moe_layer(xb, rids, rw, w13.gemv_f32, w2.gemv_f32,
-                      shared=[(w13.gemv_f32(E + s), w2.gemv_f32(E + s)) for s in range(S)])
+                          torch.from_numpy(rids).to(gpu), out_dtype=torch.float32, path=path)
+    f13, f2 = (w13.gemv_f32, w2.gemv_f32) if path == 1 else (w13.deq_f32, w2.deq_f32)
+    ref = O.moe_layer(xb, rids, rw, f13, f2, shared=[(f13(E + s), f2(E + s)) for s in range(S)])
     assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
 
 
