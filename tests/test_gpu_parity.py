@@ -502,6 +502,53 @@ def test_moe_layer_qwen_decode_full_shape(gpu):
         assert rel_maxabs(out, ref) <= TOL, T
 
 
+@pytest.mark.parametrize("fmt", ["bl4", "ref", "nested"])
+def test_prefill_deepseek_shape(gpu, fmt):
+    """Grouped MFMA prefill at the DeepSeek-V2-Lite expert shape (H2048 I1408): 8 routed
+    experts top-2 + 1 shared, T=512, so tiles of 256 rows (shared expert), about 128-row
+    routed tiles and the tail split all occur; every format's ring loader at full K.  Oracle
+    on the touched experts' GPU-dequantised weights (dequantisation is bit-exact separately)."""
+    import torch
+    from block_lut_amd import ops
+    from block_lut_amd.formats import (BL4Stack, MoEWeights, NestedExpert, NestedStack,
+                                       RefStack)
+    H, I, E, S, k, T = 2048, 1408, 8, 1, 2, 512
+    g = torch.Generator(device=gpu).manual_seed(31)
+
+    def stack(M, K):
+        if fmt == "bl4":
+            codes = torch.randint(0, 256, (E + S, M, K // 2), dtype=torch.uint8, generator=g, device=gpu)
+            tabs = torch.sort(torch.randn((E + S, M, K // 64, 16), generator=g, device=gpu) * 0.02, dim=-1).values
+            return BL4Stack(codes, tabs.to(torch.bfloat16))
+        if fmt == "ref":
+            codes = torch.randint(0, 256, (E + S, M, K), dtype=torch.uint8, generator=g, device=gpu)
+            am = (torch.rand((E + S, M * K // 128), generator=g, device=gpu) * 0.05 + 0.01).to(torch.bfloat16)
+            cb = torch.sort(torch.randn(256, generator=g, device=gpu)).values.to(torch.bfloat16)
+            return RefStack(codes, am, cb, 128)
+        ex = []
+        n = M * K
+        for e in range(E + S):
+            b = [2, 3, 4][e % 3]
+            size = n // 4 + (n // 8 if b >= 3 else 0) + (n // 8 if b >= 4 else 0)
+            planes = torch.randint(0, 256, (size,), dtype=torch.uint8, generator=g, device=gpu)
+            tab = torch.sort(torch.randn((M, K // 64, 1 << b), generator=g, device=gpu) * 0.02, dim=-1).values
+            ex.append(NestedExpert(b, planes, tab.to(torch.bfloat16)))
+        return NestedStack(ex, M, K)
+
+    moe = MoEWeights(stack(2 * I, H), stack(H, I), H, I, E, S)
+    rng = np.random.default_rng(512)
+    xb = _x(rng, T, H)
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    rw, rids = O.route(lg, k)
+    out = ops.moe_forward(moe, to_dev_bf16(xb, gpu), torch.from_numpy(rw).to(gpu),
+                          torch.from_numpy(rids).to(gpu), out_dtype=torch.float32, path=2).cpu().numpy()
+    d13 = {e: O.bf16_to_f32(bf16_bits(ops.dequant(moe.w13, e, 1)[0])) for e in range(E + S)}
+    d2 = {e: O.bf16_to_f32(bf16_bits(ops.dequant(moe.w2, e, 1)[0])) for e in range(E + S)}
+    ref = O.moe_layer(xb, rids, rw, d13.__getitem__, d2.__getitem__,
+                      shared=[(d13[E + s], d2[E + s]) for s in range(S)])
+    assert rel_maxabs(out, ref) <= TOL
+
+
 def test_moe_layer_mixtral_shape(gpu):
     """Mixtral-8x7B layer shape (H4096 I14336, 8 experts top-2 with renormalisation): K spans
     two (W13) and seven (W2) 2048-column decode chunks, and the MFMA path runs 112 n-tiles per
