@@ -295,6 +295,28 @@ def main():
         log(f"[bench] prefill DeepSeek T=2048: {sec * 1e6:.0f} us, {flops / sec / 1e12:.1f} TFLOP/s")
         del lay, sp, g
         torch.cuda.empty_cache()
+        # the same prefill on the reference's own REF format (uint8 codes into
+        # one bf16[256] codebook, bf16 absmax per 128 weights)
+        from block_lut_amd.formats import RefStack
+        cbk = torch.sort(torch.randn(256, device=dev)).values.to(torch.bfloat16)
+
+        def ref_stack(E, M, K):
+            codes = torch.randint(0, 256, (E, M, K), dtype=torch.uint8, device=dev)
+            am = (torch.rand((E, M * K // 128), device=dev) * 0.05 + 0.01).to(torch.bfloat16)
+            return RefStack(codes, am, cbk, 128)
+
+        E2 = d["E"] + d["S"]
+        lay = MoEWeights(ref_stack(E2, 2 * d["I"], d["H"]), ref_stack(E2, d["H"], d["I"]),
+                         d["H"], d["I"], d["E"], d["S"])
+        sp = Step(lay, d, 2048)
+        g = graph_of([lambda: sp.run(path=ops.PATH_MFMA)])
+        time_graph(g, 2)
+        sec = time_graph(g, 10) / 10
+        extra["prefill_ref_dsv2_T2048_us"] = round(sec * 1e6, 1)
+        extra["prefill_ref_dsv2_T2048_TFLOPs"] = round(flops / sec / 1e12, 1)
+        log(f"[bench] prefill DeepSeek T=2048, REF format: {sec * 1e6:.0f} us, {flops / sec / 1e12:.1f} TFLOP/s")
+        del lay, sp, g
+        torch.cuda.empty_cache()
         ceil = measured_ceilings(torch, dev, d)
         extra.update(ceil)
         extra["prefill_dsv2_T2048_frac_hipblaslt_ceiling"] = round(
