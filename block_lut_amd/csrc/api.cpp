@@ -68,6 +68,10 @@ struct MoeLayout {
     size_t sync, route, topk_w, topk_ids, pair_ids, pair_w, offsets, perm, inv, active, act, y, total;
 };
 
+// Room for two K-split partial results of the down projection when that is
+// small (the split fills the GPU when the grouped down GEMM has few tiles).
+size_t prefill_y_splits(size_t P, int H) { return P * (size_t)H * 4 <= (size_t(32) << 20) ? 2 : 1; }
+
 MoeLayout moe_layout(const lutmoe_moe_desc* d, int T, int k) {
     const int E_tot = d->num_routed + d->num_shared;
     const size_t P = (size_t)T * (k + d->num_shared);
@@ -84,7 +88,7 @@ MoeLayout moe_layout(const lutmoe_moe_desc* d, int T, int k) {
     L.inv = o;      o = align_up(o + P * 4);
     L.active = o;   o = align_up(o + (E_tot + 1) * 4);
     L.act = o;      o = align_up(o + P * d->inter * 2);
-    L.y = o;        o = align_up(o + P * d->hidden * 4);
+    L.y = o;        o = align_up(o + P * d->hidden * 4 * prefill_y_splits(P, d->hidden));
     L.total = o;
     return L;
 }
@@ -369,8 +373,10 @@ int moe_forward_impl(const lutmoe_moe_desc* d, const void* x, const float* topk_
         (rc = launch_prefill_gate_up(d, (const uint16_t*)x, r, act, (int)P, s)))
         return rc;
     if (stages & LUTMOE_STAGE_DOWN) {
-        if ((rc = launch_prefill_down(d, act, r, y, (int)P, s))) return rc;
-        return launch_combine(y, r.inv, T, ke, d->hidden, out, out_dtype, s);
+        int nsplit = 1;
+        if ((rc = launch_prefill_down(d, act, r, y, (int)P, (int)prefill_y_splits(P, d->hidden), &nsplit, s)))
+            return rc;
+        return launch_combine(y, r.inv, T, ke, d->hidden, out, out_dtype, s, nsplit, (int64_t)P * d->hidden);
     }
     return LUTMOE_OK;
 }

@@ -509,7 +509,11 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int I = d.inter, H = d.hidden;
     const int K = kGateUp ? H : I;
-    const int nkb = K / kBK;
+    // K steps [kb0, kb0 + nkb) of this CTA: all of K, or split z of gridDim.z
+    // (down projection only; partial results go to separate y buffers)
+    const int nsplit = kGateUp ? 1 : (int)gridDim.z, zs = kGateUp ? 0 : (int)blockIdx.z;
+    const int kb0 = (K / kBK) * zs / nsplit;
+    const int nkb = (K / kBK) * (zs + 1) / nsplit - kb0;
     const int n0 = blockIdx.x * (kGateUp ? kBN / 2 : kBN);
     const int nvalid = min(kBM, ti.n - ti.m0);
 
@@ -720,13 +724,13 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
     // prologue: stages 0..2 in flight; wait for stage 0, then issue the LDS
     // reads of k-substep 0's fragments
     const int npro = min(kStages, nkb);
-    for (int st = 0; st < npro; ++st) issue(st, ring + st * kSlot);
+    for (int st = 0; st < npro; ++st) issue(kb0 + st, ring + st * kSlot);
     ring_wait_barrier<kDma>(npro - 1);
     u32x4_t codes[kNC];
     float am[2] = {0.f, 0.f};
     bf16x8_t bf[2], af[NMT];
     read_codes(ring, codes);
-    read_am(ring, 0, am);
+    read_am(ring, kb0, am);
     Lookup8 lk0 = frag_b(ring, codes, 0, 0), lk1 = frag_b(ring, codes, 0, 1);
     frag_a(ring, 0, af, 0, NMT);
 
@@ -757,9 +761,9 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
                 // in flight) and every read of this slot is done (its values
                 // are in registers) -> refill it with stage kb+3
                 ring_wait_barrier<kDma>(kb + 2 < nkb ? 1 : 0);
-                if (kb + 3 < nkb) issue(kb + 3, sl);
+                if (kb + 3 < nkb) issue(kb0 + kb + 3, sl);
                 read_codes(nsl, codes_n);
-                read_am(nsl, kb + 1, am_n);
+                read_am(nsl, kb0 + kb + 1, am_n);
                 frag_a(nsl, 0, af_n, 0, kHalfA);
                 lk0 = frag_b(nsl, codes_n, 0, 0);
             } else {
@@ -864,10 +868,12 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
 
 template <bool kGateUp, int kFmt>
 __global__ __launch_bounds__(256, 1) void prefill_ring_kernel(lutmoe_moe_desc d, const uint16_t* __restrict__ src,
-                                                              MoeRouting rt, void* __restrict__ dst, int ncu) {
+                                                              MoeRouting rt, void* __restrict__ dst, int ncu,
+                                                              int64_t split_stride) {
     __shared__ __attribute__((aligned(16))) uint8_t ring[RingSlot<kFmt>::kLds];
     const TileInfo ti = find_tile(rt, blockIdx.y, ncu);
     if (ti.e < 0) return;
+    if (!kGateUp) dst = (float*)dst + blockIdx.z * split_stride;   // this K split's partial y
     if constexpr (kFmt == LUTMOE_FMT_REF) {
         // fp32 codebook after the stages (ordered before its first read by
         // the prologue's barrier)
@@ -956,36 +962,45 @@ int launch_prefill_gate_up(const lutmoe_moe_desc* d, const uint16_t* x, const Mo
     const dim3 grid(nx, max_tiles(P, r.num_experts_total) + tail_rows_max(nx, ncu));
     if (d->w13.format == LUTMOE_FMT_REF && ring)
         hipLaunchKernelGGL((prefill_ring_kernel<true, LUTMOE_FMT_REF>), grid, dim3(256), 0, s, *d, x, r, (void*)act,
-                           ncu);
+                           ncu, (int64_t)0);
     else if (d->w13.format == LUTMOE_FMT_REF)
         hipLaunchKernelGGL((prefill_kernel<true, LUTMOE_FMT_REF>), grid, dim3(256), 0, s, *d, x, r, (void*)act, ncu);
     else if (d->w13.format == LUTMOE_FMT_NESTED)
         hipLaunchKernelGGL((prefill_ring_kernel<true, LUTMOE_FMT_NESTED>), grid, dim3(256), 0, s, *d, x, r,
-                           (void*)act, ncu);
+                           (void*)act, ncu, (int64_t)0);
     else
         hipLaunchKernelGGL((prefill_ring_kernel<true, LUTMOE_FMT_BL4>), grid, dim3(256), 0, s, *d, x, r, (void*)act,
-                           ncu);
+                           ncu, (int64_t)0);
     return check_launch();
 }
 
 int launch_prefill_down(const lutmoe_moe_desc* d, const uint16_t* act, const MoeRouting& r,
-                        float* y_pos, int P, hipStream_t s) {
+                        float* y_pos, int P, int max_split, int* nsplit, hipStream_t s) {
     const bool ring = ring_offsets_fit(d, r, P);
     if (d->w2.format != LUTMOE_FMT_REF && !ring) return LUTMOE_EUNSUPPORTED;
     const int nx = (d->hidden + kBN - 1) / kBN, ncu = cu_count();
-    const dim3 grid(nx, max_tiles(P, r.num_experts_total) + tail_rows_max(nx, ncu));
+    // K split in two when the tiles (at most ceil(P/256) + active experts rows
+    // of nx CTAs) would leave CUs idle: each half accumulates into its own y
+    const int E_tot = r.num_experts_total;
+    const int64_t rows_est = (P + kBM - 1) / kBM + (P < E_tot ? P : E_tot);
+    const int ns = ring && max_split >= 2 && ncu > 0 && (int64_t)nx * rows_est < ncu &&
+                           d->w2.cols / kBK >= 2 * kStages ? 2 : 1;
+    *nsplit = ns;
+    const int ncu_tail = ns > 1 ? 0 : ncu;   // one round: no tail split
+    const dim3 grid(nx, max_tiles(P, E_tot) + tail_rows_max(nx, ncu_tail), ns);
+    const int64_t stride = (int64_t)P * d->hidden;
     if (d->w2.format == LUTMOE_FMT_REF && ring)
         hipLaunchKernelGGL((prefill_ring_kernel<false, LUTMOE_FMT_REF>), grid, dim3(256), 0, s, *d, act, r,
-                           (void*)y_pos, ncu);
+                           (void*)y_pos, ncu_tail, stride);
     else if (d->w2.format == LUTMOE_FMT_REF)
         hipLaunchKernelGGL((prefill_kernel<false, LUTMOE_FMT_REF>), grid, dim3(256), 0, s, *d, act, r, (void*)y_pos,
                            ncu);
     else if (d->w2.format == LUTMOE_FMT_NESTED)
         hipLaunchKernelGGL((prefill_ring_kernel<false, LUTMOE_FMT_NESTED>), grid, dim3(256), 0, s, *d, act, r,
-                           (void*)y_pos, ncu);
+                           (void*)y_pos, ncu_tail, stride);
     else
         hipLaunchKernelGGL((prefill_ring_kernel<false, LUTMOE_FMT_BL4>), grid, dim3(256), 0, s, *d, act, r,
-                           (void*)y_pos, ncu);
+                           (void*)y_pos, ncu_tail, stride);
     return check_launch();
 }
 

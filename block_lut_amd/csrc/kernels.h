@@ -72,14 +72,18 @@ int launch_permute(const int32_t* pair_ids, int T, int k_eff, int E_tot, int32_t
 int launch_route_pairs(const int32_t* topk_ids, const float* topk_w, int T, int k, int E, int S,
                        int32_t* offsets, int32_t* perm, int32_t* inv, int32_t* active, int32_t* pair_ids,
                        float* pair_w, hipStream_t s);
+// nsplit > 1: y_pos holds nsplit partial results (K splits of the down
+// projection), split_stride floats apart, summed per position first.
 int launch_combine(const float* y_pos, const int32_t* inv, int T, int k_eff, int H,
-                   void* out, int out_dtype, hipStream_t s);
+                   void* out, int out_dtype, hipStream_t s, int nsplit = 1, int64_t split_stride = 0);
 
 // gemm.hip (prefill, MFMA)
 int launch_prefill_gate_up(const lutmoe_moe_desc* d, const uint16_t* x, const MoeRouting& r,
                            uint16_t* act, int P, hipStream_t s);
+// y_pos holds room for max_split partial results of P x H floats; *nsplit
+// returns how many K splits ran (combine sums them).
 int launch_prefill_down(const lutmoe_moe_desc* d, const uint16_t* act, const MoeRouting& r,
-                        float* y_pos, int P, hipStream_t s);
+                        float* y_pos, int P, int max_split, int* nsplit, hipStream_t s);
 
 // encode.hip
 int launch_bl4_encode(const float* w, int64_t nblocks, int n_iter, uint8_t* codes,

@@ -271,9 +271,12 @@ __global__ __launch_bounds__(1024) void permute_chunk_kernel(PairSrc ps, int P, 
     }
 }
 
+// out[t] = sum over the token's positions p (slot order) of y[p], each y[p]
+// itself the sum of nsplit partial rows (K-split down projection) at stride
+// sstride, added in split order.
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ y, const int32_t* __restrict__ inv,
                                                       int T, int ke, int H, void* __restrict__ out,
-                                                      int out_dtype) {
+                                                      int out_dtype, int nsplit, int64_t sstride) {
     const int hq = H / 4;
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= (int64_t)T * hq) return;
@@ -282,7 +285,11 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
     for (int q = 0; q < ke; ++q) {
         const int p = inv[(int64_t)t * ke + q];
         if (p < 0) continue;
-        const float4 v = *reinterpret_cast<const float4*>(y + (int64_t)p * H + h);
+        float4 v = *reinterpret_cast<const float4*>(y + (int64_t)p * H + h);
+        for (int sp = 1; sp < nsplit; ++sp) {
+            const float4 u = *reinterpret_cast<const float4*>(y + sp * sstride + (int64_t)p * H + h);
+            v.x += u.x; v.y += u.y; v.z += u.z; v.w += u.w;
+        }
         s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
     }
     if (out_dtype == LUTMOE_DTYPE_F32) {
@@ -347,10 +354,10 @@ int launch_route_pairs(const int32_t* topk_ids, const float* topk_w, int T, int 
 }
 
 int launch_combine(const float* y_pos, const int32_t* inv, int T, int k_eff, int H, void* out,
-                   int out_dtype, hipStream_t s) {
+                   int out_dtype, hipStream_t s, int nsplit, int64_t split_stride) {
     const int64_t n = (int64_t)T * (H / 4);
     hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, y_pos,
-                       inv, T, k_eff, H, out, out_dtype);
+                       inv, T, k_eff, H, out, out_dtype, nsplit, split_stride);
     return check_launch();
 }
 
