@@ -419,4 +419,13 @@ int lutmoe_bl4_encode(const float* w, int64_t nblocks, int n_iter, uint8_t* code
     return launch_bl4_encode(w, nblocks, n_iter, codes, tables_f16, stream_of(stream));
 }
 
+int lutmoe_ref_encode(const void* w_bf16, const float* codebook, int64_t n, int block_size, uint8_t* codes,
+                      void* absmax_bf16, void* stream) {
+    if (n < 0 || block_size <= 0) return LUTMOE_EINVAL;
+    if (n == 0) return LUTMOE_OK;
+    if (!w_bf16 || !codebook || !codes || !absmax_bf16) return LUTMOE_EINVAL;
+    return launch_ref_encode((const uint16_t*)w_bf16, codebook, n, block_size, codes, (uint16_t*)absmax_bf16,
+                             stream_of(stream));
+}
+
 }  // extern "C"

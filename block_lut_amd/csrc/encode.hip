@@ -192,6 +192,47 @@ __global__ __launch_bounds__(256) void bl4_encode_kernel(const float* __restrict
     }
 }
 
+// REF encoder (the reference's encode_blocklut_kernel,
+// vllm_lut/fast_encode.py:22-72): bf16 weights, one fp32[256] codebook,
+// blocks of block_size consecutive weights.  Per block: absmax = max |w|
+// (fp32, at least 1e-10); each weight w / absmax (IEEE fp32 division) gets
+// the index of the nearest codebook entry, the first one on equal distances
+// (a scan of all 256 entries: the codebook need not be sorted); absmax is
+// stored as bf16 (round to nearest even).  One wave per block; the codebook
+// sits in LDS and every lane reads the same entry (a broadcast).
+__global__ __launch_bounds__(256) void ref_encode_kernel(const uint16_t* __restrict__ w,
+                                                         const float* __restrict__ codebook, int64_t n,
+                                                         int block_size, int64_t nblocks,
+                                                         uint8_t* __restrict__ codes,
+                                                         uint16_t* __restrict__ absmax) {
+    __shared__ float s_cb[256];
+    s_cb[threadIdx.x] = codebook[threadIdx.x];
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    for (int64_t b = (int64_t)blockIdx.x * 4 + wv; b < nblocks; b += (int64_t)gridDim.x * 4) {
+        const int64_t start = b * block_size;
+        const int len = (int)min((int64_t)block_size, n - start);
+        float mx = 0.f;
+        for (int i = lane; i < len; i += 64) mx = fmaxf(mx, fabsf(bf16_to_f32(w[start + i])));
+        mx = fmaxf(wave_reduce_max(mx), 1e-10f);
+        for (int i = lane; i < len; i += 64) {
+            const float v = bf16_to_f32(w[start + i]) / mx;
+            float bd = fabsf(v - s_cb[0]);
+            int best = 0;
+#pragma unroll 8
+            for (int c = 1; c < 256; ++c) {
+                const float dd = fabsf(v - s_cb[c]);
+                if (dd < bd) {
+                    bd = dd;
+                    best = c;
+                }
+            }
+            codes[start + i] = (uint8_t)best;
+        }
+        if (lane == 0) absmax[b] = (uint16_t)f32_to_bf16(mx);
+    }
+}
+
 }  // namespace
 
 namespace lutmoe_host {
@@ -202,6 +243,16 @@ int launch_bl4_encode(const float* w, int64_t nblocks, int n_iter, uint8_t* code
     if (ctas > 65536) ctas = 65536;
     hipLaunchKernelGGL(bl4_encode_kernel, dim3((unsigned)ctas), dim3(256), 0, s, w, nblocks,
                        n_iter, codes, tables);
+    return check_launch();
+}
+
+int launch_ref_encode(const uint16_t* w, const float* codebook, int64_t n, int block_size, uint8_t* codes,
+                      uint16_t* absmax, hipStream_t s) {
+    const int64_t nblocks = (n + block_size - 1) / block_size;
+    int64_t ctas = (nblocks + 3) / 4;
+    if (ctas > 65536) ctas = 65536;
+    hipLaunchKernelGGL(ref_encode_kernel, dim3((unsigned)ctas), dim3(256), 0, s, w, codebook, n, block_size,
+                       nblocks, codes, absmax);
     return check_launch();
 }
 

@@ -264,6 +264,27 @@ def bl4_encode(weight: torch.Tensor, n_iter: int = 50) -> Tuple[torch.Tensor, to
     return codes, tables
 
 
+def ref_encode(weight: torch.Tensor, codebook: torch.Tensor, block_size: int = 128
+               ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """REF encoder on the GPU (the reference's encode_lut, vllm_lut/fast_encode.py:22-72):
+    bf16 weights (any shape, flattened) and an fp32[256] codebook -> (uint8 codes [N],
+    bf16 absmax [ceil(N / block_size)])."""
+    _dev(weight, torch.bfloat16, "weight")
+    _dev(codebook, torch.float32, "codebook")
+    if codebook.numel() != 256:
+        raise ValueError("codebook must hold 256 entries")
+    if block_size <= 0:
+        raise ValueError("block_size must be positive")
+    w = weight.contiguous().reshape(-1)
+    cb = codebook.contiguous()
+    n = w.numel()
+    codes = torch.empty(n, dtype=torch.uint8, device=w.device)
+    absmax = torch.empty(-(-n // block_size), dtype=torch.bfloat16, device=w.device)
+    N.check("lutmoe_ref_encode", N.lib().lutmoe_ref_encode(w.data_ptr(), cb.data_ptr(), n, block_size,
+                                                           codes.data_ptr(), absmax.data_ptr(), _stream()))
+    return codes, absmax
+
+
 def _any_tensor(w: WeightStack) -> torch.Tensor:
     for name in ("codes", "tables", "absmax"):
         t = getattr(w, name, None)

@@ -216,6 +216,16 @@ int lutmoe_moe_forward_logits(const lutmoe_moe_desc* d, const void* x_dev, const
 int lutmoe_bl4_encode(const float* w_dev, int64_t nblocks, int n_iter, uint8_t* codes_dev,
                       uint16_t* tables_f16_dev, void* stream);
 
+/* REF encoder, replacing encode_blocklut_kernel / launch_encode
+ * (vllm_lut/fast_encode.py:22-72, 80-99): bf16 weights [n] and an fp32[256]
+ * codebook -> uint8 codes [n] (nearest entry of w / absmax, first index on
+ * equal distances) and bf16 absmax [ceil(n / block_size)] (max |w| of each
+ * block of block_size weights, at least 1e-10).  Asynchronous on `stream`
+ * (the reference synchronises the device after the launch); IEEE division
+ * (the reference builds with fast math). */
+int lutmoe_ref_encode(const void* w_bf16_dev, const float* codebook_dev, int64_t n, int block_size,
+                      uint8_t* codes_dev, void* absmax_bf16_dev, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -152,6 +152,29 @@ def ref_quantize(weight, codebook_bf16, block_size: int = REF_BLOCK, input_is_bf
     return idx[:n], f32_to_bf16(absmax.reshape(-1))             # :298-304
 
 
+def ref_encode_fast(w_bf16_bits, codebook_f32, block_size: int = REF_BLOCK):
+    """encode_blocklut_kernel (vllm_lut/fast_encode.py:22-72): bf16 weights, fp32[256]
+    codebook.  Per block of block_size weights (the last one shorter, no padding):
+    absmax = max |w| in fp32, at least 1e-10 (:43-47); v = w / absmax in fp32 (:51, IEEE
+    here); index of the nearest codebook entry, the first one on equal distances (strict <
+    in the scan, :54-62, which is numpy's argmin); absmax stored as bf16 (:68).
+    Returns (indices uint8 [N], absmax bf16 bits [ceil(N / block_size)])."""
+    w = bf16_to_f32(np.asarray(w_bf16_bits, np.uint16).reshape(-1))
+    cb = np.asarray(codebook_f32, np.float32).reshape(-1)
+    n = w.size
+    nb = -(-n // block_size)
+    idx = np.empty(n, np.uint8)
+    am = np.empty(nb, np.float32)
+    for b in range(nb):
+        blk = w[b * block_size:(b + 1) * block_size]
+        m = np.float32(max(np.float32(np.abs(blk).max()), np.float32(1e-10)))
+        am[b] = m
+        v = (blk / m).astype(np.float32)
+        d = np.abs(v[:, None] - cb[None, :]).astype(np.float32)
+        idx[b * block_size:b * block_size + blk.size] = d.argmin(axis=1)
+    return idx, f32_to_bf16(am)
+
+
 def ref_dequant(indices, absmax_bf16, codebook_bf16, block_size: int = REF_BLOCK) -> np.ndarray:
     """decompress_blocklut (quantizer.py:449-477) == cuda_blocklut_recover_to_bf16
     (csrc/kernels/tensor_recover.cu:101-142): bf16(f32(cb[c]) * f32(absmax[blk]))."""

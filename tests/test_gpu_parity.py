@@ -502,6 +502,65 @@ def test_moe_layer_qwen_decode_full_shape(gpu):
         assert rel_maxabs(out, ref) <= TOL, T
 
 
+@pytest.mark.parametrize("n,block_size,sorted_cb", [(128 * 300 + 77, 128, True), (5000, 64, False),
+                                                    (4097, 100, True), (1, 128, True)])
+def test_ref_encode_bit_exact(gpu, n, block_size, sorted_cb):
+    """GPU REF encoder (encode_lut) vs the oracle's restatement of encode_blocklut_kernel:
+    codes and bf16 absmax bit-identical, with a short last block, an all-zero block, weights
+    on exact midpoints between entries (first index wins) and an unsorted codebook."""
+    import torch
+    from block_lut_amd import fast_encode, ops
+    rng = np.random.default_rng(n + block_size)
+    cb = rng.uniform(-1, 1, 256).astype(np.float32)
+    if sorted_cb:
+        cb = np.sort(cb)
+    w = rng.standard_normal(n).astype(np.float32) * 0.02
+    if n > 3 * block_size:
+        w[block_size:2 * block_size] = 0.0                     # all-zero block
+        s = np.sort(cb)
+        m = ((s[100:120] + s[101:121]) / 2).astype(np.float32)  # midpoints, absmax 1
+        w[2 * block_size:2 * block_size + 20] = m
+        w[2 * block_size + 20] = 1.0
+    wb = O.f32_to_bf16(w)
+    wt = torch.from_numpy(wb.view(np.int16)).view(torch.bfloat16).to(gpu)
+    codes, am = ops.ref_encode(wt, torch.from_numpy(cb).to(gpu), block_size)
+    ic, ia = O.ref_encode_fast(wb, cb, block_size)
+    assert np.array_equal(codes.cpu().numpy(), ic)
+    assert np.array_equal(am.view(torch.int16).cpu().numpy().view(np.uint16), ia)
+    c2, a2 = fast_encode.encode_lut(wt, torch.from_numpy(cb).to(gpu), block_size)
+    assert torch.equal(c2, codes.cpu()) and torch.equal(a2, am.cpu())
+
+
+def test_ref_encode_expert_size_roundtrip(gpu):
+    """A whole Qwen W13 expert (5.77 M weights) encoded on the GPU: sampled blocks match the
+    oracle, and the GPU dequantisation of the result is within the codebook's resolution."""
+    import torch
+    from block_lut_amd import ops
+    from block_lut_amd.formats import RefStack
+    M, K = 2816, 2048
+    g = torch.Generator(device=gpu).manual_seed(9)
+    w = (torch.randn((M, K), generator=g, device=gpu) * 0.02).to(torch.bfloat16)
+    cb = torch.sort(torch.randn(256, generator=g, device=gpu) * 0.5).values
+    cb = cb / cb.abs().max()
+    codes, am = ops.ref_encode(w, cb, 128)
+    wb = w.view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1)
+    rng = np.random.default_rng(9)
+    for b in rng.choice(M * K // 128, 40, replace=False):
+        ic, ia = O.ref_encode_fast(wb[b * 128:(b + 1) * 128], cb.cpu().numpy(), 128)
+        assert np.array_equal(codes[b * 128:(b + 1) * 128].cpu().numpy(), ic)
+        assert am[b].view(torch.int16).item() & 0xffff == int(ia[0])
+    st = RefStack(codes.view(1, M, K), am.view(1, -1), cb.to(torch.bfloat16), 128)
+    deq = ops.dequant(st, 0, 1)[0].float()
+    err = (deq - w.float()).abs().max().item()
+    # nearest-entry error: half the widest gap of the (bf16-stored) codebook, plus bf16
+    # rounding of the entries, the absmax and the product, times the largest absmax
+    # (w / absmax lies in [-1, 1]: beyond the outermost entries the whole distance counts)
+    cbs = cb.to(torch.bfloat16).float().cpu().numpy()
+    worst = max(np.diff(cbs).max() / 2, 1.0 - cbs.max(), cbs.min() + 1.0)
+    bound = (worst + 3 * 2.0 ** -8) * float(am.float().max())
+    assert err <= bound * 1.01, (err, bound)
+
+
 @pytest.mark.parametrize("fmt", ["bl4", "ref", "nested"])
 def test_prefill_deepseek_shape(gpu, fmt):
     """Grouped MFMA prefill at the DeepSeek-V2-Lite expert shape (H2048 I1408): 8 routed

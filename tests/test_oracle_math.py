@@ -80,6 +80,43 @@ def test_ref_gemv_vs_torch_matmul():
     assert np.abs(got - ref).max() <= 1e-6 * np.abs(ref).max()
 
 
+def test_ref_encode_fast_equals_golden_pinned_quantize_on_bf16_codebooks():
+    """With an fp32 codebook holding bf16 values and bf16 weights, the fast encoder's rule
+    (fp32 absmax and division, first nearest entry) is the quantizer's fp32 branch, which the
+    reference's own outputs pin (test_oracle_golden)."""
+    rng = np.random.default_rng(21)
+    cb_bf16 = O.f32_to_bf16(np.sort(rng.standard_normal(256).astype(np.float32)))
+    w = O.f32_to_bf16(rng.standard_normal(128 * 37 + 51).astype(np.float32) * 0.02)
+    idx, am = O.ref_encode_fast(w, O.bf16_to_f32(cb_bf16), 128)
+    idx2, am2 = O.ref_quantize(O.bf16_to_f32(w), cb_bf16, 128)
+    assert np.array_equal(idx, idx2) and np.array_equal(am, am2)
+
+
+def test_ref_encode_fast_argmin_ties_and_zero_block():
+    """Every index is a nearest entry of w / absmax (fp32), ties go to the first index
+    (exact midpoints of a non-uniform codebook, and duplicated entries), an all-zero block
+    keeps absmax 1e-10 and maps to the entry nearest 0; an unsorted codebook is scanned
+    whole."""
+    cb = np.sort(np.random.default_rng(3).uniform(-1, 1, 256)).astype(np.float32)
+    cb[10] = cb[11]                                   # duplicated entry: index 10 wins
+    mids = ((cb[20:40] + cb[21:41]) / 2).astype(np.float32)
+    # weights equal to the midpoints (absmax 1: include +-1 so w / absmax == w)
+    w = np.concatenate([mids, np.float32([1.0, -1.0, cb[11], 0.5])])
+    wb = O.f32_to_bf16(w)
+    idx, am = O.ref_encode_fast(wb, cb, 64)
+    v = O.bf16_to_f32(wb) / np.float32(1.0)
+    d = np.abs(v[:, None] - cb[None, :])
+    first = np.array([np.flatnonzero(row == row.min())[0] for row in d])
+    assert np.array_equal(idx, first)
+    assert idx[w.size - 2] == 10 or abs(O.bf16_to_f32(wb)[w.size - 2] - cb[10]) > 0
+    zi, zam = O.ref_encode_fast(np.zeros(64, np.uint16), cb, 64)
+    assert np.all(zi == np.abs(cb).argmin())
+    assert zam[0] == O.f32_to_bf16(np.float32(1e-10))
+    perm = np.random.default_rng(4).permutation(256)
+    pi, _ = O.ref_encode_fast(wb, cb[perm], 64)
+    assert np.array_equal(cb[perm][pi], cb[first])
+
+
 def test_bitplane_pack_roundtrip_all_codes():
     codes = np.tile(np.arange(256, dtype=np.uint8), 4)
     packed = O.bitplane_pack_ref(codes)
