@@ -138,3 +138,50 @@ class NestedExpertset:
                            to_dev_bf16(self.table_bf16(e), device))
               for e, b in enumerate(self.bits)]
         return NestedStack(ex, self.M, self.K)
+
+
+# ------------------------------------------------------------------ GGUF files
+# A minimal GGUF v3 writer for the loader tests: the layout of the GGUF
+# specification (header, typed metadata, tensor infos, data aligned to 32
+# bytes), as convert_lut.py's GGUFWriter produces it.  BLOCKLUT8's type id is
+# defined in the reference's (absent) patched gguf-py; any id works for the
+# loader, which sizes tensors by their offsets.
+GGUF_BLOCKLUT8_TEST_ID = 1024
+
+
+def write_gguf(path, kv, tensors, align=32):
+    """kv: list of (key, value) with value bool / int (uint32) / float / str / list of
+    uint16; tensors: list of (name, dims, type_id, raw bytes)."""
+    import struct
+
+    def s(x):
+        b = x.encode()
+        return struct.pack("<Q", len(b)) + b
+
+    def val(v):
+        if isinstance(v, bool):
+            return struct.pack("<I", 7) + struct.pack("<?", v)
+        if isinstance(v, int):
+            return struct.pack("<I", 4) + struct.pack("<I", v)
+        if isinstance(v, float):
+            return struct.pack("<I", 6) + struct.pack("<f", v)
+        if isinstance(v, str):
+            return struct.pack("<I", 8) + s(v)
+        a = np.asarray(v, dtype=np.uint16)
+        return struct.pack("<I", 9) + struct.pack("<IQ", 2, a.size) + a.tobytes()
+
+    head = struct.pack("<IIQQ", 0x46554747, 3, len(tensors), len(kv))
+    head += b"".join(s(k) + val(v) for k, v in kv)
+    off = 0
+    infos, blobs = b"", []
+    for name, dims, tid, raw in tensors:
+        infos += s(name) + struct.pack("<I", len(dims)) + b"".join(struct.pack("<Q", d) for d in dims)
+        infos += struct.pack("<IQ", tid, off)
+        raw = bytes(raw)
+        pad = (-len(raw)) % align
+        blobs.append(raw + b"\0" * pad)
+        off += len(raw) + pad
+    body = head + infos
+    body += b"\0" * ((-len(body)) % align)
+    with open(path, "wb") as f:
+        f.write(body + b"".join(blobs))

@@ -561,6 +561,87 @@ def test_ref_encode_expert_size_roundtrip(gpu):
     assert err <= bound * 1.01, (err, bound)
 
 
+def test_checkpoint_loaders(gpu, tmp_path):
+    """The reference's on-disk layouts -> device stacks: convert_checkpoint.py tensors
+    (flattened uint8 codes, `<name>.absmax`, `model._lut_codebook`) and convert_lut.py GGUF
+    files (BLOCKLUT8 blobs [codes | absmax]; nested files as bit-plane sections read at
+    tiers 0/1/2 with the full / mapped64 / mapped16 tables).  Codes, absmax and tables
+    arrive bit-exact (dequantisation equal to the oracle's), and a layer built from the
+    converted tensors matches the oracle."""
+    import torch
+    from block_lut_amd import checkpoint as C
+    from block_lut_amd import ops
+    from lutmoe_testutil import GGUF_BLOCKLUT8_TEST_ID, write_gguf
+    E, H, I = 4, 256, 128
+    rng = np.random.default_rng(77)
+    cb = golden_codebook()
+    q = {}
+    for e in range(E):
+        for p, shape in (("gate", (I, H)), ("up", (I, H)), ("down", (H, I))):
+            w = (rng.standard_normal(shape) * 0.02).astype(np.float32)
+            q[C.expert_key(0, e, p)] = O.ref_quantize(w, cb, 128)
+
+    def bf16_t(bits):
+        return torch.from_numpy(np.asarray(bits, np.uint16).view(np.int16)).view(torch.bfloat16)
+
+    def deq_check(stack, codes_of, table_bits):
+        for e in range(E):
+            got = bf16_bits(ops.dequant(stack, e, 1)[0]).reshape(-1)
+            c, a = codes_of(e)
+            assert np.array_equal(got, O.ref_dequant(c, a, table_bits, 128))
+
+    def w13_of(e, mask=0xFF):
+        g, u = q[C.expert_key(0, e, "gate")], q[C.expert_key(0, e, "up")]
+        return np.concatenate([g[0], u[0]]) & mask, np.concatenate([g[1], u[1]])
+
+    def w2_of(e, mask=0xFF):
+        d = q[C.expert_key(0, e, "down")]
+        return d[0] & mask, d[1]
+
+    # convert_checkpoint.py layout
+    td = {"model._lut_codebook": bf16_t(cb)}
+    for k, (idx, am) in q.items():
+        td[k] = torch.from_numpy(idx.copy())
+        td[k + ".absmax"] = bf16_t(am)
+    lay = C.load_converted_layer(td, 0, E, H, I, device=gpu)
+    deq_check(lay.w13, w13_of, cb)
+    deq_check(lay.w2, w2_of, cb)
+    T = 40
+    xb = _x(rng, T, H)
+    rw, rids = O.route(rng.standard_normal((T, E)).astype(np.float32), 2)
+    out = ops.moe_forward(lay, to_dev_bf16(xb, gpu), torch.from_numpy(rw).to(gpu),
+                          torch.from_numpy(rids).to(gpu), out_dtype=torch.float32, path=2).cpu().numpy()
+    deq = lambda f: (lambda e: O.bf16_to_f32(O.ref_dequant(*f(e), cb, 128)))
+    ref = O.moe_layer(xb, rids, rw, lambda e: deq(w13_of)(e).reshape(2 * I, H),
+                      lambda e: deq(w2_of)(e).reshape(H, I))
+    assert rel_maxabs(out, ref) <= TOL
+
+    # GGUF, plain and nested
+    for nested in (False, True):
+        tens = []
+        for k, (idx, am) in q.items():
+            body = O.bitplane_pack_ref(idx) if nested else idx
+            tens.append((k, (idx.size,), GGUF_BLOCKLUT8_TEST_ID, np.concatenate([body, am.view(np.uint8)]).tobytes()))
+        kv = [("lut-moe.enabled", True), ("lut-moe.block_size", 128), ("lut-moe.k", 256),
+              ("lut-moe.nested_lut", nested), ("lut-moe.lut_table", cb.tolist())]
+        if nested:
+            kv += [("lut-moe.lut_mapped64", cb[:64].tolist()), ("lut-moe.lut_mapped16", cb[:16].tolist())]
+        path = str(tmp_path / f"m{int(nested)}.gguf")
+        write_gguf(path, kv, tens)
+        g = C.read_gguf(path)
+        for tier in ((0, 1, 2) if nested else (0,)):
+            mask, tab = {0: (0xFF, cb), 1: (0x3F, cb[:64]), 2: (0x0F, cb[:16])}[tier]
+            tab256 = np.full(256, tab[-1], np.uint16)
+            tab256[:tab.size] = tab
+            lay = C.load_gguf_layer(g, 0, E, H, I, tier=tier, device=gpu)
+            for e in range(E):
+                c13, a13 = w13_of(e, mask)
+                assert np.array_equal(lay.w13.codes[e].cpu().numpy().reshape(-1), c13)
+                assert np.array_equal(bf16_bits(lay.w13.absmax[e]).reshape(-1), a13)
+            deq_check(lay.w13, lambda e: w13_of(e, mask), tab256)
+            deq_check(lay.w2, lambda e: w2_of(e, mask), tab256)
+
+
 @pytest.mark.parametrize("fmt", ["bl4", "ref", "nested"])
 def test_prefill_deepseek_shape(gpu, fmt):
     """Grouped MFMA prefill at the DeepSeek-V2-Lite expert shape (H2048 I1408): 8 routed

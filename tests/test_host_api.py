@@ -5,6 +5,7 @@ import os
 import subprocess
 import sys
 
+import numpy as np
 import pytest
 import torch
 
@@ -106,3 +107,30 @@ def test_bench_refuses_more_than_one_gpu():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
                        capture_output=True, text=True)
     assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+def test_gguf_reader_roundtrip_and_expert_names(tmp_path):
+    """read_gguf parses what a GGUF v3 writer produces (typed metadata, arrays, tensor
+    infos, 32-byte aligned data) and sizes an unknown-type tensor by the next offset."""
+    from block_lut_amd import checkpoint as C
+    from lutmoe_testutil import GGUF_BLOCKLUT8_TEST_ID, write_gguf
+    rng = np.random.default_rng(0)
+    a = rng.integers(0, 256, 1000, dtype=np.uint8)
+    b = rng.integers(0, 256, 333, dtype=np.uint8)
+    lut = rng.integers(0, 65536, 256, dtype=np.uint16)
+    p = str(tmp_path / "t.gguf")
+    write_gguf(p, [("lut-moe.enabled", True), ("lut-moe.block_size", 128), ("general.name", "x"),
+                   ("lut-moe.lut_table", lut.tolist()), ("hparams.eps", 1e-6)],
+               [("model.layers.0.mlp.experts.0.gate_proj.weight", (1000,), GGUF_BLOCKLUT8_TEST_ID, a.tobytes()),
+                ("model.norm.weight", (333,), 0, b.tobytes())])
+    g = C.read_gguf(p)
+    assert g.kv["lut-moe.enabled"] is True and g.kv["lut-moe.block_size"] == 128
+    assert g.kv["general.name"] == "x" and np.array_equal(g.kv["lut-moe.lut_table"], lut)
+    dims, tid, raw = g.tensors["model.layers.0.mlp.experts.0.gate_proj.weight"]
+    assert dims == (1000,) and tid == GGUF_BLOCKLUT8_TEST_ID
+    assert np.array_equal(raw[:1000], a)
+    assert np.array_equal(g.tensors["model.norm.weight"][2][:333], b)
+    assert C.is_expert_tensor("model.layers.3.mlp.experts.7.down_proj.weight")
+    assert C.is_expert_tensor("blk.3.ffn_up_exps.weight")
+    assert not C.is_expert_tensor("model.layers.3.mlp.shared_expert.down_proj.weight")
+    assert not C.is_expert_tensor("model.layers.3.mlp.gate.weight")
