@@ -64,13 +64,17 @@ class LUTMoELayer(nn.Module):
         self.renormalize = renormalize
         self.routed_scaling_factor = routed_scaling_factor
         self.gate = nn.Parameter(gate_weight, requires_grad=False)   # [E, H]
+        self._gate_f32: Optional[torch.Tensor] = None                  # fp32 copy, made once
         self._ws: Optional[torch.Tensor] = None
 
     def forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
         shape = hidden_states.shape
         x = hidden_states.reshape(-1, shape[-1])
         xb = x if x.dtype == torch.bfloat16 else x.to(torch.bfloat16)
-        logits = F.linear(xb.float(), self.gate.float())
+        # fp32 router logits (MoEGate.forward, modeling_deepseek.py:423-470)
+        if self._gate_f32 is None or self._gate_f32.device != self.gate.device:
+            self._gate_f32 = self.gate.detach().float()
+        logits = F.linear(xb.float(), self._gate_f32)
         need = ops.moe_workspace_bytes(self.moe, xb.shape[0], self.top_k)
         if self._ws is None or self._ws.numel() < need or self._ws.device != xb.device:
             self._ws = ops.new_workspace(self.moe, xb.shape[0], self.top_k, xb.device)
