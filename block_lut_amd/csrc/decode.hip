@@ -633,6 +633,7 @@ struct Rows8N {
     u32x4_t tw[kRows];
 };
 
+template <int kBits>
 __device__ __forceinline__ void load_rows8n(const NestedView& v, const int (&rows)[kRows], int K, int cc,
                                             int lane, Rows8N& b) {
     const bool ok = cc * kWChunk + 32 * lane < K;
@@ -643,8 +644,11 @@ __device__ __forceinline__ void load_rows8n(const NestedView& v, const int (&row
         const auto q = __builtin_amdgcn_raw_buffer_load_b64(v.planes, (int)(i0 / 4), 0, 0);
         b.f01[r][0] = q[0];
         b.f01[r][1] = q[1];
-        b.f2[r] = __builtin_amdgcn_raw_buffer_load_b32(v.planes, (int)(v.p2_off + i0 / 8), 0, 0);
-        b.f3[r] = __builtin_amdgcn_raw_buffer_load_b32(v.planes, (int)(v.p3_off + i0 / 8), 0, 0);
+        // the tier's planes only (uniform branches: a 2-bit expert issues two
+        // loads per row instead of four)
+        // the tier's planes only (a 2-bit expert issues two loads per row, not four)
+        b.f2[r] = kBits >= 3 ? __builtin_amdgcn_raw_buffer_load_b32(v.planes, (int)(v.p2_off + i0 / 8), 0, 0) : 0u;
+        b.f3[r] = kBits >= 4 ? __builtin_amdgcn_raw_buffer_load_b32(v.planes, (int)(v.p3_off + i0 / 8), 0, 0) : 0u;
         const uint32_t tofs = ((i0 >> 6) << (v.bits + 1)) + ((uint32_t)(lane & 1) << v.bits);
         b.tw[r] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(v.table, (int)tofs, 0, 0));
     }
@@ -654,7 +658,7 @@ __device__ __forceinline__ void load_rows8n(const NestedView& v, const int (&row
 // lane's share (for b < 4 the two lanes of a block write overlapping bytes
 // with the same values, and a lookup only reads the first 2^(b+1) bytes);
 // codes are rebuilt as BL4 nibbles and looked up as for BL4.
-template <int TB>
+template <int TB, int kBits>
 __device__ __forceinline__ void compute_rows8n(const Rows8N& b, const uint32_t (&xs)[TB][16], bool ok, int bits,
                                                int lane, uint8_t* slot, int nt, float (&acc)[kRows][TB]) {
     const uint32_t tab = lds_addr(slot) + ((lane >> 1) << 5);
@@ -667,7 +671,7 @@ __device__ __forceinline__ void compute_rows8n(const Rows8N& b, const uint32_t (
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const uint32_t f01 = b.f01[r][j >> 1] >> (16 * (j & 1));
-            const uint32_t w = nested_nibbles8(f01, b.f2[r] >> (8 * j), b.f3[r] >> (8 * j));
+            const uint32_t w = nested_nibbles8<kBits>(f01, b.f2[r] >> (8 * j), b.f3[r] >> (8 * j));
             uint32_t xj[TB][4];
 #pragma unroll
             for (int t = 0; t < TB; ++t)
@@ -679,20 +683,30 @@ __device__ __forceinline__ void compute_rows8n(const Rows8N& b, const uint32_t (
     wave_lds_sync();
 }
 
-template <int TB>
-__device__ __forceinline__ void nested_rows8(const NestedView& v, const int (&rows)[kRows], int K, int lane,
-                                             uint8_t* slot, const uint16_t* const (&xrow)[TB], int nt,
-                                             float (&acc)[kRows][TB]) {
+template <int TB, int kBits>
+__device__ __forceinline__ void nested_rows8_tier(const NestedView& v, const int (&rows)[kRows], int K, int lane,
+                                                  uint8_t* slot, const uint16_t* const (&xrow)[TB], int nt,
+                                                  float (&acc)[kRows][TB]) {
     const int nch = (K + kWChunk - 1) / kWChunk;
     for (int cc = 0; cc < nch; ++cc) {
         Rows8N b;
         uint32_t xs[TB][16];
         load_x8<TB>(xrow, K, cc, lane, nt, xs);
         __builtin_amdgcn_sched_barrier(0);
-        load_rows8n(v, rows, K, cc, lane, b);
+        load_rows8n<kBits>(v, rows, K, cc, lane, b);
         __builtin_amdgcn_sched_barrier(0);
-        compute_rows8n<TB>(b, xs, cc * kWChunk + 32 * lane < K, v.bits, lane, slot, nt, acc);
+        compute_rows8n<TB, kBits>(b, xs, cc * kWChunk + 32 * lane < K, kBits, lane, slot, nt, acc);
     }
+}
+
+// the expert's tier is wave-uniform: one code path per tier
+template <int TB>
+__device__ __forceinline__ void nested_rows8(const NestedView& v, const int (&rows)[kRows], int K, int lane,
+                                             uint8_t* slot, const uint16_t* const (&xrow)[TB], int nt,
+                                             float (&acc)[kRows][TB]) {
+    if (v.bits == 2) nested_rows8_tier<TB, 2>(v, rows, K, lane, slot, xrow, nt, acc);
+    else if (v.bits == 3) nested_rows8_tier<TB, 3>(v, rows, K, lane, slot, xrow, nt, acc);
+    else nested_rows8_tier<TB, 4>(v, rows, K, lane, slot, xrow, nt, acc);
 }
 
 // ---- REF experts (the reference's uint8 codes, bf16 absmax per block_size

@@ -144,7 +144,7 @@ struct NestedView {
 __device__ __forceinline__ NestedView nested_view(const lutmoe_weights& w, int e) {
     const uint8_t* pl = ((const uint8_t* const*)w.codes)[e];
     const uint16_t* tb = ((const uint16_t* const*)w.tables)[e];
-    const int b = w.tier_bits[e];
+    const int b = __builtin_amdgcn_readfirstlane((int)w.tier_bits[e]);   // uniform: scalar branches on it
     const uint32_t n = (uint32_t)w.rows * (uint32_t)w.cols;   // < 2^32 (checked on the host)
     NestedView v;
     v.planes = __builtin_amdgcn_make_buffer_rsrc((void*)pl, 0, (int)(n / 4 + (b >= 3 ? n / 8 : 0) + (b >= 4 ? n / 8 : 0)),
@@ -160,15 +160,20 @@ __device__ __forceinline__ NestedView nested_view(const lutmoe_weights& w, int e
 // j) for 8 consecutive columns: f01 = their 2-bit fields (column j at bits
 // 2j..2j+1), f2 / f3 = their bit-2 / bit-3 planes (column j at bit j; zero
 // for lower tiers).  Fields are spread to nibbles by shift-or-mask steps.
+// kBits (2, 3 or 4; 0 = not known at compile time): planes a tier does not
+// have are skipped.
+template <int kBits = 0>
 __device__ __forceinline__ uint32_t nested_nibbles8(uint32_t f01, uint32_t f2, uint32_t f3) {
     uint32_t x = f01 & 0xffffu;
     x = (x | (x << 8)) & 0x00ff00ffu;   // 4 fields per byte in bytes 0, 2
     x = (x | (x << 4)) & 0x0f0f0f0fu;   // 2 fields per byte
     x = (x | (x << 2)) & 0x33333333u;   // field j in the low 2 bits of nibble j
+    if constexpr (kBits == 2) return x;
     uint32_t y = f2 & 0xffu;            // bit j -> bit 4j
     y = (y | (y << 12)) & 0x000f000fu;
     y = (y | (y << 6)) & 0x03030303u;
     y = (y | (y << 3)) & 0x11111111u;
+    if constexpr (kBits == 3) return x | (y << 2);
     uint32_t z = f3 & 0xffu;
     z = (z | (z << 12)) & 0x000f000fu;
     z = (z | (z << 6)) & 0x03030303u;
