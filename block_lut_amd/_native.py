@@ -55,7 +55,7 @@ class lutmoe_weights(ctypes.Structure):
         ("tier_bits", ctypes.c_void_p),
         ("absmax_per_expert", ctypes.c_int64),
         ("block_size", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("codebook_stride", ctypes.c_int32),
     ]
 
 
@@ -90,6 +90,7 @@ PROTOTYPES = {
     "launch_lut_gemv_kernel": (None, [P, P, P, P, P, I32, I32, I32]),
     "lutmoe_ref_gemv": (I32, [P, P, P, P, P, I32, I32, I32, I32, I32, I32, P]),
     "lutmoe_unpack_6bit": (I32, [P, P, I64, P]),
+    "lutmoe_merge_bitplane": (I32, [P, P, I64, I32, P]),
     "lutmoe_dequant": (I32, [WP, I32, I32, P, P]),
     "lutmoe_gemv": (I32, [WP, I32, P, I32, P, I32, P]),
     "lutmoe_bl4_tables_from_f16": (I32, [P, P, I64, P]),

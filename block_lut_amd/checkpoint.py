@@ -17,7 +17,11 @@ per weight into a bf16[256] codebook, one bf16 absmax per 128 consecutive weight
   (memory-mapped, nothing executed), `load_gguf_layer` builds a layer at a tier: 8-bit
   codes with the full table, or the low 6 / 4 bits (unpacked on the GPU by
   `lutmoe_unpack_6bit` / `lut_moe_launch_unpack_4bit`) with the mapped table, as the
-  reference's tier reader (`csrc/tensor_engine/tensor_engine.cpp:504-548`).
+  reference's tier reader (`csrc/tensor_engine/tensor_engine.cpp:504-548`); the tier may
+  differ per expert (the reference keeps one per expert node).  `upgrade_gguf_experts`
+  promotes resident experts to a higher-precision tier by reading only the sections they
+  lack and merging them into the device codes (`lutmoe_merge_bitplane`), where the
+  reference reloads the whole expert (`csrc/topology/model_topology.cpp:74-80`).
 
 The BLOCKLUT8 type id lives in the reference's patched gguf-py, which is not part of it;
 tensors are therefore recognised by name (`is_expert_tensor`, `convert_lut.py:143-176`)
@@ -26,7 +30,7 @@ and sized by the offset of the next tensor, whatever their type id.
 from __future__ import annotations
 
 import struct
-from typing import Dict, Mapping, Optional, Tuple
+from typing import Dict, Iterable, Mapping, Optional, Sequence, Tuple, Union
 
 import numpy as np
 import torch
@@ -35,7 +39,10 @@ from . import ops
 from .formats import MoEWeights, RefStack
 
 __all__ = ["read_gguf", "GGUFFile", "is_expert_tensor", "expert_key", "load_converted_layer",
-           "load_gguf_layer"]
+           "load_gguf_layer", "upgrade_gguf_experts"]
+
+# tier -> metadata key of its table (convert_lut.py:113-140; tensor_engine.hpp:287-291)
+_TIER_TABLE = {0: "lut-moe.lut_table", 1: "lut-moe.lut_mapped64", 2: "lut-moe.lut_mapped16"}
 
 GGUF_MAGIC = 0x46554747
 _SCALARS = {0: "<B", 1: "<b", 2: "<H", 3: "<h", 4: "<I", 5: "<i", 6: "<f", 7: "<?", 10: "<Q",
@@ -201,41 +208,100 @@ def _tier_codes(raw_codes: np.ndarray, n: int, nested: bool, tier: int, device) 
     if tier == 1:
         return c6
     high = torch.from_numpy(np.array(raw_codes[n // 2 + n // 4:n])).to(device)
-    h = high.reshape(-1, 1).repeat_interleave(4, dim=1)
-    shifts = torch.tensor([0, 2, 4, 6], dtype=torch.uint8, device=device)
-    hi2 = ((h >> shifts) & 3).reshape(-1)
-    return c6 | (hi2 << 6)
+    return ops.merge_bitplane_(c6, high, 6)
+
+
+def _tier_table(g: "GGUFFile", tier: int) -> torch.Tensor:
+    key = _TIER_TABLE[tier]
+    if key not in g.kv:
+        raise ValueError(f"{key} missing from the GGUF metadata")
+    return _table256(np.asarray(g.kv[key]))
 
 
 def load_gguf_layer(g: GGUFFile, layer: int, num_experts: int, hidden: int, inter: int,
-                    tier: int = 0, device="cuda", num_shared: int = 0) -> MoEWeights:
+                    tier: Union[int, Sequence[int]] = 0, device="cuda",
+                    num_shared: int = 0) -> MoEWeights:
     """One MoE layer from a convert_lut.py GGUF file (expert tensors named as
     `expert_key`).  tier 0: 8-bit codes with `lut-moe.lut_table`; tiers 1 / 2 (nested
     files only): the low 6 / 4 bits with `lut-moe.lut_mapped64` / `lut-moe.lut_mapped16`
-    padded to 256 entries."""
+    padded to 256 entries.  ``tier`` is one tier for every expert or one per expert
+    (num_experts entries); mixed tiers give the stacks one codebook row per expert.
+    The stacks record the tiers in ``.tiers`` (read by `upgrade_gguf_experts`)."""
     bs = int(g.kv.get("lut-moe.block_size", 128))
     nested = bool(g.kv.get("lut-moe.nested_lut", False))
-    key = {0: "lut-moe.lut_table", 1: "lut-moe.lut_mapped64", 2: "lut-moe.lut_mapped16"}[tier]
-    if key not in g.kv:
-        raise ValueError(f"{key} missing from the GGUF metadata")
-    cb = _table256(np.asarray(g.kv[key]))
+    tiers = [int(tier)] * num_experts if isinstance(tier, (int, np.integer)) else [int(t) for t in tier]
+    if len(tiers) != num_experts or any(t not in _TIER_TABLE for t in tiers):
+        raise ValueError("tier must be 0, 1 or 2, or a list of those with one entry per expert")
+    tables = {t: _tier_table(g, t) for t in sorted(set(tiers))}
+    cb = tables[tiers[0]] if len(tables) == 1 else torch.stack([tables[t] for t in tiers])
 
-    def proj(name, n):
+    def proj(name, n, t):
         dims, _, raw = g.tensors[name]
         codes, am = _split_blocklut(raw, n, bs)
-        return (_tier_codes(codes, n, nested, tier, device),
+        return (_tier_codes(codes, n, nested, t, device),
                 torch.from_numpy(np.array(am).view(np.int16)).view(torch.bfloat16))
 
     n13, n2 = inter * hidden, hidden * inter
     c13, a13, c2, a2 = [], [], [], []
     for e in range(num_experts):
-        cg, ag = proj(expert_key(layer, e, "gate"), n13)
-        cu, au = proj(expert_key(layer, e, "up"), n13)
-        cd, ad = proj(expert_key(layer, e, "down"), n2)
+        cg, ag = proj(expert_key(layer, e, "gate"), n13, tiers[e])
+        cu, au = proj(expert_key(layer, e, "up"), n13, tiers[e])
+        cd, ad = proj(expert_key(layer, e, "down"), n2, tiers[e])
         c13.append(torch.cat([cg, cu]))
         a13.append(torch.cat([ag, au]))
         c2.append(cd)
         a2.append(ad)
     w13 = _stack(c13, a13, cb, bs, 2 * inter, hidden, device)
     w2 = _stack(c2, a2, cb, bs, hidden, inter, device)
+    w13.tiers = w2.tiers = tiers
     return MoEWeights(w13, w2, hidden, inter, num_experts - num_shared, num_shared)
+
+
+def upgrade_gguf_experts(moe: MoEWeights, g: GGUFFile, layer: int, experts: Iterable[int],
+                         tier: int) -> MoEWeights:
+    """Promote resident experts of a layer built by `load_gguf_layer` from a nested
+    GGUF file to ``tier`` (0 or 1; a lower tier number has more bits) in place.
+
+    Only the sections the resident codes lack are read from the file: bits 4-5 (the mid
+    section, n/4 bytes) for tier 2 -> 1, bits 6-7 (the high section) for 1 -> 0, both
+    for 2 -> 0 -- the deltas between the reference's per-tier read sizes
+    (`csrc/tensor_engine/tensor_engine.cpp:504-510`) -- and merged into the device codes
+    by `lutmoe_merge_bitplane`; the experts then use the new tier's table.  The
+    result equals `load_gguf_layer` at the new tiers.  Experts already at ``tier`` or
+    above are left alone; the call is stream-ordered with the layer's other work."""
+    w13, w2 = moe.w13, moe.w2
+    tiers = getattr(w13, "tiers", None)
+    if tiers is None or not isinstance(w13, RefStack) or not isinstance(w2, RefStack):
+        raise ValueError("the layer must come from load_gguf_layer")
+    if not g.kv.get("lut-moe.nested_lut", False):
+        raise ValueError("tier upgrades need a nested (bit-plane) GGUF file")
+    if tier not in (0, 1):
+        raise ValueError("the target tier must be 0 or 1")
+    inter, hidden = moe.inter, moe.hidden
+    n13, n2 = inter * hidden, hidden * inter
+    dev = w13.codes.device
+    up = [int(e) for e in experts if tiers[int(e)] > tier]
+    if not up:
+        return moe
+    for e in up:
+        secs = ([("mid", 4)] if tiers[e] == 2 else []) + ([("high", 6)] if tier == 0 else [])
+        for stack, name, n, row0 in ((w13, "gate", n13, 0), (w13, "up", n13, inter),
+                                     (w2, "down", n2, 0)):
+            raw = g.tensors[expert_key(layer, e, name)][2]
+            codes = stack.codes[e, row0:row0 + n // stack.cols].reshape(-1)
+            for sec, shift in secs:
+                a = n // 2 if sec == "mid" else n // 2 + n // 4
+                plane = torch.from_numpy(np.array(raw[a:a + n // 4])).to(dev)
+                ops.merge_bitplane_(codes, plane, shift)
+        tiers[e] = tier
+    table = _tier_table(g, tier).to(dev)
+    for stack in (w13, w2):
+        if stack.codebook_stride == 0 and all(t == tier for t in tiers):
+            stack.codebook = table
+        else:
+            if stack.codebook_stride == 0:
+                stack.codebook = stack.codebook.reshape(1, 256).repeat(stack.num_experts, 1)
+                stack.codebook_stride = 256
+            stack.codebook[up] = table
+    moe._desc = None
+    return moe

@@ -40,6 +40,7 @@ int validate_weights(const lutmoe_weights* w) {
     switch (w->format) {
         case LUTMOE_FMT_REF:
             if (!w->codebook || w->block_size <= 0 || w->absmax_per_expert <= 0) return LUTMOE_EINVAL;
+            if (w->codebook_stride != 0 && w->codebook_stride < 256) return LUTMOE_EINVAL;
             if ((int64_t)w->rows * w->cols >= (1ll << 31)) return LUTMOE_EUNSUPPORTED;
             return LUTMOE_OK;
         case LUTMOE_FMT_BL4:
@@ -212,6 +213,13 @@ int lutmoe_ref_gemv(const void* x, const void* indices, const void* codebook, co
                            y_dtype, stream_of(stream));
 }
 
+int lutmoe_merge_bitplane(uint8_t* codes, const uint8_t* plane, int64_t n, int shift, void* stream) {
+    if (n < 0 || (n % 4) || shift < 0 || shift > 6 || (shift & 1)) return LUTMOE_EINVAL;
+    if (n == 0) return LUTMOE_OK;
+    if (!codes || !plane) return LUTMOE_EINVAL;
+    return launch_merge_bitplane(codes, plane, n, shift, stream_of(stream));
+}
+
 int lutmoe_unpack_6bit(const uint8_t* packed, uint8_t* out, int64_t n, void* stream) {
     if (n < 0 || (n % 4)) return LUTMOE_EINVAL;
     if (n == 0) return LUTMOE_OK;
@@ -231,8 +239,9 @@ int lutmoe_dequant(const lutmoe_weights* w, int e0, int ne, void* out, void* str
         case LUTMOE_FMT_REF:
             return launch_ref_dequant((uint16_t*)out, (const uint8_t*)w->codes + e0 * n,
                                       (const uint16_t*)w->tables + e0 * w->absmax_per_expert,
-                                      (const uint16_t*)w->codebook, n, w->absmax_per_expert,
-                                      w->block_size, ne, n, n, stream_of(stream));
+                                      (const uint16_t*)w->codebook + (int64_t)e0 * w->codebook_stride, n,
+                                      w->absmax_per_expert, w->block_size, ne, n, n, stream_of(stream),
+                                      w->codebook_stride);
         case LUTMOE_FMT_BL4: {
             if (!aligned(out, 16)) return LUTMOE_EALIGN;
             const int64_t nbl = n / 64;
@@ -331,6 +340,12 @@ int moe_forward_impl(const lutmoe_moe_desc* d, const void* x, const float* topk_
     char* ws = (char*)workspace;
     uint16_t* act = (uint16_t*)(ws + L.act);
     hipStream_t s = stream_of(stream);
+    // the older decode pair (gemv.hip) reads one REF codebook per CTA across
+    // experts: per-expert codebooks go through the decode layer or the MFMA path
+    if (gemv && !decode_v2_supported(d, T, k) && d->w2.format == LUTMOE_FMT_REF && d->w2.codebook_stride) {
+        if (force_path == 1) return LUTMOE_EUNSUPPORTED;
+        gemv = false;
+    }
     if (gemv && decode_v2_supported(d, T, k)) {
         // routing + permutation happen inside both decode kernels
         return launch_decode_v2(d, (const uint16_t*)x, topk_w, topk_ids, logits, T, k, renorm,

@@ -45,6 +45,11 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
 
 // silu(g) * u = g * u / (1 + exp(-g)), with the hardware reciprocal (1 ulp in
 // fp32; callers round the result to bf16).
+// REF: expert e's bf16[256] codebook (codebook_stride 0: one for all experts).
+__device__ __forceinline__ const uint16_t* ref_codebook(const lutmoe_weights& w, int e) {
+    return (const uint16_t*)w.codebook + (int64_t)e * w.codebook_stride;
+}
+
 __device__ __forceinline__ float silu_mul(float g, float u) {
     return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
 }

@@ -746,7 +746,7 @@ __device__ __forceinline__ void ref_rows8(const lutmoe_weights& w, int e, const 
     const int64_t nb = w.absmax_per_expert;
     const int bs = w.block_size;
     // codebook -> the slot (8 bytes per lane), issued with the first chunk's loads
-    const uint2 cbv = reinterpret_cast<const uint2*>(w.codebook)[lane];
+    const uint2 cbv = reinterpret_cast<const uint2*>(ref_codebook(w, e))[lane];
     const uint32_t cbase = lds_addr(slot);
     const int nch = (K + kWChunk - 1) / kWChunk;
     for (int cc = 0; cc < nch; ++cc) {

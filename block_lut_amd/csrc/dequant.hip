@@ -10,6 +10,9 @@
 //                  reference's copy-to-upper-half + expand.
 //  unpack_6bit   : the 6-bit tier unpack the reference runs on the CPU
 //                  (csrc/tensor_engine/tensor_engine.cpp:535-548).
+//  merge_bitplane: in-place tier upgrade of resident codes by one 2-bit
+//                  section (the delta a tier promotion reads,
+//                  tensor_engine.cpp:504-510).
 #include "common.h"
 #include "kernels.h"
 
@@ -21,12 +24,12 @@ constexpr int kRefVec = 16;   // codes per thread in ref_dequant
 
 __global__ __launch_bounds__(256) void ref_dequant_kernel(
     uint16_t* __restrict__ out, const uint8_t* __restrict__ idx,
-    const uint16_t* __restrict__ absmax, const uint16_t* __restrict__ cb, int n, int nb,
+    const uint16_t* __restrict__ absmax, const uint16_t* __restrict__ cb, int64_t cb_stride, int n, int nb,
     int bs, int64_t out_stride, int64_t idx_stride, int vec_ok) {
     __shared__ float s_cb[256];
-    s_cb[threadIdx.x] = bf16_to_f32(cb[threadIdx.x]);
-    __syncthreads();
     const int e = blockIdx.y;
+    s_cb[threadIdx.x] = bf16_to_f32(cb[e * cb_stride + threadIdx.x]);
+    __syncthreads();
     const uint8_t* ip = idx + e * idx_stride;
     const uint16_t* ap = absmax + (int64_t)e * nb;
     uint16_t* op = out + e * out_stride;
@@ -194,6 +197,40 @@ __global__ __launch_bounds__(256) void unpack_6bit_kernel(const uint8_t* __restr
     }
 }
 
+// In place: code i takes the 2-bit field (plane[i/4] >> 2*(i%4)) & 3 at bits
+// [shift, shift+2), replacing what was there (so a merge is idempotent).
+// The plane layout is the mid/high section of a BLOCKLUT8 bit-plane file
+// (convert_lut.py:95-110: 4 codes per byte, code 4i in bits 0-1); shift 4
+// merges the mid section (the field rule of tensor_engine.cpp:535-548),
+// shift 6 the high one.  A thread handles 16 codes: one plane dword, one
+// code dwordx4 read-modify-write.
+__global__ __launch_bounds__(256) void merge_bitplane_kernel(uint8_t* __restrict__ codes,
+                                                             const uint8_t* __restrict__ plane, int64_t n,
+                                                             int shift, int vec_ok) {
+    const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t i0 = q * 16;
+    if (i0 >= n) return;
+    if (vec_ok && i0 + 16 <= n) {
+        const uint32_t p = *reinterpret_cast<const uint32_t*>(plane + q * 4);
+        uint4 c = *reinterpret_cast<const uint4*>(codes + i0);
+        uint32_t cw[4] = {c.x, c.y, c.z, c.w};
+        const uint32_t keep = ~(0x03030303u << shift);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t b = (p >> (8 * k)) & 0xffu;
+            // field j of the byte -> bits 0-1 of byte j
+            const uint32_t f = (b & 0x03u) | ((b & 0x0cu) << 6) | ((b & 0x30u) << 12) | ((b & 0xc0u) << 18);
+            cw[k] = (cw[k] & keep) | (f << shift);
+        }
+        *reinterpret_cast<uint4*>(codes + i0) = make_uint4(cw[0], cw[1], cw[2], cw[3]);
+    } else {
+        const int64_t end = min(n, i0 + 16);
+        const uint32_t keep = ~(0x03u << shift);
+        for (int64_t i = i0; i < end; ++i)
+            codes[i] = (uint8_t)((codes[i] & keep) | (((plane[i >> 2] >> (2 * (i & 3))) & 0x03u) << shift));
+    }
+}
+
 inline int grid1(int64_t work, int per_cta) { return (int)((work + per_cta - 1) / per_cta); }
 
 }  // namespace
@@ -203,11 +240,11 @@ namespace lutmoe_host {
 int launch_ref_dequant(uint16_t* out, const uint8_t* idx, const uint16_t* absmax,
                        const uint16_t* cb, int64_t n_per_expert, int64_t nb_per_expert,
                        int block_size, int num_experts, int64_t out_stride,
-                       int64_t idx_stride, hipStream_t s) {
+                       int64_t idx_stride, hipStream_t s, int64_t cb_stride) {
     const int vec_ok = ((uintptr_t)idx % 16 == 0) && ((uintptr_t)out % 16 == 0) &&
                        (idx_stride % 16 == 0) && (out_stride % 8 == 0);
     dim3 grid(grid1(n_per_expert, 256 * kRefVec), num_experts);
-    hipLaunchKernelGGL(ref_dequant_kernel, grid, dim3(256), 0, s, out, idx, absmax, cb,
+    hipLaunchKernelGGL(ref_dequant_kernel, grid, dim3(256), 0, s, out, idx, absmax, cb, cb_stride,
                        (int)n_per_expert, (int)nb_per_expert, block_size, out_stride,
                        idx_stride, vec_ok);
     return check_launch();
@@ -251,6 +288,13 @@ int launch_unpack_4bit_inplace(uint8_t* data, int64_t n, hipStream_t s) {
         m = h;
     }
     hipLaunchKernelGGL(unpack_base_kernel, dim3(1), dim3(1024), 0, s, data, (int)m);
+    return check_launch();
+}
+
+int launch_merge_bitplane(uint8_t* codes, const uint8_t* plane, int64_t n, int shift, hipStream_t s) {
+    const int vec_ok = ((uintptr_t)codes % 16 == 0) && ((uintptr_t)plane % 4 == 0);
+    hipLaunchKernelGGL(merge_bitplane_kernel, dim3(grid1(n, 256 * 16)), dim3(256), 0, s, codes, plane, n,
+                       shift, vec_ok);
     return check_launch();
 }
 

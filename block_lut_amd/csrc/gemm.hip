@@ -877,7 +877,7 @@ __global__ __launch_bounds__(256, 1) void prefill_ring_kernel(lutmoe_moe_desc d,
     if constexpr (kFmt == LUTMOE_FMT_REF) {
         // fp32 codebook after the stages (ordered before its first read by
         // the prologue's barrier)
-        const uint16_t* cb = (const uint16_t*)(kGateUp ? d.w13 : d.w2).codebook;
+        const uint16_t* cb = ref_codebook(kGateUp ? d.w13 : d.w2, ti.e);
         reinterpret_cast<float*>(ring + kStages * RingSlot<kFmt>::kBytes)[threadIdx.x] = bf16_to_f32(cb[threadIdx.x]);
     }
     const int nmt = (min(kBM, ti.n - ti.m0) + 31) / 32;
@@ -900,7 +900,7 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(lutmoe_moe_desc d,
     const TileInfo ti = find_tile(rt, blockIdx.y, ncu);
     if (ti.e < 0) return;
     if (kFmt == LUTMOE_FMT_REF) {
-        const uint16_t* cb = (const uint16_t*)(kGateUp ? d.w13 : d.w2).codebook;
+        const uint16_t* cb = ref_codebook(kGateUp ? d.w13 : d.w2, ti.e);
         s_cb[threadIdx.x] = bf16_to_f32(cb[threadIdx.x]);
     }
     const int nmt = (min(kBM, ti.n - ti.m0) + 31) / 32;

@@ -134,10 +134,10 @@ struct RefDec {
 };
 
 template <class Dec>
-__device__ __forceinline__ void init_cb(const lutmoe_weights&, float*) {}
+__device__ __forceinline__ void init_cb(const lutmoe_weights&, int, float*) {}
 template <>
-__device__ __forceinline__ void init_cb<RefDec>(const lutmoe_weights& w, float* s_cb) {
-    const uint16_t* cb = (const uint16_t*)w.codebook;
+__device__ __forceinline__ void init_cb<RefDec>(const lutmoe_weights& w, int e, float* s_cb) {
+    const uint16_t* cb = ref_codebook(w, e);
     for (int i = threadIdx.x; i < 256; i += blockDim.x) s_cb[i] = bf16_to_f32(cb[i]);
 }
 
@@ -176,7 +176,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(lutmoe_weights w, int expert,
                                                    void* __restrict__ y, int y_dtype) {
     __shared__ __attribute__((aligned(16))) uint8_t s_slot[4 * kSlot];
     __shared__ float s_cb[256];
-    init_cb<Dec>(w, s_cb);
+    init_cb<Dec>(w, expert, s_cb);
     __syncthreads();
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int M = w.rows, K = w.cols;
@@ -232,9 +232,9 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(lutmoe_moe_desc d,
     __shared__ float s_cb[256];
     const int a = blockIdx.y;
     if (a >= rt.active[0]) return;
-    init_cb<Dec>(d.w13, s_cb);
-    __syncthreads();
     const int e = rt.active[1 + a];
+    init_cb<Dec>(d.w13, e, s_cb);
+    __syncthreads();
     const int p0 = rt.offsets[e], n = rt.offsets[e + 1] - p0;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int I = d.inter, H = d.hidden;
@@ -299,7 +299,7 @@ __global__ __launch_bounds__(256) void decode_down_combine_kernel(lutmoe_moe_des
     __shared__ __attribute__((aligned(16))) uint8_t s_slot[4 * kSlot];
     __shared__ float s_cb[256];
     extern __shared__ float s_y[];   // [P][8]
-    init_cb<Dec>(d.w2, s_cb);
+    init_cb<Dec>(d.w2, 0, s_cb);   // one codebook for all experts (the host checks)
     __syncthreads();
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int I = d.inter, H = d.hidden;

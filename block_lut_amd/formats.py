@@ -2,7 +2,8 @@
 
 REF  (the reference's format, vllm_lut/quant_method.py:117-163):
      codes uint8 [E, M, K], absmax bf16 [E, nb] (nb = ceil(M*K/block_size)),
-     codebook bf16 [256].
+     codebook bf16 [256], or [E, 256] when experts sit at different tiers
+     (each row the table of its expert's tier).
 BL4  (4-bit, per-64-block codebooks): codes uint8 [E, M, K/2] (even element in
      the low nibble), tables bf16 [E, M, K/64, 16] holding the dequantised
      entries bf16(fp16 codebook) -- the fp16 codebooks are the wire format,
@@ -48,7 +49,9 @@ class WeightStack:
 
 
 class RefStack(WeightStack):
-    """The reference's uint8 + bf16 absmax + global bf16[256] codebook stack."""
+    """The reference's uint8 + bf16 absmax + bf16[256] codebook stack.  ``codebook`` is
+    one bf16[256] table for all experts, or [E, 256]: one per expert (tiered experts,
+    csrc/tensor_engine/tensor_engine.hpp:287-291)."""
 
     format = N.FMT_REF
 
@@ -61,9 +64,13 @@ class RefStack(WeightStack):
         self.codes = _dev(codes, torch.uint8, "codes")
         self.absmax = _dev(absmax, torch.bfloat16, "absmax")
         self.codebook = _dev(codebook, torch.bfloat16, "codebook")
-        if self.codebook.numel() != 256:
-            raise ValueError("REF codebook must have 256 entries")
         self.num_experts, self.rows, self.cols = self.codes.shape
+        if self.codebook.dim() == 2 and tuple(self.codebook.shape) == (self.num_experts, 256):
+            self.codebook_stride = 256
+        elif self.codebook.numel() == 256:
+            self.codebook_stride = 0
+        else:
+            raise ValueError("REF codebook must be [256] or [num_experts, 256]")
         self.block_size = int(block_size)
         if self.absmax.shape[0] != self.num_experts:
             raise ValueError("absmax must have one row per expert")
@@ -84,6 +91,7 @@ class RefStack(WeightStack):
         d.tier_bits = None
         d.absmax_per_expert = self.absmax.shape[1]
         d.block_size = self.block_size
+        d.codebook_stride = self.codebook_stride
         return d
 
     def hbm_bytes_per_expert(self) -> int:

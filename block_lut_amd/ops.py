@@ -77,6 +77,24 @@ def unpack_6bit(packed: torch.Tensor, num_elements: int) -> torch.Tensor:
     return out
 
 
+def merge_bitplane_(codes: torch.Tensor, plane: torch.Tensor, shift: int) -> torch.Tensor:
+    """In place: code i of ``codes`` takes the 2-bit field
+    ``(plane[i // 4] >> 2 * (i % 4)) & 3`` at bits [shift, shift + 2) -- one
+    BLOCKLUT8 mid (shift 4) or high (shift 6) section merged into resident
+    codes, a tier upgrade that reads only the new section
+    (csrc/tensor_engine/tensor_engine.cpp:504-510 read sizes)."""
+    _dev(codes, torch.uint8, "codes")
+    _dev(plane, torch.uint8, "plane")
+    n = codes.numel()
+    if n % 4 or plane.numel() < n // 4:
+        raise ValueError("codes must be a multiple of 4 and the plane hold codes/4 bytes")
+    if plane.device != codes.device:
+        raise ValueError("codes and plane must be on the same device")
+    N.check("lutmoe_merge_bitplane", N.lib().lutmoe_merge_bitplane(codes.data_ptr(), plane.data_ptr(), n,
+                                                                   int(shift), _stream()))
+    return codes
+
+
 def blocklut_recover(indices: torch.Tensor, absmax: torch.Tensor, lut: torch.Tensor) -> torch.Tensor:
     """lut_moe_launch_blocklut_recover (tensor_recover.cu:144-159), 128-element blocks."""
     _dev(indices, torch.uint8, "indices")

@@ -61,11 +61,16 @@ typedef struct lutmoe_weights {
                                   BL4: bf16 tables [E][M][K/64][16].
                                   NL: device array of E pointers (uint16_t*) to
                                   each expert's bf16 table [M][K/64][2^b].       */
-    const void* codebook;      /* REF: bf16[256] global codebook; else NULL.     */
+    const void* codebook;      /* REF: bf16[256] codebook(s); else NULL.         */
     const int8_t* tier_bits;   /* NL: device int8 [E] with b in {2,3,4}.         */
     int64_t absmax_per_expert; /* REF: absmax entries per expert.                */
     int32_t block_size;        /* REF: absmax block (reference default 128).     */
-    int32_t reserved;
+    int32_t codebook_stride;   /* REF: 0 = one codebook for every expert (the
+                                  reference's model._codebook); else >= 256:
+                                  expert e uses codebook + e*codebook_stride,
+                                  i.e. the table of its own tier
+                                  (csrc/tensor_engine/tensor_engine.hpp:287-291
+                                  selects it per expert node).                 */
 } lutmoe_weights;
 
 /* Fused-MoE layer description: routed experts 0..E-1, plus num_shared
@@ -135,6 +140,17 @@ int lutmoe_ref_gemv(const void* x_dev, const void* indices_dev, const void* code
  * tensor_engine.cpp:535-548): 6-bit codes = low nibble | mid 2 bits << 4 from
  * the [low | mid] sections of `packed`, written to `out` (n bytes). */
 int lutmoe_unpack_6bit(const uint8_t* packed_dev, uint8_t* out_dev, int64_t n, void* stream);
+
+/* Progressive tier upgrade of resident codes (the reference reloads the whole
+ * expert on a promotion, csrc/topology/model_topology.cpp:74-80, reading
+ * the tier's prefix of the bit-plane file, tensor_engine.cpp:504-510): in
+ * place, code i of codes_dev[n] takes the 2-bit field
+ * (plane[i/4] >> 2*(i%4)) & 3 at bits [shift, shift+2), replacing them.
+ * plane_dev holds n/4 bytes laid out as a BLOCKLUT8 mid/high section
+ * (llama-cpp-port/scripts/convert_lut.py:95-110).  shift 4: tier 2 -> 1
+ * (the mid section; same field rule as tensor_engine.cpp:535-548), shift 6:
+ * tier 1 -> 0 (the high section).  n % 4 == 0; shift in {0, 2, 4, 6}. */
+int lutmoe_merge_bitplane(uint8_t* codes_dev, const uint8_t* plane_dev, int64_t n, int shift, void* stream);
 
 /* ---- generic (all formats) --------------------------------------------- */
 

@@ -234,6 +234,23 @@ def unpack_6bit_ref(packed, n: int) -> np.ndarray:
     return (low | (mid << 4)).astype(np.uint8)
 
 
+def merge_bitplane_ref(codes, plane, shift: int) -> np.ndarray:
+    """Tier upgrade by one 2-bit section: code i takes (plane[i // 4] >> 2 * (i % 4)) & 3
+    at bits [shift, shift + 2), replacing them.  The field rule is the reference's CPU
+    6-bit unpack (csrc/tensor_engine/tensor_engine.cpp:535-548: mid bits << 4) and the
+    section layout its packer's (llama-cpp-port/scripts/convert_lut.py:95-110); the
+    high section (shift 6) follows the same layout."""
+    c = np.asarray(codes, np.uint8).reshape(-1).copy()
+    p = np.asarray(plane, np.uint8).reshape(-1)
+    n = c.size
+    assert n % 4 == 0 and p.size >= n // 4 and shift in (0, 2, 4, 6)
+    f = np.empty(n, np.uint8)
+    for j in range(4):
+        f[j::4] = (p[: n // 4] >> (2 * j)) & 0x03
+    keep = np.uint8(0xFF ^ (0x03 << shift))
+    return ((c & keep) | (f << shift)).astype(np.uint8)
+
+
 def nested_tables_prefix_pad(lut256_f32) -> tuple:
     """build_nested_luts (llama-cpp-port/scripts/convert_lut.py:113-140): the K-entry
     tier tables are the first K sorted centroids padded with the last one; all bf16 bits."""

@@ -61,30 +61,52 @@ class BL4Expertset:
                                   to_dev_f16(self.tables, device))
 
 
-class RefExpertset:
-    """E REF matrices quantized by the oracle's restatement of LUTQuantizer.quantize."""
+TIER_MASK = {0: 0xFF, 1: 0x3F, 2: 0x0F}
 
-    def __init__(self, E, M, K, seed, std=0.02, block_size=128):
+
+def tier_tables(cb_bits):
+    """Tier 0 / 1 / 2 tables of a sorted 256-entry codebook: itself and its first 64 /
+    16 entries padded with their last (convert_lut.py:113-140 prefix-pad rule)."""
+    cb_bits = np.asarray(cb_bits, np.uint16)
+
+    def pad(k):
+        t = np.full(256, cb_bits[k - 1], np.uint16)
+        t[:k] = cb_bits[:k]
+        return t
+    return {0: cb_bits.copy(), 1: pad(64), 2: pad(16)}
+
+
+class RefExpertset:
+    """E REF matrices quantized by the oracle's restatement of LUTQuantizer.quantize.
+    With ``tiers`` (one of 0/1/2 per expert) expert e keeps the low 8/6/4 code bits and
+    its tier's table: the stack then carries one codebook per expert."""
+
+    def __init__(self, E, M, K, seed, std=0.02, block_size=128, tiers=None):
         rng = np.random.default_rng(seed)
         self.E, self.M, self.K, self.bs = E, M, K, block_size
         self.cb = golden_codebook()
+        self.tiers = list(tiers) if tiers is not None else None
+        tabs = tier_tables(self.cb)
+        self.cbs = [tabs[t] for t in self.tiers] if self.tiers else [self.cb] * E
         nb = -(-M * K // block_size)
         self.codes = np.empty((E, M, K), np.uint8)
         self.absmax = np.empty((E, nb), np.uint16)
         for e in range(E):
             w = (rng.standard_normal((M, K)) * std).astype(np.float32)
             idx, am = O.ref_quantize(w, self.cb, block_size)
+            if self.tiers:
+                idx = idx & TIER_MASK[self.tiers[e]]
             self.codes[e] = idx.reshape(M, K)
             self.absmax[e] = am
 
     def deq_f32(self, e) -> np.ndarray:
-        return O.bf16_to_f32(O.ref_dequant(self.codes[e], self.absmax[e], self.cb, self.bs)).reshape(
+        return O.bf16_to_f32(O.ref_dequant(self.codes[e], self.absmax[e], self.cbs[e], self.bs)).reshape(
             self.M, self.K)
 
     def gemv_f32(self, e) -> np.ndarray:
         """Weights as the reference's decode GEMV sees them: f32(cb[c]) * f32(absmax)
         without the bf16 rounding of the dequantised tensor (vllm_lut/cuda_lut_gemv.py:50-57)."""
-        cb = O.bf16_to_f32(self.cb)
+        cb = O.bf16_to_f32(self.cbs[e])
         am = O.bf16_to_f32(self.absmax[e])
         blk = np.minimum(np.arange(self.M * self.K) // self.bs, am.size - 1)
         return (cb[self.codes[e].reshape(-1)] * am[blk]).astype(np.float32).reshape(self.M, self.K)
@@ -92,8 +114,9 @@ class RefExpertset:
     def stack(self, device):
         import torch
         from block_lut_amd.formats import RefStack
+        cb = np.stack(self.cbs) if self.tiers else self.cb
         return RefStack(torch.from_numpy(self.codes).to(device), to_dev_bf16(self.absmax, device),
-                        to_dev_bf16(self.cb, device), self.bs)
+                        to_dev_bf16(cb, device), self.bs)
 
 
 class NestedExpertset:

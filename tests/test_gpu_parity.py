@@ -135,6 +135,24 @@ def test_unpack_6bit(gpu):
     assert np.array_equal(got.cpu().numpy(), codes & 0x3F)
 
 
+@pytest.mark.parametrize("n,off", [(4, 0), (20, 0), (4096 + 12, 0), (1 << 20, 0), (4096, 1), (8200, 3)])
+def test_merge_bitplane(gpu, n, off):
+    """In-place merge of a 2-bit section at every shift vs the oracle, bit-exact; odd
+    offsets take the byte path; the bytes around the codes stay untouched."""
+    import torch
+    from block_lut_amd import ops
+    rng = np.random.default_rng(n + off)
+    codes = rng.integers(0, 256, off + n + 16, dtype=np.uint8)
+    plane = rng.integers(0, 256, off + n // 4 + 4, dtype=np.uint8)
+    for shift in (0, 2, 4, 6):
+        dc = torch.from_numpy(codes).to(gpu)
+        dp = torch.from_numpy(plane).to(gpu)
+        ops.merge_bitplane_(dc[off:off + n], dp[off:off + n // 4], shift)
+        got = dc.cpu().numpy()
+        assert np.array_equal(got[off:off + n], O.merge_bitplane_ref(codes[off:off + n], plane[off:off + n // 4], shift))
+        assert np.array_equal(got[:off], codes[:off]) and np.array_equal(got[off + n:], codes[off + n:])
+
+
 # --------------------------------------------------------------------- GEMV
 
 @pytest.mark.parametrize("T", [1, 2, 3, 5])
@@ -399,6 +417,38 @@ def test_moe_layer_ref_block_sizes(gpu, block_size, T, path):
     assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
 
 
+@pytest.mark.parametrize("T,path", [(1, 1), (3, 1), (9, 1), (40, 2), (300, 2)])
+def test_moe_layer_ref_per_expert_codebook(gpu, T, path):
+    """REF experts at different tiers (tier 0 / 1 / 2 codes with the full / first-64 /
+    first-16 tables, one codebook row per expert) through decode and prefill, plus per-
+    expert dequantisation (bit-exact) and the single-expert GEMV."""
+    import torch
+    from block_lut_amd import ops
+    from block_lut_amd.formats import MoEWeights
+    E, S, k, H, I = 8, 1, 2, 256, 192
+    tiers = [0, 2, 1, 2, 0, 1, 1, 2, 0]
+    w13 = RefExpertset(E + S, 2 * I, H, seed=90, tiers=tiers)
+    w2 = RefExpertset(E + S, H, I, seed=91, tiers=tiers)
+    moe = MoEWeights(w13.stack(gpu), w2.stack(gpu), H, I, E, S)
+    assert moe.w13.codebook_stride == 256
+    rng = np.random.default_rng(900 + T)
+    xb = _x(rng, T, H)
+    rw, rids = O.route(rng.standard_normal((T, E)).astype(np.float32), k)
+    out = ops.moe_forward(moe, to_dev_bf16(xb, gpu), torch.from_numpy(rw).to(gpu),
+                          torch.from_numpy(rids).to(gpu), out_dtype=torch.float32, path=path)
+    f13, f2 = (w13.gemv_f32, w2.gemv_f32) if path == 1 else (w13.deq_f32, w2.deq_f32)
+    ref = O.moe_layer(xb, rids, rw, f13, f2, shared=[(f13(E + s), f2(E + s)) for s in range(S)])
+    assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
+    if T == 1:
+        deq = bf16_bits(ops.dequant(moe.w2, 2, 5))
+        for j in range(5):
+            assert np.array_equal(deq[j].reshape(-1), O.ref_dequant(w2.codes[2 + j], w2.absmax[2 + j], w2.cbs[2 + j]))
+        for e in (1, 5):
+            xa = _x(rng, 2, I)
+            y = ops.gemv(moe.w2, to_dev_bf16(xa, gpu), expert=e, out_dtype=torch.float32)
+            assert rel_maxabs(y.cpu().numpy(), O.bf16_to_f32(xa) @ w2.gemv_f32(e).T) <= TOL
+
+
 @pytest.mark.parametrize("T,path,renorm,E", [(1, 1, False, 12), (3, 1, True, 12), (32, 1, False, 12),
                                              (40, 2, False, 12), (300, 2, True, 12),
                                              (2, 1, True, 130), (5, 2, False, 130)])
@@ -640,6 +690,95 @@ def test_checkpoint_loaders(gpu, tmp_path):
                 assert np.array_equal(bf16_bits(lay.w13.absmax[e]).reshape(-1), a13)
             deq_check(lay.w13, lambda e: w13_of(e, mask), tab256)
             deq_check(lay.w2, lambda e: w2_of(e, mask), tab256)
+
+
+def test_gguf_tier_upgrade(gpu, tmp_path):
+    """Experts of a nested GGUF file loaded at mixed tiers (one codebook row per expert),
+    then promoted in place (2 -> 1, 2 -> 0, 1 -> 0) from the sections they lack: codes
+    and codebooks equal a fresh load at the new tiers, the two layers give identical
+    outputs on the decode and prefill paths, and those match the oracle.  A layer loaded
+    at one tier keeps one shared codebook while every expert moves together."""
+    import torch
+    from block_lut_amd import checkpoint as C
+    from block_lut_amd import ops
+    from lutmoe_testutil import GGUF_BLOCKLUT8_TEST_ID, TIER_MASK, tier_tables, write_gguf
+    E, H, I, k = 6, 256, 128, 2
+    rng = np.random.default_rng(78)
+    cb = golden_codebook()
+    tabs = tier_tables(cb)
+    q, tens = {}, []
+    for e in range(E):
+        for p, shape in (("gate", (I, H)), ("up", (I, H)), ("down", (H, I))):
+            w = (rng.standard_normal(shape) * 0.02).astype(np.float32)
+            idx, am = O.ref_quantize(w, cb, 128)
+            key = C.expert_key(0, e, p)
+            q[key] = (idx, am)
+            tens.append((key, (idx.size,), GGUF_BLOCKLUT8_TEST_ID,
+                         np.concatenate([O.bitplane_pack_ref(idx), am.view(np.uint8)]).tobytes()))
+    kv = [("lut-moe.enabled", True), ("lut-moe.block_size", 128), ("lut-moe.k", 256),
+          ("lut-moe.nested_lut", True), ("lut-moe.lut_table", cb.tolist()),
+          ("lut-moe.lut_mapped64", cb[:64].tolist()), ("lut-moe.lut_mapped16", cb[:16].tolist())]
+    path = str(tmp_path / "tiers.gguf")
+    write_gguf(path, kv, tens)
+    g = C.read_gguf(path)
+
+    def parts(e):
+        return [q[C.expert_key(0, e, p)] for p in ("gate", "up", "down")]
+
+    def check(lay, tiers):
+        for e, t in enumerate(tiers):
+            (gi, ga), (ui, ua), (di, da) = parts(e)
+            assert np.array_equal(lay.w13.codes[e].cpu().numpy().reshape(-1), np.concatenate([gi, ui]) & TIER_MASK[t])
+            assert np.array_equal(lay.w2.codes[e].cpu().numpy().reshape(-1), di & TIER_MASK[t])
+            for st in (lay.w13, lay.w2):
+                row = st.codebook if st.codebook_stride == 0 else st.codebook[e]
+                assert np.array_equal(bf16_bits(row).reshape(-1), tabs[t])
+
+    def oracle_out(tiers, xb, rids, rw, gemv):
+        def mat(e, which):
+            (gi, ga), (ui, ua), (di, da) = parts(e)
+            c, a, shape = ((np.concatenate([gi, ui]), np.concatenate([ga, ua]), (2 * I, H)) if which == 13
+                           else (di, da, (H, I)))
+            c = c & TIER_MASK[tiers[e]]
+            tab = O.bf16_to_f32(tabs[tiers[e]])
+            if gemv:
+                am = O.bf16_to_f32(a)
+                return (tab[c] * am[np.arange(c.size) // 128]).astype(np.float32).reshape(shape)
+            return O.bf16_to_f32(O.ref_dequant(c, a, tabs[tiers[e]], 128)).reshape(shape)
+        return O.moe_layer(xb, rids, rw, lambda e: mat(e, 13), lambda e: mat(e, 2))
+
+    def run(lay, xb, rids, rw, path):
+        return ops.moe_forward(lay, to_dev_bf16(xb, gpu), torch.from_numpy(rw).to(gpu),
+                               torch.from_numpy(rids).to(gpu), out_dtype=torch.float32, path=path)
+
+    lay = C.load_gguf_layer(g, 0, E, H, I, tier=[2, 1, 0, 2, 2, 1], device=gpu)
+    assert lay.w13.codebook_stride == 256
+    check(lay, [2, 1, 0, 2, 2, 1])
+    C.upgrade_gguf_experts(lay, g, 0, [0, 1], 1)
+    C.upgrade_gguf_experts(lay, g, 0, [3, 5], 0)
+    now = [1, 1, 0, 0, 2, 0]
+    assert lay.w13.tiers == now
+    check(lay, now)
+    fresh = C.load_gguf_layer(g, 0, E, H, I, tier=now, device=gpu)
+    for T, path in ((1, 1), (5, 1), (40, 2)):
+        xb = _x(rng, T, H)
+        rw, rids = O.route(rng.standard_normal((T, E)).astype(np.float32), k)
+        a, b = run(lay, xb, rids, rw, path), run(fresh, xb, rids, rw, path)
+        assert torch.equal(a, b)
+        assert rel_maxabs(a.cpu().numpy(), oracle_out(now, xb, rids, rw, path == 1)) <= TOL
+
+    lay2 = C.load_gguf_layer(g, 0, E, H, I, tier=2, device=gpu)
+    assert lay2.w13.codebook_stride == 0
+    C.upgrade_gguf_experts(lay2, g, 0, range(E), 1)
+    assert lay2.w13.codebook_stride == 0
+    check(lay2, [1] * E)
+    C.upgrade_gguf_experts(lay2, g, 0, [2], 0)
+    assert lay2.w13.codebook_stride == 256
+    check(lay2, [1, 1, 0, 1, 1, 1])
+    xb = _x(rng, 3, H)
+    rw, rids = O.route(rng.standard_normal((3, E)).astype(np.float32), k)
+    assert rel_maxabs(run(lay2, xb, rids, rw, 1).cpu().numpy(),
+                      oracle_out([1, 1, 0, 1, 1, 1], xb, rids, rw, True)) <= TOL
 
 
 @pytest.mark.parametrize("fmt", ["bl4", "ref", "nested"])

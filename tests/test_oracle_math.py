@@ -128,6 +128,30 @@ def test_bitplane_pack_roundtrip_all_codes():
     assert packed[0] == (codes[0] & 15) | ((codes[1] & 15) << 4)
 
 
+def test_merge_bitplane_rebuilds_codes_from_sections():
+    """A tier upgrade by merging sections: the low nibble (tier 2) plus the mid section at
+    bit 4 equals the reference's 6-bit unpack (tier 1), plus the high section at bit 6 the
+    original codes (tier 0), for every code value in shuffled order.  The fields replace
+    what the target bits held (a planted wrong bit there is overwritten) and a second
+    merge changes nothing; code 4i+j takes bits 2j..2j+1 of plane byte i."""
+    rng = np.random.default_rng(12)
+    codes = rng.permutation(np.tile(np.arange(256, dtype=np.uint8), 8))
+    n = codes.size
+    packed = O.bitplane_pack_ref(codes)
+    mid, high = packed[n // 2:n // 2 + n // 4], packed[n // 2 + n // 4:]
+    c4 = O.unpack_4bit_ref(packed, n)
+    c6 = O.merge_bitplane_ref(c4, mid, 4)
+    assert np.array_equal(c6, O.unpack_6bit_ref(packed, n))
+    c8 = O.merge_bitplane_ref(c6, high, 6)
+    assert np.array_equal(c8, codes)
+    assert np.array_equal(O.merge_bitplane_ref(c8, high, 6), codes)
+    noisy = (c4 | (rng.integers(0, 4, n, dtype=np.uint8) << 4)).astype(np.uint8)
+    assert np.array_equal(O.merge_bitplane_ref(noisy, mid, 4), c6)
+    assert list(O.merge_bitplane_ref(np.zeros(4, np.uint8), np.array([0b11100100], np.uint8), 0)) == [0, 1, 2, 3]
+    lo = O.merge_bitplane_ref(O.merge_bitplane_ref(np.zeros(n, np.uint8), mid, 0), high, 2)
+    assert np.array_equal(lo, (codes >> 4) & 0x0F)
+
+
 # ------------------------------------------------------------------- BL4
 
 def _bl4(w, n_iter=30):
