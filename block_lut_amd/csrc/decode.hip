@@ -845,14 +845,14 @@ __global__ __launch_bounds__(64 * kGuWaves, TB <= 2 ? 3 : 2) void bl4_decode_gat
     __shared__ __attribute__((aligned(16))) uint8_t s_slot[kGuWaves * kSlot];
     if constexpr (kPre) {
         gate_up_body<TB, kFmt>(A, GlobalRouteView{A.route}, s_slot);
-    } else if (blockIdx.x == 0 && blockIdx.y == 0) {
-        // this CTA also publishes the routing (with the pair weights) for the
-        // down kernel
-        const WaveRoute r = wave_pairs<true>(A);
-        if (threadIdx.x < 64) wave_route_publish(A, r);
-        gate_up_body<TB, kFmt>(A, WaveRouteView{r}, s_slot);
     } else {
-        gate_up_body<TB, kFmt>(A, WaveRouteView{wave_pairs<false>(A)}, s_slot);
+        // the first CTA also publishes the routing (with the pair weights)
+        // for the down kernel; one copy of the body for all CTAs keeps the
+        // kernel's code small
+        const bool pub = blockIdx.x == 0 && blockIdx.y == 0;
+        const WaveRoute r = pub ? wave_pairs<true>(A) : wave_pairs<false>(A);
+        if (pub && threadIdx.x < 64) wave_route_publish(A, r);
+        gate_up_body<TB, kFmt>(A, WaveRouteView{r}, s_slot);
     }
 }
 
