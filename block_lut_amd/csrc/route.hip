@@ -70,6 +70,43 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
     }
 }
 
+// E <= 64: lane e holds logit e; max, softmax sum and each of the k top-k
+// rounds are DPP wave reductions (no LDS round trips).  A round takes the
+// largest order-preserving key; the lowest lane holding it wins (ties ->
+// lower expert id; -0 == +0; NaN is never selected, and a round with only
+// NaN left yields id -1 and weight 0).
+__global__ __launch_bounds__(256) void route_topk_wave_kernel(const float* __restrict__ logits, int T, int E,
+                                                              int k, int renorm, float scaling,
+                                                              float* __restrict__ w, int32_t* __restrict__ ids) {
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= T) return;
+    const float v = lane < E ? logits[(int64_t)t * E + lane] : -INFINITY;
+    const float mx = wave_reduce_max(v);
+    const float sum = wave_reduce(lane < E ? expf(v - mx) : 0.f);
+    int key = lane < E ? float_key(v) : INT_MIN;
+    float wsel = 0.f, wsum = 0.f;
+    int isel = -1;
+    for (int j = 0; j < k; ++j) {
+        const int m = wave_max_i32(key);
+        const uint64_t b = __ballot(lane < E && key == m && m != INT_MIN);
+        const int sel = b ? (int)__builtin_ctzll(b) : -1;
+        float p = 0.f;
+        if (sel >= 0) {
+            const float vs = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), sel));
+            p = expf(vs - mx) / sum;
+        }
+        wsum += p;
+        if (lane == j) { wsel = p; isel = sel; }
+        if (lane == sel) key = INT_MIN;
+    }
+    if (lane < k) {
+        const float x = renorm ? wsel / wsum : wsel;
+        w[(int64_t)t * k + lane] = x * scaling;
+        ids[(int64_t)t * k + lane] = isel;
+    }
+}
+
 __global__ __launch_bounds__(256) void build_pairs_kernel(const int32_t* __restrict__ topk_ids,
                                                           const float* __restrict__ topk_w,
                                                           int T, int k, int E, int S,
@@ -147,10 +184,12 @@ __global__ __launch_bounds__(256) void permute_kernel(const int32_t* __restrict_
 // s < k and shared expert E + s - k after that.  One CTA of 16 waves per
 // 1024 consecutive pairs, no global scratch and no waiting between CTAs.
 // Each CTA
-//   (a) histograms all P pairs and the pairs before its chunk: every wave
-//       loads 16 blocks of 64 ids before it uses any (one memory round trip
-//       for P <= 16K), groups equal ids with match_lanes, and the lowest lane
-//       of a group adds the group size (one LDS atomic per distinct id per 64),
+//   (a) histograms all P pairs and the pairs before its chunk: the T*k
+//       routed ids are read as one flat array, 16 independent loads per
+//       thread before any is used, one LDS atomic each (routed id q is pair
+//       (q/k)*ke + q%k, and it lies before the chunk exactly when q is below
+//       a threshold computed once); the S shared experts' counts are closed
+//       forms,
 //   (b) wave w counts sub-chunk w (64 pairs) per expert and ranks each pair
 //       among the equal ids before it (stable),
 //   (c) offsets = exclusive scan of the totals; per expert, an exclusive scan
@@ -160,7 +199,7 @@ __global__ __launch_bounds__(256) void permute_kernel(const int32_t* __restrict_
 // CTA 0 also writes offsets and the active-expert list.  Requires E_tot <= 512.
 constexpr int kPermChunk = 1024;
 constexpr int kPermSub = kPermChunk / 64;   // = waves per CTA
-constexpr int kPermLoads = 16;              // id blocks in flight per wave in (a)
+constexpr int kPermLoads = 16;              // routed ids in flight per thread in (a)
 
 struct PairSrc {
     const int32_t* topk_ids;   // [T][k]
@@ -168,9 +207,12 @@ struct PairSrc {
     int T, k, ke, E;           // ke = k + S; shared expert s has id E + s
 };
 
+// Expert of pair i; routed ids outside [0, E) -> -1 (the pair is dropped).
 __device__ __forceinline__ int pair_expert(const PairSrc& ps, int i) {
     const int t = i / ps.ke, s = i - t * ps.ke;
-    return s < ps.k ? ps.topk_ids[(int64_t)t * ps.k + s] : ps.E + (s - ps.k);
+    if (s >= ps.k) return ps.E + (s - ps.k);
+    const int id = ps.topk_ids[(int64_t)t * ps.k + s];
+    return id >= 0 && id < ps.E ? id : -1;
 }
 
 __global__ __launch_bounds__(1024) void permute_chunk_kernel(PairSrc ps, int P, int E_tot, int nbits,
@@ -189,32 +231,37 @@ __global__ __launch_bounds__(1024) void permute_chunk_kernel(PairSrc ps, int P, 
     const uint64_t lt = (1ull << lane) - 1ull;
     for (int i = tid; i < (3 + kPermSub) * E_tot + 1; i += blockDim.x) sm[i] = 0;
     __syncthreads();
-    // (a) id blocks wv, wv + 16, ... of 64; block index * 64 is a multiple of
-    // 64 and c0 of 1024, so a block is wholly before the chunk or not
-    for (int b0 = wv; b0 * 64 < P; b0 += kPermSub * kPermLoads) {
+    // (a) routed ids q < qc are pairs before the chunk: tokens below c0/ke
+    // entirely, and of token c0/ke its slots below c0 % ke
+    const int nq = ps.T * ps.k;
+    const int qc = (c0 / ps.ke) * ps.k + min(c0 % ps.ke, ps.k);
+    for (int q0 = tid; q0 < nq; q0 += kPermLoads * (int)blockDim.x) {
         int idv[kPermLoads];
 #pragma unroll
         for (int u = 0; u < kPermLoads; ++u) {
-            const int i = (b0 + u * kPermSub) * 64 + lane;
-            idv[u] = i < P ? pair_expert(ps, i) : -1;
+            const int q = q0 + u * (int)blockDim.x;
+            idv[u] = q < nq ? ps.topk_ids[q] : -1;
         }
 #pragma unroll
         for (int u = 0; u < kPermLoads; ++u) {
-            const int blk = b0 + u * kPermSub;
-            if (blk * 64 >= P) break;
             const int id = idv[u];
-            const bool ok = id >= 0 && id < E_tot;
-            const uint64_t m = match_lanes(id, ok, nbits);
-            if (ok && (m & lt) == 0) {
-                atomicAdd(&h_all[id], __popcll(m));
-                if (blk * 64 < c0) atomicAdd(&h_bef[id], __popcll(m));
+            if (id >= 0 && id < ps.E) {
+                atomicAdd(&h_all[id], 1);
+                if (q0 + u * (int)blockDim.x < qc) atomicAdd(&h_bef[id], 1);
             }
         }
+    }
+    // shared expert s: slot k + s of every token; pairs before the chunk are
+    // the tokens t with t*ke + k + s < c0
+    for (int s = tid; s < ps.ke - ps.k; s += blockDim.x) {
+        const int64_t lim = (int64_t)c0 - ps.k - s;
+        h_all[ps.E + s] = ps.T;
+        h_bef[ps.E + s] = lim <= 0 ? 0 : (int)min((int64_t)ps.T, (lim + ps.ke - 1) / ps.ke);
     }
     // (b) wave wv: sub-chunk wv
     const int i = c0 + wv * 64 + lane;
     const int id = i < P ? pair_expert(ps, i) : -1;
-    const bool ok = id >= 0 && id < E_tot;
+    const bool ok = id >= 0;
     const uint64_t m = match_lanes(id, ok, nbits);
     const int rk = __popcll(m & lt);
     if (ok && rk == 0) sub[wv * E_tot + id] = __popcll(m);
@@ -307,8 +354,12 @@ namespace lutmoe_host {
 
 int launch_route_topk(const float* logits, int T, int E, int k, int renorm, float scaling,
                       float* w, int32_t* ids, hipStream_t s) {
-    hipLaunchKernelGGL(route_topk_kernel, dim3((T + 3) / 4), dim3(256), 0, s, logits, T, E,
-                       k, renorm, scaling, w, ids);
+    if (E <= 64 && k <= 64)
+        hipLaunchKernelGGL(route_topk_wave_kernel, dim3((T + 3) / 4), dim3(256), 0, s, logits, T, E, k, renorm,
+                           scaling, w, ids);
+    else
+        hipLaunchKernelGGL(route_topk_kernel, dim3((T + 3) / 4), dim3(256), 0, s, logits, T, E,
+                           k, renorm, scaling, w, ids);
     return check_launch();
 }
 
