@@ -268,7 +268,11 @@ def upgrade_gguf_experts(moe: MoEWeights, g: GGUFFile, layer: int, experts: Iter
     (`csrc/tensor_engine/tensor_engine.cpp:504-510`) -- and merged into the device codes
     by `lutmoe_merge_bitplane`; the experts then use the new tier's table.  The
     result equals `load_gguf_layer` at the new tiers.  Experts already at ``tier`` or
-    above are left alone; the call is stream-ordered with the layer's other work."""
+    above are left alone; the call is stream-ordered with the layer's other work.
+
+    Codes and codebook rows change in place, so graphs captured earlier stay valid,
+    except on the first mixed-tier promotion of a layer loaded at one tier: its shared
+    codebook then becomes one row per expert (a new tensor; capture again)."""
     w13, w2 = moe.w13, moe.w2
     tiers = getattr(w13, "tiers", None)
     if tiers is None or not isinstance(w13, RefStack) or not isinstance(w2, RefStack):
@@ -288,7 +292,7 @@ def upgrade_gguf_experts(moe: MoEWeights, g: GGUFFile, layer: int, experts: Iter
         for stack, name, n, row0 in ((w13, "gate", n13, 0), (w13, "up", n13, inter),
                                      (w2, "down", n2, 0)):
             raw = g.tensors[expert_key(layer, e, name)][2]
-            codes = stack.codes[e, row0:row0 + n // stack.cols].reshape(-1)
+            codes = stack.codes[e, row0:row0 + n // stack.cols].view(-1)   # a view: merged in place
             for sec, shift in secs:
                 a = n // 2 if sec == "mid" else n // 2 + n // 4
                 plane = torch.from_numpy(np.array(raw[a:a + n // 4])).to(dev)
@@ -297,7 +301,7 @@ def upgrade_gguf_experts(moe: MoEWeights, g: GGUFFile, layer: int, experts: Iter
     table = _tier_table(g, tier).to(dev)
     for stack in (w13, w2):
         if stack.codebook_stride == 0 and all(t == tier for t in tiers):
-            stack.codebook = table
+            stack.codebook.copy_(table.reshape(stack.codebook.shape))
         else:
             if stack.codebook_stride == 0:
                 stack.codebook = stack.codebook.reshape(1, 256).repeat(stack.num_experts, 1)
