@@ -31,7 +31,7 @@ def test_header_declares_the_expected_surface():
                  "launch_lut_gemv_kernel", "lutmoe_ref_gemv", "lutmoe_dequant", "lutmoe_gemv",
                  "lutmoe_route_topk", "lutmoe_permute", "lutmoe_moe_forward",
                  "lutmoe_moe_forward_logits", "lutmoe_moe_workspace_size", "lutmoe_strerror",
-                 "lutmoe_bl4_encode"):
+                 "lutmoe_bl4_encode", "lutmoe_ref_encode", "lutmoe_merge_bitplane"):
         assert must in names
 
 
@@ -103,6 +103,19 @@ def test_validation_before_any_hip_call(lib):
     assert lib.lutmoe_unpack_6bit(P(1), P(1), 6, None) == N.LUTMOE_EINVAL
     assert lib.lutmoe_bl4_encode(P(1), 4, 0, P(1), P(1), None) == N.LUTMOE_EINVAL
     assert lib.lutmoe_bl4_tables_from_f16(P(0x104), P(0x100), 8, None) == N.LUTMOE_EALIGN
+    # tier upgrade: n a multiple of 4, shift even in [0, 6], pointers unless n == 0
+    assert lib.lutmoe_merge_bitplane(P(1), P(1), 6, 4, None) == N.LUTMOE_EINVAL
+    assert lib.lutmoe_merge_bitplane(P(1), P(1), 8, 5, None) == N.LUTMOE_EINVAL
+    assert lib.lutmoe_merge_bitplane(P(1), P(1), 8, 8, None) == N.LUTMOE_EINVAL
+    assert lib.lutmoe_merge_bitplane(None, P(1), 8, 4, None) == N.LUTMOE_EINVAL
+    assert lib.lutmoe_merge_bitplane(None, None, 0, 4, None) == N.LUTMOE_OK
+    # REF codebook stride: 0 (shared) or at least one 256-entry codebook per expert
+    w = _bl4_weights(N)
+    w.format, w.codebook, w.absmax_per_expert, w.block_size = N.FMT_REF, 0x30000, 256, 128
+    w.codebook_stride = 100
+    assert lib.lutmoe_dequant(ctypes.byref(w), 0, 1, P(0x100), None) == N.LUTMOE_EINVAL
+    w.codebook_stride = -256
+    assert lib.lutmoe_dequant(ctypes.byref(w), 0, 1, P(0x100), None) == N.LUTMOE_EINVAL
 
 
 def test_moe_validation(lib):
