@@ -25,3 +25,24 @@ def fused_lut_moe(x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.T
     xb = x2 if x2.dtype == torch.bfloat16 else x2.to(torch.bfloat16)
     out = ops.moe_forward(moe, xb.contiguous(), topk_weights, topk_ids, out_dtype=torch.bfloat16)
     return out if x2.dtype == torch.bfloat16 else out.to(x2.dtype)
+
+
+# torch.library op, so that torch.compile graphs can hold the fused layer (the
+# fake kernel gives the output's shape and dtype without running anything)
+ops._lib_def.define("fused_lut_moe(Tensor x, Tensor topk_ids, Tensor topk_weights, Tensor w13_weight, "
+                    "Tensor w13_absmax, Tensor w2_weight, Tensor w2_absmax, Tensor codebook, "
+                    "int block_size=128) -> Tensor")
+
+
+@torch.library.impl(ops._lib_def, "fused_lut_moe", "CUDA")
+def _fused_lut_moe_impl(x, topk_ids, topk_weights, w13_weight, w13_absmax, w2_weight, w2_absmax, codebook,
+                        block_size=128):
+    return fused_lut_moe(x, topk_ids, topk_weights, w13_weight, w13_absmax, w2_weight, w2_absmax, codebook,
+                         block_size)
+
+
+@torch.library.register_fake("lutmoe::fused_lut_moe")
+def _fused_lut_moe_fake(x, topk_ids, topk_weights, w13_weight, w13_absmax, w2_weight, w2_absmax, codebook,
+                        block_size=128):
+    shape = (1, x.shape[0]) if x.dim() == 1 else tuple(x.shape)
+    return x.new_empty(shape)

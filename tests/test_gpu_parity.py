@@ -417,6 +417,32 @@ def test_moe_layer_ref_block_sizes(gpu, block_size, T, path):
     assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
 
 
+@pytest.mark.parametrize("T", [1, 7, 40])
+def test_fused_lut_moe_reference_signature(gpu, T):
+    """fused_lut_moe(x, topk_ids, topk_weights, w13, w13_absmax, w2, w2_absmax, codebook)
+    (vllm_lut/fast_moe.py:30-43) on the reference's REF tensors, also as the torch op
+    lutmoe::fused_lut_moe (identical output); decode sizes follow the reference GEMV's
+    (x * cb) * absmax products, prefill its dequantise-then-GEMM branch."""
+    import torch
+    import block_lut_amd.fast_moe as FM
+    E, k, H, I = 8, 2, 256, 192
+    w13 = RefExpertset(E, 2 * I, H, seed=60)
+    w2 = RefExpertset(E, H, I, seed=61)
+    rng = np.random.default_rng(600 + T)
+    xb = _x(rng, T, H)
+    rw, rids = O.route(rng.standard_normal((T, E)).astype(np.float32), k)
+    args = (to_dev_bf16(xb, gpu), torch.from_numpy(rids).to(gpu), torch.from_numpy(rw).to(gpu),
+            torch.from_numpy(w13.codes).to(gpu), to_dev_bf16(w13.absmax, gpu),
+            torch.from_numpy(w2.codes).to(gpu), to_dev_bf16(w2.absmax, gpu), to_dev_bf16(w13.cb, gpu))
+    out = FM.fused_lut_moe(*args)
+    assert out.dtype == torch.bfloat16 and tuple(out.shape) == (T, H)
+    assert torch.equal(torch.ops.lutmoe.fused_lut_moe(*args), out)
+    f13, f2 = (w13.gemv_f32, w2.gemv_f32) if T <= 32 else (w13.deq_f32, w2.deq_f32)
+    ref = O.moe_layer(xb, rids, rw, f13, f2)
+    # bf16 output: the tolerance adds half an ulp of bf16 relative to max|ref|
+    assert rel_maxabs(O.bf16_to_f32(bf16_bits(out)), ref) <= TOL + 2.0 ** -8
+
+
 @pytest.mark.parametrize("T,path", [(1, 1), (3, 1), (9, 1), (40, 2), (300, 2)])
 def test_moe_layer_ref_per_expert_codebook(gpu, T, path):
     """REF experts at different tiers (tier 0 / 1 / 2 codes with the full / first-64 /

@@ -134,3 +134,25 @@ def test_gguf_reader_roundtrip_and_expert_names(tmp_path):
     assert C.is_expert_tensor("blk.3.ffn_up_exps.weight")
     assert not C.is_expert_tensor("model.layers.3.mlp.shared_expert.down_proj.weight")
     assert not C.is_expert_tensor("model.layers.3.mlp.gate.weight")
+
+
+def test_fused_lut_moe_op_fake_shapes():
+    """lutmoe::fused_lut_moe is a torch.library op whose fake kernel gives the layer's
+    output shape and dtype (what torch.compile traces), without a GPU."""
+    import torch
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    import block_lut_amd.fast_moe  # noqa: F401  (registers the op)
+    E, H, I, T, k = 4, 256, 128, 5, 2
+    with FakeTensorMode():
+        x = torch.empty(T, H, dtype=torch.bfloat16)
+        ids = torch.empty(T, k, dtype=torch.int32)
+        w = torch.empty(T, k, dtype=torch.float32)
+        w13 = torch.empty(E, 2 * I, H, dtype=torch.uint8)
+        w2 = torch.empty(E, H, I, dtype=torch.uint8)
+        a13 = torch.empty(E, 2 * I * H // 128, dtype=torch.bfloat16)
+        a2 = torch.empty(E, H * I // 128, dtype=torch.bfloat16)
+        cb = torch.empty(256, dtype=torch.bfloat16)
+        out = torch.ops.lutmoe.fused_lut_moe(x, ids, w, w13, a13, w2, a2, cb)
+        assert tuple(out.shape) == (T, H) and out.dtype == torch.bfloat16
+        out1 = torch.ops.lutmoe.fused_lut_moe(x[0], ids[:1], w[:1], w13, a13, w2, a2, cb)
+        assert tuple(out1.shape) == (1, H)
