@@ -288,6 +288,7 @@ def main():
         g = graph_of([lambda: sp.run(path=ops.PATH_MFMA)])
         time_graph(g, 2)
         sec = time_graph(g, 10) / 10
+        sec_pf = sec
         flops = 6 * d["H"] * d["I"] * 2048 * (d["k"] + d["S"])
         extra["prefill_dsv2_T2048_us"] = round(sec * 1e6, 1)
         extra["prefill_dsv2_T2048_TFLOPs"] = round(flops / sec / 1e12, 1)
@@ -317,10 +318,24 @@ def main():
         log(f"[bench] prefill DeepSeek T=2048, REF format: {sec * 1e6:.0f} us, {flops / sec / 1e12:.1f} TFLOP/s")
         del lay, sp, g
         torch.cuda.empty_cache()
+        # the main decode workload (T tokens, rotating layer copies) on the REF format
+        Eq = c["E"] + c["S"]
+        rl = [MoEWeights(ref_stack(Eq, 2 * c["I"], c["H"]), ref_stack(Eq, c["H"], c["I"]),
+                         c["H"], c["I"], c["E"], c["S"]) for _ in range(a.layers)]
+        rs = [Step(L, c, T) for L in rl]
+        g = graph_of([s.run for s in rs])
+        time_graph(g, 2)
+        sec_r = time_graph(g, 8) / (8 * len(rs))
+        b_r = sum(s.U * 3 * c["H"] * c["I"] * (1 + 2 / 128) + 2 * T * c["H"] * 2 for s in rs) / len(rs)
+        extra[f"decode_ref_T{T}_us_per_layer"] = round(sec_r * 1e6, 2)
+        extra[f"decode_ref_T{T}_TBs"] = round(b_r / sec_r / 1e12, 3)
+        log(f"[bench] decode T={T}, REF format: {sec_r * 1e6:.1f} us/layer, {b_r / sec_r / 1e12:.3f} TB/s")
+        del rl, rs, g
+        torch.cuda.empty_cache()
         ceil = measured_ceilings(torch, dev, d)
         extra.update(ceil)
         extra["prefill_dsv2_T2048_frac_hipblaslt_ceiling"] = round(
-            flops / sec / 1e12 / ceil["ceiling_hipblaslt_bf16_TFLOPs"], 4)
+            flops / sec_pf / 1e12 / ceil["ceiling_hipblaslt_bf16_TFLOPs"], 4)
         extra["decode_T1_frac_device_copy_ceiling"] = round(
             result["value"] * 1e3 / ceil["ceiling_device_copy_GBs"], 4)
         extra.update(nested_tiers(a, ops, N, torch, dev, NestedExpert, NestedStack, MoEWeights,
