@@ -516,6 +516,13 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
     const int nkb = (K / kBK) * (zs + 1) / nsplit - kb0;
     const int n0 = blockIdx.x * (kGateUp ? kBN / 2 : kBN);
     const int nvalid = min(kBM, ti.n - ti.m0);
+    // down projection: the routing weight of tile row tid, loaded now (two
+    // dependent loads) so that the K loop hides them; the epilogue reads it
+    // from LDS
+    float pw_row = 0.f;
+    if constexpr (!kGateUp) {
+        if (tid < nvalid) pw_row = rt.pair_w[rt.perm[ti.p0 + ti.m0 + tid]];
+    }
 
     // ---- loader side (all offsets 32-bit, from scalar bases; the host
     // checks the sizes).  The tile's first NMT*32 activation rows are
@@ -832,8 +839,12 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
         }
     } else {
         // y_pos tile [256 positions][256 h] fp32 times the routing weight, in
-        // two halves of 128 positions
+        // two halves of 128 positions (128 KB of LDS each); the rows' weights
+        // after them
         float* st = reinterpret_cast<float*>(ring);
+        float* s_pw = reinterpret_cast<float*>(ring + 128 * 256 * 4);
+        static_assert(128 * 256 * 4 + kBM * 4 <= RingSlot<kFmt>::kLds, "epilogue LDS");
+        s_pw[tid] = pw_row;
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf) {
             if (4 * hf < NMT) {
@@ -852,7 +863,7 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
                 if (n0 + 4 * chunk < H) {
                     for (int r = tid >> 6; r < 128 && 128 * hf + r < nvalid; r += 4) {
                         const int p = ti.p0 + ti.m0 + 128 * hf + r;
-                        const float pw = rt.pair_w[rt.perm[p]];
+                        const float pw = s_pw[128 * hf + r];
                         float4 v = *reinterpret_cast<const float4*>(&st[r * 256 + 4 * chunk]);
                         v.x *= pw;
                         v.y *= pw;
