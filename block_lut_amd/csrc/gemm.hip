@@ -360,7 +360,15 @@ __device__ __forceinline__ void prefill_tile(const lutmoe_moe_desc& d, const uin
     }
 
     // ---- epilogue.  D layout: lane (n = lane%32, h = lane/32), element i ->
-    // row m = 8*(i/4) + 4*h + (i%4), column n.
+    // row m = 8*(i/4) + 4*h + (i%4), column n.  The down projection's rows'
+    // routing weights go to LDS first (the A buffers are free once every
+    // fragment read is done), so the stores wait on no global load.
+    float* s_pw = reinterpret_cast<float*>(&s_a[0][0]);
+    if constexpr (!kGateUp) {
+        __syncthreads();
+        if (tid < nvalid) s_pw[tid] = rt.pair_w[rt.perm[ti.p0 + ti.m0 + tid]];
+        __syncthreads();
+    }
 #pragma unroll
     for (int mt = 0; mt < NMT; ++mt) {
 #pragma unroll
@@ -374,7 +382,7 @@ __device__ __forceinline__ void prefill_tile(const lutmoe_moe_desc& d, const uin
                     ((uint16_t*)dst)[(int64_t)p * I + ii] =
                         (uint16_t)f32_to_bf16(silu_mul(acc[mt][0][i], acc[mt][1][i]));
             } else {
-                const float pw = rt.pair_w[rt.perm[p]];
+                const float pw = s_pw[m];
 #pragma unroll
                 for (int nt = 0; nt < 2; ++nt) {
                     const int h = n0 + 64 * wv + 32 * nt + bn;

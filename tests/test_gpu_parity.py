@@ -417,6 +417,32 @@ def test_moe_layer_ref_block_sizes(gpu, block_size, T, path):
     assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
 
 
+@pytest.mark.parametrize("T,path", [(40, 2), (300, 2), (3, 1)])
+def test_moe_layer_ref_short_odd_absmax(gpu, T, path):
+    """REF stacks whose absmax rows hold one entry fewer than ceil(M*K/128) (an odd count):
+    the last block index is clamped to the last entry, as decompress_blocklut does
+    (vllm_lut/quantizer.py:473-474), and prefill takes the register-staged kernel (the
+    DMA ring reads absmax in aligned pairs and needs an even count)."""
+    import torch
+    from block_lut_amd import ops
+    from block_lut_amd.formats import MoEWeights
+    E, S, k, H, I = 6, 1, 2, 256, 192
+    w13 = RefExpertset(E + S, 2 * I, H, seed=70)
+    w2 = RefExpertset(E + S, H, I, seed=71)
+    for w in (w13, w2):
+        w.absmax = np.ascontiguousarray(w.absmax[:, :-1])
+        assert w.absmax.shape[1] % 2 == 1
+    moe = MoEWeights(w13.stack(gpu), w2.stack(gpu), H, I, E, S)
+    rng = np.random.default_rng(700 + T)
+    xb = _x(rng, T, H)
+    rw, rids = O.route(rng.standard_normal((T, E)).astype(np.float32), k)
+    out = ops.moe_forward(moe, to_dev_bf16(xb, gpu), torch.from_numpy(rw).to(gpu),
+                          torch.from_numpy(rids).to(gpu), out_dtype=torch.float32, path=path)
+    f13, f2 = (w13.gemv_f32, w2.gemv_f32) if path == 1 else (w13.deq_f32, w2.deq_f32)
+    ref = O.moe_layer(xb, rids, rw, f13, f2, shared=[(f13(E + s), f2(E + s)) for s in range(S)])
+    assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
+
+
 @pytest.mark.parametrize("T", [1, 7, 40])
 def test_fused_lut_moe_reference_signature(gpu, T):
     """fused_lut_moe(x, topk_ids, topk_weights, w13, w13_absmax, w2, w2_absmax, codebook)
