@@ -417,6 +417,53 @@ def test_moe_layer_ref_block_sizes(gpu, block_size, T, path):
     assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
 
 
+@pytest.mark.parametrize("fmt,T", [("bl4", 1), ("bl4", 8), ("bl4", 300), ("ref", 1), ("ref", 300),
+                                   ("nested", 4), ("nested", 150)])
+def test_moe_layer_graph_replays(gpu, fmt, T):
+    """The layer captured in a HIP graph (router logits in, output out, one workspace):
+    four replays, each after new inputs were copied into the captured buffers and an eager
+    call on other buffers ran in between, every replay bit-identical to the eager layer
+    on the same inputs (the decode counters left zero by each call, no stale routing)."""
+    import torch
+    from block_lut_amd import ops
+    from block_lut_amd.formats import MoEWeights
+    E, S, k, H, I = 8, 1, 2, 256, 192
+    if fmt == "nested":
+        w13 = NestedExpertset([2, 3, 4, 4, 3, 2, 4, 3, 2], 2 * I, H, seed=80)
+        w2 = NestedExpertset([2, 3, 4, 4, 3, 2, 4, 3, 2], H, I, seed=81)
+    else:
+        w13, w2 = _moe_case(fmt, E, S, H, I, seed=82)
+    moe = MoEWeights(w13.stack(gpu), w2.stack(gpu), H, I, E, S)
+    rng = np.random.default_rng(800 + T)
+    x = torch.empty((T, H), dtype=torch.bfloat16, device=gpu)
+    lg = torch.empty((T, E), dtype=torch.float32, device=gpu)
+    out = torch.empty((T, H), dtype=torch.float32, device=gpu)
+    ws = ops.new_workspace(moe, T, k, gpu)
+    x2, lg2 = torch.empty_like(x), torch.empty_like(lg)
+    out2 = torch.empty_like(out)
+    ws2 = ops.new_workspace(moe, T, k, gpu)
+
+    def fill(xt, lt):
+        xt.copy_(to_dev_bf16(_x(rng, T, H), gpu))
+        lt.copy_(torch.from_numpy(rng.standard_normal((T, E)).astype(np.float32)).to(gpu))
+
+    fill(x, lg)
+    ops.moe_forward_logits(moe, x, lg, k, out=out, workspace=ws)   # warm-up outside capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ops.moe_forward_logits(moe, x, lg, k, out=out, workspace=ws)
+    for rep in range(4):
+        fill(x, lg)
+        fill(x2, lg2)
+        ops.moe_forward_logits(moe, x2, lg2, k, out=out2, workspace=ws2)   # eager work between replays
+        g.replay()
+        torch.cuda.synchronize()
+        eager = ops.moe_forward_logits(moe, x, lg, k, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {rep}"
+
+
 @pytest.mark.parametrize("T,path", [(40, 2), (300, 2), (3, 1)])
 def test_moe_layer_ref_short_odd_absmax(gpu, T, path):
     """REF stacks whose absmax rows hold one entry fewer than ceil(M*K/128) (an odd count):
