@@ -955,11 +955,16 @@ __global__ __launch_bounds__(256, TB <= 2 ? 3 : 2) void bl4_decode_down_y(Decode
         for (int r = 0; r < kRows; ++r)
 #pragma unroll
             for (int t = 0; t < TB; ++t) acc[r][t] = 0.f;
+        // the positions' routing weights (two dependent loads each) issued
+        // ahead of the weight loads, which hide them
+        float pwv[TB];
+#pragma unroll
+        for (int t = 0; t < TB; ++t) pwv[t] = rv.weight_at(sl.p0 + tb + min(t, nt - 1));
         expert_rows8<kFmt, TB>(A.d.w2, sl.e, rows, I, lane, slot, xrow, nt, acc);
 #pragma unroll
         for (int t = 0; t < TB; ++t) {
             const int p = sl.p0 + tb + min(t, nt - 1);
-            const float pw = rv.weight_at(p);
+            const float pw = pwv[t];
             float v[kRows];
 #pragma unroll
             for (int r = 0; r < kRows; ++r) v[r] = acc[r][t];
