@@ -1,8 +1,8 @@
 """CPU oracle for the LUT-dequant MoE expert path -- TEST INFRASTRUCTURE ONLY.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline``
-leg may import this package, and only as the checker (or, for the CPU
-baseline, as the timed CPU restatement).  The product package
+leg may import this package, and only to check results against (or, for the
+CPU baseline, as the timed CPU restatement).  The product package
 ``block_lut_amd`` never imports it and fails loudly when its HIP library is
 missing.
 

@@ -2,7 +2,8 @@
  * CPU oracle (test infrastructure only) for the LUT-dequant MoE expert path.
  *
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load
- * this library, and only as the checker.  The product path never calls it.
+ * this library, and only to check results against.  The product path never
+ * calls it.
  *
  * What lives here (the parts that must be bit-exact with the HIP kernels and
  * are too slow in numpy at test sizes):

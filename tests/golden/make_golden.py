@@ -1,5 +1,5 @@
-"""Writes the golden fixtures under tests/golden/ (run in the build container,
-where the reference checkout exists at /root/reference; never on the GPU box).
+"""Writes the golden fixtures under tests/golden/ (run where the reference
+checkout exists at /root/reference; the tests only read the fixtures).
 
 codebooks.npz   derived data from the reference's shipped codebook files
                 (models/{qwen,deepseek}/*.npy), loaded with numpy
