@@ -434,6 +434,13 @@ int lutmoe_bl4_encode(const float* w, int64_t nblocks, int n_iter, uint8_t* code
     return launch_bl4_encode(w, nblocks, n_iter, codes, tables_f16, stream_of(stream));
 }
 
+int lutmoe_kmeans_1d(const float* data, int64_t n, float* centroids, int k, int n_iter, int32_t* assign_ws,
+                     void* stream) {
+    if (n <= 0 || n >= (1ll << 31) || k < 1 || k > 256 || n_iter < 0) return LUTMOE_EINVAL;
+    if (!data || !centroids || !assign_ws) return LUTMOE_EINVAL;
+    return launch_kmeans_1d(data, n, centroids, k, n_iter, assign_ws, stream_of(stream));
+}
+
 int lutmoe_ref_encode(const void* w_bf16, const float* codebook, int64_t n, int block_size, uint8_t* codes,
                       void* absmax_bf16, void* stream) {
     if (n < 0 || block_size <= 0) return LUTMOE_EINVAL;

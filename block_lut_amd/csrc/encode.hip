@@ -233,6 +233,62 @@ __global__ __launch_bounds__(256) void ref_encode_kernel(const uint16_t* __restr
     }
 }
 
+// 1-D Lloyd k-means (LUTQuantizer._train_kmeans iterations,
+// vllm_lut/quantizer.py:158-173): every sample joins its nearest centroid by
+// |x - c| (the first one on equal distances, as argmin), then every centroid
+// with members becomes their mean (one without members keeps its value).
+// The assignment runs one thread per sample with the k <= 256 centroids in
+// LDS; the update one CTA per centroid, which sums its members in a fixed
+// order (strided by thread, then a fixed tree), so results do not depend on
+// scheduling.
+__global__ __launch_bounds__(256) void kmeans1d_assign_kernel(const float* __restrict__ x, int64_t n,
+                                                              const float* __restrict__ cent, int k,
+                                                              int32_t* __restrict__ asg) {
+    __shared__ float s_c[256];
+    if ((int)threadIdx.x < k) s_c[threadIdx.x] = cent[threadIdx.x];
+    __syncthreads();
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const float v = x[i];
+    float bd = fabsf(v - s_c[0]);
+    int bj = 0;
+    for (int j = 1; j < k; ++j) {
+        const float d = fabsf(v - s_c[j]);
+        if (d < bd) {
+            bd = d;
+            bj = j;
+        }
+    }
+    asg[i] = bj;
+}
+
+__global__ __launch_bounds__(256) void kmeans1d_update_kernel(const float* __restrict__ x, int64_t n,
+                                                              const int32_t* __restrict__ asg,
+                                                              float* __restrict__ cent) {
+    __shared__ float s_sum[256];
+    __shared__ int s_cnt[256];
+    const int j = blockIdx.x, t = threadIdx.x;
+    float sum = 0.f;
+    int cnt = 0;
+    for (int64_t i = t; i < n; i += 256) {
+        if (asg[i] == j) {
+            sum += x[i];
+            ++cnt;
+        }
+    }
+    s_sum[t] = sum;
+    s_cnt[t] = cnt;
+    __syncthreads();
+    for (int h = 128; h > 0; h >>= 1) {
+        if (t < h) {
+            s_sum[t] += s_sum[t + h];
+            s_cnt[t] += s_cnt[t + h];
+        }
+        __syncthreads();
+    }
+    if (t == 0 && s_cnt[0] > 0) cent[j] = s_sum[0] / (float)s_cnt[0];
+}
+
 }  // namespace
 
 namespace lutmoe_host {
@@ -244,6 +300,18 @@ int launch_bl4_encode(const float* w, int64_t nblocks, int n_iter, uint8_t* code
     hipLaunchKernelGGL(bl4_encode_kernel, dim3((unsigned)ctas), dim3(256), 0, s, w, nblocks,
                        n_iter, codes, tables);
     return check_launch();
+}
+
+int launch_kmeans_1d(const float* x, int64_t n, float* cent, int k, int n_iter, int32_t* asg, hipStream_t s) {
+    const unsigned grid = (unsigned)((n + 255) / 256);
+    for (int it = 0; it < n_iter; ++it) {
+        hipLaunchKernelGGL(kmeans1d_assign_kernel, dim3(grid), dim3(256), 0, s, x, n, cent, k, asg);
+        int rc = check_launch();
+        if (rc) return rc;
+        hipLaunchKernelGGL(kmeans1d_update_kernel, dim3((unsigned)k), dim3(256), 0, s, x, n, asg, cent);
+        if ((rc = check_launch())) return rc;
+    }
+    return LUTMOE_OK;
 }
 
 int launch_ref_encode(const uint16_t* w, const float* codebook, int64_t n, int block_size, uint8_t* codes,

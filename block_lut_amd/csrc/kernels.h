@@ -89,6 +89,7 @@ int launch_prefill_down(const lutmoe_moe_desc* d, const uint16_t* act, const Moe
 // encode.hip
 int launch_bl4_encode(const float* w, int64_t nblocks, int n_iter, uint8_t* codes,
                       uint16_t* tables, hipStream_t s);
+int launch_kmeans_1d(const float* x, int64_t n, float* cent, int k, int n_iter, int32_t* asg, hipStream_t s);
 int launch_ref_encode(const uint16_t* w, const float* codebook, int64_t n, int block_size, uint8_t* codes,
                       uint16_t* absmax, hipStream_t s);
 

@@ -242,6 +242,17 @@ int lutmoe_bl4_encode(const float* w_dev, int64_t nblocks, int n_iter, uint8_t* 
 int lutmoe_ref_encode(const void* w_bf16_dev, const float* codebook_dev, int64_t n, int block_size,
                       uint8_t* codes_dev, void* absmax_bf16_dev, void* stream);
 
+/* The Lloyd iterations of LUTQuantizer._train_kmeans (vllm_lut/quantizer.py:
+ * 158-173) on the device: n_iter rounds of "each sample joins its nearest
+ * centroid by |x - c| (first on equal distances), each centroid with members
+ * becomes their mean".  data: fp32 [n] (the training samples, already
+ * subsampled); centroids: fp32 [k] in (the initial pick) and out; k <= 256;
+ * assign_ws: int32 [n] scratch.  Sums run in a fixed order (results do not
+ * depend on scheduling); they differ from torch's own summation order in the
+ * last bits.  Sorting and the bf16 store (:176-177) are left to the caller. */
+int lutmoe_kmeans_1d(const float* data_dev, int64_t n, float* centroids_dev, int k, int n_iter,
+                     int32_t* assign_ws_dev, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -103,6 +103,12 @@ def test_validation_before_any_hip_call(lib):
     assert lib.lutmoe_unpack_6bit(P(1), P(1), 6, None) == N.LUTMOE_EINVAL
     assert lib.lutmoe_bl4_encode(P(1), 4, 0, P(1), P(1), None) == N.LUTMOE_EINVAL
     assert lib.lutmoe_bl4_tables_from_f16(P(0x104), P(0x100), 8, None) == N.LUTMOE_EALIGN
+    # 1-D k-means: 1 <= k <= 256, n >= 1, n_iter >= 0, pointers
+    assert lib.lutmoe_kmeans_1d(P(1), 10, P(1), 0, 3, P(1), None) == N.LUTMOE_EINVAL
+    assert lib.lutmoe_kmeans_1d(P(1), 10, P(1), 257, 3, P(1), None) == N.LUTMOE_EINVAL
+    assert lib.lutmoe_kmeans_1d(P(1), 0, P(1), 16, 3, P(1), None) == N.LUTMOE_EINVAL
+    assert lib.lutmoe_kmeans_1d(P(1), 10, P(1), 16, -1, P(1), None) == N.LUTMOE_EINVAL
+    assert lib.lutmoe_kmeans_1d(P(1), 10, None, 16, 3, P(1), None) == N.LUTMOE_EINVAL
     # tier upgrade: n a multiple of 4, shift even in [0, 6], pointers unless n == 0
     assert lib.lutmoe_merge_bitplane(P(1), P(1), 6, 4, None) == N.LUTMOE_EINVAL
     assert lib.lutmoe_merge_bitplane(P(1), P(1), 8, 5, None) == N.LUTMOE_EINVAL

@@ -417,6 +417,28 @@ def test_moe_layer_ref_block_sizes(gpu, block_size, T, path):
     assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
 
 
+@pytest.mark.parametrize("n,k,n_iter", [(300_000, 256, 4), (5000, 256, 12), (100, 256, 3), (4096, 16, 25)])
+def test_train_kmeans_matches_oracle(gpu, n, k, n_iter):
+    """Codebook training (LUTQuantizer._train_kmeans) with the Lloyd iterations on the GPU
+    vs the oracle restatement (pinned by the reference's golden vectors): same subsample
+    and initial pick from the seeded permutations (n > 200k takes the subsample path, n < k
+    pads with zeros), the same assignments; means summed in another order, so the bf16
+    codebooks agree to one bf16 ulp and almost all entries exactly."""
+    from block_lut_amd.quantizer import train_kmeans
+    rng = np.random.default_rng(n + k)
+    w = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    blk = np.abs(np.pad(w, (0, -n % 128)).reshape(-1, 128)).max(axis=1)
+    data = (w / np.repeat(np.maximum(blk, 1e-10), 128)[:n]).astype(np.float32)
+    import torch
+    got = O.f32_to_bf16(train_kmeans(torch.from_numpy(data).to(gpu), k, n_iter, seed=5).float().numpy())
+    ref = O.train_kmeans_ref(data, k, n_iter, seed=5)
+    gf, rf = O.bf16_to_f32(got), O.bf16_to_f32(ref)
+    assert np.all(np.diff(gf) >= 0)
+    ulp = np.abs(rf) * 2.0 ** -7 + 1e-30
+    assert np.all(np.abs(gf - rf) <= ulp), np.max(np.abs(gf - rf) / ulp)
+    assert np.mean(got == ref) >= 0.95
+
+
 @pytest.mark.parametrize("fmt,T", [("bl4", 1), ("bl4", 8), ("bl4", 300), ("ref", 1), ("ref", 300),
                                    ("nested", 4), ("nested", 150)])
 def test_moe_layer_graph_replays(gpu, fmt, T):
