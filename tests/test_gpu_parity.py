@@ -439,6 +439,24 @@ def test_train_kmeans_matches_oracle(gpu, n, k, n_iter):
     assert np.mean(got == ref) >= 0.95
 
 
+def test_train_nested_codebooks(gpu):
+    """LUTQuantizer._train_nested_codebooks: the 64-entry codebook within one bf16 ulp of
+    the oracle's k-means, and both 256-entry tables built from it (16 entries by the
+    reference's greedy merge in bf16)."""
+    import torch
+    from block_lut_amd.quantizer import build_mapped_table, greedy_merge, train_nested_codebooks
+    rng = np.random.default_rng(33)
+    data = np.clip(rng.standard_normal(20000) * 0.3, -1, 1).astype(np.float32)
+    m64, m16 = train_nested_codebooks(torch.from_numpy(data).to(gpu), n_iter=10, seed=9)
+    assert m64.dtype == torch.bfloat16 and m64.numel() == 256 and m16.numel() == 256
+    c64 = m64[:64]
+    assert torch.equal(m64, build_mapped_table(c64, 256))
+    assert torch.equal(m16, build_mapped_table(greedy_merge(c64, 16), 256))
+    ref = O.bf16_to_f32(O.train_kmeans_ref(data, 64, 10, seed=9))
+    got = c64.float().numpy()
+    assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0 ** -7 + 1e-30)
+
+
 @pytest.mark.parametrize("fmt,T", [("bl4", 1), ("bl4", 8), ("bl4", 300), ("ref", 1), ("ref", 300),
                                    ("nested", 4), ("nested", 150)])
 def test_moe_layer_graph_replays(gpu, fmt, T):

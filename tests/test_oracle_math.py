@@ -316,3 +316,20 @@ def test_cpu_baseline_dequant_matches_oracle():
     tb = torch.from_numpy(O.bl4_tables_bf16(tab16).view(np.int16)).view(torch.bfloat16)
     got = bl4_dequant_torch(torch.from_numpy(codes), tb).view(torch.int16).numpy().view(np.uint16)
     assert np.array_equal(got, O.bl4_dequant(codes, tab16))
+
+
+def test_product_nested_table_helpers_match_the_oracle():
+    """block_lut_amd.quantizer.greedy_merge / build_mapped_table (host code of the product)
+    against the oracle's restatements, which the reference's golden vectors pin; the
+    merge's effective rule (the first two entries, every step) on unsorted input too."""
+    import torch
+    from block_lut_amd.quantizer import build_mapped_table, greedy_merge
+    rng = np.random.default_rng(21)
+    for n, tk in ((64, 16), (40, 7), (16, 16)):
+        c = rng.standard_normal(n).astype(np.float32)
+        got = greedy_merge(torch.from_numpy(c), tk).numpy()
+        assert np.array_equal(got, O.greedy_merge_ref(c, tk))
+    for k in (16, 64, 100, 256):
+        c = np.sort(rng.standard_normal(k)).astype(np.float32)
+        got = build_mapped_table(torch.from_numpy(c), 256).view(torch.int16).numpy().view(np.uint16)
+        assert np.array_equal(got, O.build_mapped_table_ref(c, 256))
