@@ -213,6 +213,13 @@ int lutmoe_ref_gemv(const void* x, const void* indices, const void* codebook, co
                            y_dtype, stream_of(stream));
 }
 
+int lutmoe_pack_bitplanes(const uint8_t* codes, int64_t n, uint8_t* packed, void* stream) {
+    if (n < 0 || (n % 4)) return LUTMOE_EINVAL;
+    if (n == 0) return LUTMOE_OK;
+    if (!codes || !packed) return LUTMOE_EINVAL;
+    return launch_pack_bitplanes(codes, n, packed, stream_of(stream));
+}
+
 int lutmoe_merge_bitplane(uint8_t* codes, const uint8_t* plane, int64_t n, int shift, void* stream) {
     if (n < 0 || (n % 4) || shift < 0 || shift > 6 || (shift & 1)) return LUTMOE_EINVAL;
     if (n == 0) return LUTMOE_OK;

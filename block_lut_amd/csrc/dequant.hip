@@ -10,6 +10,8 @@
 //                  reference's copy-to-upper-half + expand.
 //  unpack_6bit   : the 6-bit tier unpack the reference runs on the CPU
 //                  (csrc/tensor_engine/tensor_engine.cpp:535-548).
+//  pack_bitplanes: one-byte codes -> the three bit-plane sections (the
+//                  inverse of the unpacks; convert_lut.py:95-110).
 //  merge_bitplane: in-place tier upgrade of resident codes by one 2-bit
 //                  section (the delta a tier promotion reads,
 //                  tensor_engine.cpp:504-510).
@@ -231,6 +233,55 @@ __global__ __launch_bounds__(256) void merge_bitplane_kernel(uint8_t* __restrict
     }
 }
 
+// One-byte codes [n] -> [low nibbles n/2 | bits 4-5 n/4 | bits 6-7 n/4]
+// (llama-cpp-port/scripts/convert_lut.py:95-110, runtime/model_offload.py:
+// 747-766): low byte i = code 2i | code 2i+1 << 4; mid / high byte i holds
+// codes 4i..4i+3, code 4i+k in bits 2k, 2k+1.  A thread packs 16 codes (one
+// dwordx4 load; 8 + 4 + 4 bytes stored).
+__device__ __forceinline__ uint32_t fields4(uint32_t f) {   // bytes' 2-bit fields -> one byte
+    return (f & 0x3u) | ((f >> 6) & 0xcu) | ((f >> 12) & 0x30u) | ((f >> 18) & 0xc0u);
+}
+
+__global__ __launch_bounds__(256) void pack_bitplanes_kernel(const uint8_t* __restrict__ codes, int64_t n,
+                                                             uint8_t* __restrict__ out, int vec_ok) {
+    const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t i0 = q * 16;
+    if (i0 >= n) return;
+    uint8_t* low = out;
+    uint8_t* mid = out + n / 2;
+    uint8_t* high = out + n / 2 + n / 4;
+    if (vec_ok && i0 + 16 <= n) {
+        const uint4 c = *reinterpret_cast<const uint4*>(codes + i0);
+        const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+        uint32_t lo[2] = {0u, 0u}, m = 0u, h = 0u;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t t = w[k] & 0x0f0f0f0fu;   // nibbles of codes 4k..4k+3
+            const uint32_t b = (t & 0xfu) | ((t >> 4) & 0xf0u) | ((t >> 8) & 0xf00u) | ((t >> 12) & 0xf000u);
+            lo[k >> 1] |= b << (16 * (k & 1));
+            m |= fields4((w[k] >> 4) & 0x03030303u) << (8 * k);
+            h |= fields4((w[k] >> 6) & 0x03030303u) << (8 * k);
+        }
+        *reinterpret_cast<uint2*>(low + i0 / 2) = make_uint2(lo[0], lo[1]);
+        *reinterpret_cast<uint32_t*>(mid + i0 / 4) = m;
+        *reinterpret_cast<uint32_t*>(high + i0 / 4) = h;
+    } else {
+        const int64_t end = min(n, i0 + 16);
+        for (int64_t i = i0; i < end; i += 4) {
+            uint32_t m = 0u, h = 0u;
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t v = codes[i + k];
+                m |= ((v >> 4) & 3u) << (2 * k);
+                h |= ((v >> 6) & 3u) << (2 * k);
+            }
+            low[i / 2] = (uint8_t)((codes[i] & 0xfu) | ((codes[i + 1] & 0xfu) << 4));
+            low[i / 2 + 1] = (uint8_t)((codes[i + 2] & 0xfu) | ((codes[i + 3] & 0xfu) << 4));
+            mid[i / 4] = (uint8_t)m;
+            high[i / 4] = (uint8_t)h;
+        }
+    }
+}
+
 inline int grid1(int64_t work, int per_cta) { return (int)((work + per_cta - 1) / per_cta); }
 
 }  // namespace
@@ -288,6 +339,12 @@ int launch_unpack_4bit_inplace(uint8_t* data, int64_t n, hipStream_t s) {
         m = h;
     }
     hipLaunchKernelGGL(unpack_base_kernel, dim3(1), dim3(1024), 0, s, data, (int)m);
+    return check_launch();
+}
+
+int launch_pack_bitplanes(const uint8_t* codes, int64_t n, uint8_t* out, hipStream_t s) {
+    const int vec_ok = ((uintptr_t)codes % 16 == 0) && ((uintptr_t)out % 8 == 0) && (n % 16 == 0);
+    hipLaunchKernelGGL(pack_bitplanes_kernel, dim3(grid1(n, 256 * 16)), dim3(256), 0, s, codes, n, out, vec_ok);
     return check_launch();
 }
 

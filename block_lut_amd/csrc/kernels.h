@@ -14,6 +14,7 @@ int launch_ref_dequant(uint16_t* out, const uint8_t* idx, const uint16_t* absmax
                        int block_size, int num_experts, int64_t out_stride,
                        int64_t idx_stride, hipStream_t s, int64_t cb_stride = 0);
 int launch_merge_bitplane(uint8_t* codes, const uint8_t* plane, int64_t n, int shift, hipStream_t s);
+int launch_pack_bitplanes(const uint8_t* codes, int64_t n, uint8_t* out, hipStream_t s);
 int launch_bl4_dequant(uint16_t* out, const uint8_t* codes, const uint16_t* tables,
                        int64_t nblocks, hipStream_t s);
 int launch_nested_dequant(uint16_t* out, const lutmoe_weights* w, int e0, int ne,

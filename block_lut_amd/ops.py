@@ -77,6 +77,18 @@ def unpack_6bit(packed: torch.Tensor, num_elements: int) -> torch.Tensor:
     return out
 
 
+def pack_bitplanes(codes: torch.Tensor) -> torch.Tensor:
+    """One-byte codes -> the BLOCKLUT8 bit-plane sections [low n/2 | mid n/4 | high n/4]
+    (convert_lut.py:95-110), on the device."""
+    _dev(codes, torch.uint8, "codes")
+    n = codes.numel()
+    if n % 4:
+        raise ValueError("bit-plane packing needs a multiple of 4 codes")
+    out = torch.empty(n, dtype=torch.uint8, device=codes.device)
+    N.check("lutmoe_pack_bitplanes", N.lib().lutmoe_pack_bitplanes(codes.data_ptr(), n, out.data_ptr(), _stream()))
+    return out
+
+
 def merge_bitplane_(codes: torch.Tensor, plane: torch.Tensor, shift: int) -> torch.Tensor:
     """In place: code i of ``codes`` takes the 2-bit field
     ``(plane[i // 4] >> 2 * (i % 4)) & 3`` at bits [shift, shift + 2) -- one

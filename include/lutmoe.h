@@ -141,6 +141,13 @@ int lutmoe_ref_gemv(const void* x_dev, const void* indices_dev, const void* code
  * the [low | mid] sections of `packed`, written to `out` (n bytes). */
 int lutmoe_unpack_6bit(const uint8_t* packed_dev, uint8_t* out_dev, int64_t n, void* stream);
 
+/* Bit-plane packing (llama-cpp-port/scripts/convert_lut.py:95-110,
+ * runtime/model_offload.py:747-766), the inverse of the unpacks above:
+ * codes_dev[n] (one byte per code) -> packed_dev[n] = [low nibbles n/2 |
+ * bits 4-5 n/4 | bits 6-7 n/4]; low byte i = code 2i | code 2i+1 << 4, mid /
+ * high byte i holds code 4i+k in bits 2k..2k+1.  n % 4 == 0. */
+int lutmoe_pack_bitplanes(const uint8_t* codes_dev, int64_t n, uint8_t* packed_dev, void* stream);
+
 /* Progressive tier upgrade of resident codes (the reference reloads the whole
  * expert on a promotion, csrc/topology/model_topology.cpp:74-80, reading
  * the tier's prefix of the bit-plane file, tensor_engine.cpp:504-510): in

@@ -103,6 +103,10 @@ def test_validation_before_any_hip_call(lib):
     assert lib.lutmoe_unpack_6bit(P(1), P(1), 6, None) == N.LUTMOE_EINVAL
     assert lib.lutmoe_bl4_encode(P(1), 4, 0, P(1), P(1), None) == N.LUTMOE_EINVAL
     assert lib.lutmoe_bl4_tables_from_f16(P(0x104), P(0x100), 8, None) == N.LUTMOE_EALIGN
+    # bit-plane packing: n a multiple of 4
+    assert lib.lutmoe_pack_bitplanes(P(1), 6, P(1), None) == N.LUTMOE_EINVAL
+    assert lib.lutmoe_pack_bitplanes(None, 8, P(1), None) == N.LUTMOE_EINVAL
+    assert lib.lutmoe_pack_bitplanes(None, 0, None, None) == N.LUTMOE_OK
     # 1-D k-means: 1 <= k <= 256, n >= 1, n_iter >= 0, pointers
     assert lib.lutmoe_kmeans_1d(P(1), 10, P(1), 0, 3, P(1), None) == N.LUTMOE_EINVAL
     assert lib.lutmoe_kmeans_1d(P(1), 10, P(1), 257, 3, P(1), None) == N.LUTMOE_EINVAL

@@ -136,6 +136,23 @@ def test_unpack_6bit(gpu):
 
 
 @pytest.mark.parametrize("n,off", [(4, 0), (20, 0), (4096 + 12, 0), (1 << 20, 0), (4096, 1), (8200, 3)])
+def test_pack_bitplanes(gpu, n, off):
+    """Bit-plane packing vs the oracle, bit-exact (odd offsets and sizes take the byte
+    path), and the round trip through the GPU unpacks and the tier merges."""
+    import torch
+    from block_lut_amd import ops
+    rng = np.random.default_rng(n * 3 + off)
+    codes = rng.integers(0, 256, off + n, dtype=np.uint8)
+    dc = torch.from_numpy(codes).to(gpu)[off:]
+    got = ops.pack_bitplanes(dc)
+    assert np.array_equal(got.cpu().numpy(), O.bitplane_pack_ref(codes[off:]))
+    c6 = ops.unpack_6bit(got, n)
+    assert np.array_equal(c6.cpu().numpy(), codes[off:] & 0x3F)
+    ops.merge_bitplane_(c6, got[n // 2 + n // 4:], 6)
+    assert np.array_equal(c6.cpu().numpy(), codes[off:])
+
+
+@pytest.mark.parametrize("n,off", [(4, 0), (20, 0), (4096 + 12, 0), (1 << 20, 0), (4096, 1), (8200, 3)])
 def test_merge_bitplane(gpu, n, off):
     """In-place merge of a 2-bit section at every shift vs the oracle, bit-exact; odd
     offsets take the byte path; the bytes around the codes stay untouched."""
