@@ -840,10 +840,99 @@ __device__ __forceinline__ void gate_up_body(const DecodeArgs& A, const RV& rv, 
     }
 }
 
+// BL4 gate/up with 2 intermediate indices per wave (2 gate + 2 up rows): twice
+// the waves of gate_up_body, each with half the serial work.  At one token
+// per pass the kernel is bound by each wave's instruction and latency chain
+// at about 1.4 waves per SIMD, and twice the waves shorten it (T=1 gate/up
+// 10.5 -> 9.6 us); with two or more tokens per pass the waves carry enough
+// work and the 4-index body is as fast or faster (T=2: 16.7 vs 17.9 us).
+static_assert(kGuWaves == 1, "gate_up_body4 assumes one wave per CTA");
+template <int TB>
+constexpr bool gu2_for() { return TB == 1; }
+template <int TB, class RV>
+__device__ __forceinline__ void gate_up_body4(const DecodeArgs& A, const RV& rv, uint8_t* slot) {
+    const SlotRef sl = rv.work(blockIdx.y);
+    if (sl.e < 0) return;
+    const int lane = threadIdx.x & 63;
+    const int I = A.d.inter, H = A.d.hidden, ke = A.k + A.d.num_shared;
+    const int i0 = blockIdx.x * 2;
+    if (i0 >= I) return;
+    const int i1 = min(i0 + 1, I - 1);
+    const int rows[4] = {i0, i1, I + i0, I + i1};
+    const int64_t per = (int64_t)A.d.w13.rows * (H / 2);
+    const uint8_t* codes = (const uint8_t*)A.d.w13.codes + sl.e * per;
+    const uint8_t* tabs = (const uint8_t*)A.d.w13.tables + sl.e * per;
+    const uint32_t tab = lds_addr(slot) + ((lane >> 1) << 5);
+    const u32x4_t z = {0u, 0u, 0u, 0u};
+    const int nch = (H + kWChunk - 1) / kWChunk;
+    for (int tb = 0; tb < sl.n; tb += TB) {
+        const int nt = min(TB, sl.n - tb);
+        const uint16_t* xrow[TB];
+#pragma unroll
+        for (int t = 0; t < TB; ++t) {
+            const int tok = rv.pair_at(sl.p0 + tb + min(t, nt - 1)) / ke;
+            xrow[t] = A.x + (int64_t)min(max(tok, 0), A.T - 1) * H;
+        }
+        float acc[4][TB];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int t = 0; t < TB; ++t) acc[r][t] = 0.f;
+        for (int cc = 0; cc < nch; ++cc) {
+            uint32_t xs[TB][16];
+            load_x8<TB>(xrow, H, cc, lane, nt, xs);
+            __builtin_amdgcn_sched_barrier(0);
+            const bool ok = cc * kWChunk + 32 * lane < H;
+            u32x4_t cw[4], tw[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t off = (int64_t)rows[r] * (H / 2) + (ok ? cc * (kWChunk / 2) + 16 * lane : 0);
+                cw[r] = *reinterpret_cast<const u32x4_t*>(codes + off);
+                tw[r] = *reinterpret_cast<const u32x4_t*>(tabs + off);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                *reinterpret_cast<u32x4_t*>(slot + r * 1024 + 16 * lane) = ok ? tw[r] : z;
+                wave_lds_sync();
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    uint32_t xj[TB][4];
+#pragma unroll
+                    for (int t = 0; t < TB; ++t)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) xj[t][i] = xs[t][4 * j + i];
+                    bl4_dot8<TB>(cw[r][j], tab + r * 1024, xj, nt, acc[r]);
+                }
+            }
+            wave_lds_sync();
+        }
+#pragma unroll
+        for (int t = 0; t < TB; ++t) {
+            const float g0 = wave_reduce(acc[0][t]), g1 = wave_reduce(acc[1][t]);
+            const float u0 = wave_reduce(acc[2][t]), u1 = wave_reduce(acc[3][t]);
+            if (lane == 0 && t < nt) {
+                uint16_t* a = A.act + (int64_t)(sl.p0 + tb + t) * I;
+                a[i0] = (uint16_t)f32_to_bf16(silu_mul(g0, u0));
+                if (i0 + 1 < I) a[i0 + 1] = (uint16_t)f32_to_bf16(silu_mul(g1, u1));
+            }
+        }
+    }
+}
+
 template <int TB, bool kPre, int kFmt>
 __global__ __launch_bounds__(64 * kGuWaves, TB <= 2 ? 3 : 2) void bl4_decode_gate_up(DecodeArgs A) {
     __shared__ __attribute__((aligned(16))) uint8_t s_slot[kGuWaves * kSlot];
-    if constexpr (kPre) {
+    if constexpr (gu2_for<TB>() && kFmt == LUTMOE_FMT_BL4) {
+        if constexpr (kPre) {
+            gate_up_body4<TB>(A, GlobalRouteView{A.route}, s_slot);
+        } else {
+            const bool pub = blockIdx.x == 0 && blockIdx.y == 0;
+            const WaveRoute r = pub ? wave_pairs<true>(A) : wave_pairs<false>(A);
+            if (pub && threadIdx.x < 64) wave_route_publish(A, r);
+            gate_up_body4<TB>(A, WaveRouteView{r}, s_slot);
+        }
+    } else if constexpr (kPre) {
         gate_up_body<TB, kFmt>(A, GlobalRouteView{A.route}, s_slot);
     } else {
         // the first CTA also publishes the routing (with the pair weights)
@@ -1314,7 +1403,8 @@ int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* t
     // (at most P, and at most one more per slot than ceil(P / TB))
     const int max_work = pre ? std::min(P, max_active + (P + tb_for(T) - 1) / tb_for(T)) : max_active;
     if (stages & LUTMOE_STAGE_GATE_UP) {
-        const dim3 grid((d->inter + 4 * kGuWaves - 1) / (4 * kGuWaves), max_work);
+        const int per_cta = (fmt_idx == 0 && tb_for(T) == 1) ? 2 : 4 * kGuWaves;   // intermediate indices per CTA
+        const dim3 grid((d->inter + per_cta - 1) / per_cta, max_work);
         LUTMOE_DECODE_LAUNCH(bl4_decode_gate_up, pre, grid, dim3(64 * kGuWaves), 0)
         if ((rc = check_launch())) return rc;
     }
