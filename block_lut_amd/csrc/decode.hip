@@ -849,6 +849,48 @@ __device__ __forceinline__ void gate_up_body(const DecodeArgs& A, const RV& rv, 
 static_assert(kGuWaves == 1, "gate_up_body4 assumes one wave per CTA");
 template <int TB>
 constexpr bool gu2_for() { return TB == 1; }
+
+// Four BL4 rows over all of K (as bl4_rows8 for 8): per 2048-column chunk the
+// activations, then both loads of every row, then row by row the table
+// staging and the lookups; the wave's LDS slot holds 4 rows' tables (4 KB).
+template <int TB>
+__device__ __forceinline__ void bl4_rows4(const uint8_t* __restrict__ codes, const uint8_t* __restrict__ tabs,
+                                          const int (&rows)[4], int K, int lane, uint8_t* slot,
+                                          const uint16_t* const (&xrow)[TB], int nt, float (&acc)[4][TB]) {
+    const uint32_t tab = lds_addr(slot) + ((lane >> 1) << 5);
+    const u32x4_t z = {0u, 0u, 0u, 0u};
+    const int nch = (K + kWChunk - 1) / kWChunk;
+    for (int cc = 0; cc < nch; ++cc) {
+        uint32_t xs[TB][16];
+        load_x8<TB>(xrow, K, cc, lane, nt, xs);
+        __builtin_amdgcn_sched_barrier(0);
+        const bool ok = cc * kWChunk + 32 * lane < K;
+        u32x4_t cw[4], tw[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t off = (int64_t)rows[r] * (K / 2) + (ok ? cc * (kWChunk / 2) + 16 * lane : 0);
+            cw[r] = *reinterpret_cast<const u32x4_t*>(codes + off);
+            tw[r] = *reinterpret_cast<const u32x4_t*>(tabs + off);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            *reinterpret_cast<u32x4_t*>(slot + r * 1024 + 16 * lane) = ok ? tw[r] : z;
+            wave_lds_sync();
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                uint32_t xj[TB][4];
+#pragma unroll
+                for (int t = 0; t < TB; ++t)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) xj[t][i] = xs[t][4 * j + i];
+                bl4_dot8<TB>(cw[r][j], tab + r * 1024, xj, nt, acc[r]);
+            }
+        }
+        wave_lds_sync();
+    }
+}
+
 template <int TB, class RV>
 __device__ __forceinline__ void gate_up_body4(const DecodeArgs& A, const RV& rv, uint8_t* slot) {
     const SlotRef sl = rv.work(blockIdx.y);
@@ -862,9 +904,6 @@ __device__ __forceinline__ void gate_up_body4(const DecodeArgs& A, const RV& rv,
     const int64_t per = (int64_t)A.d.w13.rows * (H / 2);
     const uint8_t* codes = (const uint8_t*)A.d.w13.codes + sl.e * per;
     const uint8_t* tabs = (const uint8_t*)A.d.w13.tables + sl.e * per;
-    const uint32_t tab = lds_addr(slot) + ((lane >> 1) << 5);
-    const u32x4_t z = {0u, 0u, 0u, 0u};
-    const int nch = (H + kWChunk - 1) / kWChunk;
     for (int tb = 0; tb < sl.n; tb += TB) {
         const int nt = min(TB, sl.n - tb);
         const uint16_t* xrow[TB];
@@ -878,35 +917,7 @@ __device__ __forceinline__ void gate_up_body4(const DecodeArgs& A, const RV& rv,
         for (int r = 0; r < 4; ++r)
 #pragma unroll
             for (int t = 0; t < TB; ++t) acc[r][t] = 0.f;
-        for (int cc = 0; cc < nch; ++cc) {
-            uint32_t xs[TB][16];
-            load_x8<TB>(xrow, H, cc, lane, nt, xs);
-            __builtin_amdgcn_sched_barrier(0);
-            const bool ok = cc * kWChunk + 32 * lane < H;
-            u32x4_t cw[4], tw[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int64_t off = (int64_t)rows[r] * (H / 2) + (ok ? cc * (kWChunk / 2) + 16 * lane : 0);
-                cw[r] = *reinterpret_cast<const u32x4_t*>(codes + off);
-                tw[r] = *reinterpret_cast<const u32x4_t*>(tabs + off);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                *reinterpret_cast<u32x4_t*>(slot + r * 1024 + 16 * lane) = ok ? tw[r] : z;
-                wave_lds_sync();
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    uint32_t xj[TB][4];
-#pragma unroll
-                    for (int t = 0; t < TB; ++t)
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) xj[t][i] = xs[t][4 * j + i];
-                    bl4_dot8<TB>(cw[r][j], tab + r * 1024, xj, nt, acc[r]);
-                }
-            }
-            wave_lds_sync();
-        }
+        bl4_rows4<TB>(codes, tabs, rows, H, lane, slot, xrow, nt, acc);
 #pragma unroll
         for (int t = 0; t < TB; ++t) {
             const float g0 = wave_reduce(acc[0][t]), g1 = wave_reduce(acc[1][t]);
@@ -1002,14 +1013,62 @@ __device__ __forceinline__ void down_body(const DecodeArgs& A, const RV& rv, uin
     }
 }
 
+// BL4 down at one token per pass with 4 output rows per CTA (twice the CTAs
+// of down_body, half the serial work per wave; the reason as for
+// gate_up_body4).  Wave wv runs the active slots wv, wv+4, ..
+template <class RV>
+__device__ __forceinline__ void down_body4(const DecodeArgs& A, const RV& rv, uint8_t* s_slot, float* s_y) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int I = A.d.inter, H = A.d.hidden, ke = A.k + A.d.num_shared;
+    const int h0 = blockIdx.x * 4;
+    int rows[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) rows[r] = min(h0 + r, H - 1);
+    uint8_t* slot = s_slot + wv * kSlot;
+    const int64_t per = (int64_t)A.d.w2.rows * (I / 2);
+    const int nact = rv.nact();
+    for (int a = wv; a < nact; a += (int)(blockDim.x >> 6)) {
+        const SlotRef sl = rv.slot(a);
+        for (int p = sl.p0; p < sl.p0 + sl.n; ++p) {
+            const uint16_t* xrow[1] = {A.act + (int64_t)p * I};
+            float acc[4][1] = {{0.f}, {0.f}, {0.f}, {0.f}};
+            bl4_rows4<1>((const uint8_t*)A.d.w2.codes + sl.e * per, (const uint8_t*)A.d.w2.tables + sl.e * per,
+                         rows, I, lane, slot, xrow, 1, acc);
+            const float pw = rv.weight_at(p);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float y = wave_reduce(acc[r][0]);
+                if (lane == r) s_y[p * 4 + r] = y * pw;
+            }
+        }
+    }
+    __syncthreads();
+    const int T = A.T;
+    for (int base = 0; base < T * 4; base += blockDim.x) {
+        const int idx = base + threadIdx.x;
+        const int t = min(idx / 4, T - 1), r = idx % 4;
+        float sum = 0.f;
+        for (int q = 0; q < ke; ++q) {
+            const int pos = rv.pos_of(t * ke + q);
+            if (pos >= 0) sum += s_y[pos * 4 + r];
+        }
+        if (idx < T * 4 && h0 + r < H) {
+            const int64_t o = (int64_t)t * H + h0 + r;
+            if (A.out_dtype == LUTMOE_DTYPE_F32) ((float*)A.out)[o] = sum;
+            else ((uint16_t*)A.out)[o] = (uint16_t)f32_to_bf16(sum);
+        }
+    }
+}
+
 template <int TB, bool kPre, int kFmt>
 __global__ __launch_bounds__(256, TB <= 2 ? 3 : 2) void bl4_decode_down(DecodeArgs A) {
     __shared__ __attribute__((aligned(16))) uint8_t s_slot[4 * kSlot];
-    extern __shared__ float s_y[];   // [P][8]
+    extern __shared__ float s_y[];   // [P][8] ([P][4] for down_body4)
     if constexpr (kPre) {
         __shared__ RouteOut R;
         load_route(A, R);
-        down_body<TB, kFmt>(A, LdsRouteView{&R}, s_slot, s_y);
+        if constexpr (gu2_for<TB>() && kFmt == LUTMOE_FMT_BL4) down_body4(A, LdsRouteView{&R}, s_slot, s_y);
+        else down_body<TB, kFmt>(A, LdsRouteView{&R}, s_slot, s_y);
     } else {
         down_body<TB, kFmt>(A, WaveRouteView{wave_pairs<true>(A)}, s_slot, s_y);
     }
@@ -1409,7 +1468,8 @@ int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* t
         if ((rc = check_launch())) return rc;
     }
     if (stages & LUTMOE_STAGE_DOWN) {
-        const dim3 grid((d->hidden + kRows - 1) / kRows);
+        const int hrows = (fmt_idx == 0 && tb_for(T) == 1) ? 4 : kRows;   // output rows per CTA (down_body4: 4)
+        const dim3 grid((d->hidden + hrows - 1) / hrows);
         const size_t lds = (size_t)P * kRows * sizeof(float);
         // the routing comes from the copy in the workspace (written by the
         // gate/up kernel's first CTA, or by decode_route_kernel)
