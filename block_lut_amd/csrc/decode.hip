@@ -82,6 +82,7 @@ struct DecodeArgs {
     const int32_t* topk_ids;   // [T][k] (ids mode)
     const float* logits;       // [T][E] fp32 (logits mode: topk_ids == nullptr)
     int T, k, renorm;
+    int tb;                    // tokens per pass of the expert loops (1, 2 or 4)
     float scaling;
     uint16_t* act;             // [P][I] bf16
     void* out;
@@ -508,7 +509,7 @@ __device__ __forceinline__ void put_chunks(const DecodeArgs& A, const RouteOut& 
     __shared__ int s_wsum[32];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int nact = R.nact;
-    const int TB = A.T <= 1 ? 1 : A.T <= 2 ? 2 : 4;   // tokens per pass (the host's tb_for)
+    const int TB = A.tb;   // tokens per pass
     const int pv = nact > 0 ? R.aoff[nact - 1] + R.an[nact - 1] : 0;
     const int navg = nact > 0 ? (pv + nact - 1) / nact : 1;
     const int C = TB * max(1, (navg + TB / 2) / TB);
@@ -1365,7 +1366,13 @@ __global__ __launch_bounds__(256, 2) void nested_gemv_kernel(lutmoe_weights w, i
 }
 
 // tokens per pass: T=1 and T=2 recompute routing per CTA, larger T read it
-inline int tb_for(int T) { return T <= 1 ? 1 : T <= 2 ? 2 : 4; }
+// Tokens per pass of the expert loops (fmt_idx: 0 BL4, 1 nested, 2 REF).  Up
+// to 16 tokens most active experts hold one or two of them, and a 4-token BL4
+// pass would spend its FMAs and activation loads on empty positions (Qwen
+// shape, MI355X: 2-token passes take T=4/8/16 from 58/85/121 to 50/72/108 us
+// per layer; at T=32 4-token passes stay ahead, 159 vs 173 us).  The nested
+// kernels lose with 2-token passes at T=16 (127 -> 140 us) and keep 4.
+inline int tb_for(int T, int fmt_idx) { return T <= 1 ? 1 : T <= (fmt_idx == 0 ? 16 : 2) ? 2 : 4; }
 
 }  // namespace
 
@@ -1424,19 +1431,21 @@ int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* t
     // T <= 2 with the pairs in one wave: both kernels route in registers; else
     // one routing kernel writes the workspace copy both kernels read.
     const bool pre = T > 2 || !(P <= 64 && (topk_ids != nullptr || d->num_routed <= 64));
+    const bool nested = d->w13.format == LUTMOE_FMT_NESTED;
+    const int fmt_idx = nested ? 1 : d->w13.format == LUTMOE_FMT_REF ? 2 : 0;
+    const int tb = tb_for(T, fmt_idx);
+    A.tb = tb;   // before the routing launch: its chunking reads it
     int rc;
     if (pre && (stages & LUTMOE_STAGE_ROUTE)) {
         hipLaunchKernelGGL(decode_route_kernel, dim3(1), dim3(1024), 0, s, A);
         if ((rc = check_launch())) return rc;
     }
-    const bool nested = d->w13.format == LUTMOE_FMT_NESTED;
-    const int fmt_idx = nested ? 1 : d->w13.format == LUTMOE_FMT_REF ? 2 : 0;
     if (kFusedDecodeEnabled && fmt_idx == 0 && stages == LUTMOE_STAGE_ALL && sync_ws) {
         // one persistent launch: enough CTAs for one item each
         const int items = max_active * ((d->inter + 15) / 16) + (d->hidden + kRows - 1) / kRows;
         const size_t lds = (size_t)P * kRows * sizeof(float);
         DecodeSync* sy = (DecodeSync*)sync_ws;
-        switch (tb_for(T)) {
+        switch (tb) {
             case 1: hipLaunchKernelGGL((bl4_decode_fused<1, false>), dim3(items), dim3(256), lds, s, A, sy); break;
             case 2: hipLaunchKernelGGL((bl4_decode_fused<2, false>), dim3(items), dim3(256), lds, s, A, sy); break;
             default: hipLaunchKernelGGL((bl4_decode_fused<4, true>), dim3(items), dim3(256), lds, s, A, sy); break;
@@ -1450,7 +1459,7 @@ int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* t
     LUTMOE_DECODE_CASE(N + 1, TB, PRE, LUTMOE_FMT_NESTED, KERNEL, GRID, BLOCK, LDS) \
     LUTMOE_DECODE_CASE(N + 2, TB, PRE, LUTMOE_FMT_REF, KERNEL, GRID, BLOCK, LDS)
 #define LUTMOE_DECODE_LAUNCH(KERNEL, PRE, GRID, BLOCK, LDS)                 \
-    switch (tb_for(T) * 8 + ((PRE) ? 4 : 0) + fmt_idx) {                    \
+    switch (tb * 8 + ((PRE) ? 4 : 0) + fmt_idx) {                    \
         LUTMOE_DECODE_FMTS(8, 1, false, KERNEL, GRID, BLOCK, LDS)           \
         LUTMOE_DECODE_FMTS(12, 1, true, KERNEL, GRID, BLOCK, LDS)           \
         LUTMOE_DECODE_FMTS(16, 2, false, KERNEL, GRID, BLOCK, LDS)          \
@@ -1460,15 +1469,15 @@ int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* t
     }
     // work items: the active slots, cut into chunks by decode_route_kernel
     // (at most P, and at most one more per slot than ceil(P / TB))
-    const int max_work = pre ? std::min(P, max_active + (P + tb_for(T) - 1) / tb_for(T)) : max_active;
+    const int max_work = pre ? std::min(P, max_active + (P + tb - 1) / tb) : max_active;
     if (stages & LUTMOE_STAGE_GATE_UP) {
-        const int per_cta = (fmt_idx == 0 && tb_for(T) == 1) ? 2 : 4 * kGuWaves;   // intermediate indices per CTA
+        const int per_cta = (fmt_idx == 0 && tb == 1) ? 2 : 4 * kGuWaves;   // intermediate indices per CTA
         const dim3 grid((d->inter + per_cta - 1) / per_cta, max_work);
         LUTMOE_DECODE_LAUNCH(bl4_decode_gate_up, pre, grid, dim3(64 * kGuWaves), 0)
         if ((rc = check_launch())) return rc;
     }
     if (stages & LUTMOE_STAGE_DOWN) {
-        const int hrows = (fmt_idx == 0 && tb_for(T) == 1) ? 4 : kRows;   // output rows per CTA (down_body4: 4)
+        const int hrows = (fmt_idx == 0 && tb == 1) ? 4 : kRows;   // output rows per CTA (down_body4: 4)
         const dim3 grid((d->hidden + hrows - 1) / hrows);
         const size_t lds = (size_t)P * kRows * sizeof(float);
         // the routing comes from the copy in the workspace (written by the
@@ -1477,7 +1486,7 @@ int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* t
             // many experts: y + combine, every slot in parallel
             const dim3 gy((d->hidden + kRows - 1) / kRows, (max_work + 3) / 4);
 #define LUTMOE_DOWN_Y(TB, FMT) hipLaunchKernelGGL((bl4_decode_down_y<TB, FMT>), gy, dim3(256), 0, s, A, y_ws)
-            switch (tb_for(T) * 4 + fmt_idx) {
+            switch (tb * 4 + fmt_idx) {
                 case 4: LUTMOE_DOWN_Y(1, LUTMOE_FMT_BL4); break;
                 case 5: LUTMOE_DOWN_Y(1, LUTMOE_FMT_NESTED); break;
                 case 6: LUTMOE_DOWN_Y(1, LUTMOE_FMT_REF); break;
