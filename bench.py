@@ -250,7 +250,8 @@ def main():
                    "avg_distinct_experts": round(sum(s.U for s in steps) / len(steps), 3)},
         "us_per_token": round(us_per_token, 3),
         "tokens_per_s": round(T / (ms_per_step / 1e3), 1),
-        "roofline": {"bound": "hbm", "kernel": "bl4_decode_gate_up<1>",
+        # template argument = tokens per pass (1 at T=1, 2 up to T=16, else 4)
+        "roofline": {"bound": "hbm", "kernel": f"bl4_decode_gate_up<{1 if T <= 1 else 2 if T <= 16 else 4}>",
                      "achieved": round(ach_gu, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(ach_gu / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "avg_launch_us": round(dur_gu * 1e6, 3),
