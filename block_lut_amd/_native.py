@@ -67,6 +67,7 @@ class lutmoe_moe_desc(ctypes.Structure):
         ("inter", ctypes.c_int32),
         ("num_routed", ctypes.c_int32),
         ("num_shared", ctypes.c_int32),
+        ("shared_gate", ctypes.c_void_p),
     ]
 
 

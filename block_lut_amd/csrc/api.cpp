@@ -108,6 +108,7 @@ int validate_moe(const lutmoe_moe_desc* d) {
     if (d->w13.num_experts < E_tot || d->w2.num_experts < E_tot) return LUTMOE_EINVAL;
     if (d->w13.format != d->w2.format) return LUTMOE_EUNSUPPORTED;
     if (H % 64 || I % 64) return LUTMOE_EUNSUPPORTED;
+    if (d->shared_gate && !aligned(d->shared_gate, 16)) return LUTMOE_EALIGN;
     if (d->w13.format == LUTMOE_FMT_REF) {
         if ((rc = validate_ref_vector(&d->w13)) || (rc = validate_ref_vector(&d->w2))) return rc;
     }
@@ -337,9 +338,9 @@ int moe_forward_impl(const lutmoe_moe_desc* d, const void* x, const float* topk_
     const bool lds_ok = P * 8 * 4 <= 48 * 1024;
     bool gemv = force_path == 1 || (force_path == 0 && T <= 32 && lds_ok);
     if (gemv && !lds_ok) return LUTMOE_EUNSUPPORTED;
-    // NestedLUT decodes only through the decode-layer kernels; otherwise the
-    // grouped MFMA path
-    if (d->w13.format == LUTMOE_FMT_NESTED && gemv && !decode_v2_supported(d, T, k)) {
+    // the decode-layer kernels take up to 320 experts and 512 (token, slot)
+    // pairs; anything else runs on the grouped MFMA path
+    if (gemv && !decode_v2_supported(d, T, k)) {
         if (force_path == 1) return LUTMOE_EUNSUPPORTED;
         gemv = false;
     }
@@ -347,13 +348,7 @@ int moe_forward_impl(const lutmoe_moe_desc* d, const void* x, const float* topk_
     char* ws = (char*)workspace;
     uint16_t* act = (uint16_t*)(ws + L.act);
     hipStream_t s = stream_of(stream);
-    // the older decode pair (gemv.hip) reads one REF codebook per CTA across
-    // experts: per-expert codebooks go through the decode layer or the MFMA path
-    if (gemv && !decode_v2_supported(d, T, k) && d->w2.format == LUTMOE_FMT_REF && d->w2.codebook_stride) {
-        if (force_path == 1) return LUTMOE_EUNSUPPORTED;
-        gemv = false;
-    }
-    if (gemv && decode_v2_supported(d, T, k)) {
+    if (gemv) {
         // routing + permutation happen inside both decode kernels
         return launch_decode_v2(d, (const uint16_t*)x, topk_w, topk_ids, logits, T, k, renorm,
                                 scaling, act, ws + L.route, ws + L.sync, (float*)(ws + L.y), out, out_dtype, stages, s);
@@ -381,15 +376,10 @@ int moe_forward_impl(const lutmoe_moe_desc* d, const void* x, const float* topk_
         if ((rc = launch_route_pairs(topk_ids, topk_w, T, k, E, S, (int32_t*)r.offsets, (int32_t*)r.perm,
                                      (int32_t*)r.inv, (int32_t*)r.active, pair_ids, pair_w, s)))
             return rc;
-    }
-    const int max_active = (int)(P < E_tot ? P : E_tot);
-    if (gemv) {
-        if ((stages & LUTMOE_STAGE_GATE_UP) &&
-            (rc = launch_decode_gate_up(d, (const uint16_t*)x, r, act, max_active, s)))
+        if (d->shared_gate && S > 0 &&
+            (rc = launch_shared_gate((const uint16_t*)x, (const uint16_t*)d->shared_gate, T, d->hidden, k, S,
+                                     pair_w, s)))
             return rc;
-        if (stages & LUTMOE_STAGE_DOWN)
-            return launch_decode_down_combine(d, act, r, out, out_dtype, max_active, s);
-        return LUTMOE_OK;
     }
     if ((stages & LUTMOE_STAGE_GATE_UP) &&
         (rc = launch_prefill_gate_up(d, (const uint16_t*)x, r, act, (int)P, s)))

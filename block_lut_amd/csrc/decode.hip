@@ -113,7 +113,14 @@ __device__ void cta_route(const DecodeArgs& A, RouteOut& R, RouteScratch& X) {
                 w = 1.0f;
             }
             X.pid[p] = e;
-            R.pw[p] = w;
+            if (s < k || !A.d.shared_gate) R.pw[p] = w;   // gated shared slots: below
+        }
+        if (A.d.shared_gate && S > 0) {
+            for (int t = wv; t < T; t += (int)(blockDim.x >> 6)) {
+                const float sw = shared_gate_weight(A.x + (int64_t)t * A.d.hidden,
+                                                    (const uint16_t*)A.d.shared_gate, A.d.hidden);
+                if (lane < S) R.pw[t * ke + k + lane] = sw;
+            }
         }
     } else {
         // logits mode, wave per token: softmax in fp32; top-k by logit (softmax
@@ -175,9 +182,13 @@ __device__ void cta_route(const DecodeArgs& A, RouteOut& R, RouteScratch& X) {
                     R.pw[t * ke + lane] = (A.renorm ? pj / wsum : pj) * A.scaling;
                 }
             }
+            const float sw = A.d.shared_gate && S > 0
+                                 ? shared_gate_weight(A.x + (int64_t)t * A.d.hidden,
+                                                      (const uint16_t*)A.d.shared_gate, A.d.hidden)
+                                 : 1.0f;
             if (lane < S) {
                 X.pid[t * ke + k + lane] = E + lane;
-                R.pw[t * ke + k + lane] = 1.0f;
+                R.pw[t * ke + k + lane] = sw;
             }
         }
     }
@@ -313,6 +324,14 @@ __device__ __forceinline__ WaveRoute wave_pairs(const DecodeArgs& A) {
             }
             if (kWeights && lane >= t * ke && lane < t * ke + k) w = (A.renorm ? w / wsum : w) * A.scaling;
             if (lane >= t * ke + k && lane < (t + 1) * ke) { e = E + lane - t * ke - k; w = 1.0f; }
+        }
+    }
+    if (kWeights && A.d.shared_gate && S > 0) {
+        // Qwen's gated shared expert: its slots of token t weigh sigmoid(x_t . g)
+        for (int t = 0; t < T; ++t) {
+            const float sw = shared_gate_weight(A.x + (int64_t)t * A.d.hidden, (const uint16_t*)A.d.shared_gate,
+                                                A.d.hidden);
+            if (lane >= t * ke + k && lane < (t + 1) * ke) w = sw;
         }
     }
     int less = 0, before = 0, cnt = 0;
@@ -738,15 +757,54 @@ __device__ __forceinline__ void load_rows8r(const uint8_t* __restrict__ codes, c
     }
 }
 
+// 32 REF byte codes against the fp32[256] codebook at LDS byte address
+// `cbase`, with the weights the reference's dequantisation produces:
+// w = bf16_rne(cb[c] * absmax) (the product of two bf16 values is exact in
+// fp32; v_cvt_pk_bf16_f32 rounds to nearest even), then g[t] += x_t . w with
+// one v_dot2_f32_bf16 per weight pair.
+template <int TB>
+__device__ __forceinline__ void ref_dot32_deq(const u32x4_t (&cw)[2], uint32_t cbase, float a,
+                                              const uint32_t (&x)[TB][16], int nt, float (&g)[TB]) {
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+        const uint32_t w = cw[d >> 2][d & 3];
+        const uint32_t we = (w << 2) & 0x03fc03fcu;   // 4 * code of columns 4d, 4d+2 (16-bit fields)
+        const uint32_t wo = (w >> 6) & 0x03fc03fcu;   // 4 * code of columns 4d+1, 4d+3
+        const float c0 = __uint_as_float(lds_ld32(add_word<0>(cbase, we)));
+        const float c1 = __uint_as_float(lds_ld32(add_word<0>(cbase, wo)));
+        const float c2 = __uint_as_float(lds_ld32(add_word<1>(cbase, we)));
+        const float c3 = __uint_as_float(lds_ld32(add_word<1>(cbase, wo)));
+        const f32x2_t q0 = {c0 * a, c1 * a}, q1 = {c2 * a, c3 * a};
+        const uint32_t p0 = __builtin_bit_cast(uint32_t, __builtin_convertvector(q0, bf16x2v_t));
+        const uint32_t p1 = __builtin_bit_cast(uint32_t, __builtin_convertvector(q1, bf16x2v_t));
+#pragma unroll
+        for (int t = 0; t < TB; ++t) {
+            if (t < nt) {
+                g[t] = dot2_bf16(p0, x[t][2 * d], g[t]);
+                g[t] = dot2_bf16(p1, x[t][2 * d + 1], g[t]);
+            }
+        }
+    }
+}
+
+// REF rows of one expert.  One token per pass (TB == 1, i.e. T == 1) follows
+// the reference's decode GEMV (vllm_lut/quant_method.py:250-260 ->
+// cuda_lut_gemv.py:50-57): fp32 (x * cb) * absmax, factored per 32 columns.
+// Several tokens (TB > 1, T >= 2) follow its other branch (quant_method.py:
+// 261-277): the dequantised bf16 weights bf16(cb * absmax), then the matmul.
 template <int TB>
 __device__ __forceinline__ void ref_rows8(const lutmoe_weights& w, int e, const int (&rows)[kRows], int K, int lane,
                                           uint8_t* slot, const uint16_t* const (&xrow)[TB], int nt,
                                           float (&acc)[kRows][TB]) {
+    constexpr bool kDeq = TB > 1;
     const uint8_t* codes = (const uint8_t*)w.codes + (int64_t)e * w.rows * w.cols;
     const uint16_t* am = (const uint16_t*)w.tables + (int64_t)e * w.absmax_per_expert;
     const int64_t nb = w.absmax_per_expert;
     const int bs = w.block_size;
-    // codebook -> the slot (8 bytes per lane), issued with the first chunk's loads
+    // codebook -> the slot (4 entries per lane: bf16, or fp32 for the
+    // dequantising branch), issued with the first chunk's loads
     const uint2 cbv = reinterpret_cast<const uint2*>(ref_codebook(w, e))[lane];
     const uint32_t cbase = lds_addr(slot);
     const int nch = (K + kWChunk - 1) / kWChunk;
@@ -758,19 +816,28 @@ __device__ __forceinline__ void ref_rows8(const lutmoe_weights& w, int e, const 
         load_rows8r(codes, am, nb, bs, rows, K, cc, lane, b);
         __builtin_amdgcn_sched_barrier(0);
         if (cc == 0) {
-            *reinterpret_cast<uint2*>(slot + 8 * lane) = cbv;
+            if constexpr (kDeq) {
+                const u32x4_t f = {cbv.x << 16, cbv.x & 0xffff0000u, cbv.y << 16, cbv.y & 0xffff0000u};
+                *reinterpret_cast<u32x4_t*>(slot + 16 * lane) = f;
+            } else {
+                *reinterpret_cast<uint2*>(slot + 8 * lane) = cbv;
+            }
             wave_lds_sync();
         }
         const bool ok = cc * kWChunk + 32 * lane < K;
 #pragma unroll
         for (int r = 0; r < kRows; ++r) {
-            float g[TB];
-#pragma unroll
-            for (int t = 0; t < TB; ++t) g[t] = 0.f;
-            ref_dot32<TB>(b.cw[r], cbase, xs, nt, g);
             const float a = ok ? bf16_to_f32(b.am[r]) : 0.f;   // lanes past K contribute nothing
+            if constexpr (kDeq) {
+                ref_dot32_deq<TB>(b.cw[r], cbase, a, xs, nt, acc[r]);
+            } else {
+                float g[TB];
 #pragma unroll
-            for (int t = 0; t < TB; ++t) acc[r][t] = fmaf(a, g[t], acc[r][t]);
+                for (int t = 0; t < TB; ++t) g[t] = 0.f;
+                ref_dot32<TB>(b.cw[r], cbase, xs, nt, g);
+#pragma unroll
+                for (int t = 0; t < TB; ++t) acc[r][t] = fmaf(a, g[t], acc[r][t]);
+            }
         }
     }
     wave_lds_sync();

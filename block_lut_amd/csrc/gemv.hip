@@ -13,17 +13,15 @@
 // lookup is one ds_read_u16 per weight at  slot + 32*g + 2*code; the two
 // looked-up bf16 values of an element pair feed one v_dot2_f32_bf16 with the
 // activation pair.  Partial sums are reduced across the wave at the end.
+// These serve the single-matrix entry points (lutmoe_gemv, lut_gemv and
+// launch_lut_gemv_kernel); the MoE layer's decode kernels are in decode.hip.
 //
 // Reference behaviour restated: lut_gemv_kernel
-// (vllm_lut/cuda_lut_gemv.py:23-80) and the decode branch of
-// LUTFusedMoEMethod.apply (vllm_lut/quant_method.py:250-260): per routed
-// expert gate_up = GEMV(W13, x); act = silu(gate) * up; y = GEMV(W2, act);
-// out += w_k * y.
+// (vllm_lut/cuda_lut_gemv.py:23-80).
 #include "common.h"
 #include "kernels.h"
 
 using namespace lutmoe;
-using lutmoe_host::MoeRouting;
 
 namespace {
 
@@ -217,147 +215,6 @@ __global__ __launch_bounds__(256) void gemv_kernel(lutmoe_weights w, int expert,
     }
 }
 
-// ------------------------------------------------ MoE decode stage 1: gate/up
-
-// CTA (blockIdx.x = group of 4 intermediate indices, blockIdx.y = active
-// expert slot): rows i0..i0+3 (gate) and I+i0..I+i0+3 (up); the 4 waves split
-// the K chunks; partials meet in LDS; SwiGLU in the epilogue.
-template <class Dec, int TB>
-__global__ __launch_bounds__(256) void decode_gate_up_kernel(lutmoe_moe_desc d,
-                                                             const uint16_t* __restrict__ x,
-                                                             MoeRouting rt,
-                                                             uint16_t* __restrict__ act) {
-    __shared__ __attribute__((aligned(16))) uint8_t s_slot[4 * kSlot];
-    __shared__ float s_red[4][kRows][TB];
-    __shared__ float s_cb[256];
-    const int a = blockIdx.y;
-    if (a >= rt.active[0]) return;
-    const int e = rt.active[1 + a];
-    init_cb<Dec>(d.w13, e, s_cb);
-    __syncthreads();
-    const int p0 = rt.offsets[e], n = rt.offsets[e + 1] - p0;
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int I = d.inter, H = d.hidden;
-    const int i0 = blockIdx.x * 4;
-    int rows[kRows];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int i = min(i0 + j, I - 1);
-        rows[j] = i;
-        rows[4 + j] = I + i;
-    }
-    Dec dec;
-    bind_cb(dec, s_cb);
-    dec.set_expert(d.w13, e);
-    const int nblk_k = H / kBlockBL;
-    const int nch = (H + kChunk - 1) / kChunk;
-    uint8_t* slot = s_slot + wv * kSlot;
-    for (int tb = 0; tb < n; tb += TB) {
-        const int nt = min(TB, n - tb);
-        const uint16_t* xrow[TB];
-#pragma unroll
-        for (int t = 0; t < TB; ++t) {
-            const int pair = rt.perm[p0 + tb + min(t, nt - 1)];
-            xrow[t] = x + (int64_t)(pair / rt.k_eff) * H;
-        }
-        float acc[kRows][TB];
-#pragma unroll
-        for (int r = 0; r < kRows; ++r)
-#pragma unroll
-            for (int t = 0; t < TB; ++t) acc[r][t] = 0.f;
-        for (int c = wv; c < nch; c += 4) octet_chunk<Dec, TB>(dec, rows, c, nblk_k, lane, slot, xrow, nt, acc);
-#pragma unroll
-        for (int r = 0; r < kRows; ++r)
-#pragma unroll
-            for (int t = 0; t < TB; ++t) {
-                const float v = wave_sum(acc[r][t]);
-                if (lane == 0) s_red[wv][r][t] = v;
-            }
-        __syncthreads();
-        const int tid = threadIdx.x;
-        if (tid < 4 * nt) {
-            const int j = tid & 3, t = tid >> 2;
-            const float g = s_red[0][j][t] + s_red[1][j][t] + s_red[2][j][t] + s_red[3][j][t];
-            const float u = s_red[0][4 + j][t] + s_red[1][4 + j][t] + s_red[2][4 + j][t] + s_red[3][4 + j][t];
-            if (i0 + j < I)
-                act[(int64_t)(p0 + tb + t) * I + i0 + j] = (uint16_t)f32_to_bf16(silu_mul(g, u));
-        }
-        __syncthreads();
-    }
-}
-
-// ------------------------------------------- MoE decode stage 2: down+combine
-
-// CTA owns output rows h0..h0+7 for every token; wave w handles active
-// experts w, w+4, ...; per-position results (already times the routing
-// weight) meet in LDS and are summed per token in slot order.
-template <class Dec, int TB>
-__global__ __launch_bounds__(256) void decode_down_combine_kernel(lutmoe_moe_desc d,
-                                                                  const uint16_t* __restrict__ act,
-                                                                  MoeRouting rt, void* __restrict__ out,
-                                                                  int out_dtype) {
-    __shared__ __attribute__((aligned(16))) uint8_t s_slot[4 * kSlot];
-    __shared__ float s_cb[256];
-    extern __shared__ float s_y[];   // [P][8]
-    init_cb<Dec>(d.w2, 0, s_cb);   // one codebook for all experts (the host checks)
-    __syncthreads();
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int I = d.inter, H = d.hidden;
-    const int h0 = blockIdx.x * kRows;
-    int rows[kRows];
-#pragma unroll
-    for (int r = 0; r < kRows; ++r) rows[r] = min(h0 + r, H - 1);
-    const int nact = rt.active[0];
-    const int nblk_k = I / kBlockBL;
-    const int nch = (I + kChunk - 1) / kChunk;
-    uint8_t* slot = s_slot + wv * kSlot;
-    Dec dec;
-    bind_cb(dec, s_cb);
-    for (int a = wv; a < nact; a += 4) {
-        const int e = rt.active[1 + a];
-        const int p0 = rt.offsets[e], n = rt.offsets[e + 1] - p0;
-        dec.set_expert(d.w2, e);
-        for (int tb = 0; tb < n; tb += TB) {
-            const int nt = min(TB, n - tb);
-            const uint16_t* xrow[TB];
-#pragma unroll
-            for (int t = 0; t < TB; ++t) xrow[t] = act + (int64_t)(p0 + tb + min(t, nt - 1)) * I;
-            float acc[kRows][TB];
-#pragma unroll
-            for (int r = 0; r < kRows; ++r)
-#pragma unroll
-                for (int t = 0; t < TB; ++t) acc[r][t] = 0.f;
-            for (int c = 0; c < nch; ++c) octet_chunk<Dec, TB>(dec, rows, c, nblk_k, lane, slot, xrow, nt, acc);
-#pragma unroll
-            for (int t = 0; t < TB; ++t) {
-                const int p = p0 + tb + min(t, nt - 1);
-                const float pw = rt.pair_w[rt.perm[p]];
-#pragma unroll
-                for (int r = 0; r < kRows; ++r) {
-                    const float v = wave_sum(acc[r][t]);
-                    if (lane == 0 && t < nt) s_y[p * kRows + r] = v * pw;
-                }
-            }
-        }
-    }
-    __syncthreads();
-    const int T = rt.T, ke = rt.k_eff;
-    for (int idx = threadIdx.x; idx < T * kRows; idx += 256) {
-        const int t = idx / kRows, r = idx % kRows;
-        if (h0 + r >= H) continue;
-        float s = 0.f;
-        for (int q = 0; q < ke; ++q) {
-            const int pos = rt.inv[t * ke + q];
-            if (pos >= 0) s += s_y[pos * kRows + r];
-        }
-        const int64_t o = (int64_t)t * H + h0 + r;
-        if (out_dtype == LUTMOE_DTYPE_F32) ((float*)out)[o] = s;
-        else ((uint16_t*)out)[o] = (uint16_t)f32_to_bf16(s);
-    }
-}
-
-// ------------------------------------------------------------- REF lut_gemv
-
 // Reference-shaped single-vector GEMV on REF weights for any K / block size:
 // one wave per row, scalar lanes, exact reference product order
 // (x * cb) * absmax per element.  Used when the vector path's alignment
@@ -495,43 +352,5 @@ int launch_bl4_gemv(const lutmoe_weights* w, int expert, const uint16_t* x, int 
     return gemv_dispatch<Bl4Dec>(w, expert, x, T, y, y_dtype, s);
 }
 
-
-template <class Dec>
-static int gate_up_dispatch(const lutmoe_moe_desc* d, const uint16_t* x, const MoeRouting& r,
-                            uint16_t* act, int max_active, int T, hipStream_t s) {
-    const dim3 grid((d->inter + 3) / 4, max_active);
-    switch (tb_for(T)) {
-        case 1: hipLaunchKernelGGL((decode_gate_up_kernel<Dec, 1>), grid, dim3(256), 0, s, *d, x, r, act); break;
-        case 2: hipLaunchKernelGGL((decode_gate_up_kernel<Dec, 2>), grid, dim3(256), 0, s, *d, x, r, act); break;
-        default: hipLaunchKernelGGL((decode_gate_up_kernel<Dec, 4>), grid, dim3(256), 0, s, *d, x, r, act); break;
-    }
-    return check_launch();
-}
-
-int launch_decode_gate_up(const lutmoe_moe_desc* d, const uint16_t* x, const MoeRouting& r,
-                          uint16_t* act, int max_active, hipStream_t s) {
-    if (d->w13.format == LUTMOE_FMT_REF) return gate_up_dispatch<RefDec>(d, x, r, act, max_active, r.T, s);
-    return gate_up_dispatch<Bl4Dec>(d, x, r, act, max_active, r.T, s);
-}
-
-template <class Dec>
-static int down_dispatch(const lutmoe_moe_desc* d, const uint16_t* act, const MoeRouting& r,
-                         void* out, int out_dtype, hipStream_t s) {
-    const dim3 grid((d->hidden + kRows - 1) / kRows);
-    const size_t lds = (size_t)r.T * r.k_eff * kRows * sizeof(float);
-    switch (tb_for(r.T)) {
-        case 1: hipLaunchKernelGGL((decode_down_combine_kernel<Dec, 1>), grid, dim3(256), lds, s, *d, act, r, out, out_dtype); break;
-        case 2: hipLaunchKernelGGL((decode_down_combine_kernel<Dec, 2>), grid, dim3(256), lds, s, *d, act, r, out, out_dtype); break;
-        default: hipLaunchKernelGGL((decode_down_combine_kernel<Dec, 4>), grid, dim3(256), lds, s, *d, act, r, out, out_dtype); break;
-    }
-    return check_launch();
-}
-
-int launch_decode_down_combine(const lutmoe_moe_desc* d, const uint16_t* act,
-                               const MoeRouting& r, void* out, int out_dtype, int,
-                               hipStream_t s) {
-    if (d->w2.format == LUTMOE_FMT_REF) return down_dispatch<RefDec>(d, act, r, out, out_dtype, s);
-    return down_dispatch<Bl4Dec>(d, act, r, out, out_dtype, s);
-}
 
 }  // namespace lutmoe_host

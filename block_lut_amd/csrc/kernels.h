@@ -32,8 +32,8 @@ int launch_bl4_gemv(const lutmoe_weights* w, int expert, const uint16_t* x, int 
 int launch_nested_gemv(const lutmoe_weights* w, int expert, const uint16_t* x, int T,
                        void* y, int y_dtype, hipStream_t s);
 
-// Decode MoE stages (grouped LUT-GEMV).  Pairs are (token, slot) with
-// k_eff = k + num_shared slots per token; positions are permuted pairs.
+// Routing of the grouped MFMA path.  Pairs are (token, slot) with k_eff =
+// k + num_shared slots per token; positions are permuted pairs.
 struct MoeRouting {
     const int32_t* offsets;   // [E_tot+1]
     const int32_t* perm;      // [P] pair index at each position
@@ -44,11 +44,6 @@ struct MoeRouting {
     int k_eff;
     int num_experts_total;    // E + S
 };
-int launch_decode_gate_up(const lutmoe_moe_desc* d, const uint16_t* x, const MoeRouting& r,
-                          uint16_t* act, int max_active, hipStream_t s);
-int launch_decode_down_combine(const lutmoe_moe_desc* d, const uint16_t* act,
-                               const MoeRouting& r, void* out, int out_dtype,
-                               int max_active, hipStream_t s);
 
 // decode.hip (BL4 decode layer, routing recomputed inside each CTA)
 bool decode_v2_supported(const lutmoe_moe_desc* d, int T, int k);
@@ -74,6 +69,9 @@ int launch_permute(const int32_t* pair_ids, int T, int k_eff, int E_tot, int32_t
 int launch_route_pairs(const int32_t* topk_ids, const float* topk_w, int T, int k, int E, int S,
                        int32_t* offsets, int32_t* perm, int32_t* inv, int32_t* active, int32_t* pair_ids,
                        float* pair_w, hipStream_t s);
+// shared slots k..k+S-1 of every token t: pair_w = sigmoid(x_t . gate)
+int launch_shared_gate(const uint16_t* x, const uint16_t* gate, int T, int H, int k, int S, float* pair_w,
+                       hipStream_t s);
 // nsplit > 1: y_pos holds nsplit partial results (K splits of the down
 // projection), split_stride floats apart, summed per position first.
 int launch_combine(const float* y_pos, const int32_t* inv, int T, int k_eff, int H,

@@ -254,6 +254,25 @@ __device__ __forceinline__ float wave_reduce(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
+// sigmoid(x . g) over H bf16 values with fp32 accumulation (Qwen's shared-
+// expert gate, customized/qwen.py:99-100).  Whole wave; the result is
+// uniform.  H % 8 == 0 and both pointers 16-byte aligned.
+__device__ __forceinline__ float shared_gate_weight(const uint16_t* __restrict__ x, const uint16_t* __restrict__ g,
+                                                    int H) {
+    const int lane = threadIdx.x & 63;
+    float s = 0.f;
+    for (int c = lane * 8; c < H; c += 512) {
+        const uint4 xv = *reinterpret_cast<const uint4*>(x + c);
+        const uint4 gv = *reinterpret_cast<const uint4*>(g + c);
+        s = dot2_bf16(xv.x, gv.x, s);
+        s = dot2_bf16(xv.y, gv.y, s);
+        s = dot2_bf16(xv.z, gv.z, s);
+        s = dot2_bf16(xv.w, gv.w, s);
+    }
+    const float z = wave_reduce(s);
+    return 1.0f / (1.0f + __expf(-z));
+}
+
 template <int CTRL, int RMASK>
 __device__ __forceinline__ float dpp_or_neg_inf(float x) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(

@@ -125,6 +125,17 @@ __global__ __launch_bounds__(256) void build_pairs_kernel(const int32_t* __restr
     }
 }
 
+// Qwen's gated shared expert (customized/qwen.py:99-100): the shared slots
+// k..k+S-1 of token t weigh sigmoid(x_t . g).  One wave per token.
+__global__ __launch_bounds__(256) void shared_gate_kernel(const uint16_t* __restrict__ x,
+                                                          const uint16_t* __restrict__ g, int T, int H,
+                                                          int k, int S, float* __restrict__ pair_w) {
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (t >= T) return;   // wave-uniform
+    const float sw = shared_gate_weight(x + (int64_t)t * H, g, H);
+    if (lane < S) pair_w[(int64_t)t * (k + S) + k + lane] = sw;
+}
+
 // One CTA per expert id e.  Every CTA builds the full histogram in LDS
 // (redundantly; P is small), derives offsets[e] and e's rank among active
 // experts, then stably compacts the pairs routed to e.
@@ -368,6 +379,12 @@ int launch_build_pairs(const int32_t* topk_ids, const float* topk_w, int T, int 
     const int n = T * (k + S);
     hipLaunchKernelGGL(build_pairs_kernel, dim3((n + 255) / 256), dim3(256), 0, s, topk_ids,
                        topk_w, T, k, E, S, pair_ids, pair_w);
+    return check_launch();
+}
+
+int launch_shared_gate(const uint16_t* x, const uint16_t* gate, int T, int H, int k, int S, float* pair_w,
+                       hipStream_t s) {
+    hipLaunchKernelGGL(shared_gate_kernel, dim3((T + 3) / 4), dim3(256), 0, s, x, gate, T, H, k, S, pair_w);
     return check_launch();
 }
 

@@ -199,7 +199,13 @@ class NestedStack(WeightStack):
 
 @dataclass
 class MoEWeights:
-    """Routed experts 0..E-1 followed by num_shared always-on experts."""
+    """Routed experts 0..E-1 followed by num_shared always-on expert slots.
+
+    A shared expert with intermediate size m*I takes m slots (``split_shared_bl4`` /
+    ``split_shared_ref`` cut its matrices).  Shared slots weigh 1 (DeepSeek's shared
+    experts, customized/deepseek.py:111-115) or, with ``shared_gate`` (bf16 [H], the
+    weight of Qwen's shared_expert_gate Linear(H, 1)), sigmoid(x . shared_gate) per token
+    (customized/qwen.py:42-43, 99-100)."""
 
     w13: WeightStack
     w2: WeightStack
@@ -207,6 +213,7 @@ class MoEWeights:
     inter: int
     num_routed: int
     num_shared: int = 0
+    shared_gate: Optional[torch.Tensor] = None
     _desc: Optional[N.lutmoe_moe_desc] = field(default=None, repr=False)
 
     def __post_init__(self):
@@ -217,6 +224,13 @@ class MoEWeights:
         tot = self.num_routed + self.num_shared
         if self.w13.num_experts < tot or self.w2.num_experts < tot:
             raise ValueError("weight stacks hold fewer experts than routed + shared")
+        if self.shared_gate is not None:
+            g = _dev(self.shared_gate, torch.bfloat16, "shared_gate")
+            if g.numel() != self.hidden:
+                raise ValueError(f"shared_gate must hold {self.hidden} values (hidden size)")
+            if self.num_shared == 0:
+                raise ValueError("shared_gate given but the layer has no shared expert slots")
+            self.shared_gate = g.reshape(-1)
 
     def desc(self) -> N.lutmoe_moe_desc:
         if self._desc is None:
@@ -225,8 +239,68 @@ class MoEWeights:
             d.w2 = self.w2.desc()
             d.hidden, d.inter = self.hidden, self.inter
             d.num_routed, d.num_shared = self.num_routed, self.num_shared
+            d.shared_gate = None if self.shared_gate is None else self.shared_gate.data_ptr()
             self._desc = d
         return self._desc
+
+
+def _slot_count(shared_inter: int, inter: int) -> int:
+    if shared_inter % inter:
+        raise ValueError(f"shared intermediate size {shared_inter} is not a multiple of {inter}")
+    return shared_inter // inter
+
+
+def split_shared_bl4(codes13: torch.Tensor, tables13: torch.Tensor, codes2: torch.Tensor,
+                     tables2: torch.Tensor, inter: int):
+    """One BL4 shared expert with intermediate size m*I -> m slots of intermediate size I.
+
+    codes13 [2*m*I, H/2] and tables13 [2*m*I, H/64, 16] hold gate rows [0, m*I) and up
+    rows [m*I, 2*m*I); codes2 [H, m*I/2], tables2 [H, m*I/64, 16].  Slot j takes gate and
+    up rows [j*I, (j+1)*I) and down columns [j*I, (j+1)*I) (whole 64-weight blocks, so
+    I % 64 == 0).  SwiGLU acts per intermediate index, so the slots' outputs sum to the
+    expert's.  Returns (codes13 [m, 2I, H/2], tables13 [m, 2I, H/64, 16],
+    codes2 [m, H, I/2], tables2 [m, H, I/64, 16]); tables keep their dtype."""
+    if inter % 64:
+        raise ValueError("splitting a BL4 shared expert needs I % 64 == 0")
+    m = _slot_count(codes13.shape[0] // 2, inter)
+    Is = m * inter
+    c13, t13, c2, t2 = [], [], [], []
+    for j in range(m):
+        g, u = slice(j * inter, (j + 1) * inter), slice(Is + j * inter, Is + (j + 1) * inter)
+        c13.append(torch.cat([codes13[g], codes13[u]]))
+        t13.append(torch.cat([tables13[g], tables13[u]]))
+        c2.append(codes2[:, j * inter // 2:(j + 1) * inter // 2])
+        t2.append(tables2[:, j * inter // 64:(j + 1) * inter // 64])
+    return (torch.stack(c13).contiguous(), torch.stack(t13).contiguous(), torch.stack(c2).contiguous(),
+            torch.stack(t2).contiguous())
+
+
+def split_shared_ref(codes13: torch.Tensor, absmax13: torch.Tensor, codes2: torch.Tensor,
+                     absmax2: torch.Tensor, inter: int, block_size: int = 128):
+    """One REF shared expert with intermediate size m*I -> m slots of intermediate size I.
+
+    codes13 [2*m*I, H], absmax13 [2*m*I*H / block_size]; codes2 [H, m*I], absmax2
+    [H*m*I / block_size] (absmax blocks of the row-major flattened matrices).  Each slot
+    gets the absmax entries of its own elements, so every absmax block must lie inside
+    one slot row: H, I and m*I multiples of block_size.  Returns (codes13 [m, 2I, H],
+    absmax13 [m, 2I*H/bs], codes2 [m, H, I], absmax2 [m, H*I/bs])."""
+    H = codes13.shape[1]
+    m = _slot_count(codes13.shape[0] // 2, inter)
+    Is = m * inter
+    if H % block_size or inter % block_size:
+        raise ValueError("splitting a REF shared expert needs H and I multiples of block_size")
+    a13 = absmax13.reshape(2 * Is, H // block_size)
+    a2 = absmax2.reshape(H, Is // block_size)
+    nb = inter // block_size
+    c13, b13, c2, b2 = [], [], [], []
+    for j in range(m):
+        g, u = slice(j * inter, (j + 1) * inter), slice(Is + j * inter, Is + (j + 1) * inter)
+        c13.append(torch.cat([codes13[g], codes13[u]]))
+        b13.append(torch.cat([a13[g], a13[u]]).reshape(-1))
+        c2.append(codes2[:, j * inter:(j + 1) * inter])
+        b2.append(a2[:, j * nb:(j + 1) * nb].reshape(-1))
+    return (torch.stack(c13).contiguous(), torch.stack(b13).contiguous(), torch.stack(c2).contiguous(),
+            torch.stack(b2).contiguous())
 
 
 def _stream() -> int:

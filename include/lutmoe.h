@@ -74,8 +74,14 @@ typedef struct lutmoe_weights {
 } lutmoe_weights;
 
 /* Fused-MoE layer description: routed experts 0..E-1, plus num_shared
- * always-on experts stored after them (expert ids E..E+S-1 of the same
- * stacks), each applied with weight 1.0 (customized/deepseek.py:111-115). */
+ * always-on expert slots stored after them (expert ids E..E+S-1 of the same
+ * stacks).  A shared expert whose intermediate size is m*I occupies m slots
+ * (gate/up rows and down columns split at multiples of I: SwiGLU acts per
+ * intermediate index, so the slots' outputs sum to the expert's).  Every
+ * shared slot of token t is applied with weight 1.0 (DeepSeek,
+ * customized/deepseek.py:111-115), or, when shared_gate is set, with
+ * sigmoid(x[t] . shared_gate) computed in fp32 (Qwen's shared_expert_gate,
+ * customized/qwen.py:42-43, 99-100). */
 typedef struct lutmoe_moe_desc {
     lutmoe_weights w13;        /* [E+S][2I][H]: gate rows [0,I), up rows [I,2I) */
     lutmoe_weights w2;         /* [E+S][H][I]                                   */
@@ -83,6 +89,7 @@ typedef struct lutmoe_moe_desc {
     int32_t inter;             /* I                                             */
     int32_t num_routed;        /* E                                             */
     int32_t num_shared;        /* S                                             */
+    const void* shared_gate;   /* bf16 [H] (device) or NULL                     */
 } lutmoe_moe_desc;
 
 /* ---- library ---------------------------------------------------------- */

@@ -388,6 +388,33 @@ def bl4_dequant(packed, tables_f16) -> np.ndarray:
     return tb[np.arange(M)[:, None], blk, codes]
 
 
+_F16_BF16_F32 = None
+
+
+def bl4_dequant_f32(packed, tables_f16, row_chunk: int = 1024) -> np.ndarray:
+    """float32 [M, K] values of the dequantised BL4 matrix (bl4_dequant's bf16
+    values widened), gathered per 64-weight block with take_along_axis, a few
+    rows at a time so that large matrices (Mixtral's 28672 x 4096) stay within
+    a bounded amount of host memory."""
+    global _F16_BF16_F32
+    if _F16_BF16_F32 is None:   # every fp16 pattern -> its bf16 value (bl4_tables_bf16) as f32
+        _F16_BF16_F32 = bf16_to_f32(bl4_tables_bf16(np.arange(65536, dtype=np.uint16)))
+    p = np.asarray(packed, np.uint8)
+    M, Kh = p.shape
+    K = 2 * Kh
+    nb = K // BL_BLOCK
+    tb = np.asarray(tables_f16, np.uint16).reshape(M, nb, 16)
+    out = np.empty((M, K), np.float32)
+    for r0 in range(0, M, row_chunk):
+        r1 = min(M, r0 + row_chunk)
+        t = _F16_BF16_F32[tb[r0:r1]]                                       # [m, nb, 16]
+        c = p[r0:r1].reshape(r1 - r0, nb, 32)
+        o = out[r0:r1].reshape(r1 - r0, nb, 64)
+        o[..., 0::2] = np.take_along_axis(t, (c & 0x0F).astype(np.intp), axis=2)
+        o[..., 1::2] = np.take_along_axis(t, (c >> 4).astype(np.intp), axis=2)
+    return out
+
+
 # --------------------------------------------------------------------------
 # NestedLUT 2/3/4-bit tiers
 # --------------------------------------------------------------------------
@@ -441,6 +468,38 @@ def nested_unpack_planes(planes: dict, bits: int) -> np.ndarray:
     return c
 
 
+def nested_planes_split(buf, bits: int, M: int, K: int) -> dict:
+    """One expert's device buffer of bit-plane sections [p01 M*K/4 | p2 M*K/8 |
+    p3 M*K/8] (a tier-b expert holds the first 2, 3 or all of them) -> the
+    section dict of nested_pack_planes (rows of the row-major matrix)."""
+    b = np.asarray(buf, np.uint8).reshape(-1)
+    n = M * K
+    pl = {"p01": b[: n // 4].reshape(M, K // 4)}
+    if bits >= 3:
+        pl["p2"] = b[n // 4: n // 4 + n // 8].reshape(M, K // 8)
+    if bits >= 4:
+        pl["p3"] = b[n // 4 + n // 8: n // 2].reshape(M, K // 8)
+    return pl
+
+
+def nested_dequant_f32(codes, tables_f16, bits: int, row_chunk: int = 1024) -> np.ndarray:
+    """float32 [M, K] values of nested_dequant (its bf16 values widened), gathered per
+    64-weight block with take_along_axis, a few rows at a time."""
+    global _F16_BF16_F32
+    if _F16_BF16_F32 is None:
+        _F16_BF16_F32 = bf16_to_f32(bl4_tables_bf16(np.arange(65536, dtype=np.uint16)))
+    c = np.asarray(codes, np.uint8)
+    M, K = c.shape
+    nb, ne = K // BL_BLOCK, 1 << bits
+    tb = np.asarray(tables_f16, np.uint16).reshape(M, nb, ne)
+    out = np.empty((M, K), np.float32)
+    for r0 in range(0, M, row_chunk):
+        r1 = min(M, r0 + row_chunk)
+        idx = (c[r0:r1] & (ne - 1)).reshape(r1 - r0, nb, 64).astype(np.intp)
+        out[r0:r1] = np.take_along_axis(_F16_BF16_F32[tb[r0:r1]], idx, axis=2).reshape(r1 - r0, K)
+    return out
+
+
 def nested_dequant(codes, tables_f16, bits: int) -> np.ndarray:
     """bf16 bits [M, K]: T_b[code & (2^b - 1)] with T_b the tier-b table [M, K/64, 2^b]."""
     c = np.asarray(codes, np.int64) & ((1 << bits) - 1)
@@ -492,20 +551,25 @@ def silu_mul_f32(g, u) -> np.ndarray:
     return (g / (np.float32(1) + np.exp(-g)) * np.asarray(u, np.float32)).astype(np.float32)
 
 
-def moe_layer(x_bf16, ids, weights, w13_f32, w2_f32, shared=None, act_round_bf16: bool = True):
+def moe_layer(x_bf16, ids, weights, w13_f32, w2_f32, shared=None, act_round_bf16: bool = True,
+              shared_w=None):
     """fp32 restatement of the fused-MoE apply (vllm_lut/quant_method.py:230-279,
     vllm_lut/fast_moe.py:30-80) with float64 accumulation:
       gu = x @ W13[e]^T ; a = silu(gu[:, :I]) * gu[:, I:] (fp32) ; a -> bf16 (the input
       dtype of the down projection, as the reference's lut_gemv/F.linear take bf16);
       y = a @ W2[e]^T ; out[t] = sum_k w[t,k] * y_{e_k}[t]  (+ shared experts, weight 1).
     w13_f32 / w2_f32: callables e -> float32 dequantised matrices [2I, H] / [H, I].
-    shared: list of callables pairs (w13, w2) for always-on experts (customized/deepseek.py:111-115).
-    Returns float64 [T, H]."""
+    shared: list of matrix pairs (w13, w2) for always-on experts (customized/deepseek.py:111-115).
+    shared_w: None (every shared expert with weight 1) or float [T] per-token weights of the
+    shared experts (Qwen's sigmoid(x . g), customized/qwen.py:99-100).
+    w2_f32 may return a subset of W2's rows (output columns): the result then has that
+    many columns.
+    Returns float64 [T, H] (or [T, rows of the W2 given])."""
     x = bf16_to_f32(x_bf16).astype(np.float64)
     ids = np.asarray(ids, np.int64)
     wts = np.asarray(weights, np.float32)
-    T, H = x.shape
-    out = np.zeros((T, H), np.float64)
+    T = x.shape[0]
+    out = None
 
     def expert(rows, W13, W2):
         gu = x[rows] @ W13.astype(np.float64).T
@@ -515,10 +579,20 @@ def moe_layer(x_bf16, ids, weights, w13_f32, w2_f32, shared=None, act_round_bf16
             a = bf16_to_f32(f32_to_bf16(a))
         return a.astype(np.float64) @ W2.astype(np.float64).T
 
+    def acc(rows, y):   # rows are distinct: top-k picks distinct experts per token
+        nonlocal out
+        if out is None:
+            out = np.zeros((T, y.shape[1]), np.float64)
+        out[rows] += y
+
     for e in np.unique(ids):
         tok, slot = np.nonzero(ids == e)
         y = expert(tok, w13_f32(int(e)), w2_f32(int(e)))
-        out[tok] += wts[tok, slot][:, None].astype(np.float64) * y
+        acc(tok, wts[tok, slot][:, None].astype(np.float64) * y)
+    sw = None if shared_w is None else np.asarray(shared_w, np.float64).reshape(T, 1)
     for (W13, W2) in (shared or []):
-        out += expert(np.arange(T), W13, W2)
+        y = expert(np.arange(T), W13, W2)
+        acc(np.arange(T), y if sw is None else sw * y)
+    if out is None:
+        out = np.zeros((T, x.shape[1]), np.float64)
     return out

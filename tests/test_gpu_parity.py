@@ -348,6 +348,16 @@ def test_permute_drops_out_of_range(gpu):
 
 # --------------------------------------------------------------- MoE layer
 
+def _ref_semantics(w13, w2, T, path):
+    """Weights of the reference's REF layer as the oracle sees them: one token takes
+    lut_gemv's unrounded (x * cb) * absmax products (vllm_lut/quant_method.py:250-260),
+    several tokens the dequantised bf16(cb * absmax) weights and a matmul (:261-277).  The
+    grouped MFMA path (path 2) always computes with the dequantised weights."""
+    if T == 1 and path != 2:
+        return w13.gemv_f32, w2.gemv_f32
+    return w13.deq_f32, w2.deq_f32
+
+
 def _moe_case(fmt, E, S, H, I, seed):
     cls = BL4Expertset if fmt == "bl4" else RefExpertset
     w13 = cls(E + S, 2 * I, H, seed=seed)
@@ -375,7 +385,7 @@ def test_moe_layer(gpu, fmt, T, path):
     # REF decode follows the reference's lut_gemv (unrounded cb*absmax products),
     # REF prefill its dequant-then-GEMM branch (bf16 weights); BL4 weights are the
     # bf16 table entries on both paths.
-    f13, f2 = (w13.gemv_f32, w2.gemv_f32) if (fmt == "ref" and path == 1) else (w13.deq_f32, w2.deq_f32)
+    f13, f2 = _ref_semantics(w13, w2, T, path) if fmt == "ref" else (w13.deq_f32, w2.deq_f32)
     ref = O.moe_layer(xb, rids, rw, f13, f2, shared=[(f13(E + s), f2(E + s)) for s in range(S)])
     assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
 
@@ -396,7 +406,7 @@ def test_moe_layer_skewed_routing(gpu, fmt, T):
         f13, f2 = w13.deq_f32, w2.deq_f32
     else:
         w13, w2 = _moe_case(fmt, E, S, H, I, seed=90 + T)
-        f13, f2 = (w13.gemv_f32, w2.gemv_f32) if fmt == "ref" else (w13.deq_f32, w2.deq_f32)
+        f13, f2 = _ref_semantics(w13, w2, T, 1) if fmt == "ref" else (w13.deq_f32, w2.deq_f32)
     moe = MoEWeights(w13.stack(gpu), w2.stack(gpu), H, I, E, S)
     rng = np.random.default_rng(900 + T)
     xb = _x(rng, T, H)
@@ -429,7 +439,7 @@ def test_moe_layer_ref_block_sizes(gpu, block_size, T, path):
     rw, rids = O.route(rng.standard_normal((T, E)).astype(np.float32), k)
     out = ops.moe_forward(moe, to_dev_bf16(xb, gpu), torch.from_numpy(rw).to(gpu),
                           torch.from_numpy(rids).to(gpu), out_dtype=torch.float32, path=path)
-    f13, f2 = (w13.gemv_f32, w2.gemv_f32) if path == 1 else (w13.deq_f32, w2.deq_f32)
+    f13, f2 = _ref_semantics(w13, w2, T, path)
     ref = O.moe_layer(xb, rids, rw, f13, f2, shared=[(f13(E + s), f2(E + s)) for s in range(S)])
     assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
 
@@ -542,7 +552,7 @@ def test_moe_layer_ref_short_odd_absmax(gpu, T, path):
     rw, rids = O.route(rng.standard_normal((T, E)).astype(np.float32), k)
     out = ops.moe_forward(moe, to_dev_bf16(xb, gpu), torch.from_numpy(rw).to(gpu),
                           torch.from_numpy(rids).to(gpu), out_dtype=torch.float32, path=path)
-    f13, f2 = (w13.gemv_f32, w2.gemv_f32) if path == 1 else (w13.deq_f32, w2.deq_f32)
+    f13, f2 = _ref_semantics(w13, w2, T, path)
     ref = O.moe_layer(xb, rids, rw, f13, f2, shared=[(f13(E + s), f2(E + s)) for s in range(S)])
     assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
 
@@ -567,7 +577,7 @@ def test_fused_lut_moe_reference_signature(gpu, T):
     out = FM.fused_lut_moe(*args)
     assert out.dtype == torch.bfloat16 and tuple(out.shape) == (T, H)
     assert torch.equal(torch.ops.lutmoe.fused_lut_moe(*args), out)
-    f13, f2 = (w13.gemv_f32, w2.gemv_f32) if T <= 32 else (w13.deq_f32, w2.deq_f32)
+    f13, f2 = _ref_semantics(w13, w2, T, 0)
     ref = O.moe_layer(xb, rids, rw, f13, f2)
     # bf16 output: the tolerance adds half an ulp of bf16 relative to max|ref|
     assert rel_maxabs(O.bf16_to_f32(bf16_bits(out)), ref) <= TOL + 2.0 ** -8
@@ -592,7 +602,7 @@ def test_moe_layer_ref_per_expert_codebook(gpu, T, path):
     rw, rids = O.route(rng.standard_normal((T, E)).astype(np.float32), k)
     out = ops.moe_forward(moe, to_dev_bf16(xb, gpu), torch.from_numpy(rw).to(gpu),
                           torch.from_numpy(rids).to(gpu), out_dtype=torch.float32, path=path)
-    f13, f2 = (w13.gemv_f32, w2.gemv_f32) if path == 1 else (w13.deq_f32, w2.deq_f32)
+    f13, f2 = _ref_semantics(w13, w2, T, path)
     ref = O.moe_layer(xb, rids, rw, f13, f2, shared=[(f13(E + s), f2(E + s)) for s in range(S)])
     assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
     if T == 1:
@@ -659,9 +669,11 @@ def test_moe_layer_from_logits_ties(gpu, T, E, renorm):
                          "on its first GPU runs (E=8, S=1, k=2, H=512, I=320, T=1); it is switched off "
                          "(kFusedDecodeEnabled) until the cause is found on the CPU")
 def test_moe_layer_fused_decode(gpu):
-    """Layer through the persistent decode kernel: must match the per-stage
-    kernels bit for bit (same GEMV arithmetic, same combine order)."""
+    """Layer through the persistent decode kernel (one launch, all stages) against the
+    per-stage kernels (routing + gate/up, then down + combine, in a second workspace) bit
+    for bit, and against the oracle."""
     import torch
+    from block_lut_amd import _native as N
     from block_lut_amd import ops
     from block_lut_amd.formats import MoEWeights
     E, S, k, H, I, T = 8, 1, 2, 512, 320, 1
@@ -672,16 +684,47 @@ def test_moe_layer_fused_decode(gpu):
     lg = rng.standard_normal((T, E)).astype(np.float32)
     rw, rids = O.route(lg, k)
     args = (moe, to_dev_bf16(xb, gpu), torch.from_numpy(rw).to(gpu), torch.from_numpy(rids).to(gpu))
+    fused = ops.moe_forward(*args, out_dtype=torch.float32, path=1, workspace=ops.new_workspace(moe, T, k, gpu))
     ws = ops.new_workspace(moe, T, k, gpu)
-    fused = ops.moe_forward(*args, out_dtype=torch.float32, path=1, workspace=ws)
-    staged = ops.moe_forward(*args, out_dtype=torch.float32, path=1, workspace=ws,
-                             stages=7)
+    staged = torch.empty_like(fused)
+    ops.moe_forward(*args, out=staged, path=1, workspace=ws, stages=N.STAGE_ROUTE | N.STAGE_GATE_UP)
+    ops.moe_forward(*args, out=staged, path=1, workspace=ws, stages=N.STAGE_DOWN)
     assert torch.equal(fused, staged)
+    ref = O.moe_layer(xb, rids, rw, w13.deq_f32, w2.deq_f32,
+                      shared=[(w13.deq_f32(E + s), w2.deq_f32(E + s)) for s in range(S)])
+    assert rel_maxabs(fused.cpu().numpy(), ref) <= TOL
+
+
+@pytest.mark.parametrize("T", [1, 2, 5])
+def test_ref_decode_follows_reference_branch(gpu, T):
+    """REF decode picks the reference's branch by token count (vllm_lut/quant_method.py:
+    250-277): one token takes lut_gemv's unrounded (x * cb) * absmax products, several tokens
+    the dequantised bf16(cb * absmax) weights.  The layer must sit much closer to its own
+    branch's oracle than to the other branch's (the two differ by the bf16 rounding of
+    every weight, about 1e-3 of the output's range)."""
+    import torch
+    from block_lut_amd import ops
+    from block_lut_amd.formats import MoEWeights
+    E, S, k, H, I = 8, 0, 2, 512, 320
+    w13, w2 = _moe_case("ref", E, S, H, I, seed=123 + T)
+    moe = MoEWeights(w13.stack(gpu), w2.stack(gpu), H, I, E, S)
+    rng = np.random.default_rng(40 + T)
+    xb = _x(rng, T, H)
+    rw, rids = O.route(rng.standard_normal((T, E)).astype(np.float32), k)
+    out = ops.moe_forward(moe, to_dev_bf16(xb, gpu), torch.from_numpy(rw).to(gpu),
+                          torch.from_numpy(rids).to(gpu), out_dtype=torch.float32, path=1).cpu().numpy()
+    gemv = O.moe_layer(xb, rids, rw, w13.gemv_f32, w2.gemv_f32)
+    deq = O.moe_layer(xb, rids, rw, w13.deq_f32, w2.deq_f32)
+    own, other = (gemv, deq) if T == 1 else (deq, gemv)
+    e_own, e_other = rel_maxabs(out, own), rel_maxabs(out, other)
+    assert e_own <= TOL
+    assert e_own < 0.25 * e_other, (e_own, e_other)
 
 
 def test_moe_layer_qwen_decode_full_shape(gpu):
-    """Full Qwen1.5-MoE layer shape (H2048 I1408 E60 top-4), T=1 and T=8, BL4 weights from the
-    GPU encoder; oracle on the touched experts' GPU-dequantised weights (bit-exact separately)."""
+    """Full Qwen1.5-MoE layer shape (H2048 I1408 E60 top-4), T=1, 8 and 32, BL4 weights from the
+    GPU encoder; the oracle dequantises the touched experts on the host from the encoder's
+    codes and fp16 codebooks."""
     import torch
     from block_lut_amd import ops
     from block_lut_amd.formats import BL4Stack, MoEWeights
@@ -694,17 +737,26 @@ def test_moe_layer_qwen_decode_full_shape(gpu):
     c2, t2 = ops.bl4_encode(w2, n_iter=4)
     del w2
     moe = MoEWeights(BL4Stack.from_fp16(c13, t13), BL4Stack.from_fp16(c2, t2), H, I, E, 0)
-    for T in (1, 8):
+    d13, d2 = {}, {}
+
+    def host13(e):
+        if e not in d13:
+            d13[e] = O.bl4_dequant_f32(c13[e].cpu().numpy(), t13[e].cpu().numpy().view(np.uint16))
+        return d13[e]
+
+    def host2(e):
+        if e not in d2:
+            d2[e] = O.bl4_dequant_f32(c2[e].cpu().numpy(), t2[e].cpu().numpy().view(np.uint16))
+        return d2[e]
+
+    for T in (1, 8, 32):
         rng = np.random.default_rng(T)
         xb = _x(rng, T, H)
         lg = rng.standard_normal((T, E)).astype(np.float32)
         out = ops.moe_forward_logits(moe, to_dev_bf16(xb, gpu), torch.from_numpy(lg).to(gpu), k,
                                      out_dtype=torch.float32).cpu().numpy()
         rw, rids = O.route(lg, k)
-        used = sorted(set(rids.reshape(-1).tolist()))
-        d13 = {e: O.bf16_to_f32(bf16_bits(ops.dequant(moe.w13, e, 1)[0])) for e in used}
-        d2 = {e: O.bf16_to_f32(bf16_bits(ops.dequant(moe.w2, e, 1)[0])) for e in used}
-        ref = O.moe_layer(xb, rids, rw, d13.__getitem__, d2.__getitem__)
+        ref = O.moe_layer(xb, rids, rw, host13, host2)
         assert rel_maxabs(out, ref) <= TOL, T
 
 
@@ -921,7 +973,8 @@ def test_gguf_tier_upgrade(gpu, tmp_path):
         rw, rids = O.route(rng.standard_normal((T, E)).astype(np.float32), k)
         a, b = run(lay, xb, rids, rw, path), run(fresh, xb, rids, rw, path)
         assert torch.equal(a, b)
-        assert rel_maxabs(a.cpu().numpy(), oracle_out(now, xb, rids, rw, path == 1)) <= TOL
+        # one decode token: lut_gemv's products; several tokens: the dequantised weights
+        assert rel_maxabs(a.cpu().numpy(), oracle_out(now, xb, rids, rw, T == 1 and path == 1)) <= TOL
 
     lay2 = C.load_gguf_layer(g, 0, E, H, I, tier=2, device=gpu)
     assert lay2.w13.codebook_stride == 0
@@ -934,81 +987,56 @@ def test_gguf_tier_upgrade(gpu, tmp_path):
     xb = _x(rng, 3, H)
     rw, rids = O.route(rng.standard_normal((3, E)).astype(np.float32), k)
     assert rel_maxabs(run(lay2, xb, rids, rw, 1).cpu().numpy(),
-                      oracle_out([1, 1, 0, 1, 1, 1], xb, rids, rw, True)) <= TOL
+                      oracle_out([1, 1, 0, 1, 1, 1], xb, rids, rw, False)) <= TOL
 
 
 @pytest.mark.parametrize("fmt", ["bl4", "ref", "nested"])
 def test_prefill_deepseek_shape(gpu, fmt):
     """Grouped MFMA prefill at the DeepSeek-V2-Lite expert shape (H2048 I1408): 8 routed
     experts top-2 + 1 shared, T=512, so tiles of 256 rows (shared expert), about 128-row
-    routed tiles and the tail split all occur; every format's ring loader at full K.  Oracle
-    on the touched experts' GPU-dequantised weights (dequantisation is bit-exact separately)."""
+    routed tiles and the tail split all occur; every format's ring loader at full K.  The
+    oracle dequantises the experts on the host from their codes."""
     import torch
     from block_lut_amd import ops
-    from block_lut_amd.formats import (BL4Stack, MoEWeights, NestedExpert, NestedStack,
-                                       RefStack)
+    from block_lut_amd.formats import MoEWeights
+    from gpu_weights import DevBL4, DevNested, DevRef
     H, I, E, S, k, T = 2048, 1408, 8, 1, 2, 512
     g = torch.Generator(device=gpu).manual_seed(31)
 
     def stack(M, K):
         if fmt == "bl4":
-            codes = torch.randint(0, 256, (E + S, M, K // 2), dtype=torch.uint8, generator=g, device=gpu)
-            tabs = torch.sort(torch.randn((E + S, M, K // 64, 16), generator=g, device=gpu) * 0.02, dim=-1).values
-            return BL4Stack(codes, tabs.to(torch.bfloat16))
+            return DevBL4(E + S, M, K, g, gpu)
         if fmt == "ref":
-            codes = torch.randint(0, 256, (E + S, M, K), dtype=torch.uint8, generator=g, device=gpu)
-            am = (torch.rand((E + S, M * K // 128), generator=g, device=gpu) * 0.05 + 0.01).to(torch.bfloat16)
-            cb = torch.sort(torch.randn(256, generator=g, device=gpu)).values.to(torch.bfloat16)
-            return RefStack(codes, am, cb, 128)
-        ex = []
-        n = M * K
-        for e in range(E + S):
-            b = [2, 3, 4][e % 3]
-            size = n // 4 + (n // 8 if b >= 3 else 0) + (n // 8 if b >= 4 else 0)
-            planes = torch.randint(0, 256, (size,), dtype=torch.uint8, generator=g, device=gpu)
-            tab = torch.sort(torch.randn((M, K // 64, 1 << b), generator=g, device=gpu) * 0.02, dim=-1).values
-            ex.append(NestedExpert(b, planes, tab.to(torch.bfloat16)))
-        return NestedStack(ex, M, K)
+            return DevRef(E + S, M, K, g, gpu)
+        return DevNested([[2, 3, 4][e % 3] for e in range(E + S)], M, K, g, gpu)
 
-    moe = MoEWeights(stack(2 * I, H), stack(H, I), H, I, E, S)
+    w13, w2 = stack(2 * I, H), stack(H, I)
+    moe = MoEWeights(w13.stack, w2.stack, H, I, E, S)
     rng = np.random.default_rng(512)
     xb = _x(rng, T, H)
     lg = rng.standard_normal((T, E)).astype(np.float32)
     rw, rids = O.route(lg, k)
     out = ops.moe_forward(moe, to_dev_bf16(xb, gpu), torch.from_numpy(rw).to(gpu),
                           torch.from_numpy(rids).to(gpu), out_dtype=torch.float32, path=2).cpu().numpy()
-    d13 = {e: O.bf16_to_f32(bf16_bits(ops.dequant(moe.w13, e, 1)[0])) for e in range(E + S)}
-    d2 = {e: O.bf16_to_f32(bf16_bits(ops.dequant(moe.w2, e, 1)[0])) for e in range(E + S)}
-    ref = O.moe_layer(xb, rids, rw, d13.__getitem__, d2.__getitem__,
-                      shared=[(d13[E + s], d2[E + s]) for s in range(S)])
+    ref = O.moe_layer(xb, rids, rw, w13.host, w2.host,
+                      shared=[(w13.host(E + s), w2.host(E + s)) for s in range(S)])
     assert rel_maxabs(out, ref) <= TOL
 
 
 def test_moe_layer_mixtral_shape(gpu):
     """Mixtral-8x7B layer shape (H4096 I14336, 8 experts top-2 with renormalisation): K spans
     two (W13) and seven (W2) 2048-column decode chunks, and the MFMA path runs 112 n-tiles per
-    expert.  Decode T=1 and T=3 from logits, prefill T=64 from ids on 3 experts; oracle on the
-    touched experts' GPU-dequantised weights (dequantisation is bit-exact separately)."""
+    expert.  Decode T=1 and T=3 from logits, prefill T=64 from ids on 3 experts; the oracle
+    dequantises the touched experts on the host from their codes."""
     import torch
     from block_lut_amd import ops
-    from block_lut_amd.formats import BL4Stack, MoEWeights
+    from block_lut_amd.formats import MoEWeights
+    from gpu_weights import DevBL4
     H, I, E, k = 4096, 14336, 8, 2
     g = torch.Generator(device=gpu).manual_seed(14)
-
-    def rand_stack(M, K):
-        codes = torch.randint(0, 256, (E, M, K // 2), dtype=torch.uint8, generator=g, device=gpu)
-        tabs = torch.sort(torch.randn((E, M, K // 64, 16), generator=g, device=gpu) * 0.02, dim=-1).values
-        return BL4Stack(codes, tabs.to(torch.bfloat16))
-
-    moe = MoEWeights(rand_stack(2 * I, H), rand_stack(H, I), H, I, E, 0)
-    cache = {}
-
-    def deq(w, e):
-        key = (id(w), e)
-        if key not in cache:
-            cache[key] = O.bf16_to_f32(bf16_bits(ops.dequant(w, e, 1)[0]))
-        return cache[key]
-
+    w13 = DevBL4(E, 2 * I, H, g, gpu)
+    w2 = DevBL4(E, H, I, g, gpu)
+    moe = MoEWeights(w13.stack, w2.stack, H, I, E, 0)
     for T in (1, 3):
         rng = np.random.default_rng(140 + T)
         xb = _x(rng, T, H)
@@ -1016,7 +1044,7 @@ def test_moe_layer_mixtral_shape(gpu):
         out = ops.moe_forward_logits(moe, to_dev_bf16(xb, gpu), torch.from_numpy(lg).to(gpu), k,
                                      renormalize=True, out_dtype=torch.float32, path=1).cpu().numpy()
         rw, rids = O.route(lg, k, renormalize=True)
-        ref = O.moe_layer(xb, rids, rw, lambda e: deq(moe.w13, e), lambda e: deq(moe.w2, e))
+        ref = O.moe_layer(xb, rids, rw, w13.host, w2.host)
         assert rel_maxabs(out, ref) <= TOL, T
     T = 64
     rng = np.random.default_rng(164)
@@ -1025,8 +1053,74 @@ def test_moe_layer_mixtral_shape(gpu):
     rw = rng.dirichlet(np.ones(k), size=T).astype(np.float32)
     out = ops.moe_forward(moe, to_dev_bf16(xb, gpu), torch.from_numpy(rw).to(gpu),
                           torch.from_numpy(rids).to(gpu), out_dtype=torch.float32, path=2).cpu().numpy()
-    ref = O.moe_layer(xb, rids, rw, lambda e: deq(moe.w13, e), lambda e: deq(moe.w2, e))
+    ref = O.moe_layer(xb, rids, rw, w13.host, w2.host)
     assert rel_maxabs(out, ref) <= TOL
+
+
+def _sigmoid_gate(xb, gate_bits):
+    z = O.bf16_to_f32(xb).astype(np.float64) @ O.bf16_to_f32(gate_bits).astype(np.float64)
+    return 1.0 / (1.0 + np.exp(-z))
+
+
+@pytest.mark.parametrize("fmt,T,path,logits", [("bl4", 1, 1, True), ("bl4", 2, 1, False), ("bl4", 5, 1, True),
+                                               ("bl4", 5, 1, False), ("bl4", 70, 2, True),
+                                               ("ref", 1, 1, False), ("ref", 4, 1, True), ("ref", 40, 2, False)])
+def test_moe_layer_qwen_gated_shared_expert(gpu, fmt, T, path, logits):
+    """Qwen1.5-MoE's shared expert (customized/qwen.py:40-43, 99-100): one MLP with 4x the
+    routed intermediate size, split into 4 slots of I, each token's slots weighted by
+    sigmoid(x . shared_expert_gate).  The oracle runs the unsplit shared MLP and the gate in
+    float64; decode with routing in registers (T <= 2), in the routing kernel (T = 4, 5),
+    from ids and from logits, and the MFMA path."""
+    import torch
+    from block_lut_amd import ops
+    from block_lut_amd.formats import (BL4Stack, MoEWeights, RefStack, split_shared_bl4,
+                                       split_shared_ref)
+    E, k, H, I, m = 8, 2, 512, 256, 4
+    rng = np.random.default_rng(300 + T)
+    if fmt == "bl4":
+        routed13 = BL4Expertset(E, 2 * I, H, seed=31 + T, n_iter=8)
+        routed2 = BL4Expertset(E, H, I, seed=32 + T, n_iter=8)
+        sh13 = BL4Expertset(1, 2 * m * I, H, seed=33 + T, n_iter=8)
+        sh2 = BL4Expertset(1, H, m * I, seed=34 + T, n_iter=8)
+        c13, t13, c2, t2 = split_shared_bl4(torch.from_numpy(sh13.codes[0]), torch.from_numpy(sh13.tables[0]),
+                                            torch.from_numpy(sh2.codes[0]), torch.from_numpy(sh2.tables[0]), I)
+        w13 = BL4Stack.from_fp16(torch.cat([torch.from_numpy(routed13.codes), c13]).to(gpu),
+                                 to_dev_f16(np.concatenate([routed13.tables, t13.numpy()]), gpu))
+        w2 = BL4Stack.from_fp16(torch.cat([torch.from_numpy(routed2.codes), c2]).to(gpu),
+                                to_dev_f16(np.concatenate([routed2.tables, t2.numpy()]), gpu))
+        sh_w13, sh_w2 = sh13.deq_f32(0), sh2.deq_f32(0)
+    else:
+        routed13 = RefExpertset(E, 2 * I, H, seed=31 + T)
+        routed2 = RefExpertset(E, H, I, seed=32 + T)
+        sh13 = RefExpertset(1, 2 * m * I, H, seed=33 + T)
+        sh2 = RefExpertset(1, H, m * I, seed=34 + T)
+        c13, a13, c2, a2 = split_shared_ref(torch.from_numpy(sh13.codes[0]), torch.from_numpy(sh13.absmax[0].view(np.int16)),
+                                            torch.from_numpy(sh2.codes[0]), torch.from_numpy(sh2.absmax[0].view(np.int16)), I)
+        cb = to_dev_bf16(routed13.cb, gpu)
+        w13 = RefStack(torch.cat([torch.from_numpy(routed13.codes), c13]).to(gpu),
+                       torch.cat([torch.from_numpy(routed13.absmax.view(np.int16)), a13]).to(gpu).view(torch.bfloat16),
+                       cb, 128)
+        w2 = RefStack(torch.cat([torch.from_numpy(routed2.codes), c2]).to(gpu),
+                      torch.cat([torch.from_numpy(routed2.absmax.view(np.int16)), a2]).to(gpu).view(torch.bfloat16),
+                      cb, 128)
+        sem13, sem2 = _ref_semantics(sh13, sh2, T, path)
+        sh_w13, sh_w2 = sem13(0), sem2(0)
+    gate = O.f32_to_bf16((rng.standard_normal(H) * 0.05).astype(np.float32))
+    moe = MoEWeights(w13, w2, H, I, E, m, shared_gate=to_dev_bf16(gate, gpu))
+    xb = _x(rng, T, H)
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    rw, rids = O.route(lg, k)
+    if logits:
+        out = ops.moe_forward_logits(moe, to_dev_bf16(xb, gpu), torch.from_numpy(lg).to(gpu), k,
+                                     out_dtype=torch.float32, path=path)
+    else:
+        out = ops.moe_forward(moe, to_dev_bf16(xb, gpu), torch.from_numpy(rw).to(gpu),
+                              torch.from_numpy(rids).to(gpu), out_dtype=torch.float32, path=path)
+    f13, f2 = _ref_semantics(routed13, routed2, T, path) if fmt == "ref" else (routed13.deq_f32, routed2.deq_f32)
+    sw = _sigmoid_gate(xb, gate)
+    assert sw.mean() < 0.85     # the gate moves the shared expert's weight well away from 1
+    ref = O.moe_layer(xb, rids, rw, f13, f2, shared=[(sh_w13, sh_w2)], shared_w=sw)
+    assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
 
 
 def test_moe_layer_paths_agree(gpu):

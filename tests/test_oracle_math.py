@@ -307,6 +307,85 @@ def test_moe_layer_loop_vs_dense_restatement():
     np.testing.assert_allclose(got, dense, rtol=1e-9, atol=1e-12)
 
 
+def test_moe_layer_swiglu_pinned_by_torch():
+    """oracle.moe_layer against the reference's own torch formulation of one expert
+    (vllm_lut/moe_layer.py:332-340: gate_up = F.linear(x, W13); gate, up = chunk(2);
+    F.silu(gate) * up; F.linear(act, W2)) in float64, with gate rows and up rows drawn
+    from different distributions (a gate/up swap, a missing SiLU or a SiLU on the up half
+    fails), routed weights applied per slot and a shared expert with weight 1."""
+    import torch
+    import torch.nn.functional as F
+    rng = np.random.default_rng(31)
+    T, H, I, E, k = 7, 64, 32, 4, 2
+    x = O.f32_to_bf16(rng.standard_normal((T, H)).astype(np.float32))
+    W13 = [np.concatenate([(rng.standard_normal((I, H)) * 0.3 + 0.05),      # gate rows [0, I)
+                           (rng.standard_normal((I, H)) * 0.1 - 0.02)]).astype(np.float32)  # up rows
+           for _ in range(E + 1)]
+    W2 = [(rng.standard_normal((H, I)) * 0.1).astype(np.float32) for _ in range(E + 1)]
+    w, ids = O.route(rng.standard_normal((T, E)).astype(np.float32), k)
+    got = O.moe_layer(x, ids, w, W13.__getitem__, W2.__getitem__, shared=[(W13[E], W2[E])],
+                      act_round_bf16=False)
+    xt = torch.from_numpy(O.bf16_to_f32(x).astype(np.float64))
+
+    def expert(e, rows):
+        gate, up = F.linear(xt[rows], torch.from_numpy(W13[e].astype(np.float64))).chunk(2, dim=-1)
+        return F.linear(F.silu(gate) * up, torch.from_numpy(W2[e].astype(np.float64)))
+
+    ref = torch.zeros((T, H), dtype=torch.float64)
+    for e in range(E):
+        for s in range(k):
+            m = torch.from_numpy(ids[:, s] == e)
+            if m.any():
+                ref[m] += expert(e, m) * torch.from_numpy(w[:, s].astype(np.float64))[m, None]
+    ref += expert(E, torch.ones(T, dtype=torch.bool))
+
+    def rel(a, b):   # the oracle's SwiGLU runs in fp32, torch's here in float64
+        return np.abs(a - b).max() / np.abs(b).max()
+
+    assert rel(got, ref.numpy()) <= 1e-6
+    # the check can fail: swapping the gate and up halves moves the result by O(1)
+    swapped = [np.concatenate([m[I:], m[:I]]) for m in W13]
+    bad = O.moe_layer(x, ids, w, swapped.__getitem__, W2.__getitem__, shared=[(swapped[E], W2[E])],
+                      act_round_bf16=False)
+    assert rel(bad, ref.numpy()) > 0.05
+    # the per-token shared weights (Qwen's sigmoid gate) scale only the shared expert
+    sw = rng.random(T)
+    got2 = O.moe_layer(x, ids, w, W13.__getitem__, W2.__getitem__, shared=[(W13[E], W2[E])],
+                       act_round_bf16=False, shared_w=sw)
+    ref2 = ref - expert(E, torch.ones(T, dtype=torch.bool)) * (1 - torch.from_numpy(sw))[:, None]
+    assert rel(got2, ref2.numpy()) <= 1e-6
+    # a subset of W2's rows gives those output columns
+    cols = np.array([3, 17, 40])
+    got3 = O.moe_layer(x, ids, w, W13.__getitem__, lambda e: W2[e][cols], act_round_bf16=False)
+    full = O.moe_layer(x, ids, w, W13.__getitem__, W2.__getitem__, act_round_bf16=False)
+    np.testing.assert_allclose(got3, full[:, cols], rtol=1e-12, atol=1e-15)
+
+
+def test_fast_host_dequant_matches_oracle():
+    """bl4_dequant_f32 / nested_dequant_f32 (the vectorised host dequantisers of the
+    full-shape GPU tests) equal bl4_dequant / nested_dequant, including every fp16 table
+    pattern class (zero, subnormal, inf, NaN) and more rows than one gather chunk; the
+    bit-plane section split of a device buffer gives back the codes."""
+    rng = np.random.default_rng(32)
+    M, K = 1030, 128
+    p = rng.integers(0, 256, (M, K // 2), dtype=np.uint8)
+    t = rng.integers(0, 65536, (M, K // 64, 16), dtype=np.uint16)
+    t[0, 0, :6] = [0, 1, 0x3ff, 0x7c00, 0x7e00, 0xfc01]
+    got = O.bl4_dequant_f32(p, t, row_chunk=256)
+    ref = O.bf16_to_f32(O.bl4_dequant(p, t))
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    for b in (2, 3, 4):
+        c = rng.integers(0, 16, (M, K), dtype=np.uint8)
+        tb = rng.integers(0, 65536, (M, K // 64, 1 << b), dtype=np.uint16)
+        got = O.nested_dequant_f32(c, tb, b, row_chunk=300)
+        ref = O.bf16_to_f32(O.nested_dequant(c, tb, b))
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), b
+        pl = O.nested_pack_planes(c)
+        buf = np.concatenate([pl["p01"].reshape(-1)] + [pl[n].reshape(-1) for n in ("p2", "p3")][: b - 2])
+        back = O.nested_unpack_planes(O.nested_planes_split(buf, b, M, K), b)
+        assert np.array_equal(back, c & ((1 << b) - 1)), b
+
+
 def test_cpu_baseline_dequant_matches_oracle():
     import torch
     from oracle.cpu_baseline import bl4_dequant_torch
