@@ -311,7 +311,9 @@ size_t lutmoe_moe_workspace_size(const lutmoe_moe_desc* d, int T, int k) {
     return moe_layout(d, T, k).total;
 }
 
-namespace {
+}  // extern "C"
+
+namespace lutmoe_host {
 
 // Shared body of the MoE entry points.  Exactly one of (topk_w, topk_ids) and
 // logits is given.
@@ -393,7 +395,11 @@ int moe_forward_impl(const lutmoe_moe_desc* d, const void* x, const float* topk_
     return LUTMOE_OK;
 }
 
-}  // namespace
+void set_last_error_text(const char* text) { snprintf(g_last_error, sizeof(g_last_error), "%s", text); }
+
+}  // namespace lutmoe_host
+
+extern "C" {
 
 int lutmoe_moe_forward(const lutmoe_moe_desc* d, const void* x, const float* topk_w,
                        const int32_t* topk_ids, int T, int k, void* out, int out_dtype,

@@ -45,6 +45,15 @@ struct MoeRouting {
     int num_experts_total;    // E + S
 };
 
+// api.cpp: the body shared by the MoE layer entry points (arguments as
+// lutmoe_moe_forward_stages, logits instead of topk_w/topk_ids when given),
+// and the calling thread's lutmoe_last_error text.
+int moe_forward_impl(const lutmoe_moe_desc* d, const void* x, const float* topk_w,
+                     const int32_t* topk_ids, const float* logits, int T, int k, int renorm,
+                     float scaling, void* out, int out_dtype, void* workspace, size_t ws_bytes,
+                     int force_path, int stages, void* stream);
+void set_last_error_text(const char* text);
+
 // decode.hip (BL4 decode layer, routing recomputed inside each CTA)
 bool decode_v2_supported(const lutmoe_moe_desc* d, int T, int k);
 size_t decode_route_bytes();

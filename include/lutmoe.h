@@ -95,8 +95,9 @@ typedef struct lutmoe_moe_desc {
 /* ---- library ---------------------------------------------------------- */
 const char* lutmoe_strerror(int code);
 const char* lutmoe_version(void);
-/* Last error text recorded by a void-returning reference-compatible entry
- * point on the calling thread ("" when none). */
+/* Last error text recorded on the calling thread by a void-returning
+ * reference-compatible entry point or by lutmoe_moe_forward_noalloc ("" when
+ * none). */
 const char* lutmoe_last_error(void);
 
 /* ---- reference-compatible entry points --------------------------------
@@ -214,6 +215,22 @@ int lutmoe_moe_forward(const lutmoe_moe_desc* d, const void* x_dev, const float*
                        const int32_t* topk_ids_dev, int T, int k, void* out_dev,
                        int out_dtype, void* workspace_dev, size_t workspace_bytes,
                        int force_path, void* stream);
+
+/* lutmoe_moe_forward without a workspace argument: the layer's scratch is a
+ * file-scope device array of the library, 32 MiB per GPU, held until the
+ * process ends; the call allocates nothing (no hipMalloc, hipFree or
+ * allocating library routine).  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  A layer whose
+ * workspace (lutmoe_moe_workspace_size) exceeds 32 MiB is rejected with
+ * LUTMOE_EWORKSPACE and a lutmoe_last_error text giving the sizes.  Every call
+ * on one GPU shares that GPU's scratch, which keeps the last call's contents:
+ * calls that overlap in time on one GPU race (serialise them, e.g. on one
+ * stream).  The first call on a device looks up the scratch's address and
+ * clears its counters with a kernel on `stream`. */
+int lutmoe_moe_forward_noalloc(const lutmoe_moe_desc* d, const void* x_dev, const float* topk_w_dev,
+                               const int32_t* topk_ids_dev, int T, int k, void* out_dev, int out_dtype,
+                               int force_path, void* stream);
 
 /* Stage bits of lutmoe_moe_forward_stages. */
 #define LUTMOE_STAGE_ROUTE    1   /* pair build + permutation into the workspace   */
