@@ -999,6 +999,95 @@ __device__ __forceinline__ void gate_up_body4(const DecodeArgs& A, const RV& rv,
     }
 }
 
+// One token (T = 1): the expert of active slot y, for the gate/up CTAs that
+// do not publish the routing.  The slots are the token's distinct routed
+// experts in ascending id order, then the shared experts; the top-k set is a
+// 64-bit mask chosen as wave_pairs chooses it (k rounds of a DPP wave max,
+// ties to the lower id, NaN never selected), so the slot order matches the
+// routing copy the publishing CTA writes.  A few dozen instructions where the
+// general routing takes a few hundred, run by every one of the layer's
+// thousands of one-wave CTAs.  Returns -1 past the last slot and -2 where
+// this path does not apply (more than 64 routed experts, or ids that repeat:
+// the caller then takes the general routing).
+__device__ __forceinline__ int t1_slot_expert(const DecodeArgs& A, int y) {
+    const int lane = threadIdx.x & 63;
+    const int E = A.d.num_routed, S = A.d.num_shared, k = A.k;
+    if (E > 64) return -2;
+    uint64_t sel = 0;
+    if (A.topk_ids) {
+        const int id = lane < k ? A.topk_ids[lane] : -1;
+        const bool ok = lane < k && id >= 0 && id < E;
+        for (int j = 0; j < k; ++j) {
+            const int e = __builtin_amdgcn_readlane(id, j);
+            if (e >= 0 && e < E) sel |= 1ull << e;
+        }
+        if (__popcll(sel) != __popcll(__ballot(ok))) return -2;   // a repeated id
+    } else {
+        const float v = lane < E ? A.logits[lane] : -INFINITY;
+        int key = lane < E ? float_key(v) : INT_MIN;
+        for (int j = 0; j < k; ++j) {
+            const int m = wave_max_i32(key);
+            const uint64_t b = __ballot(lane < E && key == m && m != INT_MIN);
+            if (b) {
+                const int s = (int)__builtin_ctzll(b);
+                sel |= 1ull << s;
+                if (lane == s) key = INT_MIN;
+            }
+        }
+    }
+    const int nsel = __popcll(sel);
+    if (y < nsel) {
+        for (int i = 0; i < y; ++i) sel &= sel - 1;
+        return (int)__builtin_ctzll(sel);
+    }
+    return y < nsel + S ? E + (y - nsel) : -1;
+}
+
+// One token, BL4, K = H <= 2048 (one chunk): gate/up rows i0, i0 + 1 of
+// expert e (slot y, position y) with the token's activations xs loaded
+// before the routing; SwiGLU -> act[y][i0 .. i0 + 1].
+__device__ __forceinline__ void gate_up_t1(const DecodeArgs& A, const uint32_t (&xs)[16], const uint8_t* wcodes,
+                                           const uint8_t* wtabs, int64_t per, int e, int y, uint8_t* slot) {
+    const int lane = threadIdx.x & 63;
+    const int I = A.d.inter, H = A.d.hidden;
+    const int i0 = blockIdx.x * 2;
+    const int i1 = min(i0 + 1, I - 1);
+    const int rows[4] = {i0, i1, I + i0, I + i1};
+    const uint8_t* codes = wcodes + e * per;
+    const uint8_t* tabs = wtabs + e * per;
+    const bool ok = 32 * lane < H;
+    u32x4_t cw[4], tw[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int64_t off = (int64_t)rows[r] * (H / 2) + (ok ? 16 * lane : 0);
+        cw[r] = *reinterpret_cast<const u32x4_t*>(codes + off);
+        tw[r] = *reinterpret_cast<const u32x4_t*>(tabs + off);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t tab = lds_addr(slot) + ((lane >> 1) << 5);
+    const u32x4_t z = {0u, 0u, 0u, 0u};
+    float acc[4][1] = {{0.f}, {0.f}, {0.f}, {0.f}};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        *reinterpret_cast<u32x4_t*>(slot + r * 1024 + 16 * lane) = ok ? tw[r] : z;
+        wave_lds_sync();
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            uint32_t xj[1][4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xj[0][i] = xs[4 * j + i];
+            bl4_dot8<1>(cw[r][j], tab + r * 1024, xj, 1, acc[r]);
+        }
+    }
+    const float g0 = wave_reduce(acc[0][0]), g1 = wave_reduce(acc[1][0]);
+    const float u0 = wave_reduce(acc[2][0]), u1 = wave_reduce(acc[3][0]);
+    if (lane == 0) {
+        uint16_t* a = A.act + (int64_t)y * I;
+        a[i0] = (uint16_t)f32_to_bf16(silu_mul(g0, u0));
+        if (i0 + 1 < I) a[i0 + 1] = (uint16_t)f32_to_bf16(silu_mul(g1, u1));
+    }
+}
+
 template <int TB, bool kPre, int kFmt>
 __global__ __launch_bounds__(64 * kGuWaves, TB <= 2 ? 3 : 2) void bl4_decode_gate_up(DecodeArgs A) {
     __shared__ __attribute__((aligned(16))) uint8_t s_slot[kGuWaves * kSlot];
@@ -1007,6 +1096,30 @@ __global__ __launch_bounds__(64 * kGuWaves, TB <= 2 ? 3 : 2) void bl4_decode_gat
             gate_up_body4<TB>(A, GlobalRouteView{A.route}, s_slot);
         } else {
             const bool pub = blockIdx.x == 0 && blockIdx.y == 0;
+            if (!pub && A.T == 1 && A.d.hidden <= kWChunk) {
+                // kernel arguments and the token's activations first, then the
+                // slot's expert, then the weights
+                const int lane = threadIdx.x & 63;
+                const uint8_t* wcodes = (const uint8_t*)A.d.w13.codes;
+                const uint8_t* wtabs = (const uint8_t*)A.d.w13.tables;
+                const int64_t per = (int64_t)A.d.w13.rows * (A.d.hidden / 2);
+                asm volatile("" ::"s"(wcodes), "s"(wtabs), "s"(per));
+                uint32_t xs[16];
+                const uint16_t* xp = A.x + (32 * lane < A.d.hidden ? 32 * lane : 0);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const uint4 v = *reinterpret_cast<const uint4*>(xp + 8 * q);
+                    xs[4 * q + 0] = v.x;
+                    xs[4 * q + 1] = v.y;
+                    xs[4 * q + 2] = v.z;
+                    xs[4 * q + 3] = v.w;
+                }
+                const int e = t1_slot_expert(A, blockIdx.y);
+                if (e != -2) {
+                    if (e >= 0 && blockIdx.x * 2 < A.d.inter) gate_up_t1(A, xs, wcodes, wtabs, per, e, blockIdx.y, s_slot);
+                    return;
+                }
+            }
             const WaveRoute r = pub ? wave_pairs<true>(A) : wave_pairs<false>(A);
             if (pub && threadIdx.x < 64) wave_route_publish(A, r);
             gate_up_body4<TB>(A, WaveRouteView{r}, s_slot);
@@ -1139,6 +1252,126 @@ __global__ __launch_bounds__(256, TB <= 2 ? 3 : 2) void bl4_decode_down(DecodeAr
         else down_body<TB, kFmt>(A, LdsRouteView{&R}, s_slot, s_y);
     } else {
         down_body<TB, kFmt>(A, WaveRouteView{wave_pairs<true>(A)}, s_slot, s_y);
+    }
+}
+
+// One token (T = 1), BL4: CTA x covers output rows [4x, 4x + 4); wave wv takes
+// the active slots wv, wv + 4, .. (one position each, position = slot).  An
+// expert's 4 rows are contiguous in memory (K/2 code bytes and K/2 table bytes
+// per row), so they are walked as one flat array of 16-byte units: unit u
+// covers columns [32g, 32g + 32) of row u / NU (NU = K/32, g = u % NU), and
+// lane l takes units l, l + 64, .. (kPass passes).  Every lane works whatever
+// K is (K = 1408: 176 units in 3 passes, where a row per pass leaves 20 of 64
+// lanes idle); the two halves of a 64-weight block stay on neighbouring lanes
+// because NU is even.  The routing is read from the workspace copy in place:
+// no LDS copy and no barrier before the weight loads.
+constexpr int kD1Rows = 4;
+
+template <int kPass>
+__global__ __launch_bounds__(256, 2) void bl4_decode_down1(DecodeArgs A) {
+    __shared__ __attribute__((aligned(16))) uint8_t s_slot[4][kPass * 1024];
+    __shared__ float s_y[16][kD1Rows];   // [position][row], T = 1: at most k + S <= 16 positions
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int K = A.d.inter, H = A.d.hidden, ke = A.k + A.d.num_shared;
+    const int NU = K / 32, U = kD1Rows * NU;
+    const int h0 = blockIdx.x * kD1Rows;   // H % 64 == 0: all 4 rows exist
+    const RouteOut* R = A.route;
+    // the routing fields this wave needs, in one round trip: the count, the
+    // first slot's expert and position (in bounds for any count), and the
+    // positions of the token's pairs for the combine
+    const int nact = R->nact;
+    int e_next = R->act[wv], p_next = R->aoff[wv];
+    const int inv_l = (wv == 0 && lane < ke) ? R->inv[lane] : -1;
+    const int64_t per = (int64_t)A.d.w2.rows * (K / 2);
+    const int64_t rbase = (int64_t)h0 * (K / 2);
+    const uint8_t* wcodes = (const uint8_t*)A.d.w2.codes;
+    const uint8_t* wtabs = (const uint8_t*)A.d.w2.tables;
+    // the weight bases come from the kernel arguments while the routing loads
+    // are in flight (not after them)
+    asm volatile("" ::"s"(wcodes), "s"(wtabs), "s"(per));
+    uint8_t* slot = s_slot[wv];
+    const uint32_t tab0 = lds_addr(slot) + ((lane >> 1) << 5);
+    const u32x4_t z = {0u, 0u, 0u, 0u};
+    for (int a = wv; a < nact; a += 4) {
+        const int e = e_next, p0 = p_next;
+        if (a + 4 < kMaxEtot) {
+            e_next = R->act[a + 4];
+            p_next = R->aoff[a + 4];
+        }
+        const float pw = R->pw[R->perm[p0]];
+        const uint8_t* codes = wcodes + e * per + rbase;
+        const uint8_t* tabs = wtabs + e * per + rbase;
+        const uint16_t* xr = A.act + (int64_t)p0 * K;
+        uint32_t xs[kPass][16];
+        u32x4_t cw[kPass], tw[kPass];
+#pragma unroll
+        for (int p = 0; p < kPass; ++p) {
+            const int u = 64 * p + lane;
+            const int g = u < U ? u % NU : 0;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint4 v = *reinterpret_cast<const uint4*>(xr + 32 * g + 8 * q);
+                xs[p][4 * q + 0] = v.x;
+                xs[p][4 * q + 1] = v.y;
+                xs[p][4 * q + 2] = v.z;
+                xs[p][4 * q + 3] = v.w;
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int p = 0; p < kPass; ++p) {
+            const int u = 64 * p + lane;
+            const int64_t off = u < U ? 16 * u : 0;
+            cw[p] = *reinterpret_cast<const u32x4_t*>(codes + off);
+            tw[p] = *reinterpret_cast<const u32x4_t*>(tabs + off);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        float acc[kPass];
+#pragma unroll
+        for (int p = 0; p < kPass; ++p) {
+            // units past the 4 rows stage zero tables (their loads read the first unit)
+            *reinterpret_cast<u32x4_t*>(slot + p * 1024 + 16 * lane) = 64 * p + lane < U ? tw[p] : z;
+            wave_lds_sync();
+            float s[1] = {0.f};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                uint32_t xj[1][4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) xj[0][i] = xs[p][4 * j + i];
+                bl4_dot8<1>(cw[p][j], tab0 + p * 1024, xj, 1, s);
+            }
+            acc[p] = s[0];
+        }
+        wave_lds_sync();
+        // per-row sums: unit partials through LDS, then lane 16r + j adds units
+        // r*NU + j, + 16, .. and the 16 lanes of row r reduce with DPP
+        float* part = reinterpret_cast<float*>(slot);
+#pragma unroll
+        for (int p = 0; p < kPass; ++p) part[64 * p + lane] = acc[p];
+        wave_lds_sync();
+        const int r = lane >> 4, j = lane & 15;
+        float v = 0.f;
+        for (int u = j; u < NU; u += 16) v += part[r * NU + u];
+        v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xb1, 0xf, 0xf, false));
+        v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4e, 0xf, 0xf, false));
+        v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xf, 0xf, false));
+        v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xf, 0xf, false));
+        if (j == 0) s_y[p0][r] = v * pw;
+        wave_lds_sync();   // the slot is restaged by the next active slot
+    }
+    __syncthreads();
+    // the token's slots in slot order (pair q of token 0 sits at position inv[q])
+    if (wv == 0) {
+        float sum = 0.f;
+        for (int q = 0; q < ke; ++q) {
+            const int pos = __builtin_amdgcn_readlane(inv_l, q);
+            if (pos >= 0 && lane < kD1Rows) sum += s_y[pos][lane];
+        }
+        if (lane < kD1Rows) {
+            const int64_t o = h0 + lane;
+            if (A.out_dtype == LUTMOE_DTYPE_F32) ((float*)A.out)[o] = sum;
+            else ((uint16_t*)A.out)[o] = (uint16_t)f32_to_bf16(sum);
+        }
     }
 }
 
@@ -1569,6 +1802,17 @@ int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* t
             if ((rc = check_launch())) return rc;
             const int32_t* inv = ((const RouteOut*)route_ws)->inv;
             return launch_combine(y_ws, inv, T, k + d->num_shared, d->hidden, out, out_dtype, s);
+        }
+        if (fmt_idx == 0 && tb == 1 && d->inter <= 2048) {
+            // one token, BL4: flat 16-byte units over 4 rows (every lane busy)
+            const dim3 g1(d->hidden / kD1Rows);
+            switch ((d->inter + 511) / 512) {
+                case 1: hipLaunchKernelGGL(bl4_decode_down1<1>, g1, dim3(256), 0, s, A); break;
+                case 2: hipLaunchKernelGGL(bl4_decode_down1<2>, g1, dim3(256), 0, s, A); break;
+                case 3: hipLaunchKernelGGL(bl4_decode_down1<3>, g1, dim3(256), 0, s, A); break;
+                default: hipLaunchKernelGGL(bl4_decode_down1<4>, g1, dim3(256), 0, s, A); break;
+            }
+            return check_launch();
         }
         LUTMOE_DECODE_LAUNCH(bl4_decode_down, true, grid, dim3(256), lds)
         return check_launch();
