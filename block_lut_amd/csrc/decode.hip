@@ -960,12 +960,13 @@ __device__ __forceinline__ void bl4_rows4(const uint8_t* __restrict__ codes, con
 }
 
 template <int TB, class RV>
-__device__ __forceinline__ void gate_up_body4(const DecodeArgs& A, const RV& rv, uint8_t* slot) {
+__device__ __forceinline__ void gate_up_body4(const DecodeArgs& A, const RV& rv, uint8_t* slot,
+                                              int xcol = -1) {
     const SlotRef sl = rv.work(blockIdx.y);
     if (sl.e < 0) return;
     const int lane = threadIdx.x & 63;
     const int I = A.d.inter, H = A.d.hidden, ke = A.k + A.d.num_shared;
-    const int i0 = blockIdx.x * 2;
+    const int i0 = (xcol < 0 ? (int)blockIdx.x : xcol) * 2;
     if (i0 >= I) return;
     const int i1 = min(i0 + 1, I - 1);
     const int rows[4] = {i0, i1, I + i0, I + i1};
@@ -1047,10 +1048,10 @@ __device__ __forceinline__ int t1_slot_expert(const DecodeArgs& A, int y) {
 // expert e (slot y, position y) with the token's activations xs loaded
 // before the routing; SwiGLU -> act[y][i0 .. i0 + 1].
 __device__ __forceinline__ void gate_up_t1(const DecodeArgs& A, const uint32_t (&xs)[16], const uint8_t* wcodes,
-                                           const uint8_t* wtabs, int64_t per, int e, int y, uint8_t* slot) {
+                                           const uint8_t* wtabs, int64_t per, int e, int y, int xcol, uint8_t* slot) {
     const int lane = threadIdx.x & 63;
     const int I = A.d.inter, H = A.d.hidden;
-    const int i0 = blockIdx.x * 2;
+    const int i0 = xcol * 2;
     const int i1 = min(i0 + 1, I - 1);
     const int rows[4] = {i0, i1, I + i0, I + i1};
     const uint8_t* codes = wcodes + e * per;
@@ -1079,12 +1080,49 @@ __device__ __forceinline__ void gate_up_t1(const DecodeArgs& A, const uint32_t (
             bl4_dot8<1>(cw[r][j], tab + r * 1024, xj, 1, acc[r]);
         }
     }
-    const float g0 = wave_reduce(acc[0][0]), g1 = wave_reduce(acc[1][0]);
-    const float u0 = wave_reduce(acc[2][0]), u1 = wave_reduce(acc[3][0]);
+    // reduce-scatter of the 4 row sums: lane 16j holds row j's total
+    const float v = wave_reduce4(acc[0][0], acc[1][0], acc[2][0], acc[3][0]);
+    const float up = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float up1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    const float g1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
     if (lane == 0) {
         uint16_t* a = A.act + (int64_t)y * I;
-        a[i0] = (uint16_t)f32_to_bf16(silu_mul(g0, u0));
-        if (i0 + 1 < I) a[i0 + 1] = (uint16_t)f32_to_bf16(silu_mul(g1, u1));
+        a[i0] = (uint16_t)f32_to_bf16(silu_mul(v, up));
+        if (i0 + 1 < I) a[i0 + 1] = (uint16_t)f32_to_bf16(silu_mul(g1, up1));
+    }
+}
+
+// One token, BL4, H <= 2048: CTAs of 4 independent waves (one dispatch for
+// four, no barrier); wave w of CTA (x, y) takes intermediate indices
+// 2(4x + w), +1 of slot y with its own short slot routing.  The first wave of
+// CTA (0, 0) also computes the full routing with the pair weights and
+// publishes it for the down kernel.
+__global__ __launch_bounds__(256, 3) void bl4_decode_gate_up_t1(DecodeArgs A) {
+    __shared__ __attribute__((aligned(16))) uint8_t s_slot[4][4 * 1024];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int xcol = blockIdx.x * 4 + wv;
+    const uint8_t* wcodes = (const uint8_t*)A.d.w13.codes;
+    const uint8_t* wtabs = (const uint8_t*)A.d.w13.tables;
+    const int64_t per = (int64_t)A.d.w13.rows * (A.d.hidden / 2);
+    asm volatile("" ::"s"(wcodes), "s"(wtabs), "s"(per));
+    uint32_t xs[16];
+    const uint16_t* xp = A.x + (32 * lane < A.d.hidden ? 32 * lane : 0);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint4 v = *reinterpret_cast<const uint4*>(xp + 8 * q);
+        xs[4 * q + 0] = v.x;
+        xs[4 * q + 1] = v.y;
+        xs[4 * q + 2] = v.z;
+        xs[4 * q + 3] = v.w;
+    }
+    if (blockIdx.x == 0 && blockIdx.y == 0 && wv == 0) wave_route_publish(A, wave_pairs<true>(A));
+    if (2 * xcol >= A.d.inter) return;
+    const int e = t1_slot_expert(A, blockIdx.y);
+    if (e >= 0) {
+        gate_up_t1(A, xs, wcodes, wtabs, per, e, blockIdx.y, xcol, s_slot[wv]);
+    } else if (e == -2) {
+        // ids that repeat: the general routing
+        gate_up_body4<1>(A, WaveRouteView{wave_pairs<false>(A)}, s_slot[wv], xcol);
     }
 }
 
@@ -1116,7 +1154,8 @@ __global__ __launch_bounds__(64 * kGuWaves, TB <= 2 ? 3 : 2) void bl4_decode_gat
                 }
                 const int e = t1_slot_expert(A, blockIdx.y);
                 if (e != -2) {
-                    if (e >= 0 && blockIdx.x * 2 < A.d.inter) gate_up_t1(A, xs, wcodes, wtabs, per, e, blockIdx.y, s_slot);
+                    if (e >= 0 && blockIdx.x * 2 < A.d.inter)
+                        gate_up_t1(A, xs, wcodes, wtabs, per, e, blockIdx.y, blockIdx.x, s_slot);
                     return;
                 }
             }
@@ -1294,11 +1333,7 @@ __global__ __launch_bounds__(256, 2) void bl4_decode_down1(DecodeArgs A) {
     const u32x4_t z = {0u, 0u, 0u, 0u};
     for (int a = wv; a < nact; a += 4) {
         const int e = e_next, p0 = p_next;
-        if (a + 4 < kMaxEtot) {
-            e_next = R->act[a + 4];
-            p_next = R->aoff[a + 4];
-        }
-        const float pw = R->pw[R->perm[p0]];
+        const int pair = R->perm[p0];   // its weight is loaded after the weight loads
         const uint8_t* codes = wcodes + e * per + rbase;
         const uint8_t* tabs = wtabs + e * per + rbase;
         const uint16_t* xr = A.act + (int64_t)p0 * K;
@@ -1326,6 +1361,12 @@ __global__ __launch_bounds__(256, 2) void bl4_decode_down1(DecodeArgs A) {
             tw[p] = *reinterpret_cast<const u32x4_t*>(tabs + off);
         }
         __builtin_amdgcn_sched_barrier(0);
+        // behind the weight loads: the pair weight and the next slot's fields
+        const float pw = R->pw[pair];
+        if (a + 4 < kMaxEtot) {
+            e_next = R->act[a + 4];
+            p_next = R->aoff[a + 4];
+        }
         float acc[kPass];
 #pragma unroll
         for (int p = 0; p < kPass; ++p) {
@@ -1770,7 +1811,11 @@ int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* t
     // work items: the active slots, cut into chunks by decode_route_kernel
     // (at most P, and at most one more per slot than ceil(P / TB))
     const int max_work = pre ? std::min(P, max_active + (P + tb - 1) / tb) : max_active;
-    if (stages & LUTMOE_STAGE_GATE_UP) {
+    if ((stages & LUTMOE_STAGE_GATE_UP) && fmt_idx == 0 && tb == 1 && !pre && T == 1 && d->hidden <= kWChunk) {
+        const dim3 grid((d->inter + 7) / 8, max_work);   // 4 waves x 2 intermediate indices
+        hipLaunchKernelGGL(bl4_decode_gate_up_t1, grid, dim3(256), 0, s, A);
+        if ((rc = check_launch())) return rc;
+    } else if (stages & LUTMOE_STAGE_GATE_UP) {
         const int per_cta = (fmt_idx == 0 && tb == 1) ? 2 : 4 * kGuWaves;   // intermediate indices per CTA
         const dim3 grid((d->inter + per_cta - 1) / per_cta, max_work);
         LUTMOE_DECODE_LAUNCH(bl4_decode_gate_up, pre, grid, dim3(64 * kGuWaves), 0)

@@ -330,6 +330,20 @@ __device__ __forceinline__ float wave_reduce8(const float (&v)[8]) {
     return c;
 }
 
+// Reduce-scatter of 4 per-lane partial sums over the wave: lane l returns the
+// wave total of v[l >> 4] (uniform within each 16-lane row).  The halves trade
+// v2, v3 for v0, v1 (permlane32 swap), 16-lane rows trade one of two
+// (permlane16 swap), then each row sums its value with four DPP adds.
+__device__ __forceinline__ float wave_reduce4(float v0, float v1, float v2, float v3) {
+    const float a0 = swap_sum32(v0, v2), a1 = swap_sum32(v1, v3);
+    float c = swap_sum16(a0, a1);
+    c += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, c), 0xb1, 0xf, 0xf, false));
+    c += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, c), 0x4e, 0xf, 0xf, false));
+    c += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, c), 0x141, 0xf, 0xf, false));
+    c += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, c), 0x140, 0xf, 0xf, false));
+    return c;
+}
+
 // The value of lane l + 32 in lanes l < 32 (permlane32 swap).
 __device__ __forceinline__ float from_upper_half(float v) {
     const auto s = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
