@@ -90,6 +90,8 @@ PROTOTYPES = {
     "lut_moe_launch_unpack_4bit": (None, [P, SZ, P]),
     "launch_lut_gemv_kernel": (None, [P, P, P, P, P, I32, I32, I32]),
     "lutmoe_ref_gemv": (I32, [P, P, P, P, P, I32, I32, I32, I32, I32, I32, P]),
+    "lutmoe_fused_lut_gemv": (I32, [P, P, P, P, P, I32, I32, I32, I32, I32, I32, P]),
+    "lutmoe_router_logits": (I32, [P, P, I32, I32, I32, P, I32, P]),
     "lutmoe_unpack_6bit": (I32, [P, P, I64, P]),
     "lutmoe_merge_bitplane": (I32, [P, P, I64, I32, P]),
     "lutmoe_kmeans_1d": (I32, [P, I64, P, I32, I32, P, P]),

@@ -214,6 +214,19 @@ int lutmoe_ref_gemv(const void* x, const void* indices, const void* codebook, co
                            y_dtype, stream_of(stream));
 }
 
+int lutmoe_fused_lut_gemv(const void* x, const void* indices, const void* codebook, const void* absmax,
+                          void* y, int M, int K, int T, int num_blocks, int block_size, int y_dtype,
+                          void* stream) {
+    if (M <= 0 || K <= 0 || T < 0 || num_blocks <= 0 || block_size <= 0) return LUTMOE_EINVAL;
+    if (y_dtype != LUTMOE_DTYPE_BF16 && y_dtype != LUTMOE_DTYPE_F32) return LUTMOE_EINVAL;
+    if (!x || !indices || !codebook || !absmax || !y) return LUTMOE_EINVAL;
+    if ((int64_t)M * K >= (1ll << 31)) return LUTMOE_EUNSUPPORTED;
+    if (T == 0) return LUTMOE_OK;
+    return launch_ref_gemv((const uint16_t*)x, (const uint8_t*)indices, (const uint16_t*)codebook,
+                           nullptr, (const uint16_t*)absmax, y, M, K, T, num_blocks, block_size,
+                           y_dtype, stream_of(stream), true);
+}
+
 int lutmoe_pack_bitplanes(const uint8_t* codes, int64_t n, uint8_t* packed, void* stream) {
     if (n < 0 || (n % 4)) return LUTMOE_EINVAL;
     if (n == 0) return LUTMOE_OK;
@@ -290,10 +303,21 @@ int lutmoe_bl4_tables_from_f16(const uint16_t* f16, uint16_t* bf16, int64_t n, v
 int lutmoe_route_topk(const float* logits, int T, int E, int k, int renormalize, float scaling,
                       float* topk_w, int32_t* topk_ids, void* stream) {
     if (T < 0 || E <= 0 || k <= 0 || k > E || k > 16) return LUTMOE_EINVAL;
+    if (E > 4096) return LUTMOE_EUNSUPPORTED;
     if (T == 0) return LUTMOE_OK;
     if (!logits || !topk_w || !topk_ids) return LUTMOE_EINVAL;
     return launch_route_topk(logits, T, E, k, renormalize, scaling, topk_w, topk_ids,
                              stream_of(stream));
+}
+
+int lutmoe_router_logits(const void* x, const void* gate, int T, int H, int E, float* logits, int round_bf16,
+                         void* stream) {
+    if (T < 0 || H <= 0 || E <= 0 || (H % 8) || T > 65535) return LUTMOE_EINVAL;
+    if (T == 0) return LUTMOE_OK;
+    if (!x || !gate || !logits) return LUTMOE_EINVAL;
+    if (!aligned(x, 16) || !aligned(gate, 16)) return LUTMOE_EALIGN;
+    return launch_router_logits((const uint16_t*)x, (const uint16_t*)gate, T, H, E, logits, round_bf16 ? 1 : 0,
+                                stream_of(stream));
 }
 
 int lutmoe_permute(const int32_t* topk_ids, int T, int k, int E, int32_t* offsets, int32_t* perm,

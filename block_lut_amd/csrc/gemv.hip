@@ -106,7 +106,9 @@ struct RefDec {
         }
     }
     __device__ __forceinline__ void stage(uint8_t*, int) const {}
-    template <int TB>
+    // kDeq: the dequantised weight bf16(cb * absmax) times x (fused_lut_gemv,
+    // vllm_lut/fused_kernel.py:13-46); otherwise lut_gemv's (x * cb) * absmax
+    template <int TB, bool kDeq = false>
     __device__ __forceinline__ void dot(int r, const uint8_t*, int, const uint4 (&xq)[TB], int nt,
                                         float (&acc)[TB]) const {
         float s[TB];
@@ -115,7 +117,8 @@ struct RefDec {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const uint32_t word = j < 4 ? cw[r].x : cw[r].y;
-            const float v = s_cb[(word >> (8 * (j & 3))) & 0xffu];
+            const float cv = s_cb[(word >> (8 * (j & 3))) & 0xffu];
+            const float v = kDeq ? bf16_to_f32(f32_to_bf16(cv * am[r])) : cv;
 #pragma unroll
             for (int t = 0; t < TB; ++t) {
                 if (t < nt) {
@@ -127,7 +130,7 @@ struct RefDec {
             }
         }
 #pragma unroll
-        for (int t = 0; t < TB; ++t) acc[t] = fmaf(s[t], am[r], acc[t]);
+        for (int t = 0; t < TB; ++t) acc[t] = kDeq ? acc[t] + s[t] : fmaf(s[t], am[r], acc[t]);
     }
 };
 
@@ -219,6 +222,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(lutmoe_weights w, int expert,
 // one wave per row, scalar lanes, exact reference product order
 // (x * cb) * absmax per element.  Used when the vector path's alignment
 // preconditions do not hold.
+template <bool kDeq>
 __global__ __launch_bounds__(256) void ref_gemv_generic_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ idx, const uint16_t* __restrict__ cbh,
     const float* __restrict__ cbf, const uint16_t* __restrict__ absmax, void* __restrict__ y, int M,
@@ -235,7 +239,9 @@ __global__ __launch_bounds__(256) void ref_gemv_generic_kernel(
             const int64_t flat = (int64_t)row * K + c;
             int64_t b = flat / bs;
             b = b < nb ? b : nb - 1;
-            acc += bf16_to_f32(x[(int64_t)t * K + c]) * s_cb[idx[flat]] * bf16_to_f32(absmax[b]);
+            const float xv = bf16_to_f32(x[(int64_t)t * K + c]);
+            const float cv = s_cb[idx[flat]], av = bf16_to_f32(absmax[b]);
+            acc += kDeq ? xv * bf16_to_f32(f32_to_bf16(cv * av)) : xv * cv * av;
         }
         acc = wave_sum(acc);
         if (lane == 0) {
@@ -248,7 +254,7 @@ __global__ __launch_bounds__(256) void ref_gemv_generic_kernel(
 
 // REF fast path through the octet machinery: wraps the raw reference tensors
 // in a one-expert weight description.
-template <int TB>
+template <int TB, bool kDeq>
 __global__ __launch_bounds__(256) void ref_gemv_fast_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ idx, const uint16_t* __restrict__ cbh,
     const float* __restrict__ cbf, const uint16_t* __restrict__ absmax, void* __restrict__ y, int M,
@@ -291,7 +297,7 @@ __global__ __launch_bounds__(256) void ref_gemv_fast_kernel(
             dec.load(rows, c, lane, ok);
             if (ok) {
 #pragma unroll
-                for (int r = 0; r < kRows; ++r) dec.template dot<TB>(r, nullptr, lane, xq, nt, acc[r]);
+                for (int r = 0; r < kRows; ++r) dec.template dot<TB, kDeq>(r, nullptr, lane, xq, nt, acc[r]);
             }
         }
 #pragma unroll
@@ -315,23 +321,32 @@ inline int tb_for(int T) { return T <= 1 ? 1 : T <= 2 ? 2 : 4; }
 
 namespace lutmoe_host {
 
-int launch_ref_gemv(const uint16_t* x, const uint8_t* idx, const uint16_t* cb_bf16,
-                    const float* cb_f32, const uint16_t* absmax, void* y, int M, int K, int T,
-                    int num_blocks, int block_size, int y_dtype, hipStream_t s) {
+template <bool kDeq>
+static int ref_gemv_dispatch(const uint16_t* x, const uint8_t* idx, const uint16_t* cb_bf16,
+                             const float* cb_f32, const uint16_t* absmax, void* y, int M, int K, int T,
+                             int num_blocks, int block_size, int y_dtype, hipStream_t s) {
     const bool fast = (K % 8 == 0) && (block_size % 8 == 0) && ((uintptr_t)idx % 8 == 0) &&
                       ((uintptr_t)x % 16 == 0);
     if (!fast) {
-        hipLaunchKernelGGL(ref_gemv_generic_kernel, dim3((M + 3) / 4), dim3(256), 0, s, x, idx,
+        hipLaunchKernelGGL(ref_gemv_generic_kernel<kDeq>, dim3((M + 3) / 4), dim3(256), 0, s, x, idx,
                            cb_bf16, cb_f32, absmax, y, M, K, T, num_blocks, block_size, y_dtype);
         return check_launch();
     }
     const dim3 grid((M + 4 * kRows - 1) / (4 * kRows));
     switch (tb_for(T)) {
-        case 1: hipLaunchKernelGGL(ref_gemv_fast_kernel<1>, grid, dim3(256), 0, s, x, idx, cb_bf16, cb_f32, absmax, y, M, K, T, num_blocks, block_size, y_dtype); break;
-        case 2: hipLaunchKernelGGL(ref_gemv_fast_kernel<2>, grid, dim3(256), 0, s, x, idx, cb_bf16, cb_f32, absmax, y, M, K, T, num_blocks, block_size, y_dtype); break;
-        default: hipLaunchKernelGGL(ref_gemv_fast_kernel<4>, grid, dim3(256), 0, s, x, idx, cb_bf16, cb_f32, absmax, y, M, K, T, num_blocks, block_size, y_dtype); break;
+        case 1: hipLaunchKernelGGL((ref_gemv_fast_kernel<1, kDeq>), grid, dim3(256), 0, s, x, idx, cb_bf16, cb_f32, absmax, y, M, K, T, num_blocks, block_size, y_dtype); break;
+        case 2: hipLaunchKernelGGL((ref_gemv_fast_kernel<2, kDeq>), grid, dim3(256), 0, s, x, idx, cb_bf16, cb_f32, absmax, y, M, K, T, num_blocks, block_size, y_dtype); break;
+        default: hipLaunchKernelGGL((ref_gemv_fast_kernel<4, kDeq>), grid, dim3(256), 0, s, x, idx, cb_bf16, cb_f32, absmax, y, M, K, T, num_blocks, block_size, y_dtype); break;
     }
     return check_launch();
+}
+
+int launch_ref_gemv(const uint16_t* x, const uint8_t* idx, const uint16_t* cb_bf16,
+                    const float* cb_f32, const uint16_t* absmax, void* y, int M, int K, int T,
+                    int num_blocks, int block_size, int y_dtype, hipStream_t s, bool dequant) {
+    if (dequant)
+        return ref_gemv_dispatch<true>(x, idx, cb_bf16, cb_f32, absmax, y, M, K, T, num_blocks, block_size, y_dtype, s);
+    return ref_gemv_dispatch<false>(x, idx, cb_bf16, cb_f32, absmax, y, M, K, T, num_blocks, block_size, y_dtype, s);
 }
 
 template <class Dec>

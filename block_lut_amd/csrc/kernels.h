@@ -24,9 +24,12 @@ int launch_unpack_4bit_inplace(uint8_t* data, int64_t n, hipStream_t s);
 int launch_unpack_6bit(const uint8_t* packed, uint8_t* out, int64_t n, hipStream_t s);
 
 // gemv.hip
+// dequant: y = x . bf16(cb * absmax) (fused_lut_gemv); else lut_gemv's
+// (x * cb) * absmax products
 int launch_ref_gemv(const uint16_t* x, const uint8_t* idx, const uint16_t* cb_bf16,
                     const float* cb_f32, const uint16_t* absmax, void* y, int M, int K,
-                    int T, int num_blocks, int block_size, int y_dtype, hipStream_t s);
+                    int T, int num_blocks, int block_size, int y_dtype, hipStream_t s,
+                    bool dequant = false);
 int launch_bl4_gemv(const lutmoe_weights* w, int expert, const uint16_t* x, int T, void* y,
                     int y_dtype, hipStream_t s);
 int launch_nested_gemv(const lutmoe_weights* w, int expert, const uint16_t* x, int T,
@@ -81,6 +84,10 @@ int launch_route_pairs(const int32_t* topk_ids, const float* topk_w, int T, int 
 // shared slots k..k+S-1 of every token t: pair_w = sigmoid(x_t . gate)
 int launch_shared_gate(const uint16_t* x, const uint16_t* gate, int T, int H, int k, int S, float* pair_w,
                        hipStream_t s);
+// router logits[t][e] = x[t] . gate[e] (fp32 accumulation; round_bf16: the
+// sum rounded to bf16, stored as fp32)
+int launch_router_logits(const uint16_t* x, const uint16_t* gate, int T, int H, int E, float* logits,
+                         int round_bf16, hipStream_t s);
 // nsplit > 1: y_pos holds nsplit partial results (K splits of the down
 // projection), split_stride floats apart, summed per position first.
 int launch_combine(const float* y_pos, const int32_t* inv, int T, int k_eff, int H,

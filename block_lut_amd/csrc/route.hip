@@ -23,8 +23,9 @@ using namespace lutmoe;
 
 namespace {
 
-// One wave per token: lane l holds logits l, l+64, ...; softmax in fp32;
-// top-k by logit (softmax is monotone), ties to the lower expert id.
+// One wave per token: lane l holds logits l, l+64, ... (E <= 4096: one bit
+// per held logit in a 64-bit mask); softmax in fp32; top-k by logit (softmax
+// is monotone), ties to the lower expert id.
 __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict__ logits,
                                                          int T, int E, int k, int renorm,
                                                          float scaling, float* __restrict__ w,
@@ -58,10 +59,12 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
             const int oi = __shfl_xor(bi, off, kWave);
             if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
         }
-        if ((bi & 63) == lane) taken |= 1ull << (bi >> 6);
-        const float p = expf(bv - mx) / sum;
+        // only NaN left (nothing selectable): id -1, weight 0, as the E <= 64 kernel
+        const bool none = bi == 0x7fffffff;
+        if (!none && (bi & 63) == lane) taken |= 1ull << (bi >> 6);
+        const float p = none ? 0.f : expf(bv - mx) / sum;
         wsum += p;
-        if (lane == j) { wsel = p; isel = bi; }
+        if (lane == j) { wsel = p; isel = none ? -1 : bi; }
     }
     if (lane < k) {
         const float v = renorm ? wsel / wsum : wsel;
@@ -134,6 +137,33 @@ __global__ __launch_bounds__(256) void shared_gate_kernel(const uint16_t* __rest
     if (t >= T) return;   // wave-uniform
     const float sw = shared_gate_weight(x + (int64_t)t * H, g, H);
     if (lane < S) pair_w[(int64_t)t * (k + S) + k + lane] = sw;
+}
+
+// Router gate (MoEGate.forward, models/deepseek/modeling_deepseek.py:423-470;
+// vLLM's bf16 ReplicatedLinear gate in vllm_lut/moe_layer.py:301-304):
+// logits[t][e] = x[t] . gate[e] with fp32 accumulation, optionally rounded to
+// bf16 (the gate's output dtype in the vLLM layer).  Wave w of CTA (x, t) takes
+// expert 4x + w of token t: H/512 rounds of 16-byte loads of x and of the gate
+// row, v_dot2_f32_bf16, one wave reduction.  Sized for decode (few tokens).
+__global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __restrict__ x,
+                                                            const uint16_t* __restrict__ gate, int H, int E,
+                                                            float* __restrict__ logits, int round_bf16) {
+    const int lane = threadIdx.x & 63;
+    const int e = blockIdx.x * 4 + (threadIdx.x >> 6), t = blockIdx.y;
+    if (e >= E) return;   // wave-uniform
+    const uint16_t* xr = x + (int64_t)t * H;
+    const uint16_t* gr = gate + (int64_t)e * H;
+    float s = 0.f;
+    for (int c = lane * 8; c < H; c += 512) {
+        const uint4 xv = *reinterpret_cast<const uint4*>(xr + c);
+        const uint4 gv = *reinterpret_cast<const uint4*>(gr + c);
+        s = dot2_bf16(xv.x, gv.x, s);
+        s = dot2_bf16(xv.y, gv.y, s);
+        s = dot2_bf16(xv.z, gv.z, s);
+        s = dot2_bf16(xv.w, gv.w, s);
+    }
+    s = wave_reduce(s);
+    if (lane == 0) logits[(int64_t)t * E + e] = round_bf16 ? bf16_to_f32(f32_to_bf16(s)) : s;
 }
 
 // One CTA per expert id e.  Every CTA builds the full histogram in LDS
@@ -385,6 +415,13 @@ int launch_build_pairs(const int32_t* topk_ids, const float* topk_w, int T, int 
 int launch_shared_gate(const uint16_t* x, const uint16_t* gate, int T, int H, int k, int S, float* pair_w,
                        hipStream_t s) {
     hipLaunchKernelGGL(shared_gate_kernel, dim3((T + 3) / 4), dim3(256), 0, s, x, gate, T, H, k, S, pair_w);
+    return check_launch();
+}
+
+int launch_router_logits(const uint16_t* x, const uint16_t* gate, int T, int H, int E, float* logits,
+                         int round_bf16, hipStream_t s) {
+    hipLaunchKernelGGL(router_logits_kernel, dim3((E + 3) / 4, T), dim3(256), 0, s, x, gate, H, E, logits,
+                       round_bf16);
     return check_launch();
 }
 

@@ -138,8 +138,11 @@ def gemv(w: WeightStack, x: torch.Tensor, expert: int = 0,
 
 
 def ref_gemv(x: torch.Tensor, indices: torch.Tensor, codebook: torch.Tensor, absmax: torch.Tensor,
-             block_size: int = 128, out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
-    """REF LUT-GEMV on the reference's raw tensors (cuda_lut_gemv.py:153-169)."""
+             block_size: int = 128, out_dtype: torch.dtype = torch.bfloat16,
+             dequantised: bool = False) -> torch.Tensor:
+    """REF LUT-GEMV on the reference's raw tensors: lut_gemv's (x * cb) * absmax products
+    (cuda_lut_gemv.py:153-169), or with ``dequantised`` the bf16(cb * absmax) weights of
+    fused_lut_gemv (fused_kernel.py:13-46)."""
     squeeze = x.dim() == 1
     x2 = x.unsqueeze(0) if squeeze else x
     _dev(x2, torch.bfloat16, "input")
@@ -152,11 +155,29 @@ def ref_gemv(x: torch.Tensor, indices: torch.Tensor, codebook: torch.Tensor, abs
         raise ValueError("codebook must have 256 entries")
     M, K = indices.shape
     y = torch.empty((x2.shape[0], M), dtype=out_dtype, device=x2.device)
-    N.check("lutmoe_ref_gemv",
-            N.lib().lutmoe_ref_gemv(x2.data_ptr(), indices.data_ptr(), codebook.data_ptr(),
-                                    absmax.data_ptr(), y.data_ptr(), M, K, x2.shape[0],
-                                    absmax.numel(), block_size, _out_code(out_dtype), _stream()))
+    fn = "lutmoe_fused_lut_gemv" if dequantised else "lutmoe_ref_gemv"
+    N.check(fn, getattr(N.lib(), fn)(x2.data_ptr(), indices.data_ptr(), codebook.data_ptr(),
+                                     absmax.data_ptr(), y.data_ptr(), M, K, x2.shape[0],
+                                     absmax.numel(), block_size, _out_code(out_dtype), _stream()))
     return y[0] if squeeze else y
+
+
+def router_logits(x: torch.Tensor, gate: torch.Tensor, round_bf16: bool = False,
+                  out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Router gate logits [T, E] fp32 = x [T, H] . gate [E, H]^T (bf16 inputs, fp32
+    accumulation; ``round_bf16`` rounds each logit to bf16 as a bf16 gate linear does)."""
+    _dev(x, torch.bfloat16, "x")
+    _dev(gate, torch.bfloat16, "gate")
+    T, H = x.shape
+    E = gate.shape[0]
+    if gate.shape[1] != H:
+        raise ValueError("gate must be [E, H]")
+    lg = torch.empty((T, E), dtype=torch.float32, device=x.device) if out is None else \
+        _dev(out, torch.float32, "out")
+    N.check("lutmoe_router_logits",
+            N.lib().lutmoe_router_logits(x.data_ptr(), gate.data_ptr(), T, H, E, lg.data_ptr(),
+                                         int(bool(round_bf16)), _stream()))
+    return lg
 
 
 # ---------------------------------------------------------------- routing

@@ -144,6 +144,14 @@ int lutmoe_ref_gemv(const void* x_dev, const void* indices_dev, const void* code
                     const void* absmax_dev, void* y_dev, int M, int K, int T,
                     int num_blocks, int block_size, int y_dtype, void* stream);
 
+/* fused_lut_gemv (vllm_lut/fused_kernel.py:13-46): the dequantised weights
+ * W = bf16(cb[idx] * absmax[min(i / block_size, num_blocks - 1)]) (i the
+ * flat row-major index) times each of the T vectors: y[T][M] (y_dtype) =
+ * x[T][K] . W^T with fp32 accumulation.  Arguments as lutmoe_ref_gemv. */
+int lutmoe_fused_lut_gemv(const void* x_dev, const void* indices_dev, const void* codebook_dev,
+                          const void* absmax_dev, void* y_dev, int M, int K, int T, int num_blocks,
+                          int block_size, int y_dtype, void* stream);
+
 /* CPU-side tier unpack of the reference, on the GPU (csrc/tensor_engine/
  * tensor_engine.cpp:535-548): 6-bit codes = low nibble | mid 2 bits << 4 from
  * the [low | mid] sections of `packed`, written to `out` (n bytes). */
@@ -184,9 +192,20 @@ int lutmoe_bl4_tables_from_f16(const uint16_t* f16_dev, uint16_t* bf16_dev, int6
 
 /* softmax(fp32 logits [T][E]) -> top-k (sorted descending, ties to the lower
  * id), optional renormalisation, times `scaling`; weights fp32 [T][k],
- * ids int32 [T][k] (vllm_lut/moe_layer.py:358-376). */
+ * ids int32 [T][k] (vllm_lut/moe_layer.py:358-376).  NaN logits are never
+ * selected; a round with only NaN left gives id -1 and weight 0.
+ * E <= 4096 (larger E: LUTMOE_EUNSUPPORTED). */
 int lutmoe_route_topk(const float* logits_dev, int T, int E, int k, int renormalize,
                       float scaling, float* topk_w_dev, int32_t* topk_ids_dev, void* stream);
+
+/* Router gate (MoEGate.forward, models/deepseek/modeling_deepseek.py:423-470;
+ * the bf16 gate linear of vllm_lut/moe_layer.py:301-304): logits[t][e] =
+ * x[t] . gate[e] over H with fp32 accumulation; round_bf16 != 0 rounds each
+ * logit to bf16 (the vLLM layer's logits dtype), stored as fp32.  x bf16
+ * [T][H], gate bf16 [E][H] (both 16-byte aligned, H % 8 == 0), logits fp32
+ * [T][E]; T <= 65535.  Sized for decode batches (one wave per logit). */
+int lutmoe_router_logits(const void* x_dev, const void* gate_dev, int T, int H, int E, float* logits_dev,
+                         int round_bf16, void* stream);
 
 /* Expert-major, pair-ascending permutation of the T*k (token, slot) pairs.
  * offsets int32 [E+1], perm int32 [T*k] (pair index t*k+slot at each

@@ -89,6 +89,20 @@ def test_validation_before_any_hip_call(lib):
     assert lib.lutmoe_route_topk(P(0x100), 4, 8, 9, 0, 1.0, P(0x100), P(0x100), None) == N.LUTMOE_EINVAL
     assert lib.lutmoe_route_topk(P(0x100), 4, 8, 0, 0, 1.0, P(0x100), P(0x100), None) == N.LUTMOE_EINVAL
     assert lib.lutmoe_permute(None, 4, 2, 8, P(1), P(1), P(1), P(1), None) == N.LUTMOE_EINVAL
+    # the general top-k kernel keeps one bit per held logit in 64 bits: E <= 4096
+    assert lib.lutmoe_route_topk(P(0x100), 4, 4097, 2, 0, 1.0, P(0x100), P(0x100), None) == N.LUTMOE_EUNSUPPORTED
+    assert lib.lutmoe_route_topk(P(0x100), 0, 4097, 2, 0, 1.0, P(0x100), P(0x100), None) == N.LUTMOE_EUNSUPPORTED
+    # router gate: H % 8, 16-byte alignment, pointers, T range
+    assert lib.lutmoe_router_logits(P(0x100), P(0x100), 2, 100, 8, P(0x100), 0, None) == N.LUTMOE_EINVAL
+    assert lib.lutmoe_router_logits(P(0x108), P(0x100), 2, 64, 8, P(0x100), 0, None) == N.LUTMOE_EALIGN
+    assert lib.lutmoe_router_logits(P(0x100), None, 2, 64, 8, P(0x100), 0, None) == N.LUTMOE_EINVAL
+    assert lib.lutmoe_router_logits(P(0x100), P(0x100), 70000, 64, 8, P(0x100), 0, None) == N.LUTMOE_EINVAL
+    assert lib.lutmoe_router_logits(None, None, 0, 64, 8, None, 0, None) == N.LUTMOE_OK
+    # fused_lut_gemv: the arguments of lutmoe_ref_gemv
+    assert lib.lutmoe_fused_lut_gemv(P(1), P(1), P(1), P(1), P(1), 0, 64, 1, 1, 128, 0, None) == N.LUTMOE_EINVAL
+    assert lib.lutmoe_fused_lut_gemv(P(1), P(1), P(1), P(1), P(1), 4, 64, 1, 1, 128, 5, None) == N.LUTMOE_EINVAL
+    assert lib.lutmoe_fused_lut_gemv(None, P(1), P(1), P(1), P(1), 4, 64, 1, 1, 128, 0, None) == N.LUTMOE_EINVAL
+    assert lib.lutmoe_fused_lut_gemv(P(1), P(1), P(1), P(1), P(1), 4, 64, 0, 1, 128, 0, None) == N.LUTMOE_OK
     # reference-compatible entry points
     assert lib.launch_blocklut_decompress(P(0x100), P(0x100), P(0x100), P(0x100), -1, 128, None) == -1
     assert lib.launch_blocklut_decompress(P(0x100), P(0x100), P(0x100), P(0x100), 16, 0, None) == -1

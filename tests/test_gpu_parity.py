@@ -311,6 +311,28 @@ def test_route_topk(gpu, T, E, k, renorm):
     np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=2e-6, atol=1e-7)
 
 
+@pytest.mark.parametrize("E", [40, 100])
+def test_route_topk_nan_rows(gpu, E):
+    """Rows with fewer finite logits than k: NaN is never selected, and a round with only
+    NaN left yields id -1 with weight 0, in the E <= 64 kernel and the general one alike."""
+    import torch
+    from block_lut_amd import ops
+    T, k = 3, 4
+    rng = np.random.default_rng(E)
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    lg[0, :] = np.nan
+    lg[0, [5, E - 1]] = [0.5, 2.0]          # two finite logits of four picks
+    lg[1, 3] = np.nan                       # a NaN among finite values
+    w, ids = ops.route_topk(torch.from_numpy(lg).to(gpu), k)
+    w, ids = w.cpu().numpy(), ids.cpu().numpy()
+    assert list(ids[0]) == [E - 1, 5, -1, -1]
+    assert np.all(w[0, 2:] == 0)      # (the softmax of a row holding NaN is NaN, as torch's)
+    fin = np.where(np.isnan(lg), -np.inf, lg)
+    for t in (1, 2):
+        assert list(ids[t]) == list(np.argsort(-fin[t], kind="stable")[:k])
+        assert 3 not in ids[1]
+
+
 @pytest.mark.parametrize("T,k,E", [(1, 4, 60), (32, 4, 60), (2048, 8, 66), (300, 2, 8), (1000, 3, 300),
                                    (10, 2, 600)])
 def test_permute(gpu, T, k, E):
