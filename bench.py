@@ -199,15 +199,36 @@ def main():
     log(f"[bench] building {a.layers} Qwen-shaped BL4 layers ({a.layers * c['E'] * expert_bytes(c) / 1e9:.1f} GB)")
     layers = [rand_layer(c) for _ in range(a.layers)]
     steps = [Step(L, c, T) for L in layers]
+    R = len(steps)
     g_step = graph_of([s.run for s in steps])
-    reps_w = max(1, -(-a.warmup // len(steps)))
-    reps = max(1, -(-a.steps // len(steps)))
-    K = reps * len(steps)
-    W = reps_w * len(steps)
-    time_graph(g_step, reps_w)
+    partial = {}
+
+    def run_steps(n):
+        """Exactly n layer steps in rotation order: whole rotations (one graph of all
+        layers) and a graph of the first n % R layers."""
+        full, rem = divmod(n, R)
+        for _ in range(full):
+            g_step.replay()
+        if rem:
+            if rem not in partial:
+                partial[rem] = graph_of([s.run for s in steps[:rem]])
+            partial[rem].replay()
+
+    K, W = max(1, a.steps), max(0, a.warmup)
+    if K % R and K % R not in partial:
+        partial[K % R] = graph_of([s.run for s in steps[:K % R]])
+    run_steps(W)
+    torch.cuda.synchronize()
     log(f"[bench] warmup {W} steps done; timing {K} steps")
-    secs = time_graph(g_step, reps)
-    bytes_total = reps * sum(s.bytes for s in steps)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    ev0.record()
+    run_steps(K)
+    ev1.record()
+    torch.cuda.synchronize()
+    secs = ev0.elapsed_time(ev1) / 1e3
+    full, rem = divmod(K, R)
+    bytes_total = full * sum(s.bytes for s in steps) + sum(s.bytes for s in steps[:rem])
     value_tbs = bytes_total / secs / 1e12
     ms_per_step = secs / K * 1e3
     us_per_token = ms_per_step * 1e3 / T
@@ -216,7 +237,7 @@ def main():
     # dominant kernel alone: gate/up + SwiGLU grouped LUT-GEMV
     g_gu = graph_of([lambda s=s: s.run(stages=N.STAGE_GATE_UP) for s in steps])
     time_graph(g_gu, 4)
-    r_gu = max(8, reps // 2)
+    r_gu = max(8, min(32, K // R))
     secs_gu = time_graph(g_gu, r_gu)
     dur_gu = secs_gu / (r_gu * len(steps))
     bytes_gu = sum(s.bytes_gate_up for s in steps) / len(steps)
@@ -280,7 +301,7 @@ def main():
             extra[f"decode_T{Tn}_avg_distinct_experts"] = round(sum(s.U for s in ss) / len(ss), 2)
             log(f"[bench] decode T={Tn}: {sec * 1e6:.1f} us/layer, {b / sec / 1e12:.3f} TB/s")
             del ss, g
-        del layers, steps, g_step, g_gu, g_dn, g_hot
+        del layers, steps, g_step, g_gu, g_dn, g_hot, partial
         torch.cuda.empty_cache()
         # DeepSeek-V2-Lite prefill, 2048 tokens, grouped MFMA GEMM
         d = DSV2
@@ -350,7 +371,7 @@ def main():
         y1 = torch.empty((1, 3072), dtype=torch.bfloat16, device=dev)
 
         def c1():
-            y1.copy_(ops.gemv(st1, x1))
+            ops.gemv(st1, x1, out=y1)
         g = graph_of([c1] * 32)
         time_graph(g, 2)
         sec = time_graph(g, 10) / (10 * 32)
@@ -451,6 +472,29 @@ def mixtral_stack(ops, torch, dev, rand_stack, MoEWeights, graph_of, time_graph)
     res["mixtral_prefill_T4096_TFLOPs"] = round(flops / sec / 1e12, 1)
     log(f"[bench] Mixtral prefill T=4096: {sec * 1e3:.2f} ms per {L} layers, {flops / sec / 1e12:.1f} TFLOP/s")
     del layers, x, lgs, out, ws, calls, g
+    torch.cuda.empty_cache()
+    # the dense bf16 ceiling on Mixtral's own shapes: [T*k, H] x [H, 2I] and [T*k, I] x [I, H]
+    P = T * k
+    fl = tsum = 0.0
+    for Kd, Nd in ((H, 2 * I), (I, H)):
+        a_ = torch.randn(P, Kd, device=dev).to(torch.bfloat16)
+        b_ = torch.randn(Kd, Nd, device=dev).to(torch.bfloat16)
+        o_ = torch.empty(P, Nd, dtype=torch.bfloat16, device=dev)
+        torch.mm(a_, b_, out=o_)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(10):
+            torch.mm(a_, b_, out=o_)
+        e1.record()
+        torch.cuda.synchronize()
+        tsum += e0.elapsed_time(e1) / 10 * 1e-3
+        fl += 2.0 * P * Kd * Nd
+        del a_, b_, o_
+    ceil = fl / tsum / 1e12
+    res["mixtral_ceiling_hipblaslt_bf16_TFLOPs"] = round(ceil, 1)
+    res["mixtral_prefill_T4096_frac_hipblaslt_ceiling"] = round(flops / sec / 1e12 / ceil, 4)
+    log(f"[bench] Mixtral-shape bf16 GEMM ceiling {ceil:.0f} TFLOP/s")
     return res
 
 
@@ -519,44 +563,72 @@ def nested_tiers(a, ops, N, torch, dev, NestedExpert, NestedStack, MoEWeights, g
     return out
 
 
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(a, c, T):
-    """The reference's CPU dequant + matmul path on a bounded sample of the
-    same workload (Qwen layer decode, T tokens, top-4 of 60 experts)."""
+    """The reference's CPU dequant + matmul path on a bounded sample of the same
+    workload (Qwen layer decode, T tokens, top-4 of 60 experts): 3 warm-up steps, then
+    the median of >= 20 timed steps, on all host cores and on one thread."""
+    import statistics
     import torch
     from oracle.cpu_baseline import moe_layer_step
     ncores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(ncores)
     g = torch.Generator().manual_seed(99)
     H, I, E, k = c["H"], c["I"], c["E"], c["k"]
+    t_gen = time.perf_counter()
     experts13, experts2 = {}, {}
-
-    def expert(e):
-        if e not in experts13:
-            experts13[e] = (torch.randint(0, 256, (2 * I, H // 2), dtype=torch.uint8, generator=g),
-                            torch.sort(torch.randn((2 * I, H // 64, 16), generator=g) * 0.02,
-                                       dim=-1).values.to(torch.bfloat16))
-            experts2[e] = (torch.randint(0, 256, (H, I // 2), dtype=torch.uint8, generator=g),
-                           torch.sort(torch.randn((H, I // 64, 16), generator=g) * 0.02,
-                                      dim=-1).values.to(torch.bfloat16))
-
-    steps, nbytes, t_total = 0, 0, 0.0
-    while t_total < a.cpu_seconds and steps < 1000:
+    for e in range(E):   # every expert once: the sample's steps route over all of them
+        experts13[e] = (torch.randint(0, 256, (2 * I, H // 2), dtype=torch.uint8, generator=g),
+                        torch.sort(torch.randn((2 * I, H // 64, 16), generator=g) * 0.02,
+                                   dim=-1).values.to(torch.bfloat16))
+        experts2[e] = (torch.randint(0, 256, (H, I // 2), dtype=torch.uint8, generator=g),
+                       torch.sort(torch.randn((H, I // 64, 16), generator=g) * 0.02,
+                                  dim=-1).values.to(torch.bfloat16))
+    t_gen = time.perf_counter() - t_gen
+    inputs = []
+    for _ in range(64):
         logits = torch.randn((T, E), generator=g)
         w, ids = torch.topk(torch.softmax(logits, -1), k, dim=-1)
-        for e in torch.unique(ids).tolist():
-            expert(e)
         x = torch.randn((T, H), generator=g).to(torch.bfloat16)
-        t0 = time.perf_counter()
-        moe_layer_step(x, ids, w, experts13, experts2)
-        t_total += time.perf_counter() - t0
-        nbytes += int(torch.unique(ids).numel()) * 3 * H * I * BYTES_PER_WEIGHT + 2 * T * H * 2
-        steps += 1
-    return {"value": round(nbytes / t_total / 1e12, 6), "unit": "TB/s", "cores": ncores,
-            "kind": "port",
-            "us_per_token": round(t_total / steps / T * 1e6, 1),
-            "sample": f"{steps} Qwen-shaped layer decode steps (T={T}, top-4 of 60 BL4 experts), "
-                      "torch CPU dequant gather + bf16 F.linear, "
-                      f"{t_total:.1f} s"}
+        nbytes = int(torch.unique(ids).numel()) * 3 * H * I * BYTES_PER_WEIGHT + 2 * T * H * 2
+        inputs.append((x, ids, w, nbytes))
+
+    def measure(threads, reps, warm=3):
+        torch.set_num_threads(threads)
+        for i in range(warm):
+            x, ids, w, _ = inputs[i]
+            moe_layer_step(x, ids, w, experts13, experts2)
+        times, by = [], []
+        for i in range(reps):
+            x, ids, w, nb = inputs[(warm + i) % len(inputs)]
+            t0 = time.perf_counter()
+            moe_layer_step(x, ids, w, experts13, experts2)
+            times.append(time.perf_counter() - t0)
+            by.append(nb)
+        med = statistics.median(times)
+        return med, statistics.median(by), sum(times)
+
+    med_all, by_all, tot_all = measure(ncores, 24)
+    med_one, by_one, tot_one = measure(1, 20)
+    torch.set_num_threads(ncores)
+    return {"value": round(by_all / med_all / 1e12, 6), "unit": "TB/s", "cores": ncores, "kind": "port",
+            "ms_per_step": round(med_all * 1e3, 3),
+            "us_per_token": round(med_all / T * 1e6, 1),
+            "one_thread": {"value": round(by_one / med_one / 1e12, 6), "unit": "TB/s",
+                           "ms_per_step": round(med_one * 1e3, 3)},
+            "cpu_model": cpu_model(),
+            "sample": f"Qwen-shaped layer decode steps (T={T}, top-4 of 60 BL4 experts), torch CPU "
+                      f"dequant gather + bf16 F.linear: median of 24 steps on {ncores} threads "
+                      f"({tot_all:.1f} s) and of 20 steps on 1 thread ({tot_one:.1f} s), each after "
+                      f"3 warm-up steps; weights generated beforehand ({t_gen:.1f} s, untimed)"}
 
 
 if __name__ == "__main__":

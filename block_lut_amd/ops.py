@@ -123,14 +123,19 @@ def blocklut_recover(indices: torch.Tensor, absmax: torch.Tensor, lut: torch.Ten
 # --------------------------------------------------------------------- GEMV
 
 def gemv(w: WeightStack, x: torch.Tensor, expert: int = 0,
-         out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
-    """y [T, M] = x [T, K] . W[expert]^T (fp32 accumulation)."""
+         out_dtype: torch.dtype = torch.bfloat16, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """y [T, M] = x [T, K] . W[expert]^T (fp32 accumulation); ``out`` (contiguous
+    [T, M], its dtype bf16 or fp32) receives the result without an allocation."""
     squeeze = x.dim() == 1
     x2 = x.unsqueeze(0) if squeeze else x
     _dev(x2, torch.bfloat16, "x")
     if x2.shape[1] != w.cols:
         raise ValueError(f"x has {x2.shape[1]} features, weights expect {w.cols}")
-    y = torch.empty((x2.shape[0], w.rows), dtype=out_dtype, device=x2.device)
+    if out is None:
+        y = torch.empty((x2.shape[0], w.rows), dtype=out_dtype, device=x2.device)
+    else:
+        y = _dev(out, out.dtype, "out").view(x2.shape[0], w.rows)
+        out_dtype = out.dtype
     d = w.desc()
     N.check("lutmoe_gemv", N.lib().lutmoe_gemv(ctypes.byref(d), expert, x2.data_ptr(), x2.shape[0],
                                                y.data_ptr(), _out_code(out_dtype), _stream()))

@@ -129,7 +129,7 @@ void lut_moe_launch_blocklut_recover(uint16_t* gpu_output_tensor,
  * section) become n one-byte codes. */
 void lut_moe_launch_unpack_4bit(uint8_t* gpu_data, size_t num_elements, void* tensor_stream);
 
-/* vllm_lut/cuda_lut_gemv.py:199-215 (launch_lut_gemv_kernel): fp32 codebook
+/* vllm_lut/cuda_lut_gemv.py:119-135 (launch_lut_gemv_kernel): fp32 codebook
  * [256], bf16 input [K], uint8 indices [M][K], bf16 absmax [num_blocks]
  * (128-element blocks), bf16 output [M]; default stream. */
 void launch_lut_gemv_kernel(const void* input, const void* indices, const void* codebook,
