@@ -125,6 +125,11 @@ def lib():
                 raise LutMoeNotBuilt(
                     f"{LIB_PATH} is missing: build it with `python -m block_lut_amd.csrc.build` "
                     "(there is no CPU fallback)")
+            # torch's HIP runtime first: its libamdhip64 carries the soname
+            # (libamdhip64.so.7) the library asks for, so both share one
+            # runtime.  Loaded the other way round, the process holds two HIP
+            # runtimes and device pointers of one are foreign to the other.
+            import torch  # noqa: F401
             h = ctypes.CDLL(LIB_PATH)
             for name, (res, args) in PROTOTYPES.items():
                 f = getattr(h, name)
@@ -137,6 +142,10 @@ def lib():
 def check(fn: str, rc: int) -> None:
     if rc != LUTMOE_OK:
         text = lib().lutmoe_strerror(rc).decode()
+        if rc == LUTMOE_EHIP:
+            detail = lib().lutmoe_last_error().decode()
+            if "HIP runtime error: " in detail:
+                text = detail[detail.index("HIP runtime error: "):]
         raise LutMoeError(fn, rc, text)
 
 

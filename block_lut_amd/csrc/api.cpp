@@ -14,9 +14,16 @@ namespace lutmoe_host {
 
 hipStream_t stream_of(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Per-thread text of the last failure (lutmoe_last_error).
+thread_local char g_last_error[256] = "";
+
+// A failed launch names its HIP error in the last-error text.
 int check_launch() {
     const hipError_t e = hipGetLastError();
-    return e == hipSuccess ? LUTMOE_OK : LUTMOE_EHIP;
+    if (e == hipSuccess) return LUTMOE_OK;
+    snprintf(g_last_error, sizeof(g_last_error), "HIP runtime error: %s (%s)", hipGetErrorName(e),
+             hipGetErrorString(e));
+    return LUTMOE_EHIP;
 }
 
 }  // namespace lutmoe_host
@@ -25,10 +32,14 @@ using namespace lutmoe_host;
 
 namespace {
 
-thread_local char g_last_error[256] = "";
-
 void set_last_error(const char* fn, int code) {
     if (code == LUTMOE_OK) { g_last_error[0] = 0; return; }
+    if (code == LUTMOE_EHIP && strncmp(g_last_error, "HIP runtime error: ", 19) == 0) {
+        char hip[256];
+        snprintf(hip, sizeof(hip), "%s", g_last_error);
+        snprintf(g_last_error, sizeof(g_last_error), "%s: %s", fn, hip);
+        return;
+    }
     snprintf(g_last_error, sizeof(g_last_error), "%s: %s", fn, lutmoe_strerror(code));
 }
 

@@ -97,7 +97,8 @@ const char* lutmoe_strerror(int code);
 const char* lutmoe_version(void);
 /* Last error text recorded on the calling thread by a void-returning
  * reference-compatible entry point or by lutmoe_moe_forward_noalloc ("" when
- * none). */
+ * none).  After any entry point returns LUTMOE_EHIP it names the HIP error
+ * ("HIP runtime error: hipErrorName (description)"). */
 const char* lutmoe_last_error(void);
 
 /* ---- reference-compatible entry points --------------------------------
