@@ -96,6 +96,7 @@ PROTOTYPES = {
     "lutmoe_merge_bitplane": (I32, [P, P, I64, I32, P]),
     "lutmoe_kmeans_1d": (I32, [P, I64, P, I32, I32, P, P]),
     "lutmoe_pack_bitplanes": (I32, [P, I64, P, P]),
+    "lutmoe_nested_group_planes": (I32, [P, I32, I64, P, P]),
     "lutmoe_dequant": (I32, [WP, I32, I32, P, P]),
     "lutmoe_gemv": (I32, [WP, I32, P, I32, P, I32, P]),
     "lutmoe_bl4_tables_from_f16": (I32, [P, P, I64, P]),

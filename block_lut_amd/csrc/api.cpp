@@ -259,6 +259,14 @@ int lutmoe_unpack_6bit(const uint8_t* packed, uint8_t* out, int64_t n, void* str
     return launch_unpack_6bit(packed, out, n, stream_of(stream));
 }
 
+int lutmoe_nested_group_planes(const uint8_t* planes, int bits, int64_t n, uint8_t* out, void* stream) {
+    if (n < 0 || (n % 64) || bits < 2 || bits > 4) return LUTMOE_EINVAL;
+    if (n == 0) return LUTMOE_OK;
+    if (!planes || !out) return LUTMOE_EINVAL;
+    if (!aligned(planes, 4) || !aligned(out, 4)) return LUTMOE_EALIGN;
+    return launch_nested_group_planes(planes, bits, n, out, stream_of(stream));
+}
+
 // ---------------------------------------------------------------- generic
 
 int lutmoe_dequant(const lutmoe_weights* w, int e0, int ne, void* out, void* stream) {

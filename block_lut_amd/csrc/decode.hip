@@ -645,9 +645,11 @@ __device__ __forceinline__ void bl4_rows8(const uint8_t* __restrict__ codes, con
 }
 
 // ---- NestedLUT experts (NestedView, lut_core.h).
-// The lane's 32 columns [2048cc + 32l, +32) of 8 rows: 8 bytes of p01, 4 of
-// p2, 4 of p3 per row, and 16 bytes of the row's tables starting at this
-// lane's share of its block's table (2^b bytes: entries 2^(b-1)*(l%2) ..).
+// The lane's 32 columns [2048cc + 32l, +32) of 8 rows: one 32-weight group
+// of the device layout per row (8 bytes of 2-bit fields, 4 of bit 2, 4 of
+// bit 3: the tier's 4b bytes, one load), and 16 bytes of the row's tables
+// starting at this lane's share of its block's table (2^b bytes: entries
+// 2^(b-1)*(l%2) ..).
 struct Rows8N {
     uint32_t f01[kRows][2], f2[kRows], f3[kRows];
     u32x4_t tw[kRows];
@@ -661,14 +663,26 @@ __device__ __forceinline__ void load_rows8n(const NestedView& v, const int (&row
 #pragma unroll
     for (int r = 0; r < kRows; ++r) {
         const uint32_t i0 = (uint32_t)rows[r] * (uint32_t)K + c0;
-        const auto q = __builtin_amdgcn_raw_buffer_load_b64(v.planes, (int)(i0 / 4), 0, 0);
-        b.f01[r][0] = q[0];
-        b.f01[r][1] = q[1];
-        // the tier's planes only (uniform branches: a 2-bit expert issues two
-        // loads per row instead of four)
-        // the tier's planes only (a 2-bit expert issues two loads per row, not four)
-        b.f2[r] = kBits >= 3 ? __builtin_amdgcn_raw_buffer_load_b32(v.planes, (int)(v.p2_off + i0 / 8), 0, 0) : 0u;
-        b.f3[r] = kBits >= 4 ? __builtin_amdgcn_raw_buffer_load_b32(v.planes, (int)(v.p3_off + i0 / 8), 0, 0) : 0u;
+        const int go = (int)(i0 / 32 * (4 * kBits));   // the group's bytes: the tier's only
+        if constexpr (kBits == 4) {
+            const auto q = __builtin_amdgcn_raw_buffer_load_b128(v.codes, go, 0, 0);
+            b.f01[r][0] = q[0];
+            b.f01[r][1] = q[1];
+            b.f2[r] = q[2];
+            b.f3[r] = q[3];
+        } else if constexpr (kBits == 3) {
+            const auto q = __builtin_amdgcn_raw_buffer_load_b96(v.codes, go, 0, 0);
+            b.f01[r][0] = q[0];
+            b.f01[r][1] = q[1];
+            b.f2[r] = q[2];
+            b.f3[r] = 0u;
+        } else {
+            const auto q = __builtin_amdgcn_raw_buffer_load_b64(v.codes, go, 0, 0);
+            b.f01[r][0] = q[0];
+            b.f01[r][1] = q[1];
+            b.f2[r] = 0u;
+            b.f3[r] = 0u;
+        }
         const uint32_t tofs = ((i0 >> 6) << (v.bits + 1)) + ((uint32_t)(lane & 1) << v.bits);
         b.tw[r] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(v.table, (int)tofs, 0, 0));
     }

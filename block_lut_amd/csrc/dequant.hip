@@ -99,23 +99,22 @@ __global__ __launch_bounds__(256) void bl4_dequant_kernel(
     dst[3] = make_uint4(o[12], o[13], o[14], o[15]);
 }
 
-// Nested: thread handles 32 consecutive weights (half a 64-block).
+// Nested: thread handles one 32-weight group of the device layout (half a
+// 64-block): 4b code bytes.
 __global__ __launch_bounds__(256) void nested_dequant_kernel(
     uint16_t* __restrict__ out, const uint8_t* const* __restrict__ code_ptrs,
     const uint16_t* const* __restrict__ table_ptrs, const int8_t* __restrict__ bits,
     int e0, int64_t n_per_expert) {
     const int e = e0 + blockIdx.y;
     const int b = bits[e];
-    const uint8_t* p01 = code_ptrs[e];
-    const uint8_t* p2 = p01 + n_per_expert / 4;
-    const uint8_t* p3 = p2 + n_per_expert / 8;
     const uint16_t* tab = table_ptrs[e];
-    const int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 32;
+    const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t i0 = g * 32;
     if (i0 >= n_per_expert) return;
-    const uint2 q01 = *reinterpret_cast<const uint2*>(p01 + i0 / 4);
-    const uint64_t f01 = (uint64_t)q01.x | ((uint64_t)q01.y << 32);
-    const uint32_t f2 = b >= 3 ? *reinterpret_cast<const uint32_t*>(p2 + i0 / 8) : 0u;
-    const uint32_t f3 = b >= 4 ? *reinterpret_cast<const uint32_t*>(p3 + i0 / 8) : 0u;
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(code_ptrs[e] + g * 4 * b);
+    const uint64_t f01 = (uint64_t)q[0] | ((uint64_t)q[1] << 32);
+    const uint32_t f2 = b >= 3 ? q[2] : 0u;
+    const uint32_t f3 = b >= 4 ? q[3] : 0u;
     const uint16_t* t = tab + (i0 / kBlockBL) * (1 << b);
     uint32_t o[16];
 #pragma unroll
@@ -127,7 +126,23 @@ __global__ __launch_bounds__(256) void nested_dequant_kernel(
     }
     uint4* dst = reinterpret_cast<uint4*>(out + (int64_t)blockIdx.y * n_per_expert + i0);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) dst[q] = make_uint4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]);
+    for (int q4 = 0; q4 < 4; ++q4) dst[q4] = make_uint4(o[4 * q4], o[4 * q4 + 1], o[4 * q4 + 2], o[4 * q4 + 3]);
+}
+
+// NestedLUT plane sections [p01 n/4 | p2 n/8 | p3 n/8] (the tier's prefix)
+// -> the device layout: group g (weights 32g .. 32g+31) = p01 bytes 8g..8g+7,
+// then p2 bytes 4g..4g+3 (b >= 3), then p3 bytes 4g..4g+3 (b = 4).  One
+// thread per group, dword copies (n % 64 == 0 keeps every section and
+// group 4-byte aligned).
+__global__ __launch_bounds__(256) void nested_group_planes_kernel(const uint32_t* __restrict__ planes, int b,
+                                                                  int64_t n, uint32_t* __restrict__ out) {
+    const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (g * 32 >= n) return;
+    uint32_t* o = out + g * b;
+    o[0] = planes[2 * g];
+    o[1] = planes[2 * g + 1];
+    if (b >= 3) o[2] = planes[n / 16 + g];
+    if (b >= 4) o[3] = planes[n / 16 + n / 32 + g];
 }
 
 __global__ __launch_bounds__(256) void f16_to_bf16_kernel(const uint16_t* __restrict__ in,
@@ -305,6 +320,12 @@ int launch_bl4_dequant(uint16_t* out, const uint8_t* codes, const uint16_t* tabl
                        int64_t nblocks, hipStream_t s) {
     hipLaunchKernelGGL(bl4_dequant_kernel, dim3(grid1(nblocks, 128)), dim3(256), 0, s, out,
                        codes, tables, nblocks);
+    return check_launch();
+}
+
+int launch_nested_group_planes(const uint8_t* planes, int bits, int64_t n, uint8_t* out, hipStream_t s) {
+    hipLaunchKernelGGL(nested_group_planes_kernel, dim3(grid1(n / 32, 256)), dim3(256), 0, s,
+                       (const uint32_t*)planes, bits, n, (uint32_t*)out);
     return check_launch();
 }
 

@@ -174,9 +174,11 @@ struct BStep<LUTMOE_FMT_REF> {
     }
 };
 
-// NestedLUT: the lane's 32 columns of each row from the bit planes, and the
-// first 32 bytes of the row's block-kb table (the first 2^(b+1) are the
-// tier's entries; codes never reach the rest).
+// NestedLUT: the lane's 32 columns of each row (one 32-weight group of the
+// device layout; a 16-byte load that, below tier 4, also reads the next
+// group's bytes, dropped here), and the first 32 bytes of the row's block-kb
+// table (the first 2^(b+1) are the tier's entries; codes never reach the
+// rest).
 template <>
 struct BStep<LUTMOE_FMT_NESTED> {
     uint32_t f01[2][2], f2[2], f3[2];
@@ -186,11 +188,11 @@ struct BStep<LUTMOE_FMT_NESTED> {
         for (int nt = 0; nt < 2; ++nt) {
             const uint32_t blk0 = (uint32_t)row[nt] * (uint32_t)K + (uint32_t)kb * kBK;
             const uint32_t i0 = blk0 + 32u * bh;
-            const auto q = __builtin_amdgcn_raw_buffer_load_b64(v.planes, (int)(i0 / 4), 0, 0);
+            const auto q = __builtin_amdgcn_raw_buffer_load_b128(v.codes, (int)(i0 / 32 * (4u * v.bits)), 0, 0);
             f01[nt][0] = q[0];
             f01[nt][1] = q[1];
-            f2[nt] = __builtin_amdgcn_raw_buffer_load_b32(v.planes, (int)(v.p2_off + i0 / 8), 0, 0);
-            f3[nt] = __builtin_amdgcn_raw_buffer_load_b32(v.planes, (int)(v.p3_off + i0 / 8), 0, 0);
+            f2[nt] = v.bits >= 3 ? q[2] : 0u;
+            f3[nt] = v.bits >= 4 ? q[3] : 0u;
             const uint32_t tofs = (blk0 >> 6) << (v.bits + 1);
             tab[nt][0] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(v.table, (int)tofs, 0, 0));
             tab[nt][1] =
@@ -402,9 +404,10 @@ __device__ __forceinline__ void prefill_tile(const lutmoe_moe_desc& d, const uin
 //   codes  [256 rows] x 32 B             ( 8 KB; bytes 16h.. = columns 32h..32h+31)
 //   tables [256 rows] x 32 B             ( 8 KB; the rows' bf16[16] tables)
 // Each load instruction reads whole 128-byte lines (8 lanes per A row, 2 lanes
-// per 32-byte weight-row segment; NestedLUT rows take 8 lanes of 4 bytes).
-// Only the tile's NMT*32 activation rows are loaded.  Every thread issues the
-// same kDma loads per stage (NMT + 4 for BL4, NMT + 16 for NestedLUT), so
+// per 32-byte weight-row segment; NestedLUT tiers below 4 bits pack their
+// shorter rows densely, see prefill_tile_ring).  Only the tile's NMT*32
+// activation rows are loaded.  Every thread issues the same kDma loads per
+// stage (NMT + 4 for BL4 and NestedLUT, NMT + 5 for REF), so
 // `s_waitcnt vmcnt(kDma)` means "all but the newest stage have landed".  Per step kb: k-substeps 0-2 run from slot kb%3; then a barrier
 // (stage kb+1 landed everywhere, slot kb%3 no longer read), the refill of slot
 // kb%3 with stage kb+3, and k-substep 3's MFMAs overlapped with reading and
@@ -511,7 +514,7 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
     constexpr int kNC = kRef ? 4 : 2;   // code registers (u32x4) per lane per K step
     // ring loads per thread per stage: the tile's NMT activation loads (only
     // its NMT*32 rows are loaded) and the weight loads
-    constexpr int kDma = NMT + (kNested ? 16 : kRef ? 5 : 4);
+    constexpr int kDma = NMT + (kRef ? 5 : 4);
     const lutmoe_weights& w = d.w13;
     const lutmoe_weights& w2 = d.w2;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -558,14 +561,20 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
     const uint8_t* a_base = (const uint8_t*)src;
     // BL4 codes / tables: load h of wave w covers tile rows 64w+32h .. +31,
     // two lanes per row (16 B each), so a row's 32 bytes land contiguous in
-    // LDS.  NestedLUT: load j of wave w covers tile rows 64w+8j .. +7, eight
-    // lanes (4 B each) per row: codes region = [p01 16 B | p2 8 B | p3 8 B],
-    // tables region = the tier's 2^b entries (repeated up to 32 B).  Lanes of
-    // a plane the tier does not have re-read p01 bytes (masked off when the
-    // codes are rebuilt).
+    // LDS.  NestedLUT tier b: a row's K step is 8b code bytes (its two
+    // 32-weight groups) and 2^(b+1) table bytes, both contiguous in HBM:
+    //   codes  b=4: as BL4 (LDS row stride 32, groups at 0 and 16); b=3: as
+    //          BL4 with the second lane reading bytes 8..23, so the groups
+    //          land at 0 and 20 of the 32-byte LDS row and nothing past the
+    //          row's bytes is read; b=2: load 0 covers rows 64w .. +63, one
+    //          lane (16 B) per row (LDS row stride 16), load 1 repeats it
+    //   tables b=4: as BL4; b=3: load 0 covers rows 64w .. +63, one lane
+    //          (16 B) per row, load 1 repeats it; b=2: as BL4 with 4-byte
+    //          loads (LDS row stride 2^(b+1))
+    // so every tier issues four weight loads per stage.
     const uint8_t* c_base;
     const uint8_t* t_base;
-    uint32_t w_off[kNested ? 16 : kRef ? 4 : 2];
+    uint32_t w_off[kRef || kNested ? 4 : 2];
     uint32_t c_step = 32, t_step = 32;
     int bits = 4;
     // REF: absmax block of K step kb of weight row r = min((r*K/64 + kb) / q, nb - 1)
@@ -588,21 +597,15 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
         c_base = uniform_ptr(((const uint8_t* const*)ww.codes)[ti.e]);
         t_base = uniform_ptr((const uint8_t*)((const uint16_t* const*)ww.tables)[ti.e]);
         bits = __builtin_amdgcn_readfirstlane((int)ww.tier_bits[ti.e]);
-        const uint32_t n = (uint32_t)ww.rows * (uint32_t)ww.cols;
-        const int q = lane & 7;
-        const bool has_p = q < 4 || (q < 6 ? bits >= 3 : bits >= 4);
-        c_step = has_p && q >= 4 ? 8u : 16u;
-        t_step = 2u << bits;
+        c_step = 8u * (uint32_t)bits;     // code bytes of a row's K step
+        t_step = 2u << bits;              // table bytes of a row's K step
+        const uint32_t kq = (uint32_t)(K / 64);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const uint32_t fb = (uint32_t)tile_row(64 * wv + 8 * j + (lane >> 3)) * (uint32_t)K;
-            uint32_t co;
-            if (!has_p) co = fb / 4 + 4u * (uint32_t)(q & 3);
-            else if (q < 4) co = fb / 4 + 4u * (uint32_t)q;
-            else if (q < 6) co = n / 4 + fb / 8 + 4u * (uint32_t)(q - 4);
-            else co = n / 4 + n / 8 + fb / 8 + 4u * (uint32_t)(q - 6);
-            w_off[j] = co;
-            w_off[8 + j] = (fb / 64) * t_step + 4u * (uint32_t)(q & ((1 << (bits - 1)) - 1));
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t pr = (uint32_t)tile_row(64 * wv + 32 * h + (lane >> 1)) * kq;   // lane pairs
+            const uint32_t sr = (uint32_t)tile_row(64 * wv + lane) * kq;                   // one lane per row
+            w_off[h] = bits == 2 ? sr * 16u : pr * c_step + (uint32_t)(lane & 1) * (bits == 4 ? 16u : 8u);
+            w_off[2 + h] = bits == 3 ? sr * 16u : pr * t_step + (uint32_t)(lane & 1) * (t_step / 2u);
         }
     } else {
         const int64_t per = (int64_t)ww.rows * (ww.cols / 2);
@@ -627,10 +630,28 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
             dma4((idx & ~1u) * 2u, t_base, l0 + kSlotA + kCodesB + 256 * wvu);
         } else if constexpr (kNested) {
             const uint32_t cs = (uint32_t)kb * c_step, ts = (uint32_t)kb * t_step;
+            const uint32_t tl = l0 + kSlotA + kCodesB + (uint32_t)wvu * 64u * t_step;
+            if (bits == 4) {
+                const uint32_t cl = l0 + kSlotA + (uint32_t)wvu * 2048u;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                dma4(w_off[j] + cs, c_base, l0 + kSlotA + (64 * wvu + 8 * j) * 32);
-                dma4(w_off[8 + j] + ts, t_base, l0 + kSlotA + kCodesB + (64 * wvu + 8 * j) * 32);
+                for (int h = 0; h < 2; ++h) {
+                    dma16(w_off[h] + cs, c_base, cl + h * 1024);
+                    dma16(w_off[2 + h] + ts, t_base, tl + h * 1024);
+                }
+            } else if (bits == 3) {
+                const uint32_t cl = l0 + kSlotA + (uint32_t)wvu * 2048u;
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    dma16(w_off[h] + cs, c_base, cl + h * 1024);
+                    dma16(w_off[2 + h] + ts, t_base, tl);
+                }
+            } else {
+                const uint32_t cl = l0 + kSlotA + (uint32_t)wvu * 1024u;
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    dma16(w_off[h] + cs, c_base, cl);
+                    dma4(w_off[2 + h] + ts, t_base, tl + h * 256);
+                }
             }
         } else {
             const uint8_t* cb = c_base + kb * 32;
@@ -649,12 +670,24 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
     const int L1 = kGateUp ? 128 + 32 * wv + bn : 64 * wv + 32 + bn;
 
     // BL4: codes[nt] = the lane's 16 code bytes of row Lnt.  NestedLUT:
-    // codes[nt] = dword bh of p01 (as .x) and of p01's second half (.y), p2 and
-    // p3 bytes of this lane half (.z, .w): see nested_code below.
+    // codes[nt] = the lane half's 32-weight group: its 2-bit fields (.x, .y),
+    // bit-2 and bit-3 planes (.z, .w; zero for tiers without them): see
+    // nested_code below.
     // REF: codes[2nt], codes[2nt+1] = the lane's 32 code bytes of row Lnt; am[nt]
     // = that row's absmax for K step kb (the aligned dword holds it in the
     // half its index parity selects)
     uint32_t row64[2] = {0u, 0u};
+    // NestedLUT: LDS offsets of the lane half's code group and of the rows'
+    // tables within the slot's code / table regions
+    uint32_t c_grp[2] = {0u, 0u}, t_row[2] = {(uint32_t)L0 * 32u, (uint32_t)L1 * 32u};
+    if constexpr (kNested) {
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            const uint32_t L = (uint32_t)(nt ? L1 : L0);
+            c_grp[nt] = bits == 2 ? L * 16u + (uint32_t)bh * 8u : L * 32u + (uint32_t)bh * (bits == 4 ? 16u : 20u);
+            t_row[nt] = L * t_step;
+        }
+    }
     if constexpr (kRef) {
         row64[0] = (uint32_t)tile_row(L0) * (uint32_t)(K / 64);
         row64[1] = (uint32_t)tile_row(L1) * (uint32_t)(K / 64);
@@ -678,13 +711,12 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
                 codes[2 * nt + 1] = *reinterpret_cast<const u32x4_t*>(rb + 16);
             }
         } else if constexpr (kNested) {
+            // dword reads (a tier-3 group is only 4-byte aligned); the words
+            // past the tier's group are other bytes and are dropped
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) {
-                const uint8_t* rb = sl + kSlotA + (nt ? L1 : L0) * 32;
-                const uint2 f = *reinterpret_cast<const uint2*>(rb + 8 * bh);        // p01 bytes 8bh..
-                const uint32_t f2 = *reinterpret_cast<const uint32_t*>(rb + 16 + 4 * bh);
-                const uint32_t f3 = *reinterpret_cast<const uint32_t*>(rb + 24 + 4 * bh);
-                codes[nt] = u32x4_t{f.x, f.y, bits >= 3 ? f2 : 0u, bits >= 4 ? f3 : 0u};
+                const uint32_t* g = reinterpret_cast<const uint32_t*>(sl + kSlotA + c_grp[nt]);
+                codes[nt] = u32x4_t{g[0], g[1], bits >= 3 ? g[2] : 0u, bits >= 4 ? g[3] : 0u};
             }
         } else {
             const uint8_t* cb = sl + kSlotA + bh * 16;
@@ -718,7 +750,7 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
             return lookup8_ref_issue(c[2 * (ks & 1)], c[2 * (ks & 1) + 1], lds_addr(ring + kStages * kSlot));
         } else {
             const uint32_t tbase = lds_addr(sl + kSlotA + kCodesB);
-            return lookup8_issue(nested_code(codes[nt], ks), tbase + (nt ? L1 : L0) * 32);
+            return lookup8_issue(nested_code(codes[nt], ks), tbase + t_row[nt]);
         }
     };
     // looked-up entries -> bf16x8 B fragment (REF: times the row's absmax,

@@ -19,6 +19,7 @@ int launch_bl4_dequant(uint16_t* out, const uint8_t* codes, const uint16_t* tabl
                        int64_t nblocks, hipStream_t s);
 int launch_nested_dequant(uint16_t* out, const lutmoe_weights* w, int e0, int ne,
                           hipStream_t s);
+int launch_nested_group_planes(const uint8_t* planes, int bits, int64_t n, uint8_t* out, hipStream_t s);
 int launch_f16_to_bf16(const uint16_t* in, uint16_t* out, int64_t n, hipStream_t s);
 int launch_unpack_4bit_inplace(uint8_t* data, int64_t n, hipStream_t s);
 int launch_unpack_6bit(const uint8_t* packed, uint8_t* out, int64_t n, hipStream_t s);

@@ -129,29 +129,28 @@ __device__ __forceinline__ u32x4_t lookup8_lds(uint32_t w, uint32_t tab) {
     return lookup8_combine(lookup8_issue(w, tab));
 }
 
-// A NestedLUT expert: bit-plane sections [p01 n/4 | p2 n/8 | p3 n/8] (p2
-// from tier 3 on, p3 from tier 4 on; n = rows*K) and bf16 tables
-// [rows][K/64][2^b], read through bounds-checked buffer descriptors: a tier's
-// missing plane sections and any table bytes past the end read as zero.
+// A NestedLUT expert in the device layout: the tier-b plane bytes of each 32
+// consecutive weights (flat row-major [rows][K] order) kept together, 4b
+// bytes per group: 8 bytes of 2-bit fields (weight j at bits 2j..2j+1 of the
+// little-endian 64-bit word), then 4 bytes of bit 2 (b >= 3) and 4 bytes of
+// bit 3 (b = 4), weight j at bit j.  Tables bf16 [rows][K/64][2^b].  Both are
+// read through bounds-checked buffer descriptors (bytes past the end read as
+// zero).
 constexpr int kBufWord3 = 0x00020000;   // raw buffer, dword format (gfx9)
 
 struct NestedView {
-    __amdgpu_buffer_rsrc_t planes, table;
-    uint32_t p2_off, p3_off;   // byte offsets of the p2 / p3 sections
+    __amdgpu_buffer_rsrc_t codes, table;
     int bits;
 };
 
 __device__ __forceinline__ NestedView nested_view(const lutmoe_weights& w, int e) {
-    const uint8_t* pl = ((const uint8_t* const*)w.codes)[e];
+    const uint8_t* cd = ((const uint8_t* const*)w.codes)[e];
     const uint16_t* tb = ((const uint16_t* const*)w.tables)[e];
     const int b = __builtin_amdgcn_readfirstlane((int)w.tier_bits[e]);   // uniform: scalar branches on it
     const uint32_t n = (uint32_t)w.rows * (uint32_t)w.cols;   // < 2^32 (checked on the host)
     NestedView v;
-    v.planes = __builtin_amdgcn_make_buffer_rsrc((void*)pl, 0, (int)(n / 4 + (b >= 3 ? n / 8 : 0) + (b >= 4 ? n / 8 : 0)),
-                                                 kBufWord3);
+    v.codes = __builtin_amdgcn_make_buffer_rsrc((void*)cd, 0, (int)(n / 8 * (uint32_t)b), kBufWord3);
     v.table = __builtin_amdgcn_make_buffer_rsrc((void*)tb, 0, (int)(((n / 64) << b) * 2), kBufWord3);
-    v.p2_off = n / 4;
-    v.p3_off = n / 4 + n / 8;
     v.bits = b;
     return v;
 }

@@ -152,11 +152,17 @@ class NestedExpert:
 
 
 class NestedStack(WeightStack):
-    """Per-expert NestedLUT tiers (2/3/4 bits)."""
+    """Per-expert NestedLUT tiers (2/3/4 bits).
+
+    The experts arrive as stored: bit-plane sections, a tier's prefix of
+    [p01 | p2 | p3].  On construction each expert's planes are regrouped on
+    the device (lutmoe_nested_group_planes: the planes of every 32 weights
+    together, M*K*b/8 bytes), the layout every kernel reads.  keep_planes=False
+    drops the stack's references to the plane tensors afterwards."""
 
     format = N.FMT_NESTED
 
-    def __init__(self, experts: List[NestedExpert], rows: int, cols: int):
+    def __init__(self, experts: List[NestedExpert], rows: int, cols: int, keep_planes: bool = True):
         if cols % 64:
             raise ValueError("NestedLUT needs K % 64 == 0")
         self.experts = experts
@@ -173,7 +179,16 @@ class NestedStack(WeightStack):
             if tuple(e.table.shape) != (rows, cols // 64, 1 << e.bits):
                 raise ValueError(f"expert {i}: table shape {tuple(e.table.shape)}")
         dev = experts[0].planes.device
-        self._code_ptrs = torch.tensor([e.planes.data_ptr() for e in experts], dtype=torch.int64,
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        self.codes = []
+        for e in experts:
+            g = torch.empty(n * e.bits // 8, dtype=torch.uint8, device=dev)
+            N.check("lutmoe_nested_group_planes",
+                    N.lib().lutmoe_nested_group_planes(e.planes.data_ptr(), e.bits, n, g.data_ptr(), stream))
+            self.codes.append(g)
+        if not keep_planes:
+            self.experts = [NestedExpert(e.bits, None, e.table) for e in experts]
+        self._code_ptrs = torch.tensor([g.data_ptr() for g in self.codes], dtype=torch.int64,
                                        device=dev)
         self._table_ptrs = torch.tensor([e.table.data_ptr() for e in experts], dtype=torch.int64,
                                         device=dev)

@@ -346,7 +346,7 @@ def _any_tensor(w: WeightStack) -> torch.Tensor:
         t = getattr(w, name, None)
         if isinstance(t, torch.Tensor):
             return t
-    return w.experts[0].planes  # NestedStack
+    return w.codes[0]  # NestedStack
 
 
 # ------------------------------------------------------- torch.library ops

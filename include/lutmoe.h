@@ -17,9 +17,14 @@
  *   BL4  : codes uint8 [E][M][K/2] (two 4-bit codes per byte, even element in
  *          the low nibble), tables bf16 [E][M][K/64][16] (the dequantised
  *          entries; lutmoe_bl4_tables_from_f16 converts the fp16 codebooks).
- *   NL   : NestedLUT tier b in {2,3,4} per expert: codes are bit-plane
- *          sections [p01 M*K/4 | p2 M*K/8 | p3 M*K/8] (a tier-b expert holds
- *          the first 2, 3 or all sections), tables bf16 [M][K/64][2^b].
+ *   NL   : NestedLUT tier b in {2,3,4} per expert.  Stored (and loaded
+ *          progressively) as bit-plane sections [p01 M*K/4 | p2 M*K/8 |
+ *          p3 M*K/8] (a tier-b expert holds the first 2, 3 or all sections);
+ *          on the device the codes are grouped: for each 32 consecutive
+ *          weights of the flat row-major [M][K] order, their 8 bytes of p01,
+ *          then 4 of p2 (b >= 3), then 4 of p3 (b = 4) -- 4b bytes per group,
+ *          M*K*b/8 per expert (lutmoe_nested_group_planes converts).  Tables
+ *          bf16 [M][K/64][2^b].
  */
 #ifndef LUTMOE_H
 #define LUTMOE_H
@@ -56,7 +61,7 @@ typedef struct lutmoe_weights {
     int32_t cols;              /* K                                              */
     const void* codes;         /* REF/BL4: device base of [E] code arrays.
                                   NL: device array of E pointers (uint8_t*) to
-                                  each expert's bit-plane sections.              */
+                                  each expert's grouped codes (M*K*b/8 bytes).   */
     const void* tables;        /* REF: bf16 absmax [E][absmax_per_expert].
                                   BL4: bf16 tables [E][M][K/64][16].
                                   NL: device array of E pointers (uint16_t*) to
@@ -164,6 +169,16 @@ int lutmoe_unpack_6bit(const uint8_t* packed_dev, uint8_t* out_dev, int64_t n, v
  * bits 4-5 n/4 | bits 6-7 n/4]; low byte i = code 2i | code 2i+1 << 4, mid /
  * high byte i holds code 4i+k in bits 2k..2k+1.  n % 4 == 0. */
 int lutmoe_pack_bitplanes(const uint8_t* codes_dev, int64_t n, uint8_t* packed_dev, void* stream);
+
+/* NestedLUT plane sections of one tier-b expert (planes_dev: the tier's
+ * prefix of [p01 n/4 | p2 n/8 | p3 n/8]) -> its device codes out_dev
+ * (n*b/8 bytes): group g = p01 bytes 8g..8g+7, then p2 bytes 4g..4g+3
+ * (b >= 3), then p3 bytes 4g..4g+3 (b = 4).  n = M*K weights, n % 64 == 0;
+ * both pointers 4-byte aligned.  No counterpart in the reference, whose
+ * 4/6/8-bit sections are merged into byte codes on load
+ * (csrc/tensor_engine/tensor_engine.cpp:535-548): the grouped order lets a
+ * kernel read a weight group's planes in one load. */
+int lutmoe_nested_group_planes(const uint8_t* planes_dev, int bits, int64_t n, uint8_t* out_dev, void* stream);
 
 /* Progressive tier upgrade of resident codes (the reference reloads the whole
  * expert on a promotion, csrc/topology/model_topology.cpp:74-80, reading

@@ -482,6 +482,31 @@ def nested_planes_split(buf, bits: int, M: int, K: int) -> dict:
     return pl
 
 
+def nested_group_planes(buf, bits: int, M: int, K: int) -> np.ndarray:
+    """The device order of one expert's codes (this library's own layout, no reference
+    counterpart): the plane sections of nested_planes_split regrouped so that each 32
+    consecutive weights of the flat row-major order keep their bytes together -- 8 bytes of
+    p01, then 4 of p2 (b >= 3), then 4 of p3 (b = 4); 4b bytes per group."""
+    pl = nested_planes_split(buf, bits, M, K)
+    g = M * K // 32
+    parts = [np.asarray(pl["p01"], np.uint8).reshape(g, 8)]
+    for name, bit in (("p2", 2), ("p3", 3)):
+        if bits > bit:
+            parts.append(np.asarray(pl[name], np.uint8).reshape(g, 4))
+    return np.ascontiguousarray(np.concatenate(parts, axis=1).reshape(-1))
+
+
+def nested_ungroup(grouped, bits: int, M: int, K: int) -> dict:
+    """Inverse of nested_group_planes: the section dict of nested_pack_planes."""
+    g = np.asarray(grouped, np.uint8).reshape(M * K // 32, 4 * bits)
+    pl = {"p01": np.ascontiguousarray(g[:, 0:8]).reshape(M, K // 4)}
+    if bits >= 3:
+        pl["p2"] = np.ascontiguousarray(g[:, 8:12]).reshape(M, K // 8)
+    if bits >= 4:
+        pl["p3"] = np.ascontiguousarray(g[:, 12:16]).reshape(M, K // 8)
+    return pl
+
+
 def nested_dequant_f32(codes, tables_f16, bits: int, row_chunk: int = 1024) -> np.ndarray:
     """float32 [M, K] values of nested_dequant (its bf16 values widened), gathered per
     64-weight block with take_along_axis, a few rows at a time."""

@@ -31,7 +31,8 @@ def test_header_declares_the_expected_surface():
                  "launch_lut_gemv_kernel", "lutmoe_ref_gemv", "lutmoe_dequant", "lutmoe_gemv",
                  "lutmoe_route_topk", "lutmoe_permute", "lutmoe_moe_forward",
                  "lutmoe_moe_forward_logits", "lutmoe_moe_workspace_size", "lutmoe_strerror",
-                 "lutmoe_bl4_encode", "lutmoe_ref_encode", "lutmoe_merge_bitplane"):
+                 "lutmoe_bl4_encode", "lutmoe_ref_encode", "lutmoe_merge_bitplane",
+                 "lutmoe_nested_group_planes"):
         assert must in names
 
 
@@ -121,6 +122,14 @@ def test_validation_before_any_hip_call(lib):
     assert lib.lutmoe_pack_bitplanes(P(1), 6, P(1), None) == N.LUTMOE_EINVAL
     assert lib.lutmoe_pack_bitplanes(None, 8, P(1), None) == N.LUTMOE_EINVAL
     assert lib.lutmoe_pack_bitplanes(None, 0, None, None) == N.LUTMOE_OK
+    # nested plane grouping: n % 64 == 0, tier 2..4, pointers, 4-byte alignment
+    assert lib.lutmoe_nested_group_planes(P(0x100), 4, 96, P(0x200), None) == N.LUTMOE_EINVAL
+    assert lib.lutmoe_nested_group_planes(P(0x100), 5, 128, P(0x200), None) == N.LUTMOE_EINVAL
+    assert lib.lutmoe_nested_group_planes(P(0x100), 1, 128, P(0x200), None) == N.LUTMOE_EINVAL
+    assert lib.lutmoe_nested_group_planes(None, 3, 128, P(0x200), None) == N.LUTMOE_EINVAL
+    assert lib.lutmoe_nested_group_planes(P(0x102), 3, 128, P(0x200), None) == N.LUTMOE_EALIGN
+    assert lib.lutmoe_nested_group_planes(P(0x100), 3, 128, P(0x201), None) == N.LUTMOE_EALIGN
+    assert lib.lutmoe_nested_group_planes(None, 2, 0, None, None) == N.LUTMOE_OK
     # 1-D k-means: 1 <= k <= 256, n >= 1, n_iter >= 0, pointers
     assert lib.lutmoe_kmeans_1d(P(1), 10, P(1), 0, 3, P(1), None) == N.LUTMOE_EINVAL
     assert lib.lutmoe_kmeans_1d(P(1), 10, P(1), 257, 3, P(1), None) == N.LUTMOE_EINVAL

@@ -197,6 +197,25 @@ def test_nested_dequant_bitexact(gpu):
         assert np.array_equal(bf16_bits(got[e]), es.deq_bits(e)), f"expert {e} (tier {es.bits[e]})"
 
 
+def test_nested_grouped_layout_bitexact(gpu):
+    """The device order of NestedStack's codes (lutmoe_nested_group_planes)
+    equals the oracle's regrouping of the plane sections, at every tier;
+    keep_planes=False drops the plane tensors and keeps the codes."""
+    import torch
+    from block_lut_amd.formats import NestedExpert, NestedStack
+    es = NestedExpertset([2, 3, 4], 64, 192, seed=5, n_iter=4)
+    st = es.stack(gpu)
+    for e, b in enumerate(es.bits):
+        want = O.nested_group_planes(es.planes(e), b, es.M, es.K)
+        assert np.array_equal(st.codes[e].cpu().numpy(), want), f"tier {b}"
+    ex = [NestedExpert(b, torch.from_numpy(es.planes(e)).to(gpu), to_dev_bf16(es.table_bf16(e), gpu))
+          for e, b in enumerate(es.bits)]
+    st2 = NestedStack(ex, es.M, es.K, keep_planes=False)
+    assert all(x.planes is None for x in st2.experts)
+    for e in range(es.E):
+        assert torch.equal(st2.codes[e], st.codes[e])
+
+
 @pytest.mark.parametrize("bits,M,K,T", [(2, 2816, 2048, 1), (3, 2048, 1408, 1), (4, 2048, 1408, 2),
                                         (3, 300, 640, 5), (2, 40, 4160, 3)])
 def test_nested_gemv(gpu, bits, M, K, T):

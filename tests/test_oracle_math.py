@@ -249,6 +249,38 @@ def test_nested_planes_roundtrip_and_prefix():
         assert np.array_equal(O.nested_unpack_planes(pl, b), codes & ((1 << b) - 1))
 
 
+def test_nested_grouped_layout_by_brute_force():
+    """Device order of the nested codes: weight i's tier-b code read straight from
+    the grouped bytes by the layout rule (group i // 32 at 4b bytes each: the
+    64-bit little-endian word of 2-bit fields, then the bit-2 and bit-3 words)
+    equals the plane sections' code; ungrouping restores the sections."""
+    rng = np.random.default_rng(21)
+    M, K = 3, 128
+    codes = rng.integers(0, 16, (M, K), dtype=np.uint8)
+    pl = O.nested_pack_planes(codes)
+    for b in (2, 3, 4):
+        buf = np.concatenate([pl["p01"].reshape(-1)] +
+                             [pl[p].reshape(-1) for p, bit in (("p2", 2), ("p3", 3)) if b > bit])
+        g = O.nested_group_planes(buf, b, M, K)
+        assert g.size == M * K * b // 8
+        flat = codes.reshape(-1)
+        for i in range(M * K):
+            grp = g[(i // 32) * 4 * b: (i // 32 + 1) * 4 * b]
+            j = i % 32
+            f01 = int.from_bytes(grp[0:8].tobytes(), "little")
+            c = (f01 >> (2 * j)) & 3
+            if b >= 3:
+                c |= ((int.from_bytes(grp[8:12].tobytes(), "little") >> j) & 1) << 2
+            if b >= 4:
+                c |= ((int.from_bytes(grp[12:16].tobytes(), "little") >> j) & 1) << 3
+            assert c == flat[i] & ((1 << b) - 1), (b, i)
+        back = O.nested_ungroup(g, b, M, K)
+        ref = O.nested_planes_split(buf, b, M, K)
+        assert sorted(back) == sorted(ref)
+        for name in ref:
+            assert np.array_equal(back[name], ref[name])
+
+
 def test_nested_exact_with_four_values_at_tier2():
     rng = np.random.default_rng(10)
     vals = (rng.standard_normal(4) * 0.02).astype(np.float32)
