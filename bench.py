@@ -83,6 +83,9 @@ def parse():
     p.add_argument("--pmc-sample", action="store_true",
                    help="run only a 256 MiB device copy and the decode gate/up kernel of the "
                         "default workload (for rocprofv3 --pmc passes), then exit")
+    p.add_argument("--nested-sample", action="store_true",
+                   help="run only the NestedLUT tier workload (decode T=16 and prefill T=1024, "
+                        "graph-captured, for rocprofv3 kernel traces), then exit")
     p.add_argument("--prefill-sample", action="store_true",
                    help="run only the DeepSeek-V2-Lite T=2048 prefill (graph-captured, 10 replays, "
                         "for rocprofv3 kernel traces), then exit")
@@ -186,6 +189,10 @@ def main():
         log(f"[bench] pmc sample: gate/up algorithmic bytes per launch "
             f"{sum(s.bytes_gate_up for s in steps) / len(steps):.0f}")
         return
+    if a.nested_sample:
+        res = nested_tiers(a, ops, N, torch, dev, NestedExpert, NestedStack, MoEWeights, graph_of, time_graph)
+        log(f"[bench] nested sample: {json.dumps(res)}")
+        return
     if a.prefill_sample:
         d = DSV2
         sp = Step(rand_layer(d), d, 2048)
@@ -271,8 +278,10 @@ def main():
                    "avg_distinct_experts": round(sum(s.U for s in steps) / len(steps), 3)},
         "us_per_token": round(us_per_token, 3),
         "tokens_per_s": round(T / (ms_per_step / 1e3), 1),
-        # template argument = tokens per pass (1 at T=1, 2 up to T=16, else 4)
-        "roofline": {"bound": "hbm", "kernel": f"bl4_decode_gate_up<{1 if T <= 1 else 2 if T <= 16 else 4}>",
+        # one token: the dedicated kernel; else the template argument = tokens
+        # per pass (2 up to T=16, else 4)
+        "roofline": {"bound": "hbm",
+                     "kernel": "bl4_decode_gate_up_t1" if T <= 1 else f"bl4_decode_gate_up<{2 if T <= 16 else 4}>",
                      "achieved": round(ach_gu, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(ach_gu / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "avg_launch_us": round(dur_gu * 1e6, 3),
