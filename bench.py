@@ -585,7 +585,8 @@ def cpu_model() -> str:
 def cpu_baseline(a, c, T):
     """The reference's CPU dequant + matmul path on a bounded sample of the same
     workload (Qwen layer decode, T tokens, top-4 of 60 experts): 3 warm-up steps, then
-    the median of >= 20 timed steps, on all host cores and on one thread."""
+    the median of the timed steps, on all host cores (40 % of --cpu-seconds) and on one
+    thread (60 %), at least 20 steps each."""
     import statistics
     import torch
     from oracle.cpu_baseline import moe_layer_step
@@ -610,23 +611,23 @@ def cpu_baseline(a, c, T):
         nbytes = int(torch.unique(ids).numel()) * 3 * H * I * BYTES_PER_WEIGHT + 2 * T * H * 2
         inputs.append((x, ids, w, nbytes))
 
-    def measure(threads, reps, warm=3):
+    def measure(threads, seconds, min_reps=20, warm=3):
         torch.set_num_threads(threads)
         for i in range(warm):
             x, ids, w, _ = inputs[i]
             moe_layer_step(x, ids, w, experts13, experts2)
         times, by = [], []
-        for i in range(reps):
-            x, ids, w, nb = inputs[(warm + i) % len(inputs)]
+        while len(times) < min_reps or sum(times) < seconds:
+            x, ids, w, nb = inputs[(warm + len(times)) % len(inputs)]
             t0 = time.perf_counter()
             moe_layer_step(x, ids, w, experts13, experts2)
             times.append(time.perf_counter() - t0)
             by.append(nb)
         med = statistics.median(times)
-        return med, statistics.median(by), sum(times)
+        return med, statistics.median(by), sum(times), len(times)
 
-    med_all, by_all, tot_all = measure(ncores, 24)
-    med_one, by_one, tot_one = measure(1, 20)
+    med_all, by_all, tot_all, n_all = measure(ncores, 0.4 * a.cpu_seconds)
+    med_one, by_one, tot_one, n_one = measure(1, 0.6 * a.cpu_seconds)
     torch.set_num_threads(ncores)
     return {"value": round(by_all / med_all / 1e12, 6), "unit": "TB/s", "cores": ncores, "kind": "port",
             "ms_per_step": round(med_all * 1e3, 3),
@@ -635,8 +636,8 @@ def cpu_baseline(a, c, T):
                            "ms_per_step": round(med_one * 1e3, 3)},
             "cpu_model": cpu_model(),
             "sample": f"Qwen-shaped layer decode steps (T={T}, top-4 of 60 BL4 experts), torch CPU "
-                      f"dequant gather + bf16 F.linear: median of 24 steps on {ncores} threads "
-                      f"({tot_all:.1f} s) and of 20 steps on 1 thread ({tot_one:.1f} s), each after "
+                      f"dequant gather + bf16 F.linear: median of {n_all} steps on {ncores} threads "
+                      f"({tot_all:.1f} s) and of {n_one} steps on 1 thread ({tot_one:.1f} s), each after "
                       f"3 warm-up steps; weights generated beforehand ({t_gen:.1f} s, untimed)"}
 
 
