@@ -646,8 +646,8 @@ __device__ __forceinline__ void bl4_rows8(const uint8_t* __restrict__ codes, con
 
 // ---- NestedLUT experts (NestedView, lut_core.h).
 // The lane's 32 columns [2048cc + 32l, +32) of 8 rows: one 32-weight group
-// of the device layout per row (8 bytes of 2-bit fields, 4 of bit 2, 4 of
-// bit 3: the tier's 4b bytes, one load), and 16 bytes of the row's tables
+// of the device layout per row (two 2-bit field words, the bit-2 and bit-3
+// words: the tier's 4b bytes, one load), and 16 bytes of the row's tables
 // starting at this lane's share of its block's table (2^b bytes: entries
 // 2^(b-1)*(l%2) ..).
 struct Rows8N {
@@ -704,8 +704,7 @@ __device__ __forceinline__ void compute_rows8n(const Rows8N& b, const uint32_t (
         wave_lds_sync();
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const uint32_t f01 = b.f01[r][j >> 1] >> (16 * (j & 1));
-            const uint32_t w = nested_nibbles8<kBits>(f01, b.f2[r] >> (8 * j), b.f3[r] >> (8 * j));
+            const uint32_t w = nested_code8<kBits>(b.f01[r][0], b.f01[r][1], b.f2[r], b.f3[r], j);
             uint32_t xj[TB][4];
 #pragma unroll
             for (int t = 0; t < TB; ++t)

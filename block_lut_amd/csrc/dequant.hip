@@ -4,7 +4,8 @@
 //                  (csrc/kernels/tensor_recover.cu:101-142 rule; batched over
 //                  experts like lut_decompress_kernel.cu:87-120).
 //  bl4_dequant   : BL4 codes -> bf16 through per-block bf16 tables staged in LDS.
-//  nested_dequant: NestedLUT tier-b bit-plane sections -> bf16.
+//  nested_dequant: NestedLUT tier-b device-layout codes -> bf16.
+//  nested_group_planes: NestedLUT plane sections -> the device layout.
 //  unpack_4bit   : in-place low-nibble unpack (tensor_recover.cu:161-192),
 //                  done as a race-free halving sequence instead of the
 //                  reference's copy-to-upper-half + expand.
@@ -17,6 +18,7 @@
 //                  tensor_engine.cpp:504-510).
 #include "common.h"
 #include "kernels.h"
+#include "lut_core.h"
 
 using namespace lutmoe;
 
@@ -112,16 +114,14 @@ __global__ __launch_bounds__(256) void nested_dequant_kernel(
     const int64_t i0 = g * 32;
     if (i0 >= n_per_expert) return;
     const uint32_t* q = reinterpret_cast<const uint32_t*>(code_ptrs[e] + g * 4 * b);
-    const uint64_t f01 = (uint64_t)q[0] | ((uint64_t)q[1] << 32);
-    const uint32_t f2 = b >= 3 ? q[2] : 0u;
-    const uint32_t f3 = b >= 4 ? q[3] : 0u;
+    const uint32_t f0 = q[0], f1 = q[1];
+    const uint32_t b2 = b >= 3 ? q[2] : 0u;
+    const uint32_t b3 = b >= 4 ? q[3] : 0u;
     const uint16_t* t = tab + (i0 / kBlockBL) * (1 << b);
     uint32_t o[16];
 #pragma unroll
     for (int j = 0; j < 32; ++j) {
-        const uint32_t c = (uint32_t)((f01 >> (2 * j)) & 3u) | (((f2 >> j) & 1u) << 2) |
-                           (((f3 >> j) & 1u) << 3);
-        const uint32_t v = t[c];
+        const uint32_t v = t[nested_code1(f0, f1, b2, b3, j)];
         if (j & 1) o[j >> 1] |= v << 16; else o[j >> 1] = v;
     }
     uint4* dst = reinterpret_cast<uint4*>(out + (int64_t)blockIdx.y * n_per_expert + i0);
@@ -129,20 +129,36 @@ __global__ __launch_bounds__(256) void nested_dequant_kernel(
     for (int q4 = 0; q4 < 4; ++q4) dst[q4] = make_uint4(o[4 * q4], o[4 * q4 + 1], o[4 * q4 + 2], o[4 * q4 + 3]);
 }
 
-// NestedLUT plane sections [p01 n/4 | p2 n/8 | p3 n/8] (the tier's prefix)
-// -> the device layout: group g (weights 32g .. 32g+31) = p01 bytes 8g..8g+7,
-// then p2 bytes 4g..4g+3 (b >= 3), then p3 bytes 4g..4g+3 (b = 4).  One
-// thread per group, dword copies (n % 64 == 0 keeps every section and
-// group 4-byte aligned).
+// NestedLUT plane sections [p01 n/4 | p2 n/8 | p3 n/8] (the tier's prefix;
+// p01: weight i's 2-bit field at bits 2(i%4) of byte i/4; p2 / p3: its bit 2
+// / bit 3 at bit i%8 of byte i/8) -> the device layout (NestedView,
+// lut_core.h).  One thread per 32-weight group; n % 64 == 0 keeps every
+// section and group 4-byte aligned.
+__device__ __forceinline__ uint32_t spread_fields8(uint32_t f) {   // 2-bit field j -> bits 4j..4j+1
+    uint32_t x = f & 0xffffu;
+    x = (x | (x << 8)) & 0x00ff00ffu;
+    x = (x | (x << 4)) & 0x0f0f0f0fu;
+    return (x | (x << 2)) & 0x33333333u;
+}
+__device__ __forceinline__ uint32_t spread_bits8(uint32_t v) {     // bit j -> bit 4j
+    uint32_t y = v & 0xffu;
+    y = (y | (y << 12)) & 0x000f000fu;
+    y = (y | (y << 6)) & 0x03030303u;
+    return (y | (y << 3)) & 0x11111111u;
+}
 __global__ __launch_bounds__(256) void nested_group_planes_kernel(const uint32_t* __restrict__ planes, int b,
                                                                   int64_t n, uint32_t* __restrict__ out) {
     const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (g * 32 >= n) return;
+    const uint32_t p0 = planes[2 * g], p1 = planes[2 * g + 1];   // fields of weights 0-15, 16-31
     uint32_t* o = out + g * b;
-    o[0] = planes[2 * g];
-    o[1] = planes[2 * g + 1];
-    if (b >= 3) o[2] = planes[n / 16 + g];
-    if (b >= 4) o[3] = planes[n / 16 + n / 32 + g];
+    o[0] = spread_fields8(p0) | (spread_fields8(p0 >> 16) << 2);
+    o[1] = spread_fields8(p1) | (spread_fields8(p1 >> 16) << 2);
+    for (int s = 2; s < b; ++s) {
+        const uint32_t w = planes[n / 16 + (int64_t)(s - 2) * (n / 32) + g];   // bit s of weights 0-31
+        o[s] = spread_bits8(w) | (spread_bits8(w >> 8) << 1) | (spread_bits8(w >> 16) << 2) |
+               (spread_bits8(w >> 24) << 3);
+    }
 }
 
 __global__ __launch_bounds__(256) void f16_to_bf16_kernel(const uint16_t* __restrict__ in,

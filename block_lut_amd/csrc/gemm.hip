@@ -279,8 +279,7 @@ __device__ __forceinline__ void prefill_tile(const lutmoe_moe_desc& d, const uin
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
             if constexpr (kFmt == LUTMOE_FMT_NESTED) {
-                const uint32_t wd = nested_nibbles8(b.f01[nt][ks >> 1] >> (16 * (ks & 1)), b.f2[nt] >> (8 * ks),
-                                                    b.f3[nt] >> (8 * ks));
+                const uint32_t wd = nested_code8(b.f01[nt][0], b.f01[nt][1], b.f2[nt], b.f3[nt], ks);
                 bf[nt] = __builtin_bit_cast(bf16x8_t, lookup8_reg(tb[nt], wd));
             } else if constexpr (kFmt == LUTMOE_FMT_BL4) {
                 bf[nt] = __builtin_bit_cast(bf16x8_t, lookup8_reg(tb[nt], b.codes[nt][ks]));
@@ -670,8 +669,8 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
     const int L1 = kGateUp ? 128 + 32 * wv + bn : 64 * wv + 32 + bn;
 
     // BL4: codes[nt] = the lane's 16 code bytes of row Lnt.  NestedLUT:
-    // codes[nt] = the lane half's 32-weight group: its 2-bit fields (.x, .y),
-    // bit-2 and bit-3 planes (.z, .w; zero for tiers without them): see
+    // codes[nt] = the lane half's 32-weight group: its 2-bit field words (.x,
+    // .y), bit-2 and bit-3 words (.z, .w; zero for tiers without them): see
     // nested_code below.
     // REF: codes[2nt], codes[2nt+1] = the lane's 32 code bytes of row Lnt; am[nt]
     // = that row's absmax for K step kb (the aligned dword holds it in the
@@ -728,7 +727,7 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
     // BL4 nibbles
     auto nested_code = [&](const u32x4_t& c, int ks) __attribute__((always_inline)) {
         if constexpr (kNested)
-            return nested_nibbles8(c[ks >> 1] >> (16 * (ks & 1)), c[2] >> (8 * ks), c[3] >> (8 * ks));
+            return nested_code8(c[0], c[1], c[2], c[3], ks);
         else
             return c[ks];
     };

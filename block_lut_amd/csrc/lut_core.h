@@ -129,11 +129,15 @@ __device__ __forceinline__ u32x4_t lookup8_lds(uint32_t w, uint32_t tab) {
     return lookup8_combine(lookup8_issue(w, tab));
 }
 
-// A NestedLUT expert in the device layout: the tier-b plane bytes of each 32
-// consecutive weights (flat row-major [rows][K] order) kept together, 4b
-// bytes per group: 8 bytes of 2-bit fields (weight j at bits 2j..2j+1 of the
-// little-endian 64-bit word), then 4 bytes of bit 2 (b >= 3) and 4 bytes of
-// bit 3 (b = 4), weight j at bit j.  Tables bf16 [rows][K/64][2^b].  Both are
+// A NestedLUT expert in the device layout: each 32 consecutive weights (flat
+// row-major [rows][K] order; w_j = code of weight j of the group) as 4b bytes,
+// four little-endian words of which a tier-b group holds the first b:
+//   f0: nibble n = (w_n & 3) | (w_{n+8} & 3) << 2
+//   f1: nibble n = (w_{n+16} & 3) | (w_{n+24} & 3) << 2
+//   b2: nibble n bit q = bit 2 of w_{n+8q}       (b >= 3)
+//   b3: nibble n bit q = bit 3 of w_{n+8q}       (b = 4)
+// so the codes of weights 8q .. 8q+7 are one shift and mask per word away from
+// a BL4 code dword (nested_code8).  Tables bf16 [rows][K/64][2^b].  Both are
 // read through bounds-checked buffer descriptors (bytes past the end read as
 // zero).
 constexpr int kBufWord3 = 0x00020000;   // raw buffer, dword format (gfx9)
@@ -155,29 +159,27 @@ __device__ __forceinline__ NestedView nested_view(const lutmoe_weights& w, int e
     return v;
 }
 
-// NestedLUT bit-plane sections -> BL4 code dword (nibble j = code of column
-// j) for 8 consecutive columns: f01 = their 2-bit fields (column j at bits
-// 2j..2j+1), f2 / f3 = their bit-2 / bit-3 planes (column j at bit j; zero
-// for lower tiers).  Fields are spread to nibbles by shift-or-mask steps.
-// kBits (2, 3 or 4; 0 = not known at compile time): planes a tier does not
-// have are skipped.
+// The BL4 code dword (nibble j = code of weight 8q + j) of weights
+// 8q .. 8q+7 of a device-layout group (f0, f1 = its 2-bit field words, b2 /
+// b3 = its bit-2 / bit-3 words, zero for lower tiers): one shift and mask
+// per word.  kBits (2, 3 or 4; 0 = not known at compile time): words a tier
+// does not have are skipped.
 template <int kBits = 0>
-__device__ __forceinline__ uint32_t nested_nibbles8(uint32_t f01, uint32_t f2, uint32_t f3) {
-    uint32_t x = f01 & 0xffffu;
-    x = (x | (x << 8)) & 0x00ff00ffu;   // 4 fields per byte in bytes 0, 2
-    x = (x | (x << 4)) & 0x0f0f0f0fu;   // 2 fields per byte
-    x = (x | (x << 2)) & 0x33333333u;   // field j in the low 2 bits of nibble j
+__device__ __forceinline__ uint32_t nested_code8(uint32_t f0, uint32_t f1, uint32_t b2, uint32_t b3, int q) {
+    const uint32_t f = q < 2 ? f0 : f1;
+    const uint32_t x = (q & 1 ? f >> 2 : f) & 0x33333333u;
     if constexpr (kBits == 2) return x;
-    uint32_t y = f2 & 0xffu;            // bit j -> bit 4j
-    y = (y | (y << 12)) & 0x000f000fu;
-    y = (y | (y << 6)) & 0x03030303u;
-    y = (y | (y << 3)) & 0x11111111u;
-    if constexpr (kBits == 3) return x | (y << 2);
-    uint32_t z = f3 & 0xffu;
-    z = (z | (z << 12)) & 0x000f000fu;
-    z = (z | (z << 6)) & 0x03030303u;
-    z = (z | (z << 3)) & 0x11111111u;
-    return x | (y << 2) | (z << 3);
+    const uint32_t y = (q < 3 ? b2 << (2 - q) : b2 >> 1) & 0x44444444u;
+    if constexpr (kBits == 3) return x | y;
+    return x | y | ((b3 << (3 - q)) & 0x88888888u);
+}
+
+// The code of weight j (0..31) of a device-layout group.
+__device__ __forceinline__ uint32_t nested_code1(uint32_t f0, uint32_t f1, uint32_t b2, uint32_t b3, int j) {
+    const int n = j & 7, q = j >> 3;
+    const uint32_t f = q < 2 ? f0 : f1;
+    return ((f >> (4 * n + 2 * (q & 1))) & 3u) | (((b2 >> (4 * n + q)) & 1u) << 2) |
+           (((b3 >> (4 * n + q)) & 1u) << 3);
 }
 
 // A 16-entry bf16 table held in registers as byte planes: lo[q] = low bytes

@@ -20,11 +20,13 @@
  *   NL   : NestedLUT tier b in {2,3,4} per expert.  Stored (and loaded
  *          progressively) as bit-plane sections [p01 M*K/4 | p2 M*K/8 |
  *          p3 M*K/8] (a tier-b expert holds the first 2, 3 or all sections);
- *          on the device the codes are grouped: for each 32 consecutive
- *          weights of the flat row-major [M][K] order, their 8 bytes of p01,
- *          then 4 of p2 (b >= 3), then 4 of p3 (b = 4) -- 4b bytes per group,
- *          M*K*b/8 per expert (lutmoe_nested_group_planes converts).  Tables
- *          bf16 [M][K/64][2^b].
+ *          on the device the codes are grouped: each 32 consecutive weights
+ *          of the flat row-major [M][K] order (w_j = code of weight j) are
+ *          the first b of four little-endian uint32 words -- f0: nibble n =
+ *          (w_n & 3) | (w_{n+8} & 3) << 2; f1: the same for w_{n+16},
+ *          w_{n+24}; b2: nibble n bit q = bit 2 of w_{n+8q} (b >= 3); b3:
+ *          bit 3 likewise (b = 4) -- 4b bytes per group, M*K*b/8 per expert
+ *          (lutmoe_nested_group_planes converts).  Tables bf16 [M][K/64][2^b].
  */
 #ifndef LUTMOE_H
 #define LUTMOE_H
@@ -172,12 +174,12 @@ int lutmoe_pack_bitplanes(const uint8_t* codes_dev, int64_t n, uint8_t* packed_d
 
 /* NestedLUT plane sections of one tier-b expert (planes_dev: the tier's
  * prefix of [p01 n/4 | p2 n/8 | p3 n/8]) -> its device codes out_dev
- * (n*b/8 bytes): group g = p01 bytes 8g..8g+7, then p2 bytes 4g..4g+3
- * (b >= 3), then p3 bytes 4g..4g+3 (b = 4).  n = M*K weights, n % 64 == 0;
- * both pointers 4-byte aligned.  No counterpart in the reference, whose
- * 4/6/8-bit sections are merged into byte codes on load
- * (csrc/tensor_engine/tensor_engine.cpp:535-548): the grouped order lets a
- * kernel read a weight group's planes in one load. */
+ * (n*b/8 bytes, the group words described at the top of this file).
+ * n = M*K weights, n % 64 == 0; both pointers 4-byte aligned.  No
+ * counterpart in the reference, whose 4/6/8-bit sections are merged into
+ * byte codes on load (csrc/tensor_engine/tensor_engine.cpp:535-548): the
+ * grouped order lets a kernel read a weight group in one load and turn 8 of
+ * its codes into a 4-bit code word with one shift and mask per word. */
 int lutmoe_nested_group_planes(const uint8_t* planes_dev, int bits, int64_t n, uint8_t* out_dev, void* stream);
 
 /* Progressive tier upgrade of resident codes (the reference reloads the whole

@@ -484,27 +484,44 @@ def nested_planes_split(buf, bits: int, M: int, K: int) -> dict:
 
 def nested_group_planes(buf, bits: int, M: int, K: int) -> np.ndarray:
     """The device order of one expert's codes (this library's own layout, no reference
-    counterpart): the plane sections of nested_planes_split regrouped so that each 32
-    consecutive weights of the flat row-major order keep their bytes together -- 8 bytes of
-    p01, then 4 of p2 (b >= 3), then 4 of p3 (b = 4); 4b bytes per group."""
-    pl = nested_planes_split(buf, bits, M, K)
-    g = M * K // 32
-    parts = [np.asarray(pl["p01"], np.uint8).reshape(g, 8)]
-    for name, bit in (("p2", 2), ("p3", 3)):
+    counterpart).  Each 32 consecutive weights of the flat row-major order (w_j = code of
+    weight j of the group) become the first `bits` of four little-endian uint32 words:
+      f0: nibble n = (w_n & 3) | (w_{n+8} & 3) << 2
+      f1: nibble n = (w_{n+16} & 3) | (w_{n+24} & 3) << 2
+      b2: nibble n bit q = bit 2 of w_{n+8q}   (bits >= 3)
+      b3: nibble n bit q = bit 3 of w_{n+8q}   (bits == 4)."""
+    codes = nested_unpack_planes(nested_planes_split(buf, bits, M, K), bits).reshape(-1, 32).astype(np.uint32)
+    words = []
+    f0 = np.zeros(codes.shape[0], np.uint32)
+    f1 = np.zeros(codes.shape[0], np.uint32)
+    for j in range(8):
+        f0 |= ((codes[:, j] & 3) | ((codes[:, j + 8] & 3) << 2)) << np.uint32(4 * j)
+        f1 |= ((codes[:, j + 16] & 3) | ((codes[:, j + 24] & 3) << 2)) << np.uint32(4 * j)
+    words += [f0, f1]
+    for bit in (2, 3):
         if bits > bit:
-            parts.append(np.asarray(pl[name], np.uint8).reshape(g, 4))
-    return np.ascontiguousarray(np.concatenate(parts, axis=1).reshape(-1))
+            w = np.zeros(codes.shape[0], np.uint32)
+            for j in range(8):
+                for q in range(4):
+                    w |= ((codes[:, j + 8 * q] >> np.uint32(bit)) & 1) << np.uint32(4 * j + q)
+            words.append(w)
+    return np.ascontiguousarray(np.stack(words, axis=1).astype("<u4")).view(np.uint8).reshape(-1)
 
 
 def nested_ungroup(grouped, bits: int, M: int, K: int) -> dict:
     """Inverse of nested_group_planes: the section dict of nested_pack_planes."""
-    g = np.asarray(grouped, np.uint8).reshape(M * K // 32, 4 * bits)
-    pl = {"p01": np.ascontiguousarray(g[:, 0:8]).reshape(M, K // 4)}
-    if bits >= 3:
-        pl["p2"] = np.ascontiguousarray(g[:, 8:12]).reshape(M, K // 8)
-    if bits >= 4:
-        pl["p3"] = np.ascontiguousarray(g[:, 12:16]).reshape(M, K // 8)
-    return pl
+    g = np.ascontiguousarray(np.asarray(grouped, np.uint8)).view("<u4").reshape(M * K // 32, bits)
+    codes = np.zeros((g.shape[0], 32), np.uint8)
+    for j in range(8):
+        for q in range(4):
+            f = g[:, q // 2]
+            c = (f >> np.uint32(4 * j + 2 * (q & 1))) & 3
+            for bit in (2, 3):
+                if bits > bit:
+                    c |= ((g[:, bit] >> np.uint32(4 * j + q)) & 1) << np.uint32(bit)
+            codes[:, j + 8 * q] = c.astype(np.uint8)
+    pl = nested_pack_planes(codes.reshape(M, K))
+    return {name: pl[name] for name, bit in (("p01", 0), ("p2", 2), ("p3", 3)) if bits > bit}
 
 
 def nested_dequant_f32(codes, tables_f16, bits: int, row_chunk: int = 1024) -> np.ndarray:

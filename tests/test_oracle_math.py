@@ -251,9 +251,10 @@ def test_nested_planes_roundtrip_and_prefix():
 
 def test_nested_grouped_layout_by_brute_force():
     """Device order of the nested codes: weight i's tier-b code read straight from
-    the grouped bytes by the layout rule (group i // 32 at 4b bytes each: the
-    64-bit little-endian word of 2-bit fields, then the bit-2 and bit-3 words)
-    equals the plane sections' code; ungrouping restores the sections."""
+    the grouped bytes by the layout rule (group i // 32 at 4b bytes; in the
+    group, weight j = n + 8q: its 2-bit field at bits 4n + 2(q % 2) of word q // 2,
+    its bit 2 / bit 3 at bit 4n + q of words 2 / 3) equals the plane sections'
+    code; ungrouping restores the sections."""
     rng = np.random.default_rng(21)
     M, K = 3, 128
     codes = rng.integers(0, 16, (M, K), dtype=np.uint8)
@@ -266,13 +267,14 @@ def test_nested_grouped_layout_by_brute_force():
         flat = codes.reshape(-1)
         for i in range(M * K):
             grp = g[(i // 32) * 4 * b: (i // 32 + 1) * 4 * b]
+            word = [int.from_bytes(grp[4 * w: 4 * w + 4].tobytes(), "little") for w in range(b)]
             j = i % 32
-            f01 = int.from_bytes(grp[0:8].tobytes(), "little")
-            c = (f01 >> (2 * j)) & 3
+            n, q = j % 8, j // 8
+            c = (word[q // 2] >> (4 * n + 2 * (q % 2))) & 3
             if b >= 3:
-                c |= ((int.from_bytes(grp[8:12].tobytes(), "little") >> j) & 1) << 2
+                c |= ((word[2] >> (4 * n + q)) & 1) << 2
             if b >= 4:
-                c |= ((int.from_bytes(grp[12:16].tobytes(), "little") >> j) & 1) << 3
+                c |= ((word[3] >> (4 * n + q)) & 1) << 3
             assert c == flat[i] & ((1 << b) - 1), (b, i)
         back = O.nested_ungroup(g, b, M, K)
         ref = O.nested_planes_split(buf, b, M, K)
