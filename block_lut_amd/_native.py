@@ -24,6 +24,9 @@ FMT_REF = 0
 FMT_BL4 = 1
 FMT_NESTED = 2
 
+QRULE_QUANTIZER = 0
+QRULE_MIDPOINTS = 1
+
 STAGE_ROUTE = 1
 STAGE_GATE_UP = 2
 STAGE_DOWN = 4
@@ -97,6 +100,7 @@ PROTOTYPES = {
     "lutmoe_kmeans_1d": (I32, [P, I64, P, I32, I32, P, P]),
     "lutmoe_pack_bitplanes": (I32, [P, I64, P, P]),
     "lutmoe_nested_group_planes": (I32, [P, I32, I64, P, P]),
+    "lutmoe_ref_quantize": (I32, [P, I32, P, I32, I64, I32, I32, P, P, P]),
     "lutmoe_dequant": (I32, [WP, I32, I32, P, P]),
     "lutmoe_gemv": (I32, [WP, I32, P, I32, P, I32, P]),
     "lutmoe_bl4_tables_from_f16": (I32, [P, P, I64, P]),

@@ -496,4 +496,18 @@ int lutmoe_ref_encode(const void* w_bf16, const float* codebook, int64_t n, int 
                              stream_of(stream));
 }
 
+int lutmoe_ref_quantize(const void* w, int w_dtype, const float* codebook, int n_entries, int64_t n, int block_size,
+                        int rule, uint8_t* codes, void* absmax_bf16, void* stream) {
+    if (n < 0 || block_size <= 0) return LUTMOE_EINVAL;
+    if (w_dtype != LUTMOE_DTYPE_BF16 && w_dtype != LUTMOE_DTYPE_F32) return LUTMOE_EINVAL;
+    if (rule != LUTMOE_QRULE_QUANTIZER && rule != LUTMOE_QRULE_MIDPOINTS) return LUTMOE_EINVAL;
+    if (n_entries < (rule == LUTMOE_QRULE_MIDPOINTS ? 2 : 1) || n_entries > 256) return LUTMOE_EINVAL;
+    if (n == 0) return LUTMOE_OK;
+    if (!w || !codebook || !codes || !absmax_bf16) return LUTMOE_EINVAL;
+    if (!aligned(w, w_dtype == LUTMOE_DTYPE_F32 ? 4 : 2) || !aligned(codebook, 4) || !aligned(absmax_bf16, 2))
+        return LUTMOE_EALIGN;
+    return launch_ref_quantize(w, w_dtype == LUTMOE_DTYPE_BF16, codebook, n_entries, n, block_size, rule, codes,
+                               (uint16_t*)absmax_bf16, stream_of(stream));
+}
+
 }  // extern "C"

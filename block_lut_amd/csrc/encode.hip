@@ -233,6 +233,71 @@ __global__ __launch_bounds__(256) void ref_encode_kernel(const uint16_t* __restr
     }
 }
 
+// The reference's two other REF encoding rules, one wave per block of
+// block_size weights, the codebook (or its midpoints) in LDS:
+//   kRule 0, LUTQuantizer.quantize (vllm_lut/quantizer.py:242-306, the
+//     BLOCKLUT / NESTEDLUT branch; block_size = n is its global "LUT"
+//     branch): absmax = max |w| in the weights' dtype, at least 1e-10 in that
+//     dtype (:282-283); v = w / absmax, rounded to bf16 for bf16 weights (torch
+//     divides bf16 tensors in fp32 and rounds the result, :284); code = the
+//     first nearest of the ncb entries by |v - c| in fp32 (argmin, :293-296;
+//     the codebook need not be sorted).
+//   kRule 1, the offload runtime's encoder (runtime/model_offload.py:
+//     897-907): weights as fp32; absmax at least fp32(1e-12); v = w / absmax in
+//     fp32; code = the number of midpoints fl32(fl32(c_i + c_{i+1}) / 2) of the
+//     ascending codebook below v (np.searchsorted, side "left": a value on a
+//     midpoint takes the lower entry, NaN the last).
+// absmax is stored as bf16 (round to nearest even).
+template <int kRule, bool kBf16In>
+__global__ __launch_bounds__(256) void ref_quantize_kernel(const void* __restrict__ w, const float* __restrict__ cb,
+                                                           int ncb, int64_t n, int block_size, int64_t nblocks,
+                                                           uint8_t* __restrict__ codes,
+                                                           uint16_t* __restrict__ absmax) {
+    __shared__ float s_c[256];
+    const int t = threadIdx.x;
+    if (kRule == 0 && t < ncb) s_c[t] = cb[t];
+    if (kRule == 1 && t + 1 < ncb) {
+        const float sum = cb[t] + cb[t + 1];
+        s_c[t] = sum * 0.5f;   // exact halving: equals numpy's fp32 sum / 2.0
+    }
+    __syncthreads();
+    const int lane = t & 63, wv = t >> 6;
+    auto load = [&](int64_t i) __attribute__((always_inline)) {
+        return kBf16In ? bf16_to_f32(reinterpret_cast<const uint16_t*>(w)[i]) : reinterpret_cast<const float*>(w)[i];
+    };
+    // the clamp's bound in the dtype the reference clamps in
+    const float lo = kRule == 1 ? 1e-12f : kBf16In ? bf16_to_f32(f32_to_bf16(1e-10f)) : 1e-10f;
+    for (int64_t b = (int64_t)blockIdx.x * 4 + wv; b < nblocks; b += (int64_t)gridDim.x * 4) {
+        const int64_t start = b * block_size;
+        const int len = (int)min((int64_t)block_size, n - start);
+        float mx = 0.f;
+        for (int i = lane; i < len; i += 64) mx = fmaxf(mx, fabsf(load(start + i)));
+        mx = fmaxf(wave_reduce_max(mx), lo);
+        for (int i = lane; i < len; i += 64) {
+            float v = load(start + i) / mx;
+            int code;
+            if constexpr (kRule == 0) {
+                if (kBf16In) v = bf16_to_f32(f32_to_bf16(v));
+                float bd = fabsf(v - s_c[0]);
+                code = 0;
+                for (int c = 1; c < ncb; ++c) {
+                    const float dd = fabsf(v - s_c[c]);
+                    if (dd < bd) {
+                        bd = dd;
+                        code = c;
+                    }
+                }
+            } else {
+                code = 0;
+                for (int c = 0; c + 1 < ncb; ++c) code += s_c[c] < v ? 1 : 0;
+                if (v != v) code = ncb - 1;
+            }
+            codes[start + i] = (uint8_t)code;
+        }
+        if (lane == 0) absmax[b] = (uint16_t)f32_to_bf16(mx);
+    }
+}
+
 // 1-D Lloyd k-means (LUTQuantizer._train_kmeans iterations,
 // vllm_lut/quantizer.py:158-173): every sample joins its nearest centroid by
 // |x - c| (the first one on equal distances, as argmin), then every centroid
@@ -312,6 +377,27 @@ int launch_kmeans_1d(const float* x, int64_t n, float* cent, int k, int n_iter, 
         if ((rc = check_launch())) return rc;
     }
     return LUTMOE_OK;
+}
+
+int launch_ref_quantize(const void* w, bool bf16_in, const float* codebook, int ncb, int64_t n, int block_size,
+                        int rule, uint8_t* codes, uint16_t* absmax, hipStream_t s) {
+    const int64_t nblocks = (n + block_size - 1) / block_size;
+    int64_t ctas = (nblocks + 3) / 4;
+    if (ctas > 65536) ctas = 65536;
+    const dim3 grid((unsigned)ctas), block(256);
+    if (rule == 0 && bf16_in)
+        hipLaunchKernelGGL((ref_quantize_kernel<0, true>), grid, block, 0, s, w, codebook, ncb, n, block_size, nblocks,
+                           codes, absmax);
+    else if (rule == 0)
+        hipLaunchKernelGGL((ref_quantize_kernel<0, false>), grid, block, 0, s, w, codebook, ncb, n, block_size,
+                           nblocks, codes, absmax);
+    else if (bf16_in)
+        hipLaunchKernelGGL((ref_quantize_kernel<1, true>), grid, block, 0, s, w, codebook, ncb, n, block_size, nblocks,
+                           codes, absmax);
+    else
+        hipLaunchKernelGGL((ref_quantize_kernel<1, false>), grid, block, 0, s, w, codebook, ncb, n, block_size,
+                           nblocks, codes, absmax);
+    return check_launch();
 }
 
 int launch_ref_encode(const uint16_t* w, const float* codebook, int64_t n, int block_size, uint8_t* codes,

@@ -19,6 +19,8 @@ int launch_bl4_dequant(uint16_t* out, const uint8_t* codes, const uint16_t* tabl
                        int64_t nblocks, hipStream_t s);
 int launch_nested_dequant(uint16_t* out, const lutmoe_weights* w, int e0, int ne,
                           hipStream_t s);
+int launch_ref_quantize(const void* w, bool bf16_in, const float* codebook, int ncb, int64_t n, int block_size,
+                        int rule, uint8_t* codes, uint16_t* absmax, hipStream_t s);
 int launch_nested_group_planes(const uint8_t* planes, int bits, int64_t n, uint8_t* out, hipStream_t s);
 int launch_f16_to_bf16(const uint16_t* in, uint16_t* out, int64_t n, hipStream_t s);
 int launch_unpack_4bit_inplace(uint8_t* data, int64_t n, hipStream_t s);

@@ -1,5 +1,5 @@
-"""Codebook training behind the reference's LUTQuantizer
-(vllm_lut/quantizer.py: `LUTQuantizer._train_kmeans`, :120-178).
+"""Codebook training and REF encoding behind the reference's LUTQuantizer
+(vllm_lut/quantizer.py: `LUTQuantizer`, :30-396; `_train_kmeans`, :120-178).
 
 `train_kmeans(data, k, n_iter)` returns the sorted bf16[k] codebook on the host, as the
 reference stores `lut_codebook`.  Subsampling (more than `max_samples` values: a random
@@ -10,14 +10,17 @@ iterations (:158-173) run on the GPU (`lutmoe_kmeans_1d`); the sort and the bf16
 """
 from __future__ import annotations
 
-from typing import Optional
+import os
+from typing import Dict, Optional, Tuple
 
+import numpy as np
 import torch
 
 from . import _native as N
 from .formats import _dev, _stream
 
-__all__ = ["train_kmeans", "greedy_merge", "build_mapped_table", "train_nested_codebooks"]
+__all__ = ["train_kmeans", "greedy_merge", "build_mapped_table", "train_nested_codebooks", "quantize",
+           "LUTQuantizer"]
 
 
 def train_kmeans(data: torch.Tensor, k: int = 256, n_iter: int = 20, max_samples: int = 200000,
@@ -91,3 +94,129 @@ def train_nested_codebooks(data: torch.Tensor, n_iter: int = 20, seed: Optional[
     c64 = train_kmeans(data, 64, n_iter, seed=seed, device=device)
     c16 = greedy_merge(c64, 16)
     return build_mapped_table(c64, 256), build_mapped_table(c16, 256)
+
+
+_RULES = {"quantizer": N.QRULE_QUANTIZER, "midpoints": N.QRULE_MIDPOINTS}
+
+
+def quantize(weight: torch.Tensor, codebook: torch.Tensor, block_size: int = 128,
+             rule: str = "quantizer") -> Tuple[torch.Tensor, torch.Tensor]:
+    """REF codes of `weight` (bf16 or fp32, any shape, flattened) on the GPU: uint8 [N]
+    codes and bf16 [ceil(N / block_size)] absmax, device tensors, no host sync.
+
+    rule "quantizer": LUTQuantizer.quantize (vllm_lut/quantizer.py:242-306): normalisation
+        in the weights' dtype, code = first nearest entry of `codebook` (bf16 or fp32, any
+        order, at most 256 entries).
+    rule "midpoints": the offload runtime's encoder (runtime/model_offload.py:897-907):
+        fp32 normalisation, code = np.searchsorted over the midpoints of `codebook`, which
+        must be ascending (the runtime sorts its table first)."""
+    if rule not in _RULES:
+        raise ValueError(f"rule must be one of {sorted(_RULES)}")
+    w = weight.reshape(-1)
+    if w.dtype not in (torch.bfloat16, torch.float32):
+        w = w.float()
+    w = _dev(w.contiguous(), w.dtype, "weight")
+    cb = codebook.reshape(-1).to(w.device, torch.float32).contiguous()
+    k = cb.numel()
+    if not 1 <= k <= 256:
+        raise ValueError("the codebook holds 1..256 entries")
+    if rule == "midpoints" and bool((cb[1:] < cb[:-1]).any()):
+        raise ValueError("rule 'midpoints' needs an ascending codebook")
+    n = w.numel()
+    nb = -(-n // block_size) if n else 0
+    codes = torch.empty(n, dtype=torch.uint8, device=w.device)
+    absmax = torch.empty(nb, dtype=torch.bfloat16, device=w.device)
+    dt = N.DTYPE_BF16 if w.dtype == torch.bfloat16 else N.DTYPE_F32
+    N.check("lutmoe_ref_quantize",
+            N.lib().lutmoe_ref_quantize(w.data_ptr(), dt, cb.data_ptr(), k, n, block_size, _RULES[rule],
+                                        codes.data_ptr(), absmax.data_ptr(), _stream()))
+    return codes, absmax
+
+
+class LUTQuantizer:
+    """vllm_lut/quantizer.py:30-396 with the GPU doing the work: `train` (block
+    normalisation, then the k-means of `train_kmeans`; NESTEDLUT also the nested
+    tables), `quantize` (the REF codes of one weight tensor, `quantize(rule="quantizer")`),
+    `decompress` (the REF dequantisation kernel) and `save` / `load` of the codebooks.
+    Results of `quantize` are host tensors, as the reference returns them."""
+
+    def __init__(self, code_type: str = "BLOCKLUT", block_size: int = 128, lut_size: int = 256,
+                 device: str = "cuda"):
+        if code_type not in ("LUT", "BLOCKLUT", "NESTEDLUT"):
+            raise ValueError(f"Unsupported code_type: {code_type}")
+        self.code_type = code_type
+        self.block_size = block_size
+        self.lut_size = lut_size
+        self.device = device
+        self.lut_codebook: Optional[torch.Tensor] = None       # [256] bf16
+        self.nested_mapped64: Optional[torch.Tensor] = None    # [256] bf16
+        self.nested_mapped16: Optional[torch.Tensor] = None    # [256] bf16
+
+    def _normalised(self, flat: torch.Tensor) -> torch.Tensor:
+        """Block normalisation of quantizer.py:86-104 in the tensor's dtype."""
+        n = flat.numel()
+        nb = -(-n // self.block_size)
+        if nb * self.block_size != n:
+            flat = torch.cat([flat, flat.new_zeros(nb * self.block_size - n)])
+        blocks = flat.view(-1, self.block_size)
+        am = blocks.abs().amax(dim=1, keepdim=True).clamp(min=1e-10)
+        return (blocks / am).reshape(-1)
+
+    @torch.no_grad()
+    def train(self, expert_weights: torch.Tensor, n_iter: int = 50, seed: Optional[int] = None) -> None:
+        """Codebook(s) from expert weights [E, rows, cols] or any shape (quantizer.py:65-114)."""
+        flat = expert_weights.reshape(-1).to(self.device)
+        data = flat if self.code_type == "LUT" else self._normalised(flat)
+        self.lut_codebook = train_kmeans(data, self.lut_size, n_iter, seed=seed)
+        if self.code_type == "NESTEDLUT":
+            self.nested_mapped64, self.nested_mapped16 = train_nested_codebooks(data, n_iter, seed=seed)
+
+    @torch.no_grad()
+    def quantize(self, weight: torch.Tensor, codebook: Optional[torch.Tensor] = None) -> Dict[str, torch.Tensor]:
+        """{'indices': uint8 [N], 'absmax': bf16 [nb], 'codebook': bf16 [256]} on the host
+        (quantizer.py:242-306; the LUT code type normalises by one global absmax)."""
+        if codebook is None:
+            codebook = self.lut_codebook
+        if codebook is None:
+            raise RuntimeError("LUT codebook not trained or loaded. Call train() or load() first.")
+        w = weight.to(self.device)
+        bs = self.block_size if self.code_type != "LUT" else max(1, w.numel())
+        codes, absmax = quantize(w, codebook.to(torch.bfloat16), bs, rule="quantizer")
+        return {"indices": codes.cpu(), "absmax": absmax.cpu(), "codebook": codebook.to(torch.bfloat16).cpu()}
+
+    @torch.no_grad()
+    def decompress(self, indices: torch.Tensor, absmax: torch.Tensor, codebook: torch.Tensor,
+                   out_shape: Optional[Tuple[int, ...]] = None) -> torch.Tensor:
+        """bf16(codebook[index] * absmax[block]) on the GPU (quantizer.py:312-353); one
+        absmax entry scales every weight, as for the LUT code type."""
+        from .decompress import decompress_blocklut
+        dev = torch.device(self.device)
+        out = decompress_blocklut(indices.to(dev).reshape(-1), absmax.to(dev, torch.bfloat16).reshape(-1),
+                                  codebook.to(dev, torch.bfloat16), self.block_size)
+        return out.reshape(out_shape) if out_shape is not None else out
+
+    def save(self, path: str) -> None:
+        """The codebooks as .npy files with the reference's names (quantizer.py:359-371),
+        holding their float32 values (numpy has no bf16; `load` restores the bf16 values)."""
+        os.makedirs(path, exist_ok=True)
+        for t, name in ((self.lut_codebook, "blocklut_256.npy"), (self.nested_mapped64, "nested_lut_mapped64.npy"),
+                        (self.nested_mapped16, "nested_lut_mapped16.npy")):
+            if t is not None:
+                np.save(os.path.join(path, name), t.float().cpu().numpy())
+
+    def load(self, path: str) -> bool:
+        """quantizer.py:373-396: blocklut_256.npy (or full256.npy) and the optional nested
+        tables, as bf16.  False when no codebook file is there."""
+        for name in ("blocklut_256.npy", "full256.npy"):
+            f = os.path.join(path, name)
+            if os.path.exists(f):
+                self.lut_codebook = torch.from_numpy(np.load(f, allow_pickle=False)).to(torch.bfloat16)
+                break
+        else:
+            return False
+        for attr, name in (("nested_mapped64", "nested_lut_mapped64.npy"),
+                           ("nested_mapped16", "nested_lut_mapped16.npy")):
+            f = os.path.join(path, name)
+            if os.path.exists(f):
+                setattr(self, attr, torch.from_numpy(np.load(f, allow_pickle=False)).to(torch.bfloat16))
+        return True

@@ -310,6 +310,24 @@ int lutmoe_bl4_encode(const float* w_dev, int64_t nblocks, int n_iter, uint8_t* 
 int lutmoe_ref_encode(const void* w_bf16_dev, const float* codebook_dev, int64_t n, int block_size,
                       uint8_t* codes_dev, void* absmax_bf16_dev, void* stream);
 
+/* The reference's other two REF encoding rules (codes and bf16 absmax as
+ * lutmoe_ref_encode; blocks of block_size weights, the last one shorter):
+ *   LUTMOE_QRULE_QUANTIZER: LUTQuantizer.quantize (vllm_lut/quantizer.py:
+ *     242-306; block_size = n gives its global "LUT" branch): absmax = max |w|
+ *     in the weights' dtype, at least 1e-10; w / absmax rounded to bf16 when
+ *     the weights are bf16 (:284); code = first nearest of the n_entries
+ *     codebook values (fp32 [n_entries], any order) by |v - c|.
+ *   LUTMOE_QRULE_MIDPOINTS: the offload runtime's encoder
+ *     (runtime/model_offload.py:897-907): fp32 division, absmax at least
+ *     1e-12; code = number of fp32 midpoints (c_i + c_{i+1}) / 2 of the
+ *     ascending codebook (fp32 [n_entries], n_entries >= 2) below v (a value
+ *     on a midpoint takes the lower entry, NaN the last).
+ * w_dev: bf16 or fp32 [n] (w_dtype); n_entries <= 256. */
+#define LUTMOE_QRULE_QUANTIZER 0
+#define LUTMOE_QRULE_MIDPOINTS 1
+int lutmoe_ref_quantize(const void* w_dev, int w_dtype, const float* codebook_dev, int n_entries, int64_t n,
+                        int block_size, int rule, uint8_t* codes_dev, void* absmax_bf16_dev, void* stream);
+
 /* The Lloyd iterations of LUTQuantizer._train_kmeans (vllm_lut/quantizer.py:
  * 158-173) on the device: n_iter rounds of "each sample joins its nearest
  * centroid by |x - c| (first on equal distances), each centroid with members

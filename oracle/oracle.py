@@ -175,6 +175,27 @@ def ref_encode_fast(w_bf16_bits, codebook_f32, block_size: int = REF_BLOCK):
     return idx, f32_to_bf16(am)
 
 
+def ref_encode_midpoints(weight, sorted_codebook_f32, block_size: int = REF_BLOCK):
+    """The offload runtime's encoder (runtime/model_offload.py:897-907): fp32 weights in
+    blocks of block_size (the last one zero-padded, :899), absmax = max |w| at least
+    fp32(1e-12) (:900-901), v = w / absmax in fp32 (:902), code = np.searchsorted over the
+    fp32 midpoints (c_i + c_{i+1}) / 2 of the ascending codebook (:903-904).
+    Returns (indices uint8 [N], absmax bf16 bits [nb])."""
+    x = np.asarray(weight, np.float32).reshape(-1)
+    n = x.size
+    nb = -(-n // block_size)
+    pad = nb * block_size - n
+    if pad:
+        x = np.pad(x, (0, pad))
+    blocks = x.reshape(nb, block_size)
+    am = np.maximum(np.max(np.abs(blocks), axis=1), np.float32(1e-12))
+    v = (blocks / am[:, None]).astype(np.float32).reshape(-1)
+    cb = np.asarray(sorted_codebook_f32, np.float32)
+    mid = ((cb[:-1] + cb[1:]) / np.float32(2.0)).astype(np.float32)
+    idx = np.searchsorted(mid, v).astype(np.uint8)
+    return idx[:n], f32_to_bf16(am.astype(np.float32))
+
+
 def ref_dequant(indices, absmax_bf16, codebook_bf16, block_size: int = REF_BLOCK) -> np.ndarray:
     """decompress_blocklut (quantizer.py:449-477) == cuda_blocklut_recover_to_bf16
     (csrc/kernels/tensor_recover.cu:101-142): bf16(f32(cb[c]) * f32(absmax[blk]))."""

@@ -32,7 +32,7 @@ def test_header_declares_the_expected_surface():
                  "lutmoe_route_topk", "lutmoe_permute", "lutmoe_moe_forward",
                  "lutmoe_moe_forward_logits", "lutmoe_moe_workspace_size", "lutmoe_strerror",
                  "lutmoe_bl4_encode", "lutmoe_ref_encode", "lutmoe_merge_bitplane",
-                 "lutmoe_nested_group_planes"):
+                 "lutmoe_nested_group_planes", "lutmoe_ref_quantize"):
         assert must in names
 
 
@@ -122,6 +122,17 @@ def test_validation_before_any_hip_call(lib):
     assert lib.lutmoe_pack_bitplanes(P(1), 6, P(1), None) == N.LUTMOE_EINVAL
     assert lib.lutmoe_pack_bitplanes(None, 8, P(1), None) == N.LUTMOE_EINVAL
     assert lib.lutmoe_pack_bitplanes(None, 0, None, None) == N.LUTMOE_OK
+    # REF quantize rules: dtype, rule, entry count, pointers, alignment
+    q = lib.lutmoe_ref_quantize
+    assert q(P(0x100), 7, P(0x200), 256, 128, 128, 0, P(0x300), P(0x400), None) == N.LUTMOE_EINVAL
+    assert q(P(0x100), 0, P(0x200), 256, 128, 128, 2, P(0x300), P(0x400), None) == N.LUTMOE_EINVAL
+    assert q(P(0x100), 0, P(0x200), 257, 128, 128, 0, P(0x300), P(0x400), None) == N.LUTMOE_EINVAL
+    assert q(P(0x100), 0, P(0x200), 1, 128, 128, 1, P(0x300), P(0x400), None) == N.LUTMOE_EINVAL
+    assert q(P(0x100), 0, P(0x200), 256, 128, 0, 0, P(0x300), P(0x400), None) == N.LUTMOE_EINVAL
+    assert q(None, 0, P(0x200), 256, 128, 128, 0, P(0x300), P(0x400), None) == N.LUTMOE_EINVAL
+    assert q(P(0x102), 1, P(0x200), 256, 128, 128, 0, P(0x300), P(0x400), None) == N.LUTMOE_EALIGN
+    assert q(P(0x101), 0, P(0x200), 256, 128, 128, 0, P(0x300), P(0x400), None) == N.LUTMOE_EALIGN
+    assert q(None, 0, None, 256, 0, 128, 1, None, None, None) == N.LUTMOE_OK
     # nested plane grouping: n % 64 == 0, tier 2..4, pointers, 4-byte alignment
     assert lib.lutmoe_nested_group_planes(P(0x100), 4, 96, P(0x200), None) == N.LUTMOE_EINVAL
     assert lib.lutmoe_nested_group_planes(P(0x100), 5, 128, P(0x200), None) == N.LUTMOE_EINVAL

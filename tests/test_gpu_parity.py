@@ -830,6 +830,97 @@ def test_ref_encode_bit_exact(gpu, n, block_size, sorted_cb):
     assert torch.equal(c2, codes.cpu()) and torch.equal(a2, am.cpu())
 
 
+def test_ref_quantize_rule_on_golden_vectors(gpu):
+    """LUTQuantizer.quantize's rule on the GPU reproduces the vectors written from the
+    reference itself (tests/golden/quantizer.npz: fp32 weights, a padded tail with an
+    all-zero block, bf16 weights normalised in bf16) bit for bit, through both the
+    function and the LUTQuantizer class."""
+    import os
+    import torch
+    from block_lut_amd.quantizer import LUTQuantizer, quantize
+    qv = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "quantizer.npz"),
+                 allow_pickle=False)
+    cbb = golden_codebook()
+    cb = torch.from_numpy(cbb.view(np.int16)).view(torch.bfloat16)
+    for key, bf16 in (("q_f32", False), ("q_pad", False), ("q_bf16", True)):
+        w = qv[f"{key}_w"]
+        wt = (torch.from_numpy(w.view(np.int16)).view(torch.bfloat16) if bf16 else torch.from_numpy(w)).to(gpu)
+        codes, am = quantize(wt, cb, 128)
+        assert np.array_equal(codes.cpu().numpy(), qv[f"{key}_idx"]), key
+        assert np.array_equal(am.view(torch.int16).cpu().numpy().view(np.uint16), qv[f"{key}_absmax"]), key
+        r = LUTQuantizer("BLOCKLUT", device=str(gpu)).quantize(wt, cb)
+        assert np.array_equal(r["indices"].numpy(), qv[f"{key}_idx"]), key
+
+
+@pytest.mark.parametrize("n,block_size,k,bf16", [(128 * 37 + 51, 128, 256, True), (4096, 128, 40, False),
+                                                 (1000, 100, 256, False)])
+def test_ref_quantize_rules_bitexact(gpu, n, block_size, k, bf16):
+    """Both extra REF rules against the oracle, codes and bf16 absmax bit-identical:
+    'quantizer' (normalised in the weights' dtype, first nearest of an unsorted codebook)
+    and 'midpoints' (the offload runtime's searchsorted over an ascending codebook of k
+    entries); an all-zero block, weights on exact midpoints, a short last block."""
+    import torch
+    from block_lut_amd.quantizer import quantize
+    rng = np.random.default_rng(n + k)
+    cb = np.sort(rng.uniform(-1, 1, k).astype(np.float32))
+    w = rng.standard_normal(n).astype(np.float32) * 0.02
+    w[block_size:2 * block_size] = 0.0
+    mid = ((cb[:-1] + cb[1:]) / np.float32(2)).astype(np.float32)
+    w[2 * block_size:2 * block_size + 20] = mid[5:25]
+    w[2 * block_size + 20] = 1.0
+    if bf16:
+        w = O.bf16_to_f32(O.f32_to_bf16(w))
+        wt = torch.from_numpy(O.f32_to_bf16(w).view(np.int16)).view(torch.bfloat16).to(gpu)
+    else:
+        wt = torch.from_numpy(w).to(gpu)
+    cbq = O.f32_to_bf16(cb[rng.permutation(k)])          # unsorted bf16 codebook
+    c1, a1 = quantize(wt, torch.from_numpy(cbq.view(np.int16)).view(torch.bfloat16).to(gpu), block_size)
+    i1, b1 = O.ref_quantize(w, np.pad(cbq, (0, 0)), block_size, input_is_bf16=bf16)
+    assert np.array_equal(c1.cpu().numpy(), i1)
+    assert np.array_equal(a1.view(torch.int16).cpu().numpy().view(np.uint16), b1)
+    c2, a2 = quantize(wt, torch.from_numpy(cb).to(gpu), block_size, rule="midpoints")
+    i2, b2 = O.ref_encode_midpoints(w, cb, block_size)
+    assert np.array_equal(c2.cpu().numpy(), i2)
+    assert np.array_equal(a2.view(torch.int16).cpu().numpy().view(np.uint16), b2)
+
+
+def test_lut_quantizer_train_quantize_decompress(gpu, tmp_path):
+    """LUTQuantizer end to end on the GPU: train a BLOCKLUT codebook (sorted bf16 [256]),
+    quantize (codes = the golden-pinned oracle rule on that codebook), decompress (the
+    oracle's dequantisation), save / load round trip; the LUT code type normalises by one
+    global absmax; NESTEDLUT also builds its two 256-entry tables."""
+    import torch
+    from block_lut_amd.quantizer import LUTQuantizer
+    rng = np.random.default_rng(77)
+    w = torch.from_numpy((rng.standard_normal((4, 64, 96)) * 0.02).astype(np.float32))
+    q = LUTQuantizer("BLOCKLUT", device=str(gpu))
+    q.train(w.to(gpu), n_iter=10, seed=5)
+    cb = q.lut_codebook
+    assert cb.dtype == torch.bfloat16 and cb.numel() == 256
+    assert torch.all(cb.float()[1:] >= cb.float()[:-1])
+    wb = w[1].to(torch.bfloat16)
+    r = q.quantize(wb.to(gpu))
+    cbb = cb.view(torch.int16).numpy().view(np.uint16)
+    i, a = O.ref_quantize(O.bf16_to_f32(wb.view(torch.int16).numpy().view(np.uint16)), cbb, 128,
+                          input_is_bf16=True)
+    assert np.array_equal(r["indices"].numpy(), i) and np.array_equal(
+        r["absmax"].view(torch.int16).numpy().view(np.uint16), a)
+    d = q.decompress(r["indices"], r["absmax"], r["codebook"], out_shape=(64, 96))
+    assert np.array_equal(d.view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1), O.ref_dequant(i, a, cbb))
+    q.save(str(tmp_path))
+    q2 = LUTQuantizer("BLOCKLUT", device=str(gpu))
+    assert q2.load(str(tmp_path)) and torch.equal(q2.lut_codebook, cb)
+    g = LUTQuantizer("LUT", device=str(gpu))
+    rg = g.quantize(w[2].to(gpu), cb)
+    assert rg["absmax"].numel() == 1
+    ig, ag = O.ref_quantize(w[2].numpy().reshape(-1), cbb, w[2].numel())
+    assert np.array_equal(rg["indices"].numpy(), ig)
+    nq = LUTQuantizer("NESTEDLUT", device=str(gpu))
+    nq.train(w.to(gpu), n_iter=5, seed=2)
+    assert nq.nested_mapped64.numel() == 256 and nq.nested_mapped16.numel() == 256
+    assert torch.unique(nq.nested_mapped16).numel() <= 16
+
+
 def test_ref_encode_expert_size_roundtrip(gpu):
     """A whole Qwen W13 expert (5.77 M weights) encoded on the GPU: sampled blocks match the
     oracle, and the GPU dequantisation of the result is within the codebook's resolution."""

@@ -117,6 +117,38 @@ def test_ref_encode_fast_argmin_ties_and_zero_block():
     assert np.array_equal(cb[perm][pi], cb[first])
 
 
+def test_ref_encode_midpoints_nearest_and_lower_on_midpoints():
+    """The offload encoder's searchsorted rule: every index is a nearest entry of
+    w / absmax (brute force over the sorted codebook) except within one fp32 ulp of a
+    midpoint, where the fp32 midpoint decides; a value exactly on an fp32 midpoint takes
+    the lower entry; absmax is at least fp32(1e-12) (an all-zero block maps to the entry
+    nearest 0); the zero-padded tail block gives the same codes as the block alone; a
+    codebook shorter than 256 indexes only its own entries."""
+    rng = np.random.default_rng(31)
+    cb = np.sort(rng.standard_normal(256).astype(np.float32) * 0.4)
+    w = rng.standard_normal(128 * 9 + 77).astype(np.float32) * 0.02
+    idx, am = O.ref_encode_midpoints(w, cb, 128)
+    blocks = np.concatenate([w, np.zeros(128 * 10 - w.size, np.float32)]).reshape(10, 128)
+    amax = np.maximum(np.abs(blocks).max(1), np.float32(1e-12))
+    assert np.array_equal(am, O.f32_to_bf16(amax))
+    v = (blocks / amax[:, None]).astype(np.float32).reshape(-1)[:w.size]
+    d = np.abs(v[:, None].astype(np.float64) - cb[None, :].astype(np.float64))
+    mid = ((cb[:-1] + cb[1:]) / np.float32(2)).astype(np.float32)
+    near_mid = np.abs(v[:, None] - mid[None, :]).min(1) <= np.spacing(np.abs(v)) * 2
+    ok = d[np.arange(v.size), idx] <= d.min(1) * (1 + 1e-12)
+    assert np.all(ok | near_mid) and ok.mean() > 0.99
+    # exactly on midpoints (absmax 1 via a +-1 weight): the lower entry
+    on = np.concatenate([mid[40:80], np.float32([1.0, -1.0])])
+    oi, _ = O.ref_encode_midpoints(on, cb, 128)
+    assert np.array_equal(oi[:40], np.arange(40, 80))
+    zi, zam = O.ref_encode_midpoints(np.zeros(128, np.float32), cb, 128)
+    assert np.all(zi == np.abs(cb).argmin()) and zam[0] == O.f32_to_bf16(np.float32(1e-12))
+    ti, _ = O.ref_encode_midpoints(w[128 * 9:], cb, 128)
+    assert np.array_equal(ti, idx[128 * 9:])
+    si, _ = O.ref_encode_midpoints(w, cb[::16], 128)
+    assert si.max() <= 15
+
+
 def test_bitplane_pack_roundtrip_all_codes():
     codes = np.tile(np.arange(256, dtype=np.uint8), 4)
     packed = O.bitplane_pack_ref(codes)
