@@ -20,7 +20,7 @@ from . import _native as N
 from .formats import _dev, _stream
 
 __all__ = ["train_kmeans", "greedy_merge", "build_mapped_table", "train_nested_codebooks", "quantize",
-           "LUTQuantizer"]
+           "LUTQuantizer", "cluster_counts", "merge_map", "merge_map_tables"]
 
 
 def train_kmeans(data: torch.Tensor, k: int = 256, n_iter: int = 20, max_samples: int = 200000,
@@ -220,3 +220,82 @@ class LUTQuantizer:
             if os.path.exists(f):
                 setattr(self, attr, torch.from_numpy(np.load(f, allow_pickle=False)).to(torch.bfloat16))
         return True
+
+
+# ---------------------------------------------------------------- merge-map nested tables
+# evaluation/generate_nested_lut.py:93-176, 264-269: the 256 sorted centroids are merged
+# greedily into K of them (adjacent pairs, cheapest weighted-MSE increase first), and the
+# tier-K table is indexed by the full 8-bit code through a 256 -> K map.
+
+def cluster_counts(data: torch.Tensor, centroids: torch.Tensor) -> np.ndarray:
+    """Samples per centroid (nearest of the ascending `centroids`, the lower one on a
+    midpoint), counted on `data`'s device: the weights of generate_nested_lut.py:68-85."""
+    c = centroids.reshape(-1).to(data.device, torch.float32)
+    mid = (c[:-1] + c[1:]) * 0.5
+    idx = torch.bucketize(data.reshape(-1).float(), mid)
+    return torch.bincount(idx, minlength=c.numel()).cpu().numpy().astype(np.int64)
+
+
+def merge_map(centroids, counts, target_k: int):
+    """generate_nested_lut.greedy_merge (:93-176) on the host.  Returns (merged centroids
+    float32 [K'], their counts int64 [K'], map uint8 [K] original index -> merged index).
+
+    The reference's effective rules, kept because its shipped tables follow them:
+      * the candidate adjacent pairs live in a priority queue ordered by (cost, left index,
+        right index), cost = w_a w_b (c_a - c_b)^2 / (w_a + w_b) in float64; a popped pair
+        is taken when both ends are alive and adjacent, so a pair whose left end grew since
+        it was queued can still be taken at its old cost;
+      * the right end merges into the left (weighted mean, summed weight); the left keeps
+        its index;
+      * a merged-away index maps to the first surviving index at or to its right (the
+        last survivor if none), i.e. to the group after the one that absorbed it."""
+    import heapq
+    c = np.asarray(centroids, np.float64).reshape(-1).copy()
+    w = np.asarray(counts, np.float64).reshape(-1).copy()
+    K = c.size
+    if target_k >= K:
+        return c.astype(np.float32), w.astype(np.int64), np.arange(K, dtype=np.uint8)
+    alive = np.ones(K, bool)
+    right = np.arange(1, K + 1)        # next alive index (K = none)
+    left = np.arange(-1, K - 1)        # previous alive index (-1 = none)
+
+    def cost(a, b):
+        return w[a] * w[b] * (c[a] - c[b]) ** 2 / (w[a] + w[b])
+
+    queue = [(cost(a, a + 1), a, a + 1) for a in range(K - 1)]
+    heapq.heapify(queue)
+    for _ in range(K - target_k):
+        while queue:
+            _, a, b = heapq.heappop(queue)
+            if alive[a] and alive[b] and right[a] == b:
+                break
+        else:
+            break
+        c[a] = (w[a] * c[a] + w[b] * c[b]) / (w[a] + w[b])
+        w[a] += w[b]
+        alive[b] = False
+        right[a] = right[b]
+        if right[a] < K:
+            left[right[a]] = a
+        if left[a] >= 0 and alive[left[a]]:
+            heapq.heappush(queue, (cost(left[a], a), left[a], a))
+        if right[a] < K and alive[right[a]]:
+            heapq.heappush(queue, (cost(a, right[a]), a, right[a]))
+    surv = np.flatnonzero(alive)
+    rank = np.searchsorted(surv, np.arange(K))                 # first survivor at or right of i
+    mapping = np.where(rank < surv.size, rank, surv.size - 1)
+    # none at or right of i: the nearest to its left (the last survivor)
+    return c[surv].astype(np.float32), w[surv].astype(np.int64), mapping.astype(np.uint8)
+
+
+def merge_map_tables(centroids, counts, ks=(64, 16)) -> Dict[int, Dict[str, np.ndarray]]:
+    """For each K in `ks`: {'lut': float32 [K], 'map': uint8 [256], 'mapped': bf16 bits
+    uint16 [256] = bf16(lut[map])}, the nested_lut_K / nested_map_256toK /
+    nested_lut_mappedK files of generate_nested_lut.py:264-269, from the 256 ascending
+    centroids and their counts."""
+    out = {}
+    for k in ks:
+        lut, _, mp = merge_map(centroids, counts, k)
+        mapped = torch.from_numpy(lut[mp.astype(np.int64)]).to(torch.bfloat16).view(torch.int16).numpy()
+        out[k] = {"lut": lut, "map": mp, "mapped": mapped.view(np.uint16)}
+    return out
