@@ -135,29 +135,9 @@ __device__ __forceinline__ bf16x8_t lookup8_ref(uint32_t w0, uint32_t w1, const 
     return __builtin_bit_cast(bf16x8_t, make_uint4(o[0], o[1], o[2], o[3]));
 }
 
-// One lane's B operand for one K step: its two weight rows (n-tiles), the
-// 32 columns 32h .. 32h+31 of the 64-column block kb.
-template <int kFmt>
-struct BStep;
-
-template <>
-struct BStep<LUTMOE_FMT_BL4> {
-    u32x4_t codes[2];     // 32 nibble codes per row
-    u32x4_t tab[2][2];    // the row's bf16[16] table of block kb
-    __device__ __forceinline__ void load(const uint8_t* codes_e, const uint8_t* tabs_e, const int (&row)[2],
-                                         int K, int kb, int bh) {
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-            const int64_t off = (int64_t)row[nt] * (K / 2) + kb * 32;
-            codes[nt] = *reinterpret_cast<const u32x4_t*>(codes_e + off + 16 * bh);
-            tab[nt][0] = *reinterpret_cast<const u32x4_t*>(tabs_e + off);
-            tab[nt][1] = *reinterpret_cast<const u32x4_t*>(tabs_e + off + 16);
-        }
-    }
-};
-
-template <>
-struct BStep<LUTMOE_FMT_REF> {
+// One lane's REF B operand for one K step: its two weight rows (n-tiles),
+// the 32 columns 32h .. 32h+31 of the 64-column block kb.
+struct RefBStep {
     u32x4_t codes[2][2];  // 32 byte codes per row
     float am[2];          // absmax of the row's 128-block holding these columns
     __device__ __forceinline__ void load(const uint8_t* codes_e, const uint16_t* absmax_e, const int (&row)[2],
@@ -174,37 +154,12 @@ struct BStep<LUTMOE_FMT_REF> {
     }
 };
 
-// NestedLUT: the lane's 32 columns of each row (one 32-weight group of the
-// device layout; a 16-byte load that, below tier 4, also reads the next
-// group's bytes, dropped here), and the first 32 bytes of the row's block-kb
-// table (the first 2^(b+1) are the tier's entries; codes never reach the
-// rest).
-template <>
-struct BStep<LUTMOE_FMT_NESTED> {
-    uint32_t f01[2][2], f2[2], f3[2];
-    u32x4_t tab[2][2];
-    __device__ __forceinline__ void load(const NestedView& v, const int (&row)[2], int K, int kb, int bh) {
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-            const uint32_t blk0 = (uint32_t)row[nt] * (uint32_t)K + (uint32_t)kb * kBK;
-            const uint32_t i0 = blk0 + 32u * bh;
-            const auto q = __builtin_amdgcn_raw_buffer_load_b128(v.codes, (int)(i0 / 32 * (4u * v.bits)), 0, 0);
-            f01[nt][0] = q[0];
-            f01[nt][1] = q[1];
-            f2[nt] = v.bits >= 3 ? q[2] : 0u;
-            f3[nt] = v.bits >= 4 ? q[3] : 0u;
-            const uint32_t tofs = (blk0 >> 6) << (v.bits + 1);
-            tab[nt][0] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(v.table, (int)tofs, 0, 0));
-            tab[nt][1] =
-                __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(v.table, (int)tofs + 16, 0, 0));
-        }
-    }
-};
-
-// One tile with NMT m-tiles of work (a compile-time count, so the K loop is
-// one basic block with no per-m-tile branches).
-template <bool kGateUp, int kFmt, int NMT>
-__device__ __forceinline__ void prefill_tile(const lutmoe_moe_desc& d, const uint16_t* __restrict__ src,
+// One REF tile with register-staged operands (for REF stacks the ring cannot
+// address: an odd absmax count per expert, or tables not 4-byte aligned),
+// NMT m-tiles of work (a compile-time count, so the K loop is one basic block
+// with no per-m-tile branches).
+template <bool kGateUp, int NMT>
+__device__ __forceinline__ void prefill_tile_ref(const lutmoe_moe_desc& d, const uint16_t* __restrict__ src,
                                              const MoeRouting& rt, void* __restrict__ dst,
                                              const TileInfo ti, uint16_t (*s_a)[kBM * kAStride],
                                              const float* s_cb) {
@@ -234,26 +189,10 @@ __device__ __forceinline__ void prefill_tile(const lutmoe_moe_desc& d, const uin
         b_row[0] = min(n0 + 64 * wv + bn, H - 1);
         b_row[1] = min(n0 + 64 * wv + 32 + bn, H - 1);
     }
-    const uint8_t* codes = nullptr;
-    const void* tabs = nullptr;
-    NestedView nv;
-    if constexpr (kFmt == LUTMOE_FMT_NESTED) {
-        nv = nested_view(w, ti.e);
-    } else if constexpr (kFmt == LUTMOE_FMT_BL4) {
-        const int64_t per = (int64_t)w.rows * (w.cols / 2);
-        codes = (const uint8_t*)w.codes + ti.e * per;
-        tabs = (const uint8_t*)w.tables + ti.e * per;
-    } else {
-        codes = (const uint8_t*)w.codes + (int64_t)ti.e * w.rows * w.cols;
-        tabs = (const uint16_t*)w.tables + (int64_t)ti.e * w.absmax_per_expert;
-    }
-    auto load_b = [&](BStep<kFmt>& b, int kb) __attribute__((always_inline)) {
-        if constexpr (kFmt == LUTMOE_FMT_NESTED)
-            b.load(nv, b_row, K, kb, bh);
-        else if constexpr (kFmt == LUTMOE_FMT_BL4)
-            b.load(codes, (const uint8_t*)tabs, b_row, K, kb, bh);
-        else
-            b.load(codes, (const uint16_t*)tabs, b_row, K, kb, bh, w.block_size, w.absmax_per_expert);
+    const uint8_t* codes = (const uint8_t*)w.codes + (int64_t)ti.e * w.rows * w.cols;
+    const uint16_t* absmax = (const uint16_t*)w.tables + (int64_t)ti.e * w.absmax_per_expert;
+    auto load_b = [&](RefBStep& b, int kb) __attribute__((always_inline)) {
+        b.load(codes, absmax, b_row, K, kb, bh, w.block_size, w.absmax_per_expert);
     };
     u32x4_t ra[8];
     auto load_a = [&](int kb) __attribute__((always_inline)) {
@@ -274,26 +213,11 @@ __device__ __forceinline__ void prefill_tile(const lutmoe_moe_desc& d, const uin
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[mt][nt][i] = 0.f;
 
-    auto frag_b = [&](const RegTable16 (&tb)[2], const BStep<kFmt>& b, int ks, bf16x8_t (&bf)[2])
-        __attribute__((always_inline)) {
+    auto frag_b = [&](const RefBStep& b, int ks, bf16x8_t (&bf)[2]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-            if constexpr (kFmt == LUTMOE_FMT_NESTED) {
-                const uint32_t wd = nested_code8(b.f01[nt][0], b.f01[nt][1], b.f2[nt], b.f3[nt], ks);
-                bf[nt] = __builtin_bit_cast(bf16x8_t, lookup8_reg(tb[nt], wd));
-            } else if constexpr (kFmt == LUTMOE_FMT_BL4) {
-                bf[nt] = __builtin_bit_cast(bf16x8_t, lookup8_reg(tb[nt], b.codes[nt][ks]));
-            } else {
-                bf[nt] = lookup8_ref(b.codes[nt][ks >> 1][2 * (ks & 1)], b.codes[nt][ks >> 1][2 * (ks & 1) + 1],
-                                     s_cb, b.am[nt]);
-            }
-        }
-    };
-    auto split = [&](const BStep<kFmt>& b, RegTable16 (&tb)[2]) __attribute__((always_inline)) {
-        if constexpr (kFmt != LUTMOE_FMT_REF) {
-            tb[0] = split_table16(b.tab[0][0], b.tab[0][1]);
-            tb[1] = split_table16(b.tab[1][0], b.tab[1][1]);
-        }
+        for (int nt = 0; nt < 2; ++nt)
+            bf[nt] = lookup8_ref(b.codes[nt][ks >> 1][2 * (ks & 1)], b.codes[nt][ks >> 1][2 * (ks & 1) + 1], s_cb,
+                                 b.am[nt]);
     };
     auto frag_a = [&](int buf, int ks, bf16x8_t (&af)[NMT]) __attribute__((always_inline)) {
 #pragma unroll
@@ -303,20 +227,18 @@ __device__ __forceinline__ void prefill_tile(const lutmoe_moe_desc& d, const uin
 
     // Software pipeline.  Entering step kb: A(kb) in LDS buffer kb&1 (visible
     // after the last barrier), A(kb+1) in flight to registers `ra`, the B
-    // operand of step kb in `bcur` (tables already split into `tb`), of step
-    // kb+1 in flight to `bnext`, and the step-kb fragments of k-substep 0 in
-    // bf/af.  Each k-substep computes the next substep's fragments while its
-    // MFMAs issue; substep 3 prepares step kb+1's B side.
-    BStep<kFmt> bcur, bnext;
-    RegTable16 tb[2];
+    // operand of step kb in `bcur`, of step kb+1 in flight to `bnext`, and the
+    // step-kb fragments of k-substep 0 in bf/af.  Each k-substep computes the
+    // next substep's fragments while its MFMAs issue; substep 3 prepares step
+    // kb+1's B side.
+    RefBStep bcur, bnext;
     load_a(0);
     load_b(bcur, 0);
     store_a(0);
     load_a(min(1, nkb - 1));
     load_b(bnext, min(1, nkb - 1));
-    split(bcur, tb);
     bf16x8_t bf[2], af[NMT];
-    frag_b(tb, bcur, 0, bf);
+    frag_b(bcur, 0, bf);
     __syncthreads();
     frag_a(0, 0, af);
 
@@ -335,12 +257,8 @@ __device__ __forceinline__ void prefill_tile(const lutmoe_moe_desc& d, const uin
             bf16x8_t bf_n[2], af_n[NMT];
             if (ks < 3) frag_a(buf, ks + 1, af_n);
             __builtin_amdgcn_sched_barrier(0);
-            if (ks < 3) {
-                frag_b(tb, bcur, ks + 1, bf_n);
-            } else {
-                split(bnext, tb);
-                frag_b(tb, bnext, 0, bf_n);
-            }
+            if (ks < 3) frag_b(bcur, ks + 1, bf_n);
+            else frag_b(bnext, 0, bf_n);
 #pragma unroll
             for (int mt = 0; mt < NMT; ++mt)
 #pragma unroll
@@ -941,22 +859,19 @@ __global__ __launch_bounds__(256, 1) void prefill_ring_kernel(lutmoe_moe_desc d,
     }
 }
 
-template <bool kGateUp, int kFmt>
-__global__ __launch_bounds__(256, 1) void prefill_kernel(lutmoe_moe_desc d,
-                                                         const uint16_t* __restrict__ src,
-                                                         MoeRouting rt, void* __restrict__ dst, int ncu) {
+template <bool kGateUp>
+__global__ __launch_bounds__(256, 1) void prefill_ref_kernel(lutmoe_moe_desc d, const uint16_t* __restrict__ src,
+                                                             MoeRouting rt, void* __restrict__ dst, int ncu) {
     __shared__ __attribute__((aligned(16))) uint16_t s_a[2][kBM * kAStride];
-    __shared__ float s_cb[kFmt == LUTMOE_FMT_REF ? 256 : 1];
+    __shared__ float s_cb[256];
     const TileInfo ti = find_tile(rt, blockIdx.y, ncu);
     if (ti.e < 0) return;
-    if (kFmt == LUTMOE_FMT_REF) {
-        const uint16_t* cb = ref_codebook(kGateUp ? d.w13 : d.w2, ti.e);
-        s_cb[threadIdx.x] = bf16_to_f32(cb[threadIdx.x]);
-    }
+    const uint16_t* cb = ref_codebook(kGateUp ? d.w13 : d.w2, ti.e);
+    s_cb[threadIdx.x] = bf16_to_f32(cb[threadIdx.x]);
     const int nmt = (min(kBM, ti.n - ti.m0) + 31) / 32;
     switch (nmt) {
 #define LUTMOE_TILE_CASE(n) \
-    case n: prefill_tile<kGateUp, kFmt, n>(d, src, rt, dst, ti, s_a, s_cb); break;
+    case n: prefill_tile_ref<kGateUp, n>(d, src, rt, dst, ti, s_a, s_cb); break;
         LUTMOE_TILE_CASE(1) LUTMOE_TILE_CASE(2) LUTMOE_TILE_CASE(3) LUTMOE_TILE_CASE(4)
         LUTMOE_TILE_CASE(5) LUTMOE_TILE_CASE(6) LUTMOE_TILE_CASE(7) LUTMOE_TILE_CASE(8)
 #undef LUTMOE_TILE_CASE
@@ -1014,7 +929,7 @@ int launch_prefill_gate_up(const lutmoe_moe_desc* d, const uint16_t* x, const Mo
         hipLaunchKernelGGL((prefill_ring_kernel<true, LUTMOE_FMT_REF>), grid, dim3(256), 0, s, *d, x, r, (void*)act,
                            ncu, (int64_t)0);
     else if (d->w13.format == LUTMOE_FMT_REF)
-        hipLaunchKernelGGL((prefill_kernel<true, LUTMOE_FMT_REF>), grid, dim3(256), 0, s, *d, x, r, (void*)act, ncu);
+        hipLaunchKernelGGL((prefill_ref_kernel<true>), grid, dim3(256), 0, s, *d, x, r, (void*)act, ncu);
     else if (d->w13.format == LUTMOE_FMT_NESTED)
         hipLaunchKernelGGL((prefill_ring_kernel<true, LUTMOE_FMT_NESTED>), grid, dim3(256), 0, s, *d, x, r,
                            (void*)act, ncu, (int64_t)0);
@@ -1043,7 +958,7 @@ int launch_prefill_down(const lutmoe_moe_desc* d, const uint16_t* act, const Moe
         hipLaunchKernelGGL((prefill_ring_kernel<false, LUTMOE_FMT_REF>), grid, dim3(256), 0, s, *d, act, r,
                            (void*)y_pos, ncu_tail, stride);
     else if (d->w2.format == LUTMOE_FMT_REF)
-        hipLaunchKernelGGL((prefill_kernel<false, LUTMOE_FMT_REF>), grid, dim3(256), 0, s, *d, act, r, (void*)y_pos,
+        hipLaunchKernelGGL((prefill_ref_kernel<false>), grid, dim3(256), 0, s, *d, act, r, (void*)y_pos,
                            ncu);
     else if (d->w2.format == LUTMOE_FMT_NESTED)
         hipLaunchKernelGGL((prefill_ring_kernel<false, LUTMOE_FMT_NESTED>), grid, dim3(256), 0, s, *d, act, r,

@@ -182,67 +182,6 @@ __device__ __forceinline__ uint32_t nested_code1(uint32_t f0, uint32_t f1, uint3
            (((b3 >> (4 * n + q)) & 1u) << 3);
 }
 
-// A 16-entry bf16 table held in registers as byte planes: lo[q] = low bytes
-// of entries 4q..4q+3, hi[q] = their high bytes.  Lookups are v_perm_b32 byte
-// selects (bytes 0-3 of the 8-byte source come from the second operand),
-// so they use no LDS.
-struct RegTable16 {
-    uint32_t lo[4], hi[4];
-};
-
-// t0 = entries 0..7, t1 = entries 8..15 (two bf16 per dword, even entry low).
-__device__ __forceinline__ RegTable16 split_table16(u32x4_t t0, u32x4_t t1) {
-    RegTable16 r;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const uint32_t a = q < 2 ? t0[2 * q] : t1[2 * q - 4];
-        const uint32_t b = q < 2 ? t0[2 * q + 1] : t1[2 * q - 3];
-        r.lo[q] = __builtin_amdgcn_perm(b, a, 0x06040200u);
-        r.hi[q] = __builtin_amdgcn_perm(b, a, 0x07050301u);
-    }
-    return r;
-}
-
-// Four table lookups: selector bytes `sel` (= code & 7) pick from planes 0,1
-// (codes 0..7) and planes 2,3 (codes 8..15); `mask` (0xff in each byte whose
-// code is >= 8) chooses between them.  Out: the entries' low and high bytes.
-__device__ __forceinline__ void lookup4_planes(const RegTable16& t, uint32_t sel, uint32_t mask,
-                                               uint32_t& lo, uint32_t& hi) {
-    const uint32_t l01 = __builtin_amdgcn_perm(t.lo[1], t.lo[0], sel);
-    const uint32_t l23 = __builtin_amdgcn_perm(t.lo[3], t.lo[2], sel);
-    const uint32_t h01 = __builtin_amdgcn_perm(t.hi[1], t.hi[0], sel);
-    const uint32_t h23 = __builtin_amdgcn_perm(t.hi[3], t.hi[2], sel);
-    lo = (mask & l23) | (~mask & l01);
-    hi = (mask & h23) | (~mask & h01);
-}
-
-// One BL4 code dword (8 nibbles = 8 consecutive weights, even weight in the
-// low nibble) -> 8 bf16 weights in column order, from a register table.
-// Bit 3 of an odd column's code is the sign bit of its byte, of an even
-// column's code the sign bit after a 4-bit left shift; v_perm selectors
-// 8/9/10/11 replicate the sign of bytes 1/3/5/7 of its 8-byte source, which
-// turns those bits into the byte masks in one instruction each.
-__device__ __forceinline__ u32x4_t lookup8_reg(const RegTable16& t, uint32_t w) {
-    const uint32_t sel_e = w & 0x07070707u;           // columns 0,2,4,6
-    const uint32_t sel_o = (w >> 4) & 0x07070707u;    // columns 1,3,5,7
-    const uint32_t w4 = w << 4;
-    const uint32_t m_o = __builtin_amdgcn_perm(w, w << 8, 0x0b090a08u);
-    const uint32_t m_e = __builtin_amdgcn_perm(w4, w4 << 8, 0x0b090a08u);
-    uint32_t le, he, lo_, ho;
-    lookup4_planes(t, sel_e, m_e, le, he);
-    lookup4_planes(t, sel_o, m_o, lo_, ho);
-    const uint32_t e0 = __builtin_amdgcn_perm(he, le, 0x05010400u);    // cols 0,2
-    const uint32_t e1 = __builtin_amdgcn_perm(he, le, 0x07030602u);    // cols 4,6
-    const uint32_t o0 = __builtin_amdgcn_perm(ho, lo_, 0x05010400u);   // cols 1,3
-    const uint32_t o1 = __builtin_amdgcn_perm(ho, lo_, 0x07030602u);   // cols 5,7
-    u32x4_t r;
-    r[0] = __builtin_amdgcn_perm(o0, e0, 0x05040100u);
-    r[1] = __builtin_amdgcn_perm(o0, e0, 0x07060302u);
-    r[2] = __builtin_amdgcn_perm(o1, e1, 0x05040100u);
-    r[3] = __builtin_amdgcn_perm(o1, e1, 0x07060302u);
-    return r;
-}
-
 // Full-wave sum with DPP (quad perms, half-row / row mirrors, row broadcasts);
 // the total is returned uniformly (read from lane 63).
 __device__ __forceinline__ float wave_reduce(float v) {
