@@ -1146,32 +1146,8 @@ __global__ __launch_bounds__(64 * kGuWaves, TB <= 2 ? 3 : 2) void bl4_decode_gat
         if constexpr (kPre) {
             gate_up_body4<TB>(A, GlobalRouteView{A.route}, s_slot);
         } else {
+            // (one token with H <= 2048 runs bl4_decode_gate_up_t1 instead)
             const bool pub = blockIdx.x == 0 && blockIdx.y == 0;
-            if (!pub && A.T == 1 && A.d.hidden <= kWChunk) {
-                // kernel arguments and the token's activations first, then the
-                // slot's expert, then the weights
-                const int lane = threadIdx.x & 63;
-                const uint8_t* wcodes = (const uint8_t*)A.d.w13.codes;
-                const uint8_t* wtabs = (const uint8_t*)A.d.w13.tables;
-                const int64_t per = (int64_t)A.d.w13.rows * (A.d.hidden / 2);
-                asm volatile("" ::"s"(wcodes), "s"(wtabs), "s"(per));
-                uint32_t xs[16];
-                const uint16_t* xp = A.x + (32 * lane < A.d.hidden ? 32 * lane : 0);
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const uint4 v = *reinterpret_cast<const uint4*>(xp + 8 * q);
-                    xs[4 * q + 0] = v.x;
-                    xs[4 * q + 1] = v.y;
-                    xs[4 * q + 2] = v.z;
-                    xs[4 * q + 3] = v.w;
-                }
-                const int e = t1_slot_expert(A, blockIdx.y);
-                if (e != -2) {
-                    if (e >= 0 && blockIdx.x * 2 < A.d.inter)
-                        gate_up_t1(A, xs, wcodes, wtabs, per, e, blockIdx.y, blockIdx.x, s_slot);
-                    return;
-                }
-            }
             const WaveRoute r = pub ? wave_pairs<true>(A) : wave_pairs<false>(A);
             if (pub && threadIdx.x < 64) wave_route_publish(A, r);
             gate_up_body4<TB>(A, WaveRouteView{r}, s_slot);
