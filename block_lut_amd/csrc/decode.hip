@@ -1701,7 +1701,7 @@ __global__ __launch_bounds__(256, 2) void nested_gemv_kernel(lutmoe_weights w, i
 // pass would spend its FMAs and activation loads on empty positions (Qwen
 // shape, MI355X: 2-token passes take T=4/8/16 from 58/85/121 to 50/72/108 us
 // per layer; at T=32 4-token passes stay ahead, 159 vs 173 us).  The nested
-// kernels lose with 2-token passes at T=16 (127 -> 140 us) and keep 4.
+// kernels lose with 2-token passes at T=16 (113 -> 136 us) and keep 4.
 inline int tb_for(int T, int fmt_idx) { return T <= 1 ? 1 : T <= (fmt_idx == 0 ? 16 : 2) ? 2 : 4; }
 
 }  // namespace
