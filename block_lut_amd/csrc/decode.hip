@@ -1284,9 +1284,10 @@ __global__ __launch_bounds__(256, TB <= 2 ? 3 : 2) void bl4_decode_down(DecodeAr
 }
 
 // One token (T = 1), BL4: CTA x covers output rows [4x, 4x + 4); wave wv takes
-// the active slots wv, wv + 4, .. (one position each, position = slot).  An
-// expert's 4 rows are contiguous in memory (K/2 code bytes and K/2 table bytes
-// per row), so they are walked as one flat array of 16-byte units: unit u
+// the active slots wv, wv + 4, .. (one position each, unless the token lists
+// the expert more than once).  An expert's 4 rows are contiguous in memory
+// (K/2 code bytes and K/2 table bytes per row), so they are walked as one
+// flat array of 16-byte units: unit u
 // covers columns [32g, 32g + 32) of row u / NU (NU = K/32, g = u % NU), and
 // lane l takes units l, l + 64, .. (kPass passes).  Every lane works whatever
 // K is (K = 1408: 176 units in 3 passes, where a row per pass leaves 20 of 64
@@ -1308,7 +1309,7 @@ __global__ __launch_bounds__(256, 2) void bl4_decode_down1(DecodeArgs A) {
     // first slot's expert and position (in bounds for any count), and the
     // positions of the token's pairs for the combine
     const int nact = R->nact;
-    int e_next = R->act[wv], p_next = R->aoff[wv];
+    int e_next = R->act[wv], p_next = R->aoff[wv], n_next = R->an[wv];
     const int inv_l = (wv == 0 && lane < ke) ? R->inv[lane] : -1;
     const int64_t per = (int64_t)A.d.w2.rows * (K / 2);
     const int64_t rbase = (int64_t)h0 * (K / 2);
@@ -1321,7 +1322,7 @@ __global__ __launch_bounds__(256, 2) void bl4_decode_down1(DecodeArgs A) {
     const uint32_t tab0 = lds_addr(slot) + ((lane >> 1) << 5);
     const u32x4_t z = {0u, 0u, 0u, 0u};
     for (int a = wv; a < nact; a += 4) {
-        const int e = e_next, p0 = p_next;
+        const int e = e_next, p0 = p_next, n = n_next;
         const int pair = R->perm[p0];   // its weight is loaded after the weight loads
         const uint8_t* codes = wcodes + e * per + rbase;
         const uint8_t* tabs = wtabs + e * per + rbase;
@@ -1355,6 +1356,7 @@ __global__ __launch_bounds__(256, 2) void bl4_decode_down1(DecodeArgs A) {
         if (a + 4 < kMaxEtot) {
             e_next = R->act[a + 4];
             p_next = R->aoff[a + 4];
+            n_next = R->an[a + 4];
         }
         float acc[kPass];
 #pragma unroll
@@ -1386,7 +1388,12 @@ __global__ __launch_bounds__(256, 2) void bl4_decode_down1(DecodeArgs A) {
         v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4e, 0xf, 0xf, false));
         v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xf, 0xf, false));
         v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xf, 0xf, false));
-        if (j == 0) s_y[p0][r] = v * pw;
+        if (j == 0) {
+            s_y[p0][r] = v * pw;
+            // an expert the token lists more than once: its other positions
+            // hold the same activations (one token), each with its own weight
+            for (int q = 1; q < n; ++q) s_y[p0 + q][r] = v * R->pw[R->perm[p0 + q]];
+        }
         wave_lds_sync();   // the slot is restaged by the next active slot
     }
     __syncthreads();

@@ -642,11 +642,13 @@ def moe_layer(x_bf16, ids, weights, w13_f32, w2_f32, shared=None, act_round_bf16
             a = bf16_to_f32(f32_to_bf16(a))
         return a.astype(np.float64) @ W2.astype(np.float64).T
 
-    def acc(rows, y):   # rows are distinct: top-k picks distinct experts per token
+    def acc(rows, y):
+        # a token listing an expert twice adds both pairs, as the reference's loop
+        # over the k slots does (vllm_lut/fast_moe.py:58-61)
         nonlocal out
         if out is None:
             out = np.zeros((T, y.shape[1]), np.float64)
-        out[rows] += y
+        np.add.at(out, rows, y)
 
     for e in np.unique(ids):
         tok, slot = np.nonzero(ids == e)

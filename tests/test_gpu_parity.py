@@ -431,6 +431,30 @@ def test_moe_layer(gpu, fmt, T, path):
     assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
 
 
+@pytest.mark.parametrize("fmt,T,path", [("bl4", 1, 1), ("bl4", 2, 1), ("bl4", 3, 1), ("bl4", 3, 2),
+                                        ("ref", 1, 1), ("ref", 2, 1), ("ref", 3, 1)])
+def test_moe_layer_repeated_ids(gpu, fmt, T, path):
+    """Caller-given ids that list an expert twice for one token: both pairs count, each with
+    its weight, as the reference's loop over the k slots adds them (vllm_lut/fast_moe.py:
+    58-61).  One token takes the one-token kernels' fallback routing (a slot with two
+    positions)."""
+    import torch
+    from block_lut_amd import ops
+    from block_lut_amd.formats import MoEWeights
+    E, S, k, H, I = 8, 1, 3, 512, 320
+    w13, w2 = _moe_case(fmt, E, S, H, I, seed=70 + T)
+    moe = MoEWeights(w13.stack(gpu), w2.stack(gpu), H, I, E, S)
+    rng = np.random.default_rng(700 + T)
+    xb = _x(rng, T, H)
+    rids = np.array([[5, 2, 5], [1, 1, 7], [3, 6, 3]], np.int32)[:T]
+    rw = rng.uniform(0.1, 1.0, size=(T, k)).astype(np.float32)
+    out = ops.moe_forward(moe, to_dev_bf16(xb, gpu), torch.from_numpy(rw).to(gpu),
+                          torch.from_numpy(rids).to(gpu), out_dtype=torch.float32, path=path)
+    f13, f2 = _ref_semantics(w13, w2, T, path) if fmt == "ref" else (w13.deq_f32, w2.deq_f32)
+    ref = O.moe_layer(xb, rids, rw, f13, f2, shared=[(f13(E + s), f2(E + s)) for s in range(S)])
+    assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
+
+
 @pytest.mark.parametrize("fmt,T", [("bl4", 16), ("bl4", 40), ("ref", 16), ("nested", 16)])
 def test_moe_layer_skewed_routing(gpu, fmt, T):
     """Decode with one heavily routed expert: every token picks expert 0 plus k-1 others, so

@@ -353,13 +353,20 @@ def test_permute_brute_force():
     assert np.array_equal(np.diff(off), np.bincount(ids.reshape(-1), minlength=E))
 
 
-def test_moe_layer_loop_vs_dense_restatement():
+@pytest.mark.parametrize("repeats", [False, True])
+def test_moe_layer_loop_vs_dense_restatement(repeats):
+    """The per-expert grouping of oracle.moe_layer against a dense sum over all experts
+    weighted by sum_k w[t,k] [ids[t,k] == e].  With repeats, tokens list an expert twice
+    (ids the caller passes): both pairs count, as the reference's loop over the k slots
+    adds each (vllm_lut/fast_moe.py:58-61)."""
     rng = np.random.default_rng(13)
     T, H, I, E, k = 9, 64, 32, 5, 2
     x = O.f32_to_bf16(rng.standard_normal((T, H)).astype(np.float32))
     W13 = [(rng.standard_normal((2 * I, H)) * 0.1).astype(np.float32) for _ in range(E)]
     W2 = [(rng.standard_normal((H, I)) * 0.1).astype(np.float32) for _ in range(E)]
     w, ids = O.route(rng.standard_normal((T, E)).astype(np.float32), k)
+    if repeats:
+        ids[::2, 1] = ids[::2, 0]   # every other token: its first expert twice
     got = O.moe_layer(x, ids, w, W13.__getitem__, W2.__getitem__)
     xf = O.bf16_to_f32(x).astype(np.float64)
     dense = np.zeros((T, H))
@@ -368,7 +375,7 @@ def test_moe_layer_loop_vs_dense_restatement():
         g, u = gu[:, :I].astype(np.float32), gu[:, I:].astype(np.float32)
         a = O.bf16_to_f32(O.f32_to_bf16(g / (1 + np.exp(-g)) * u)).astype(np.float64)
         y = a @ W2[e].astype(np.float64).T
-        gate = (w * (ids == e)).sum(1)
+        gate = (w.astype(np.float64) * (ids == e)).sum(1)
         dense += gate[:, None] * y
     np.testing.assert_allclose(got, dense, rtol=1e-9, atol=1e-12)
 
