@@ -1139,6 +1139,96 @@ __global__ __launch_bounds__(256, 3) void bl4_decode_gate_up_t1(DecodeArgs A) {
     }
 }
 
+// One token, REF, K = H <= 2048 (one chunk): gate rows i0, i0 + 1 and up
+// rows I + i0, I + i0 + 1 of expert e.  The lane's 32 codes of a row (32
+// bytes) against the expert's bf16[256] codebook in the wave's LDS slot, times
+// the absmax of their block: the reference's one-token products,
+// fp32 (x * cb) * absmax factored per 32 columns, as ref_rows8 computes them.
+// SwiGLU -> act[p][i0 .. i0 + 1] for the slot's positions p0 .. p0 + n - 1
+// (more than one only when the token lists the expert twice: one token, the
+// same values).
+__device__ __forceinline__ void ref_gate_up_t1(const DecodeArgs& A, const uint32_t (&xs)[16], int e, int p0, int n,
+                                               int xcol, uint8_t* slot) {
+    const int lane = threadIdx.x & 63;
+    const int I = A.d.inter, H = A.d.hidden;
+    const lutmoe_weights& w = A.d.w13;
+    const int i0 = xcol * 2;
+    const int i1 = min(i0 + 1, I - 1);
+    const int rows[4] = {i0, i1, I + i0, I + i1};
+    const uint8_t* codes = (const uint8_t*)w.codes + (int64_t)e * w.rows * w.cols;
+    const uint16_t* am = (const uint16_t*)w.tables + (int64_t)e * w.absmax_per_expert;
+    const int64_t nb = w.absmax_per_expert;
+    const bool ok = 32 * lane < H;
+    const uint2 cbv = reinterpret_cast<const uint2*>(ref_codebook(w, e))[lane];
+    u32x4_t cw[4][2];
+    uint32_t av[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int64_t off = (int64_t)rows[r] * H + (ok ? 32 * lane : 0);
+        cw[r][0] = *reinterpret_cast<const u32x4_t*>(codes + off);
+        cw[r][1] = *reinterpret_cast<const u32x4_t*>(codes + off + 16);
+        const int64_t blk = off / w.block_size;
+        av[r] = am[blk < nb ? blk : nb - 1];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    *reinterpret_cast<uint2*>(slot + 8 * lane) = cbv;
+    wave_lds_sync();
+    const uint32_t cbase = lds_addr(slot);
+    const uint32_t (&x1)[1][16] = reinterpret_cast<const uint32_t (&)[1][16]>(xs);
+    float acc[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        float g[1] = {0.f};
+        ref_dot32<1>(cw[r], cbase, x1, 1, g);
+        acc[r] = ok ? bf16_to_f32(av[r]) * g[0] : 0.f;   // lanes past K contribute nothing
+    }
+    const float v = wave_reduce4(acc[0], acc[1], acc[2], acc[3]);   // lane 16j: row j
+    const float up = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float up1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    const float g1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    if (lane == 0) {
+        const uint16_t a0 = (uint16_t)f32_to_bf16(silu_mul(v, up));
+        const uint16_t a1 = (uint16_t)f32_to_bf16(silu_mul(g1, up1));
+        for (int q = 0; q < n; ++q) {
+            uint16_t* a = A.act + (int64_t)(p0 + q) * I;
+            a[i0] = a0;
+            if (i0 + 1 < I) a[i0 + 1] = a1;
+        }
+    }
+}
+
+// One token, REF, H <= 2048: the CTA shape of bl4_decode_gate_up_t1 (four
+// independent waves, intermediate indices 2(4x + w), +1 of slot y, the slot's
+// expert from the token's top-k mask; the general routing where ids repeat),
+// each wave with the expert's codebook in its own 512 bytes of LDS.  The
+// first wave of CTA (0, 0) publishes the routing for the down kernel.
+__global__ __launch_bounds__(256, 3) void ref_decode_gate_up_t1(DecodeArgs A) {
+    __shared__ __attribute__((aligned(16))) uint8_t s_cb[4][512];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int xcol = blockIdx.x * 4 + wv;
+    uint32_t xs[16];
+    const uint16_t* xp = A.x + (32 * lane < A.d.hidden ? 32 * lane : 0);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint4 v = *reinterpret_cast<const uint4*>(xp + 8 * q);
+        xs[4 * q + 0] = v.x;
+        xs[4 * q + 1] = v.y;
+        xs[4 * q + 2] = v.z;
+        xs[4 * q + 3] = v.w;
+    }
+    if (blockIdx.x == 0 && blockIdx.y == 0 && wv == 0) wave_route_publish(A, wave_pairs<true>(A));
+    if (2 * xcol >= A.d.inter) return;
+    int e = t1_slot_expert(A, blockIdx.y), p0 = blockIdx.y, n = 1;
+    if (e == -2) {
+        // ids that repeat: the general routing (a slot may hold two positions)
+        const SlotRef sl = WaveRouteView{wave_pairs<false>(A)}.work(blockIdx.y);
+        e = sl.e;
+        p0 = sl.p0;
+        n = sl.n;
+    }
+    if (e >= 0) ref_gate_up_t1(A, xs, e, p0, n, xcol, s_cb[wv]);
+}
+
 template <int TB, bool kPre, int kFmt>
 __global__ __launch_bounds__(64 * kGuWaves, TB <= 2 ? 3 : 2) void bl4_decode_gate_up(DecodeArgs A) {
     __shared__ __attribute__((aligned(16))) uint8_t s_slot[kGuWaves * kSlot];
@@ -1398,6 +1488,115 @@ __global__ __launch_bounds__(256, 2) void bl4_decode_down1(DecodeArgs A) {
     }
     __syncthreads();
     // the token's slots in slot order (pair q of token 0 sits at position inv[q])
+    if (wv == 0) {
+        float sum = 0.f;
+        for (int q = 0; q < ke; ++q) {
+            const int pos = __builtin_amdgcn_readlane(inv_l, q);
+            if (pos >= 0 && lane < kD1Rows) sum += s_y[pos][lane];
+        }
+        if (lane < kD1Rows) {
+            const int64_t o = h0 + lane;
+            if (A.out_dtype == LUTMOE_DTYPE_F32) ((float*)A.out)[o] = sum;
+            else ((uint16_t*)A.out)[o] = (uint16_t)f32_to_bf16(sum);
+        }
+    }
+}
+
+// One token (T = 1), REF: the scheme of bl4_decode_down1 (CTA x: output rows
+// [4x, 4x + 4); wave wv: active slots wv, wv + 4, ..; the routing read from
+// the workspace copy in place) over REF rows.  An expert's 4 rows are K
+// contiguous code bytes each, walked as one flat array of 32-byte units
+// (unit u: columns [32g, 32g + 32) of row u / NU, NU = K/32, g = u % NU;
+// lane l takes units l, l + 64, ..); a unit lies inside one absmax block
+// (block_size % 64 == 0), and its sum x . cb[codes] times that absmax is the
+// reference's one-token product, fp32 (x * cb) * absmax, as ref_rows8 forms
+// it per 32 columns.  The expert's bf16[256] codebook sits in the wave's LDS.
+template <int kPass>
+__global__ __launch_bounds__(256, 2) void ref_decode_down1(DecodeArgs A) {
+    __shared__ __attribute__((aligned(16))) uint8_t s_cb[4][512];
+    __shared__ float s_part[4][kPass * 64];
+    __shared__ float s_y[16][kD1Rows];   // [position][row], T = 1: at most k + S <= 16 positions
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int K = A.d.inter, ke = A.k + A.d.num_shared;
+    const int NU = K / 32, U = kD1Rows * NU;
+    const int h0 = blockIdx.x * kD1Rows;   // H % 64 == 0: all 4 rows exist
+    const lutmoe_weights& w = A.d.w2;
+    const RouteOut* R = A.route;
+    const int nact = R->nact;
+    int e_next = R->act[wv], p_next = R->aoff[wv], n_next = R->an[wv];
+    const int inv_l = (wv == 0 && lane < ke) ? R->inv[lane] : -1;
+    const int64_t per = (int64_t)w.rows * w.cols;
+    const int64_t nb = w.absmax_per_expert;
+    const uint32_t cbase = lds_addr(s_cb[wv]);
+    float* part = s_part[wv];
+    for (int a = wv; a < nact; a += 4) {
+        const int e = e_next, p0 = p_next, n = n_next;
+        const int pair = R->perm[p0];   // its weight is loaded after the weight loads
+        const uint8_t* codes = (const uint8_t*)w.codes + e * per + (int64_t)h0 * K;
+        const uint16_t* am = (const uint16_t*)w.tables + e * nb;
+        const uint16_t* xr = A.act + (int64_t)p0 * K;
+        const uint2 cbv = reinterpret_cast<const uint2*>(ref_codebook(w, e))[lane];
+        uint32_t xs[kPass][1][16];
+#pragma unroll
+        for (int p = 0; p < kPass; ++p) {
+            const int u = 64 * p + lane;
+            const int g = u < U ? u % NU : 0;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint4 v = *reinterpret_cast<const uint4*>(xr + 32 * g + 8 * q);
+                xs[p][0][4 * q + 0] = v.x;
+                xs[p][0][4 * q + 1] = v.y;
+                xs[p][0][4 * q + 2] = v.z;
+                xs[p][0][4 * q + 3] = v.w;
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        u32x4_t cw[kPass][2];
+        uint32_t av[kPass];
+#pragma unroll
+        for (int p = 0; p < kPass; ++p) {
+            const int u = 64 * p + lane;
+            const int64_t off = u < U ? 32 * u : 0;
+            cw[p][0] = *reinterpret_cast<const u32x4_t*>(codes + off);
+            cw[p][1] = *reinterpret_cast<const u32x4_t*>(codes + off + 16);
+            const int64_t blk = ((int64_t)h0 * K + off) / w.block_size;
+            av[p] = am[blk < nb ? blk : nb - 1];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // behind the weight loads: the pair weight and the next slot's fields
+        const float pw = R->pw[pair];
+        if (a + 4 < kMaxEtot) {
+            e_next = R->act[a + 4];
+            p_next = R->aoff[a + 4];
+            n_next = R->an[a + 4];
+        }
+        *reinterpret_cast<uint2*>(s_cb[wv] + 8 * lane) = cbv;
+        wave_lds_sync();
+#pragma unroll
+        for (int p = 0; p < kPass; ++p) {
+            float g[1] = {0.f};
+            ref_dot32<1>(cw[p], cbase, xs[p], 1, g);
+            // units past the 4 rows (their loads read the first unit) add nothing
+            part[64 * p + lane] = 64 * p + lane < U ? bf16_to_f32(av[p]) * g[0] : 0.f;
+        }
+        wave_lds_sync();
+        // per-row sums: lane 16r + j adds units r*NU + j, + 16, .. and the 16
+        // lanes of row r reduce with DPP
+        const int r = lane >> 4, j = lane & 15;
+        float v = 0.f;
+        for (int u = j; u < NU; u += 16) v += part[r * NU + u];
+        v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xb1, 0xf, 0xf, false));
+        v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4e, 0xf, 0xf, false));
+        v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xf, 0xf, false));
+        v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xf, 0xf, false));
+        if (j == 0) {
+            s_y[p0][r] = v * pw;
+            // an expert the token lists more than once: the same activations
+            for (int q = 1; q < n; ++q) s_y[p0 + q][r] = v * R->pw[R->perm[p0 + q]];
+        }
+        wave_lds_sync();   // the codebook and the partials are restaged by the next slot
+    }
+    __syncthreads();
     if (wv == 0) {
         float sum = 0.f;
         for (int q = 0; q < ke; ++q) {
@@ -1807,9 +2006,10 @@ int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* t
     // work items: the active slots, cut into chunks by decode_route_kernel
     // (at most P, and at most one more per slot than ceil(P / TB))
     const int max_work = pre ? std::min(P, max_active + (P + tb - 1) / tb) : max_active;
-    if ((stages & LUTMOE_STAGE_GATE_UP) && fmt_idx == 0 && tb == 1 && !pre && T == 1 && d->hidden <= kWChunk) {
+    if ((stages & LUTMOE_STAGE_GATE_UP) && fmt_idx != 1 && tb == 1 && !pre && T == 1 && d->hidden <= kWChunk) {
         const dim3 grid((d->inter + 7) / 8, max_work);   // 4 waves x 2 intermediate indices
-        hipLaunchKernelGGL(bl4_decode_gate_up_t1, grid, dim3(256), 0, s, A);
+        if (fmt_idx == 0) hipLaunchKernelGGL(bl4_decode_gate_up_t1, grid, dim3(256), 0, s, A);
+        else hipLaunchKernelGGL(ref_decode_gate_up_t1, grid, dim3(256), 0, s, A);
         if ((rc = check_launch())) return rc;
     } else if (stages & LUTMOE_STAGE_GATE_UP) {
         const int per_cta = (fmt_idx == 0 && tb == 1) ? 2 : 4 * kGuWaves;   // intermediate indices per CTA
@@ -1852,6 +2052,17 @@ int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* t
                 case 2: hipLaunchKernelGGL(bl4_decode_down1<2>, g1, dim3(256), 0, s, A); break;
                 case 3: hipLaunchKernelGGL(bl4_decode_down1<3>, g1, dim3(256), 0, s, A); break;
                 default: hipLaunchKernelGGL(bl4_decode_down1<4>, g1, dim3(256), 0, s, A); break;
+            }
+            return check_launch();
+        }
+        if (fmt_idx == 2 && tb == 1 && d->inter <= 2048) {
+            // one token, REF: flat 32-byte units over 4 rows
+            const dim3 g1(d->hidden / kD1Rows);
+            switch ((d->inter + 511) / 512) {
+                case 1: hipLaunchKernelGGL(ref_decode_down1<1>, g1, dim3(256), 0, s, A); break;
+                case 2: hipLaunchKernelGGL(ref_decode_down1<2>, g1, dim3(256), 0, s, A); break;
+                case 3: hipLaunchKernelGGL(ref_decode_down1<3>, g1, dim3(256), 0, s, A); break;
+                default: hipLaunchKernelGGL(ref_decode_down1<4>, g1, dim3(256), 0, s, A); break;
             }
             return check_launch();
         }
