@@ -680,17 +680,21 @@ def test_moe_layer_ref_per_expert_codebook(gpu, T, path):
             assert rel_maxabs(y.cpu().numpy(), O.bf16_to_f32(xa) @ w2.gemv_f32(e).T) <= TOL
 
 
-@pytest.mark.parametrize("T,path,renorm,E", [(1, 1, False, 12), (3, 1, True, 12), (32, 1, False, 12),
-                                             (40, 2, False, 12), (300, 2, True, 12),
-                                             (2, 1, True, 130), (5, 2, False, 130)])
-def test_moe_layer_from_logits(gpu, T, path, renorm, E):
+@pytest.mark.parametrize("fmt,T,path,renorm,E", [("bl4", 1, 1, False, 12), ("bl4", 3, 1, True, 12),
+                                                 ("bl4", 32, 1, False, 12), ("bl4", 40, 2, False, 12),
+                                                 ("bl4", 300, 2, True, 12), ("bl4", 1, 1, True, 130),
+                                                 ("bl4", 2, 1, True, 130), ("bl4", 5, 2, False, 130),
+                                                 ("ref", 1, 1, False, 12), ("ref", 1, 1, True, 130),
+                                                 ("ref", 3, 1, True, 12)])
+def test_moe_layer_from_logits(gpu, fmt, T, path, renorm, E):
     """Block forward from router logits (routing inside the layer) vs oracle routing + layer;
-    E = 130 puts several logits on one lane of the in-kernel top-k."""
+    E = 130 puts several logits on one lane of the in-kernel top-k (and, for one token, routes
+    in the routing kernel before the one-token down kernels)."""
     import torch
     from block_lut_amd import ops
     from block_lut_amd.formats import MoEWeights
     S, k, H, I = 2, 3, 256, 192
-    w13, w2 = _moe_case("bl4", E, S, H, I, seed=70 + T)
+    w13, w2 = _moe_case(fmt, E, S, H, I, seed=70 + T)
     moe = MoEWeights(w13.stack(gpu), w2.stack(gpu), H, I, E, S)
     rng = np.random.default_rng(700 + T)
     xb = _x(rng, T, H)
@@ -698,8 +702,8 @@ def test_moe_layer_from_logits(gpu, T, path, renorm, E):
     out = ops.moe_forward_logits(moe, to_dev_bf16(xb, gpu), torch.from_numpy(lg).to(gpu), k,
                                  renormalize=renorm, scaling=1.0, out_dtype=torch.float32, path=path)
     rw, rids = O.route(lg, k, renormalize=renorm)
-    ref = O.moe_layer(xb, rids, rw, w13.deq_f32, w2.deq_f32,
-                      shared=[(w13.deq_f32(E + s), w2.deq_f32(E + s)) for s in range(S)])
+    f13, f2 = _ref_semantics(w13, w2, T, path) if fmt == "ref" else (w13.deq_f32, w2.deq_f32)
+    ref = O.moe_layer(xb, rids, rw, f13, f2, shared=[(f13(E + s), f2(E + s)) for s in range(S)])
     assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
 
 
