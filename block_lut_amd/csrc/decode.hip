@@ -127,17 +127,18 @@ __device__ void cta_route(const DecodeArgs& A, RouteOut& R, RouteScratch& X) {
         // is monotone): rank(e) = #{e' : l[e'] > l[e] or (l[e'] == l[e], e' < e)}.
         for (int t = wv; t < T; t += (int)(blockDim.x >> 6)) {
             const float* src = A.logits + (int64_t)t * E;
-            float mx = -INFINITY;
-            for (int e = lane; e < E; e += 64) mx = fmaxf(mx, src[e]);
+            // E <= 64: one logit per lane, read once for the softmax and the top-k
+            const float v = E <= 64 && lane < E ? src[lane] : -INFINITY;
+            float mx = fmaxf(-INFINITY, v);   // (a NaN logit drops out, as in the loop)
+            for (int e = lane; E > 64 && e < E; e += 64) mx = fmaxf(mx, src[e]);
             mx = wave_reduce_max(mx);
-            float ps = 0.f;
-            for (int e = lane; e < E; e += 64) ps += expf(src[e] - mx);
+            float ps = E <= 64 && lane < E ? expf(v - mx) : 0.f;
+            for (int e = lane; E > 64 && e < E; e += 64) ps += expf(src[e] - mx);
             const float sum = wave_reduce(ps);
             float wsum = 0.f;
             if (E <= 64) {
-                // one logit per lane; k rounds of a DPP max over int keys
-                // (ties -> lowest lane = lower expert id; NaN never selected)
-                const float v = lane < E ? src[lane] : -INFINITY;
+                // k rounds of a DPP max over int keys (ties -> lowest lane =
+                // lower expert id; NaN never selected)
                 int key = lane < E ? float_key(v) : INT_MIN;
                 for (int j = 0; j < k; ++j) {
                     const int m = wave_max_i32(key);

@@ -432,7 +432,8 @@ def test_moe_layer(gpu, fmt, T, path):
 
 
 @pytest.mark.parametrize("fmt,T,path", [("bl4", 1, 1), ("bl4", 2, 1), ("bl4", 3, 1), ("bl4", 3, 2),
-                                        ("ref", 1, 1), ("ref", 2, 1), ("ref", 3, 1)])
+                                        ("ref", 1, 1), ("ref", 2, 1), ("ref", 3, 1),
+                                        ("nested", 1, 1), ("nested", 3, 1), ("nested", 3, 2)])
 def test_moe_layer_repeated_ids(gpu, fmt, T, path):
     """Caller-given ids that list an expert twice for one token: both pairs count, each with
     its weight, as the reference's loop over the k slots adds them (vllm_lut/fast_moe.py:
@@ -442,7 +443,12 @@ def test_moe_layer_repeated_ids(gpu, fmt, T, path):
     from block_lut_amd import ops
     from block_lut_amd.formats import MoEWeights
     E, S, k, H, I = 8, 1, 3, 512, 320
-    w13, w2 = _moe_case(fmt, E, S, H, I, seed=70 + T)
+    if fmt == "nested":
+        bits = [2, 3, 4, 2, 3, 4, 3, 2, 4]
+        w13 = NestedExpertset(bits, 2 * I, H, seed=80 + T, n_iter=8)
+        w2 = NestedExpertset(bits, H, I, seed=81 + T, n_iter=8)
+    else:
+        w13, w2 = _moe_case(fmt, E, S, H, I, seed=70 + T)
     moe = MoEWeights(w13.stack(gpu), w2.stack(gpu), H, I, E, S)
     rng = np.random.default_rng(700 + T)
     xb = _x(rng, T, H)
