@@ -1387,10 +1387,10 @@ __global__ __launch_bounds__(256, TB <= 2 ? 3 : 2) void bl4_decode_down(DecodeAr
 // no LDS copy and no barrier before the weight loads.
 constexpr int kD1Rows = 4;
 
-template <int kPass>
+template <int kPass, int TB>
 __global__ __launch_bounds__(256, 2) void bl4_decode_down1(DecodeArgs A) {
     __shared__ __attribute__((aligned(16))) uint8_t s_slot[4][kPass * 1024];
-    __shared__ float s_y[16][kD1Rows];   // [position][row], T = 1: at most k + S <= 16 positions
+    __shared__ float s_y[16 * TB][kD1Rows];   // [position][row]: at most T (k + S) <= 16 T positions
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int K = A.d.inter, H = A.d.hidden, ke = A.k + A.d.num_shared;
     const int NU = K / 32, U = kD1Rows * NU;
@@ -1398,10 +1398,10 @@ __global__ __launch_bounds__(256, 2) void bl4_decode_down1(DecodeArgs A) {
     const RouteOut* R = A.route;
     // the routing fields this wave needs, in one round trip: the count, the
     // first slot's expert and position (in bounds for any count), and the
-    // positions of the token's pairs for the combine
+    // positions of the tokens' pairs for the combine
     const int nact = R->nact;
     int e_next = R->act[wv], p_next = R->aoff[wv], n_next = R->an[wv];
-    const int inv_l = (wv == 0 && lane < ke) ? R->inv[lane] : -1;
+    const int inv_l = (wv == 0 && lane < ke * TB) ? R->inv[lane] : -1;
     const int64_t per = (int64_t)A.d.w2.rows * (K / 2);
     const int64_t rbase = (int64_t)h0 * (K / 2);
     const uint8_t* wcodes = (const uint8_t*)A.d.w2.codes;
@@ -1414,89 +1414,128 @@ __global__ __launch_bounds__(256, 2) void bl4_decode_down1(DecodeArgs A) {
     const u32x4_t z = {0u, 0u, 0u, 0u};
     for (int a = wv; a < nact; a += 4) {
         const int e = e_next, p0 = p_next, n = n_next;
-        const int pair = R->perm[p0];   // its weight is loaded after the weight loads
         const uint8_t* codes = wcodes + e * per + rbase;
         const uint8_t* tabs = wtabs + e * per + rbase;
-        const uint16_t* xr = A.act + (int64_t)p0 * K;
-        uint32_t xs[kPass][16];
-        u32x4_t cw[kPass], tw[kPass];
+        // one token: a single pass (a slot's positions are the same token);
+        // two tokens: passes of up to 2 positions
+        for (int tb = 0; tb < (TB == 1 ? 1 : n); tb += TB) {
+            const int nt = TB == 1 ? 1 : min(TB, n - tb);
+            int pair[TB];   // their weights are loaded after the weight loads
 #pragma unroll
-        for (int p = 0; p < kPass; ++p) {
-            const int u = 64 * p + lane;
-            const int g = u < U ? u % NU : 0;
+            for (int t = 0; t < TB; ++t) pair[t] = R->perm[p0 + tb + min(t, nt - 1)];
+            uint32_t xs[kPass][TB][16];
+            u32x4_t cw[kPass], tw[kPass];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const uint4 v = *reinterpret_cast<const uint4*>(xr + 32 * g + 8 * q);
-                xs[p][4 * q + 0] = v.x;
-                xs[p][4 * q + 1] = v.y;
-                xs[p][4 * q + 2] = v.z;
-                xs[p][4 * q + 3] = v.w;
+            for (int p = 0; p < kPass; ++p) {
+                const int u = 64 * p + lane;
+                const int g = u < U ? u % NU : 0;
+#pragma unroll
+                for (int t = 0; t < TB; ++t) {
+                    const uint16_t* xr = A.act + (int64_t)(p0 + tb + min(t, nt - 1)) * K;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const uint4 v = *reinterpret_cast<const uint4*>(xr + 32 * g + 8 * q);
+                        xs[p][t][4 * q + 0] = v.x;
+                        xs[p][t][4 * q + 1] = v.y;
+                        xs[p][t][4 * q + 2] = v.z;
+                        xs[p][t][4 * q + 3] = v.w;
+                    }
+                }
             }
-        }
-        __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int p = 0; p < kPass; ++p) {
-            const int u = 64 * p + lane;
-            const int64_t off = u < U ? 16 * u : 0;
-            cw[p] = *reinterpret_cast<const u32x4_t*>(codes + off);
-            tw[p] = *reinterpret_cast<const u32x4_t*>(tabs + off);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        // behind the weight loads: the pair weight and the next slot's fields
-        const float pw = R->pw[pair];
-        if (a + 4 < kMaxEtot) {
-            e_next = R->act[a + 4];
-            p_next = R->aoff[a + 4];
-            n_next = R->an[a + 4];
-        }
-        float acc[kPass];
+            for (int p = 0; p < kPass; ++p) {
+                const int u = 64 * p + lane;
+                const int64_t off = u < U ? 16 * u : 0;
+                cw[p] = *reinterpret_cast<const u32x4_t*>(codes + off);
+                tw[p] = *reinterpret_cast<const u32x4_t*>(tabs + off);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            // behind the weight loads: the pair weights and the next slot's fields
+            float pw[TB];
 #pragma unroll
-        for (int p = 0; p < kPass; ++p) {
-            // units past the 4 rows stage zero tables (their loads read the first unit)
-            *reinterpret_cast<u32x4_t*>(slot + p * 1024 + 16 * lane) = 64 * p + lane < U ? tw[p] : z;
+            for (int t = 0; t < TB; ++t) pw[t] = R->pw[pair[t]];
+            if (tb == 0 && a + 4 < kMaxEtot) {
+                e_next = R->act[a + 4];
+                p_next = R->aoff[a + 4];
+                n_next = R->an[a + 4];
+            }
+            float acc[kPass][TB];
+#pragma unroll
+            for (int p = 0; p < kPass; ++p) {
+                // units past the 4 rows stage zero tables (their loads read the first unit)
+                *reinterpret_cast<u32x4_t*>(slot + p * 1024 + 16 * lane) = 64 * p + lane < U ? tw[p] : z;
+                wave_lds_sync();
+                float s[TB];
+#pragma unroll
+                for (int t = 0; t < TB; ++t) s[t] = 0.f;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    uint32_t xj[TB][4];
+#pragma unroll
+                    for (int t = 0; t < TB; ++t)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) xj[t][i] = xs[p][t][4 * j + i];
+                    bl4_dot8<TB>(cw[p][j], tab0 + p * 1024, xj, nt, s);
+                }
+#pragma unroll
+                for (int t = 0; t < TB; ++t) acc[p][t] = s[t];
+            }
             wave_lds_sync();
-            float s[1] = {0.f};
+            // per-row sums: unit partials through LDS, then lane 16r + j adds
+            // units r*NU + j, + 16, .. and the 16 lanes of row r reduce with DPP
+            float* part = reinterpret_cast<float*>(slot);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                uint32_t xj[1][4];
+            for (int t = 0; t < TB; ++t)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) xj[0][i] = xs[p][4 * j + i];
-                bl4_dot8<1>(cw[p][j], tab0 + p * 1024, xj, 1, s);
+                for (int p = 0; p < kPass; ++p) part[(t * kPass + p) * 64 + lane] = acc[p][t];
+            wave_lds_sync();
+            const int r = lane >> 4, j = lane & 15;
+#pragma unroll
+            for (int t = 0; t < TB; ++t) {
+                if (t >= nt) break;
+                const float* pt = part + t * kPass * 64;
+                float v = 0.f;
+                for (int u = j; u < NU; u += 16) v += pt[r * NU + u];
+                v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xb1, 0xf,
+                                                                           0xf, false));
+                v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4e, 0xf,
+                                                                           0xf, false));
+                v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xf,
+                                                                           0xf, false));
+                v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xf,
+                                                                           0xf, false));
+                if (j == 0) {
+                    s_y[p0 + tb + t][r] = v * pw[t];
+                    // one token listing an expert more than once: its other
+                    // positions hold the same activations, each with its own weight
+                    if constexpr (TB == 1)
+                        for (int q = 1; q < n; ++q) s_y[p0 + q][r] = v * R->pw[R->perm[p0 + q]];
+                }
             }
-            acc[p] = s[0];
+            wave_lds_sync();   // the slot is restaged by the next pass
         }
-        wave_lds_sync();
-        // per-row sums: unit partials through LDS, then lane 16r + j adds units
-        // r*NU + j, + 16, .. and the 16 lanes of row r reduce with DPP
-        float* part = reinterpret_cast<float*>(slot);
-#pragma unroll
-        for (int p = 0; p < kPass; ++p) part[64 * p + lane] = acc[p];
-        wave_lds_sync();
-        const int r = lane >> 4, j = lane & 15;
-        float v = 0.f;
-        for (int u = j; u < NU; u += 16) v += part[r * NU + u];
-        v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xb1, 0xf, 0xf, false));
-        v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4e, 0xf, 0xf, false));
-        v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xf, 0xf, false));
-        v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xf, 0xf, false));
-        if (j == 0) {
-            s_y[p0][r] = v * pw;
-            // an expert the token lists more than once: its other positions
-            // hold the same activations (one token), each with its own weight
-            for (int q = 1; q < n; ++q) s_y[p0 + q][r] = v * R->pw[R->perm[p0 + q]];
-        }
-        wave_lds_sync();   // the slot is restaged by the next active slot
     }
     __syncthreads();
-    // the token's slots in slot order (pair q of token 0 sits at position inv[q])
+    // each token's slots in slot order (pair q of token t sits at position
+    // inv[t (k + S) + q])
     if (wv == 0) {
         float sum = 0.f;
-        for (int q = 0; q < ke; ++q) {
-            const int pos = __builtin_amdgcn_readlane(inv_l, q);
-            if (pos >= 0 && lane < kD1Rows) sum += s_y[pos][lane];
+        if constexpr (TB == 1) {
+            for (int q = 0; q < ke; ++q) {
+                const int pos = __builtin_amdgcn_readlane(inv_l, q);
+                if (pos >= 0 && lane < kD1Rows) sum += s_y[pos][lane];
+            }
+        } else {
+            // lane 4t + r: token t, row r
+            const int t = lane / kD1Rows, r = lane % kD1Rows;
+            for (int q = 0; q < ke; ++q) {
+                const int pos = __shfl(inv_l, min(t, TB - 1) * ke + q, 64);
+                if (pos >= 0 && t < A.T) sum += s_y[pos][r];
+            }
         }
-        if (lane < kD1Rows) {
-            const int64_t o = h0 + lane;
+        if (lane < kD1Rows * (TB == 1 ? 1 : A.T)) {
+            const int64_t o = TB == 1 ? h0 + lane : (int64_t)(lane / kD1Rows) * H + h0 + lane % kD1Rows;
             if (A.out_dtype == LUTMOE_DTYPE_F32) ((float*)A.out)[o] = sum;
             else ((uint16_t*)A.out)[o] = (uint16_t)f32_to_bf16(sum);
         }
@@ -2045,15 +2084,19 @@ int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* t
             const int32_t* inv = ((const RouteOut*)route_ws)->inv;
             return launch_combine(y_ws, inv, T, k + d->num_shared, d->hidden, out, out_dtype, s);
         }
-        if (fmt_idx == 0 && tb == 1 && d->inter <= 2048) {
-            // one token, BL4: flat 16-byte units over 4 rows (every lane busy)
+        if (fmt_idx == 0 && (tb == 1 || (tb == 2 && T == 2)) && d->inter <= 2048) {
+            // one or two tokens, BL4: flat 16-byte units over 4 rows (every lane busy)
             const dim3 g1(d->hidden / kD1Rows);
+#define LUTMOE_DOWN1(P)                                                              \
+    if (tb == 1) hipLaunchKernelGGL((bl4_decode_down1<P, 1>), g1, dim3(256), 0, s, A); \
+    else hipLaunchKernelGGL((bl4_decode_down1<P, 2>), g1, dim3(256), 0, s, A)
             switch ((d->inter + 511) / 512) {
-                case 1: hipLaunchKernelGGL(bl4_decode_down1<1>, g1, dim3(256), 0, s, A); break;
-                case 2: hipLaunchKernelGGL(bl4_decode_down1<2>, g1, dim3(256), 0, s, A); break;
-                case 3: hipLaunchKernelGGL(bl4_decode_down1<3>, g1, dim3(256), 0, s, A); break;
-                default: hipLaunchKernelGGL(bl4_decode_down1<4>, g1, dim3(256), 0, s, A); break;
+                case 1: LUTMOE_DOWN1(1); break;
+                case 2: LUTMOE_DOWN1(2); break;
+                case 3: LUTMOE_DOWN1(3); break;
+                default: LUTMOE_DOWN1(4); break;
             }
+#undef LUTMOE_DOWN1
             return check_launch();
         }
         if (fmt_idx == 2 && tb == 1 && d->inter <= 2048) {

@@ -406,7 +406,7 @@ def _moe_case(fmt, E, S, H, I, seed):
     return w13, w2
 
 
-@pytest.mark.parametrize("fmt,T,path", [("bl4", 1, 1), ("bl4", 4, 1), ("bl4", 9, 1),
+@pytest.mark.parametrize("fmt,T,path", [("bl4", 1, 1), ("bl4", 2, 1), ("bl4", 4, 1), ("bl4", 9, 1),
                                         ("bl4", 200, 2), ("bl4", 5, 2),
                                         ("ref", 1, 1), ("ref", 2, 1), ("ref", 3, 1), ("ref", 9, 1),
                                         ("ref", 150, 2)])
