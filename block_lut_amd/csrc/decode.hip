@@ -559,23 +559,77 @@ __global__ __launch_bounds__(1024) void decode_route_kernel(DecodeArgs A) {
     put_chunks(A, R);
 }
 
-// One wave, 8 rows, one 2048-column chunk cc of K: lane l covers columns
-// [2048cc + 32l, +32), i.e. 16 bytes of every row's codes and the matching 16
-// bytes of its tables (half of the block's bf16[16]); codes and tables are
-// both K/2 bytes per row.  Two 16-byte loads per row per chunk, issued
-// without branches (lanes past K read the row start and drop the values).
+// One wave, 8 BL4 rows, one 2048-column chunk cc of K.  Codes and tables
+// are both K/2 bytes per row.  Tables: lane l loads bytes [1024cc + 16l, +16)
+// of each row's tables (half of block l/2's bf16[16]) and stages them at 16l
+// of the row's 1 KB of LDS (block g at 32g).  Codes, in one of two lane maps:
+//  * contiguous (two tokens a pass or fewer): lane l takes the row's 16 bytes
+//    at 16l, columns [2048cc + 32l, +32) of its own block's half; one load;
+//  * interleaved (four tokens a pass): lane l takes the chunk's code dwords
+//    d = l, l + 64, l + 128, l + 192 (columns [2048cc + 8d, +8)), so in each
+//    lookup step the 64 lanes use the tables of 8 consecutive blocks, which
+//    sit in 8 distinct LDS bank groups (no bank conflicts), and a row of
+//    K = 1408 (176 dwords) keeps 44 of 48 lane steps busy.  Four dword loads
+//    a row: with four tokens they pay (T = 32: 155 -> 151 us a layer); with
+//    two the extra loads and registers cost more than the conflicts (T = 8:
+//    70 -> 86 us).
+// Loads past K read nothing (interleaved) or the chunk start (contiguous),
+// and their lookups meet zero tables.
+template <int TB>
+constexpr bool bl4_interleaved() { return TB >= 4; }
+
 struct Rows8 {
-    u32x4_t cw[kRows], tw[kRows];
+    uint32_t cw[kRows][4];   // the lane's 4 code dwords of each row
+    u32x4_t tw[kRows];
 };
 
+__device__ __forceinline__ int chunk_dwords(int K, int cc) { return min(K - cc * kWChunk, kWChunk) / 8; }
+
+template <int TB>
 __device__ __forceinline__ void load_rows8(const uint8_t* __restrict__ codes, const uint8_t* __restrict__ tabs,
                                            const int (&rows)[kRows], int K, int cc, int lane, Rows8& b) {
-    const bool ok = cc * kWChunk + 32 * lane < K;
+    const int nd = chunk_dwords(K, cc);
+    const bool okt = cc * kWChunk + 32 * lane < K;
 #pragma unroll
     for (int r = 0; r < kRows; ++r) {
-        const int64_t off = (int64_t)rows[r] * (K / 2) + (ok ? cc * (kWChunk / 2) + 16 * lane : 0);
-        b.cw[r] = *reinterpret_cast<const u32x4_t*>(codes + off);
-        b.tw[r] = *reinterpret_cast<const u32x4_t*>(tabs + off);
+        // 32-bit offsets from the expert's (wave-uniform) bases
+        const uint32_t ro = (uint32_t)rows[r] * (uint32_t)(K / 2) + cc * (kWChunk / 2);
+        if constexpr (bl4_interleaved<TB>()) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                b.cw[r][q] = 0u;
+                if (lane + 64 * q < nd)
+                    b.cw[r][q] = *reinterpret_cast<const uint32_t*>(codes + (ro + 4 * lane + 256 * q));
+            }
+        } else {
+            const u32x4_t v = *reinterpret_cast<const u32x4_t*>(codes + (ro + (okt ? 16 * lane : 0)));
+#pragma unroll
+            for (int q = 0; q < 4; ++q) b.cw[r][q] = v[q];
+        }
+        b.tw[r] = *reinterpret_cast<const u32x4_t*>(tabs + (ro + (okt ? 16 * lane : 0)));
+    }
+}
+
+// The activations of the lane's BL4 code dwords in the interleaved map, up
+// to TB vectors: xs[t][4q + i] = columns 8d + 2i, 8d + 2i + 1 of chunk cc
+// (d = l + 64q); zero past K, where the codes meet zero tables.  Vectors past
+// nt are dropped.
+template <int TB>
+__device__ __forceinline__ void load_xi(const uint16_t* const (&xrow)[TB], int K, int cc, int lane,
+                                        uint32_t (&xs)[TB][16]) {
+    const int nd = chunk_dwords(K, cc);
+#pragma unroll
+    for (int t = 0; t < TB; ++t) {
+        const uint16_t* p = xrow[t] + cc * kWChunk + 8 * lane;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            uint4 v = {0u, 0u, 0u, 0u};
+            if (lane + 64 * q < nd) v = *reinterpret_cast<const uint4*>(p + 512 * q);
+            xs[t][4 * q + 0] = v.x;
+            xs[t][4 * q + 1] = v.y;
+            xs[t][4 * q + 2] = v.z;
+            xs[t][4 * q + 3] = v.w;
+        }
     }
 }
 
@@ -602,12 +656,14 @@ __device__ __forceinline__ void load_x8(const uint16_t* const (&xrow)[TB], int K
 
 // Row by row: stage row r's tables of the chunk in its 1 KB of the wave's LDS
 // slot (block g at r*1024 + 32g), then look its codes up there and
-// accumulate; row r only waits for its own loads, so the first rows are done
-// while the later ones are still arriving.
+// accumulate (code dword q: block l/2 contiguous, l/8 + 8q interleaved); row
+// r only waits for its own loads, so the first rows are done while the later
+// ones are still arriving.  `ok`: the lane's table bytes lie inside K.
 template <int TB>
 __device__ __forceinline__ void compute_rows8(const Rows8& b, const uint32_t (&xs)[TB][16], bool ok, int lane,
                                               uint8_t* slot, int nt, float (&acc)[kRows][TB]) {
-    const uint32_t tab = lds_addr(slot) + ((lane >> 1) << 5);
+    constexpr bool kInter = bl4_interleaved<TB>();
+    const uint32_t tab = lds_addr(slot) + (kInter ? (lane >> 3) << 5 : (lane >> 1) << 5);
     const u32x4_t z = {0u, 0u, 0u, 0u};
 #pragma unroll
     for (int r = 0; r < kRows; ++r) {
@@ -615,13 +671,13 @@ __device__ __forceinline__ void compute_rows8(const Rows8& b, const uint32_t (&x
         *reinterpret_cast<u32x4_t*>(slot + r * 1024 + 16 * lane) = ok ? b.tw[r] : z;
         wave_lds_sync();
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int q = 0; q < 4; ++q) {
             uint32_t xj[TB][4];
 #pragma unroll
             for (int t = 0; t < TB; ++t)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) xj[t][i] = xs[t][4 * j + i];
-            bl4_dot8<TB>(b.cw[r][j], tab + r * 1024, xj, nt, acc[r]);
+                for (int i = 0; i < 4; ++i) xj[t][i] = xs[t][4 * q + i];
+            bl4_dot8<TB>(b.cw[r][q], tab + r * 1024 + (kInter ? 256 * q : 0), xj, nt, acc[r]);
         }
     }
     wave_lds_sync();
@@ -636,9 +692,10 @@ __device__ __forceinline__ void bl4_rows8(const uint8_t* __restrict__ codes, con
     for (int cc = 0; cc < nch; ++cc) {
         Rows8 b;
         uint32_t xs[TB][16];
-        load_x8<TB>(xrow, K, cc, lane, nt, xs);
+        if constexpr (bl4_interleaved<TB>()) load_xi<TB>(xrow, K, cc, lane, xs);
+        else load_x8<TB>(xrow, K, cc, lane, nt, xs);
         __builtin_amdgcn_sched_barrier(0);
-        load_rows8(codes, tabs, rows, K, cc, lane, b);
+        load_rows8<TB>(codes, tabs, rows, K, cc, lane, b);
         // every load in flight before the first row is consumed
         __builtin_amdgcn_sched_barrier(0);
         compute_rows8<TB>(b, xs, cc * kWChunk + 32 * lane < K, lane, slot, nt, acc);
@@ -932,27 +989,36 @@ static_assert(kGuWaves == 1, "gate_up_body4 assumes one wave per CTA");
 template <int TB>
 constexpr bool gu2_for() { return TB == 1; }
 
-// Four BL4 rows over all of K (as bl4_rows8 for 8): per 2048-column chunk the
-// activations, then both loads of every row, then row by row the table
-// staging and the lookups; the wave's LDS slot holds 4 rows' tables (4 KB).
+// Four BL4 rows over all of K (as bl4_rows8 for 8, in its interleaved lane
+// map: conflict-free lookups, which for one token a pass measured faster,
+// as in bl4_decode_gate_up_t1): per 2048-column chunk the activations, then
+// the loads of every row, then row by row the table staging and the lookups;
+// the wave's LDS slot holds 4 rows' tables (4 KB).
 template <int TB>
 __device__ __forceinline__ void bl4_rows4(const uint8_t* __restrict__ codes, const uint8_t* __restrict__ tabs,
                                           const int (&rows)[4], int K, int lane, uint8_t* slot,
                                           const uint16_t* const (&xrow)[TB], int nt, float (&acc)[4][TB]) {
-    const uint32_t tab = lds_addr(slot) + ((lane >> 1) << 5);
+    const uint32_t tab = lds_addr(slot) + ((lane >> 3) << 5);
     const u32x4_t z = {0u, 0u, 0u, 0u};
     const int nch = (K + kWChunk - 1) / kWChunk;
     for (int cc = 0; cc < nch; ++cc) {
         uint32_t xs[TB][16];
-        load_x8<TB>(xrow, K, cc, lane, nt, xs);
+        load_xi<TB>(xrow, K, cc, lane, xs);
         __builtin_amdgcn_sched_barrier(0);
+        const int nd = chunk_dwords(K, cc);
         const bool ok = cc * kWChunk + 32 * lane < K;
-        u32x4_t cw[4], tw[4];
+        uint32_t cw[4][4];
+        u32x4_t tw[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int64_t off = (int64_t)rows[r] * (K / 2) + (ok ? cc * (kWChunk / 2) + 16 * lane : 0);
-            cw[r] = *reinterpret_cast<const u32x4_t*>(codes + off);
-            tw[r] = *reinterpret_cast<const u32x4_t*>(tabs + off);
+            const uint32_t ro = (uint32_t)rows[r] * (uint32_t)(K / 2) + cc * (kWChunk / 2);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                cw[r][q] = 0u;
+                if (lane + 64 * q < nd)
+                    cw[r][q] = *reinterpret_cast<const uint32_t*>(codes + (ro + 4 * lane + 256 * q));
+            }
+            tw[r] = *reinterpret_cast<const u32x4_t*>(tabs + (ro + (ok ? 16 * lane : 0)));
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -960,13 +1026,13 @@ __device__ __forceinline__ void bl4_rows4(const uint8_t* __restrict__ codes, con
             *reinterpret_cast<u32x4_t*>(slot + r * 1024 + 16 * lane) = ok ? tw[r] : z;
             wave_lds_sync();
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+            for (int q = 0; q < 4; ++q) {
                 uint32_t xj[TB][4];
 #pragma unroll
                 for (int t = 0; t < TB; ++t)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) xj[t][i] = xs[t][4 * j + i];
-                bl4_dot8<TB>(cw[r][j], tab + r * 1024, xj, nt, acc[r]);
+                    for (int i = 0; i < 4; ++i) xj[t][i] = xs[t][4 * q + i];
+                bl4_dot8<TB>(cw[r][q], tab + r * 1024 + 256 * q, xj, nt, acc[r]);
             }
         }
         wave_lds_sync();
@@ -1070,16 +1136,23 @@ __device__ __forceinline__ void gate_up_t1(const DecodeArgs& A, const uint32_t (
     const int rows[4] = {i0, i1, I + i0, I + i1};
     const uint8_t* codes = wcodes + e * per;
     const uint8_t* tabs = wtabs + e * per;
+    // code dwords l + 64q of each row and the lane's 16 table bytes, as
+    // load_rows8 takes them (conflict-free lookups)
     const bool ok = 32 * lane < H;
-    u32x4_t cw[4], tw[4];
+    uint32_t cw[4][4];
+    u32x4_t tw[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-        const int64_t off = (int64_t)rows[r] * (H / 2) + (ok ? 16 * lane : 0);
-        cw[r] = *reinterpret_cast<const u32x4_t*>(codes + off);
-        tw[r] = *reinterpret_cast<const u32x4_t*>(tabs + off);
+        const uint32_t ro = (uint32_t)rows[r] * (uint32_t)(H / 2);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            cw[r][q] = 0u;
+            if (8 * (lane + 64 * q) < H) cw[r][q] = *reinterpret_cast<const uint32_t*>(codes + (ro + 4 * lane + 256 * q));
+        }
+        tw[r] = *reinterpret_cast<const u32x4_t*>(tabs + (ro + (ok ? 16 * lane : 0)));
     }
     __builtin_amdgcn_sched_barrier(0);
-    const uint32_t tab = lds_addr(slot) + ((lane >> 1) << 5);
+    const uint32_t tab = lds_addr(slot) + ((lane >> 3) << 5);
     const u32x4_t z = {0u, 0u, 0u, 0u};
     float acc[4][1] = {{0.f}, {0.f}, {0.f}, {0.f}};
 #pragma unroll
@@ -1087,11 +1160,11 @@ __device__ __forceinline__ void gate_up_t1(const DecodeArgs& A, const uint32_t (
         *reinterpret_cast<u32x4_t*>(slot + r * 1024 + 16 * lane) = ok ? tw[r] : z;
         wave_lds_sync();
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int q = 0; q < 4; ++q) {
             uint32_t xj[1][4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) xj[0][i] = xs[4 * j + i];
-            bl4_dot8<1>(cw[r][j], tab + r * 1024, xj, 1, acc[r]);
+            for (int i = 0; i < 4; ++i) xj[0][i] = xs[4 * q + i];
+            bl4_dot8<1>(cw[r][q], tab + r * 1024 + 256 * q, xj, 1, acc[r]);
         }
     }
     // reduce-scatter of the 4 row sums: lane 16j holds row j's total
@@ -1119,11 +1192,12 @@ __global__ __launch_bounds__(256, 3) void bl4_decode_gate_up_t1(DecodeArgs A) {
     const uint8_t* wtabs = (const uint8_t*)A.d.w13.tables;
     const int64_t per = (int64_t)A.d.w13.rows * (A.d.hidden / 2);
     asm volatile("" ::"s"(wcodes), "s"(wtabs), "s"(per));
+    // the activations of the lane's code dwords l + 64q (8 columns each)
     uint32_t xs[16];
-    const uint16_t* xp = A.x + (32 * lane < A.d.hidden ? 32 * lane : 0);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        const uint4 v = *reinterpret_cast<const uint4*>(xp + 8 * q);
+        uint4 v = {0u, 0u, 0u, 0u};
+        if (8 * (lane + 64 * q) < A.d.hidden) v = *reinterpret_cast<const uint4*>(A.x + 8 * lane + 512 * q);
         xs[4 * q + 0] = v.x;
         xs[4 * q + 1] = v.y;
         xs[4 * q + 2] = v.z;
@@ -1791,7 +1865,7 @@ __device__ __forceinline__ void fused_down_item(const DecodeArgs& A, const Route
     Rows8 pre;
     if (wv < R.nact) {
         const int e = R.act[wv];
-        load_rows8((const uint8_t*)A.d.w2.codes + e * per, (const uint8_t*)A.d.w2.tables + e * per, rows, I, 0,
+        load_rows8<TB>((const uint8_t*)A.d.w2.codes + e * per, (const uint8_t*)A.d.w2.tables + e * per, rows, I, 0,
                    lane, pre);
     }
     // Wait for every act slice: poll with relaxed loads (no cache
@@ -1826,9 +1900,10 @@ __device__ __forceinline__ void fused_down_item(const DecodeArgs& A, const Route
                 for (int t = 0; t < TB; ++t) acc[r][t] = 0.f;
             for (int cc = 0; cc < nch; ++cc) {
                 // the first pass uses the prefetched rows, later ones reload
-                if (!(a == wv && tb == 0 && cc == 0)) load_rows8(codes, tabs, rows, I, cc, lane, pre);
+                if (!(a == wv && tb == 0 && cc == 0)) load_rows8<TB>(codes, tabs, rows, I, cc, lane, pre);
                 uint32_t xs[TB][16];
-                load_x8<TB>(xrow, I, cc, lane, nt, xs);
+                if constexpr (bl4_interleaved<TB>()) load_xi<TB>(xrow, I, cc, lane, xs);
+                else load_x8<TB>(xrow, I, cc, lane, nt, xs);
                 compute_rows8<TB>(pre, xs, cc * kWChunk + 32 * lane < I, lane, slot, nt, acc);
             }
 #pragma unroll
