@@ -1448,27 +1448,24 @@ __global__ __launch_bounds__(256, TB <= 2 ? 3 : 2) void bl4_decode_down(DecodeAr
     }
 }
 
-// One token (T = 1), BL4: CTA x covers output rows [4x, 4x + 4); wave wv takes
-// the active slots wv, wv + 4, .. (one position each, unless the token lists
-// the expert more than once).  An expert's 4 rows are contiguous in memory
-// (K/2 code bytes and K/2 table bytes per row), so they are walked as one
-// flat array of 16-byte units: unit u
-// covers columns [32g, 32g + 32) of row u / NU (NU = K/32, g = u % NU), and
-// lane l takes units l, l + 64, .. (kPass passes).  Every lane works whatever
-// K is (K = 1408: 176 units in 3 passes, where a row per pass leaves 20 of 64
-// lanes idle); the two halves of a 64-weight block stay on neighbouring lanes
-// because NU is even.  The routing is read from the workspace copy in place:
-// no LDS copy and no barrier before the weight loads.
+// One or two tokens (TB), BL4: CTA x covers output rows [4x, 4x + 4); wave
+// wv takes the active slots wv, wv + 4, .. (a slot holds one position per
+// token that routes to its expert, more when a token lists it twice).  A
+// slot's 4 rows run through bl4_rows4 (interleaved code dwords: every LDS
+// lookup conflict-free, and at K = 1408, 176 dwords a row, 44 of 48 lane
+// steps busy), then one 4-value reduce-scatter gives each row's sum.  The
+// routing is read from the workspace copy in place: no LDS copy and no
+// barrier before the weight loads.
 constexpr int kD1Rows = 4;
 
-template <int kPass, int TB>
+template <int TB>
 __global__ __launch_bounds__(256, 2) void bl4_decode_down1(DecodeArgs A) {
-    __shared__ __attribute__((aligned(16))) uint8_t s_slot[4][kPass * 1024];
+    __shared__ __attribute__((aligned(16))) uint8_t s_slot[4][kD1Rows * 1024];
     __shared__ float s_y[16 * TB][kD1Rows];   // [position][row]: at most T (k + S) <= 16 T positions
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int K = A.d.inter, H = A.d.hidden, ke = A.k + A.d.num_shared;
-    const int NU = K / 32, U = kD1Rows * NU;
     const int h0 = blockIdx.x * kD1Rows;   // H % 64 == 0: all 4 rows exist
+    const int rows[kD1Rows] = {h0, h0 + 1, h0 + 2, h0 + 3};
     const RouteOut* R = A.route;
     // the routing fields this wave needs, in one round trip: the count, the
     // first slot's expert and position (in bounds for any count), and the
@@ -1477,55 +1474,30 @@ __global__ __launch_bounds__(256, 2) void bl4_decode_down1(DecodeArgs A) {
     int e_next = R->act[wv], p_next = R->aoff[wv], n_next = R->an[wv];
     const int inv_l = (wv == 0 && lane < ke * TB) ? R->inv[lane] : -1;
     const int64_t per = (int64_t)A.d.w2.rows * (K / 2);
-    const int64_t rbase = (int64_t)h0 * (K / 2);
     const uint8_t* wcodes = (const uint8_t*)A.d.w2.codes;
     const uint8_t* wtabs = (const uint8_t*)A.d.w2.tables;
     // the weight bases come from the kernel arguments while the routing loads
     // are in flight (not after them)
     asm volatile("" ::"s"(wcodes), "s"(wtabs), "s"(per));
-    uint8_t* slot = s_slot[wv];
-    const uint32_t tab0 = lds_addr(slot) + ((lane >> 1) << 5);
-    const u32x4_t z = {0u, 0u, 0u, 0u};
     for (int a = wv; a < nact; a += 4) {
         const int e = e_next, p0 = p_next, n = n_next;
-        const uint8_t* codes = wcodes + e * per + rbase;
-        const uint8_t* tabs = wtabs + e * per + rbase;
         // one token: a single pass (a slot's positions are the same token);
         // two tokens: passes of up to 2 positions
         for (int tb = 0; tb < (TB == 1 ? 1 : n); tb += TB) {
             const int nt = TB == 1 ? 1 : min(TB, n - tb);
-            int pair[TB];   // their weights are loaded after the weight loads
+            int pair[TB];
+            const uint16_t* xrow[TB];
 #pragma unroll
-            for (int t = 0; t < TB; ++t) pair[t] = R->perm[p0 + tb + min(t, nt - 1)];
-            uint32_t xs[kPass][TB][16];
-            u32x4_t cw[kPass], tw[kPass];
-#pragma unroll
-            for (int p = 0; p < kPass; ++p) {
-                const int u = 64 * p + lane;
-                const int g = u < U ? u % NU : 0;
-#pragma unroll
-                for (int t = 0; t < TB; ++t) {
-                    const uint16_t* xr = A.act + (int64_t)(p0 + tb + min(t, nt - 1)) * K;
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const uint4 v = *reinterpret_cast<const uint4*>(xr + 32 * g + 8 * q);
-                        xs[p][t][4 * q + 0] = v.x;
-                        xs[p][t][4 * q + 1] = v.y;
-                        xs[p][t][4 * q + 2] = v.z;
-                        xs[p][t][4 * q + 3] = v.w;
-                    }
-                }
+            for (int t = 0; t < TB; ++t) {
+                pair[t] = R->perm[p0 + tb + min(t, nt - 1)];
+                xrow[t] = A.act + (int64_t)(p0 + tb + min(t, nt - 1)) * K;
             }
-            __builtin_amdgcn_sched_barrier(0);
+            float acc[kD1Rows][TB];
 #pragma unroll
-            for (int p = 0; p < kPass; ++p) {
-                const int u = 64 * p + lane;
-                const int64_t off = u < U ? 16 * u : 0;
-                cw[p] = *reinterpret_cast<const u32x4_t*>(codes + off);
-                tw[p] = *reinterpret_cast<const u32x4_t*>(tabs + off);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            // behind the weight loads: the pair weights and the next slot's fields
+            for (int r = 0; r < kD1Rows; ++r)
+#pragma unroll
+                for (int t = 0; t < TB; ++t) acc[r][t] = 0.f;
+            bl4_rows4<TB>(wcodes + e * per, wtabs + e * per, rows, K, lane, s_slot[wv], xrow, nt, acc);
             float pw[TB];
 #pragma unroll
             for (int t = 0; t < TB; ++t) pw[t] = R->pw[pair[t]];
@@ -1534,52 +1506,12 @@ __global__ __launch_bounds__(256, 2) void bl4_decode_down1(DecodeArgs A) {
                 p_next = R->aoff[a + 4];
                 n_next = R->an[a + 4];
             }
-            float acc[kPass][TB];
-#pragma unroll
-            for (int p = 0; p < kPass; ++p) {
-                // units past the 4 rows stage zero tables (their loads read the first unit)
-                *reinterpret_cast<u32x4_t*>(slot + p * 1024 + 16 * lane) = 64 * p + lane < U ? tw[p] : z;
-                wave_lds_sync();
-                float s[TB];
-#pragma unroll
-                for (int t = 0; t < TB; ++t) s[t] = 0.f;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    uint32_t xj[TB][4];
-#pragma unroll
-                    for (int t = 0; t < TB; ++t)
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) xj[t][i] = xs[p][t][4 * j + i];
-                    bl4_dot8<TB>(cw[p][j], tab0 + p * 1024, xj, nt, s);
-                }
-#pragma unroll
-                for (int t = 0; t < TB; ++t) acc[p][t] = s[t];
-            }
-            wave_lds_sync();
-            // per-row sums: unit partials through LDS, then lane 16r + j adds
-            // units r*NU + j, + 16, .. and the 16 lanes of row r reduce with DPP
-            float* part = reinterpret_cast<float*>(slot);
-#pragma unroll
-            for (int t = 0; t < TB; ++t)
-#pragma unroll
-                for (int p = 0; p < kPass; ++p) part[(t * kPass + p) * 64 + lane] = acc[p][t];
-            wave_lds_sync();
-            const int r = lane >> 4, j = lane & 15;
 #pragma unroll
             for (int t = 0; t < TB; ++t) {
                 if (t >= nt) break;
-                const float* pt = part + t * kPass * 64;
-                float v = 0.f;
-                for (int u = j; u < NU; u += 16) v += pt[r * NU + u];
-                v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xb1, 0xf,
-                                                                           0xf, false));
-                v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4e, 0xf,
-                                                                           0xf, false));
-                v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xf,
-                                                                           0xf, false));
-                v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xf,
-                                                                           0xf, false));
-                if (j == 0) {
+                const float v = wave_reduce4(acc[0][t], acc[1][t], acc[2][t], acc[3][t]);   // lane 16r: row r
+                if ((lane & 15) == 0) {
+                    const int r = lane >> 4;
                     s_y[p0 + tb + t][r] = v * pw[t];
                     // one token listing an expert more than once: its other
                     // positions hold the same activations, each with its own weight
@@ -1587,7 +1519,6 @@ __global__ __launch_bounds__(256, 2) void bl4_decode_down1(DecodeArgs A) {
                         for (int q = 1; q < n; ++q) s_y[p0 + q][r] = v * R->pw[R->perm[p0 + q]];
                 }
             }
-            wave_lds_sync();   // the slot is restaged by the next pass
         }
     }
     __syncthreads();
@@ -2162,16 +2093,8 @@ int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* t
         if (fmt_idx == 0 && (tb == 1 || (tb == 2 && T == 2)) && d->inter <= 2048) {
             // one or two tokens, BL4: flat 16-byte units over 4 rows (every lane busy)
             const dim3 g1(d->hidden / kD1Rows);
-#define LUTMOE_DOWN1(P)                                                              \
-    if (tb == 1) hipLaunchKernelGGL((bl4_decode_down1<P, 1>), g1, dim3(256), 0, s, A); \
-    else hipLaunchKernelGGL((bl4_decode_down1<P, 2>), g1, dim3(256), 0, s, A)
-            switch ((d->inter + 511) / 512) {
-                case 1: LUTMOE_DOWN1(1); break;
-                case 2: LUTMOE_DOWN1(2); break;
-                case 3: LUTMOE_DOWN1(3); break;
-                default: LUTMOE_DOWN1(4); break;
-            }
-#undef LUTMOE_DOWN1
+            if (tb == 1) hipLaunchKernelGGL((bl4_decode_down1<1>), g1, dim3(256), 0, s, A);
+            else hipLaunchKernelGGL((bl4_decode_down1<2>), g1, dim3(256), 0, s, A);
             return check_launch();
         }
         if (fmt_idx == 2 && tb == 1 && d->inter <= 2048) {
