@@ -983,11 +983,19 @@ __device__ __forceinline__ void gate_up_body(const DecodeArgs& A, const RV& rv, 
 // the waves of gate_up_body, each with half the serial work.  At one token
 // per pass the kernel is bound by each wave's instruction and latency chain
 // at about 1.4 waves per SIMD, and twice the waves shorten it (T=1 gate/up
-// 10.5 -> 9.6 us); with two or more tokens per pass the waves carry enough
-// work and the 4-index body is as fast or faster (T=2: 16.7 vs 17.9 us).
+// 10.5 -> 9.6 us).  gu2_for: the down kernel's 4-row body (down_body4), one
+// token a pass; gu2_gate_up_for: the gate/up body.
 static_assert(kGuWaves == 1, "gate_up_body4 assumes one wave per CTA");
 template <int TB>
 constexpr bool gu2_for() { return TB == 1; }
+// gate/up with 2 indices a wave (gate_up_body4): one token a pass, and two
+// when a routing kernel ran (T >= 3: 4 rows a wave in the interleaved map
+// keep 44 of 48 lane steps busy at H = 2048 and look up without bank
+// conflicts; T = 8: 68 -> 65 us a layer).  Where every wave routes in
+// registers (T = 2), twice the waves means twice the routing (29.4 -> 30.3 us),
+// and the 8-row body stays.
+template <int TB, bool kPre>
+constexpr bool gu2_gate_up_for() { return TB == 1 || (kPre && TB == 2); }
 
 // Four BL4 rows over all of K (as bl4_rows8 for 8, in its interleaved lane
 // map: conflict-free lookups, which for one token a pass measured faster,
@@ -1307,7 +1315,7 @@ __global__ __launch_bounds__(256, 3) void ref_decode_gate_up_t1(DecodeArgs A) {
 template <int TB, bool kPre, int kFmt>
 __global__ __launch_bounds__(64 * kGuWaves, TB <= 2 ? 3 : 2) void bl4_decode_gate_up(DecodeArgs A) {
     __shared__ __attribute__((aligned(16))) uint8_t s_slot[kGuWaves * kSlot];
-    if constexpr (gu2_for<TB>() && kFmt == LUTMOE_FMT_BL4) {
+    if constexpr (gu2_gate_up_for<TB, kPre>() && kFmt == LUTMOE_FMT_BL4) {
         if constexpr (kPre) {
             gate_up_body4<TB>(A, GlobalRouteView{A.route}, s_slot);
         } else {
@@ -1705,6 +1713,49 @@ __global__ __launch_bounds__(256, TB <= 2 ? 3 : 2) void bl4_decode_down_y(Decode
     }
 }
 
+// BL4 down when many experts are active, 4 output rows a wave: CTA (x, g)
+// covers output rows 4x..4x+3 of work items 4g..4g+3, one per wave, through
+// the interleaved 4-row loop (bl4_rows4: conflict-free lookups, and at
+// K = 1408 44 of 48 lane steps busy, where 8 rows of one 32-column unit a
+// lane leave 20 of 64 lanes idle); y[pos][h] as bl4_decode_down_y.
+template <int TB>
+__global__ __launch_bounds__(256, 2) void bl4_decode_down_y4(DecodeArgs A, float* __restrict__ y) {
+    __shared__ __attribute__((aligned(16))) uint8_t s_slot[4][4 * 1024];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const GlobalRouteView rv{A.route};
+    const SlotRef sl = rv.work(blockIdx.y * 4 + wv);
+    if (sl.e < 0) return;
+    const int I = A.d.inter, H = A.d.hidden;
+    const int h0 = blockIdx.x * 4;
+    int rows[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) rows[r] = min(h0 + r, H - 1);
+    const int64_t per = (int64_t)A.d.w2.rows * (I / 2);
+    const uint8_t* codes = (const uint8_t*)A.d.w2.codes + sl.e * per;
+    const uint8_t* tabs = (const uint8_t*)A.d.w2.tables + sl.e * per;
+    for (int tb = 0; tb < sl.n; tb += TB) {
+        const int nt = min(TB, sl.n - tb);
+        const uint16_t* xrow[TB];
+#pragma unroll
+        for (int t = 0; t < TB; ++t) xrow[t] = A.act + (int64_t)(sl.p0 + tb + min(t, nt - 1)) * I;
+        float acc[4][TB];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int t = 0; t < TB; ++t) acc[r][t] = 0.f;
+        float pwv[TB];
+#pragma unroll
+        for (int t = 0; t < TB; ++t) pwv[t] = rv.weight_at(sl.p0 + tb + min(t, nt - 1));
+        bl4_rows4<TB>(codes, tabs, rows, I, lane, s_slot[wv], xrow, nt, acc);
+#pragma unroll
+        for (int t = 0; t < TB; ++t) {
+            const float yv = wave_reduce4(acc[0][t], acc[1][t], acc[2][t], acc[3][t]);   // lane 16r: row r
+            const int r = lane >> 4;
+            if ((lane & 15) == 0 && t < nt && h0 + r < H) y[(int64_t)(sl.p0 + tb + t) * H + h0 + r] = yv * pwv[t];
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // One persistent kernel for the whole layer.  Every CTA routes, then takes
 // work items from a queue in the workspace: first the gate_up items (one per
@@ -2058,7 +2109,8 @@ int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* t
         else hipLaunchKernelGGL(ref_decode_gate_up_t1, grid, dim3(256), 0, s, A);
         if ((rc = check_launch())) return rc;
     } else if (stages & LUTMOE_STAGE_GATE_UP) {
-        const int per_cta = (fmt_idx == 0 && tb == 1) ? 2 : 4 * kGuWaves;   // intermediate indices per CTA
+        // intermediate indices per CTA (gu2_gate_up_for: 2)
+        const int per_cta = (fmt_idx == 0 && (tb == 1 || (pre && tb == 2))) ? 2 : 4 * kGuWaves;
         const dim3 grid((d->inter + per_cta - 1) / per_cta, max_work);
         LUTMOE_DECODE_LAUNCH(bl4_decode_gate_up, pre, grid, dim3(64 * kGuWaves), 0)
         if ((rc = check_launch())) return rc;
@@ -2073,11 +2125,15 @@ int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* t
             // many experts: y + combine, every slot in parallel
             const dim3 gy((d->hidden + kRows - 1) / kRows, (max_work + 3) / 4);
 #define LUTMOE_DOWN_Y(TB, FMT) hipLaunchKernelGGL((bl4_decode_down_y<TB, FMT>), gy, dim3(256), 0, s, A, y_ws)
-            switch (tb * 4 + fmt_idx) {
-                case 4: LUTMOE_DOWN_Y(1, LUTMOE_FMT_BL4); break;
+            // BL4 passes of one or two tokens: 4 rows a wave (bl4_decode_down_y4;
+            // T = 8: 72 -> 68 us a layer); four-token passes keep 8 rows a
+            // wave (T = 32: 152 against 169 us with 4)
+            const dim3 gy4((d->hidden + 3) / 4, (max_work + 3) / 4);
+            switch (tb * 4 + fmt_idx + (fmt_idx == 0 && tb <= 2 ? 64 : 0)) {
+                case 68: hipLaunchKernelGGL((bl4_decode_down_y4<1>), gy4, dim3(256), 0, s, A, y_ws); break;
+                case 72: hipLaunchKernelGGL((bl4_decode_down_y4<2>), gy4, dim3(256), 0, s, A, y_ws); break;
                 case 5: LUTMOE_DOWN_Y(1, LUTMOE_FMT_NESTED); break;
                 case 6: LUTMOE_DOWN_Y(1, LUTMOE_FMT_REF); break;
-                case 8: LUTMOE_DOWN_Y(2, LUTMOE_FMT_BL4); break;
                 case 9: LUTMOE_DOWN_Y(2, LUTMOE_FMT_NESTED); break;
                 case 10: LUTMOE_DOWN_Y(2, LUTMOE_FMT_REF); break;
                 case 16: LUTMOE_DOWN_Y(4, LUTMOE_FMT_BL4); break;
