@@ -1223,6 +1223,30 @@ def test_moe_layer_mixtral_shape(gpu):
     assert rel_maxabs(out, ref) <= TOL
 
 
+@pytest.mark.parametrize("T", [3, 20])
+def test_moe_layer_two_chunk_rows(gpu, T):
+    """Decode where both projections span two 2048-column chunks (H = 4096, I = 2304): two-
+    token passes (T = 3) and four-token passes (T = 20, the interleaved code-dword lane map of
+    the 8-row loop) against the oracle on host-dequantised weights."""
+    import torch
+    from block_lut_amd import ops
+    from block_lut_amd.formats import MoEWeights
+    from gpu_weights import DevBL4
+    E, S, k, H, I = 4, 0, 2, 4096, 2304
+    g = torch.Generator(device=gpu).manual_seed(230 + T)
+    w13 = DevBL4(E, 2 * I, H, g, gpu)
+    w2 = DevBL4(E, H, I, g, gpu)
+    moe = MoEWeights(w13.stack, w2.stack, H, I, E, S)
+    rng = np.random.default_rng(2300 + T)
+    xb = _x(rng, T, H)
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    rw, rids = O.route(lg, k)
+    out = ops.moe_forward(moe, to_dev_bf16(xb, gpu), torch.from_numpy(rw).to(gpu),
+                          torch.from_numpy(rids).to(gpu), out_dtype=torch.float32, path=1)
+    ref = O.moe_layer(xb, rids, rw, w13.host, w2.host)
+    assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
+
+
 def _sigmoid_gate(xb, gate_bits):
     z = O.bf16_to_f32(xb).astype(np.float64) @ O.bf16_to_f32(gate_bits).astype(np.float64)
     return 1.0 / (1.0 + np.exp(-z))
