@@ -658,10 +658,12 @@ __device__ __forceinline__ void load_x8(const uint16_t* const (&xrow)[TB], int K
 // slot (block g at r*1024 + 32g), then look its codes up there and
 // accumulate (code dword q: block l/2 contiguous, l/8 + 8q interleaved); row
 // r only waits for its own loads, so the first rows are done while the later
-// ones are still arriving.  `ok`: the lane's table bytes lie inside K.
+// ones are still arriving.  `ok`: the lane's table bytes lie inside K; `nd`:
+// the chunk's code dwords per row (interleaved: steps q with 64q >= nd hold
+// no code and are skipped, e.g. q = 3 at K = 1408).
 template <int TB>
 __device__ __forceinline__ void compute_rows8(const Rows8& b, const uint32_t (&xs)[TB][16], bool ok, int lane,
-                                              uint8_t* slot, int nt, float (&acc)[kRows][TB]) {
+                                              int nd, uint8_t* slot, int nt, float (&acc)[kRows][TB]) {
     constexpr bool kInter = bl4_interleaved<TB>();
     const uint32_t tab = lds_addr(slot) + (kInter ? (lane >> 3) << 5 : (lane >> 1) << 5);
     const u32x4_t z = {0u, 0u, 0u, 0u};
@@ -672,6 +674,7 @@ __device__ __forceinline__ void compute_rows8(const Rows8& b, const uint32_t (&x
         wave_lds_sync();
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
+            if (kInter && 64 * q >= nd) break;
             uint32_t xj[TB][4];
 #pragma unroll
             for (int t = 0; t < TB; ++t)
@@ -698,7 +701,7 @@ __device__ __forceinline__ void bl4_rows8(const uint8_t* __restrict__ codes, con
         load_rows8<TB>(codes, tabs, rows, K, cc, lane, b);
         // every load in flight before the first row is consumed
         __builtin_amdgcn_sched_barrier(0);
-        compute_rows8<TB>(b, xs, cc * kWChunk + 32 * lane < K, lane, slot, nt, acc);
+        compute_rows8<TB>(b, xs, cc * kWChunk + 32 * lane < K, lane, chunk_dwords(K, cc), slot, nt, acc);
     }
 }
 
@@ -1035,6 +1038,7 @@ __device__ __forceinline__ void bl4_rows4(const uint8_t* __restrict__ codes, con
             wave_lds_sync();
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
+                if (64 * q >= nd) break;   // no code dword (K = 1408: q = 3)
                 uint32_t xj[TB][4];
 #pragma unroll
                 for (int t = 0; t < TB; ++t)
@@ -1886,7 +1890,7 @@ __device__ __forceinline__ void fused_down_item(const DecodeArgs& A, const Route
                 uint32_t xs[TB][16];
                 if constexpr (bl4_interleaved<TB>()) load_xi<TB>(xrow, I, cc, lane, xs);
                 else load_x8<TB>(xrow, I, cc, lane, nt, xs);
-                compute_rows8<TB>(pre, xs, cc * kWChunk + 32 * lane < I, lane, slot, nt, acc);
+                compute_rows8<TB>(pre, xs, cc * kWChunk + 32 * lane < I, lane, chunk_dwords(I, cc), slot, nt, acc);
             }
 #pragma unroll
             for (int t = 0; t < TB; ++t) {
