@@ -69,6 +69,20 @@ struct RouteChunks {
     int cn[kMaxP];                      // its positions
 };
 
+// The routing weight of each position (pw[perm[p]]), stored after the
+// RouteChunks of the global copy: a down-projection wave that knows its first
+// position loads its weight in the same round trip as its activations,
+// instead of the pair index and then the weight.
+struct RoutePosW {
+    float w[kMaxP];
+};
+__device__ __forceinline__ float* route_pos_w(RouteOut* g) {
+    return reinterpret_cast<RoutePosW*>(reinterpret_cast<RouteChunks*>(g + 1) + 1)->w;
+}
+__device__ __forceinline__ const float* route_pos_w(const RouteOut* g) {
+    return reinterpret_cast<const RoutePosW*>(reinterpret_cast<const RouteChunks*>(g + 1) + 1)->w;
+}
+
 struct RouteScratch {
     int pid[kMaxP];                     // expert of each pair (-1: dropped)
     int rin[kMaxP];                     // rank among same-expert pairs of its 64-pair chunk
@@ -420,7 +434,7 @@ struct GlobalRouteView {
         return {C->ce[c], C->cp0[c], C->cn[c]};
     }
     __device__ int pair_at(int p) const { return R->perm[p]; }
-    __device__ float weight_at(int p) const { return R->pw[R->perm[p]]; }
+    __device__ float weight_at(int p) const { return route_pos_w(R)[p]; }
     __device__ int pos_of(int q) const { return R->inv[q]; }
 };
 
@@ -456,7 +470,10 @@ __device__ __forceinline__ void wave_route_publish(const DecodeArgs& A, const Wa
     if (lane < P) {
         g->inv[lane] = r.pos;
         g->pw[lane] = r.w;
-        if (r.pos >= 0) g->perm[r.pos] = lane;
+        if (r.pos >= 0) {
+            g->perm[r.pos] = lane;
+            route_pos_w(g)[r.pos] = r.w;
+        }
     }
     if (lane == 0) g->nact = r.nact;
     // one work item per slot
@@ -514,10 +531,12 @@ __device__ __forceinline__ void put_route(const DecodeArgs& A, const RouteOut& R
         g->aoff[i] = R.aoff[i];
         g->an[i] = R.an[i];
     }
+    float* pos_w = route_pos_w(g);
     for (int i = threadIdx.x; i < P; i += blockDim.x) {
         g->perm[i] = R.perm[i];
         g->inv[i] = R.inv[i];
         g->pw[i] = R.pw[i];
+        if (R.inv[i] >= 0) pos_w[R.inv[i]] = R.pw[i];   // pair i's position
     }
     if (threadIdx.x == 0) g->nact = R.nact;
 }
@@ -1479,6 +1498,7 @@ __global__ __launch_bounds__(256, 2) void bl4_decode_down1(DecodeArgs A) {
     const int h0 = blockIdx.x * kD1Rows;   // H % 64 == 0: all 4 rows exist
     const int rows[kD1Rows] = {h0, h0 + 1, h0 + 2, h0 + 3};
     const RouteOut* R = A.route;
+    const float* pos_w = route_pos_w(R);
     // the routing fields this wave needs, in one round trip: the count, the
     // first slot's expert and position (in bounds for any count), and the
     // positions of the tokens' pairs for the combine
@@ -1497,12 +1517,18 @@ __global__ __launch_bounds__(256, 2) void bl4_decode_down1(DecodeArgs A) {
         // two tokens: passes of up to 2 positions
         for (int tb = 0; tb < (TB == 1 ? 1 : n); tb += TB) {
             const int nt = TB == 1 ? 1 : min(TB, n - tb);
-            int pair[TB];
+            // the routing weights: two tokens, from the positions' weight
+            // array with the activations; one token, through the pair index
+            // with the activations and the weight after the lookups (measured
+            // 0.2 us faster per layer than the early weight load)
             const uint16_t* xrow[TB];
+            float pw[TB];
+            int pair = 0;
 #pragma unroll
             for (int t = 0; t < TB; ++t) {
-                pair[t] = R->perm[p0 + tb + min(t, nt - 1)];
                 xrow[t] = A.act + (int64_t)(p0 + tb + min(t, nt - 1)) * K;
+                if constexpr (TB == 1) pair = R->perm[p0];
+                else pw[t] = pos_w[p0 + tb + min(t, nt - 1)];
             }
             float acc[kD1Rows][TB];
 #pragma unroll
@@ -1510,9 +1536,7 @@ __global__ __launch_bounds__(256, 2) void bl4_decode_down1(DecodeArgs A) {
 #pragma unroll
                 for (int t = 0; t < TB; ++t) acc[r][t] = 0.f;
             bl4_rows4<TB>(wcodes + e * per, wtabs + e * per, rows, K, lane, s_slot[wv], xrow, nt, acc);
-            float pw[TB];
-#pragma unroll
-            for (int t = 0; t < TB; ++t) pw[t] = R->pw[pair[t]];
+            if constexpr (TB == 1) pw[0] = R->pw[pair];
             if (tb == 0 && a + 4 < kMaxEtot) {
                 e_next = R->act[a + 4];
                 p_next = R->aoff[a + 4];
@@ -1528,7 +1552,7 @@ __global__ __launch_bounds__(256, 2) void bl4_decode_down1(DecodeArgs A) {
                     // one token listing an expert more than once: its other
                     // positions hold the same activations, each with its own weight
                     if constexpr (TB == 1)
-                        for (int q = 1; q < n; ++q) s_y[p0 + q][r] = v * R->pw[R->perm[p0 + q]];
+                        for (int q = 1; q < n; ++q) s_y[p0 + q][r] = v * pos_w[p0 + q];
                 }
             }
         }
@@ -1649,7 +1673,7 @@ __global__ __launch_bounds__(256, 2) void ref_decode_down1(DecodeArgs A) {
         if (j == 0) {
             s_y[p0][r] = v * pw;
             // an expert the token lists more than once: the same activations
-            for (int q = 1; q < n; ++q) s_y[p0 + q][r] = v * R->pw[R->perm[p0 + q]];
+            for (int q = 1; q < n; ++q) s_y[p0 + q][r] = v * route_pos_w(R)[p0 + q];
         }
         wave_lds_sync();   // the codebook and the partials are restaged by the next slot
     }
@@ -1697,8 +1721,8 @@ __global__ __launch_bounds__(256, TB <= 2 ? 3 : 2) void bl4_decode_down_y(Decode
         for (int r = 0; r < kRows; ++r)
 #pragma unroll
             for (int t = 0; t < TB; ++t) acc[r][t] = 0.f;
-        // the positions' routing weights (two dependent loads each) issued
-        // ahead of the weight loads, which hide them
+        // the positions' routing weights (one load each, from the positions'
+        // weight array) issued ahead of the weight loads, which hide them
         float pwv[TB];
 #pragma unroll
         for (int t = 0; t < TB; ++t) pwv[t] = rv.weight_at(sl.p0 + tb + min(t, nt - 1));
@@ -2041,7 +2065,7 @@ int launch_nested_gemv(const lutmoe_weights* w, int expert, const uint16_t* x, i
     return check_launch();
 }
 
-size_t decode_route_bytes() { return sizeof(RouteOut) + sizeof(RouteChunks); }
+size_t decode_route_bytes() { return sizeof(RouteOut) + sizeof(RouteChunks) + sizeof(RoutePosW); }
 size_t decode_sync_bytes() { return sizeof(DecodeSync); }
 
 int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* topk_w,
