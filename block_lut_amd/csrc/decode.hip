@@ -1121,13 +1121,25 @@ __device__ __forceinline__ void gate_up_body4(const DecodeArgs& A, const RV& rv,
 // thousands of one-wave CTAs.  Returns -1 past the last slot and -2 where
 // this path does not apply (more than 64 routed experts, or ids that repeat:
 // the caller then takes the general routing).
-__device__ __forceinline__ int t1_slot_expert(const DecodeArgs& A, int y) {
+// The lane's routing input for t1_slot_expert: top-k id `lane` (lane < k)
+// or router logit `lane` (lane < E) as raw bits.  One load for every lane
+// (clamped index), issued before the activation loads so that the routing
+// does not wait for them.
+__device__ __forceinline__ uint32_t t1_route_input(const DecodeArgs& A) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t* src = A.topk_ids ? reinterpret_cast<const uint32_t*>(A.topk_ids)
+                                     : reinterpret_cast<const uint32_t*>(A.logits);
+    const int n = A.topk_ids ? A.k : A.d.num_routed;
+    return src[min(lane, n - 1)];
+}
+
+__device__ __forceinline__ int t1_slot_expert(const DecodeArgs& A, int y, uint32_t rin) {
     const int lane = threadIdx.x & 63;
     const int E = A.d.num_routed, S = A.d.num_shared, k = A.k;
     if (E > 64) return -2;
     uint64_t sel = 0;
     if (A.topk_ids) {
-        const int id = lane < k ? A.topk_ids[lane] : -1;
+        const int id = lane < k ? (int)rin : -1;
         const bool ok = lane < k && id >= 0 && id < E;
         for (int j = 0; j < k; ++j) {
             const int e = __builtin_amdgcn_readlane(id, j);
@@ -1135,7 +1147,7 @@ __device__ __forceinline__ int t1_slot_expert(const DecodeArgs& A, int y) {
         }
         if (__popcll(sel) != __popcll(__ballot(ok))) return -2;   // a repeated id
     } else {
-        const float v = lane < E ? A.logits[lane] : -INFINITY;
+        const float v = lane < E ? __builtin_bit_cast(float, rin) : -INFINITY;
         int key = lane < E ? float_key(v) : INT_MIN;
         for (int j = 0; j < k; ++j) {
             const int m = wave_max_i32(key);
@@ -1223,26 +1235,37 @@ __global__ __launch_bounds__(256, 3) void bl4_decode_gate_up_t1(DecodeArgs A) {
     const uint8_t* wtabs = (const uint8_t*)A.d.w13.tables;
     const int64_t per = (int64_t)A.d.w13.rows * (A.d.hidden / 2);
     asm volatile("" ::"s"(wcodes), "s"(wtabs), "s"(per));
-    // the activations of the lane's code dwords l + 64q (8 columns each)
+    const uint32_t rin = t1_route_input(A);
+    __builtin_amdgcn_sched_barrier(0);
+    // the activations of the lane's code dwords l + 64q (8 columns each):
+    // every load issued (past H: the last 8 columns, then zeroed), so none
+    // waits for another (a load under a lane condition made the compiler
+    // wait for it before issuing the next)
     uint32_t xs[16];
+    const int nd = A.d.hidden / 8;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        uint4 v = {0u, 0u, 0u, 0u};
-        if (8 * (lane + 64 * q) < A.d.hidden) v = *reinterpret_cast<const uint4*>(A.x + 8 * lane + 512 * q);
-        xs[4 * q + 0] = v.x;
-        xs[4 * q + 1] = v.y;
-        xs[4 * q + 2] = v.z;
-        xs[4 * q + 3] = v.w;
+        const int d = lane + 64 * q;
+        const uint4 v = *reinterpret_cast<const uint4*>(A.x + 8 * min(d, nd - 1));
+        const uint32_t m = d < nd ? 0xffffffffu : 0u;
+        xs[4 * q + 0] = v.x & m;
+        xs[4 * q + 1] = v.y & m;
+        xs[4 * q + 2] = v.z & m;
+        xs[4 * q + 3] = v.w & m;
     }
+    if (2 * xcol < A.d.inter) {
+        const int e = t1_slot_expert(A, blockIdx.y, rin);
+        if (e >= 0) {
+            gate_up_t1(A, xs, wcodes, wtabs, per, e, blockIdx.y, xcol, s_slot[wv]);
+        } else if (e == -2) {
+            // ids that repeat: the general routing
+            gate_up_body4<1>(A, WaveRouteView{wave_pairs<false>(A)}, s_slot[wv], xcol);
+        }
+    }
+    // after the wave's own rows (the down kernel reads the copy only after
+    // this kernel ends): publishing first put its loads ahead of every
+    // wave's routing wait
     if (blockIdx.x == 0 && blockIdx.y == 0 && wv == 0) wave_route_publish(A, wave_pairs<true>(A));
-    if (2 * xcol >= A.d.inter) return;
-    const int e = t1_slot_expert(A, blockIdx.y);
-    if (e >= 0) {
-        gate_up_t1(A, xs, wcodes, wtabs, per, e, blockIdx.y, xcol, s_slot[wv]);
-    } else if (e == -2) {
-        // ids that repeat: the general routing
-        gate_up_body4<1>(A, WaveRouteView{wave_pairs<false>(A)}, s_slot[wv], xcol);
-    }
 }
 
 // One token, REF, K = H <= 2048 (one chunk): gate rows i0, i0 + 1 and up
@@ -1312,6 +1335,8 @@ __global__ __launch_bounds__(256, 3) void ref_decode_gate_up_t1(DecodeArgs A) {
     __shared__ __attribute__((aligned(16))) uint8_t s_cb[4][512];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int xcol = blockIdx.x * 4 + wv;
+    const uint32_t rin = t1_route_input(A);
+    __builtin_amdgcn_sched_barrier(0);
     uint32_t xs[16];
     const uint16_t* xp = A.x + (32 * lane < A.d.hidden ? 32 * lane : 0);
 #pragma unroll
@@ -1322,17 +1347,19 @@ __global__ __launch_bounds__(256, 3) void ref_decode_gate_up_t1(DecodeArgs A) {
         xs[4 * q + 2] = v.z;
         xs[4 * q + 3] = v.w;
     }
-    if (blockIdx.x == 0 && blockIdx.y == 0 && wv == 0) wave_route_publish(A, wave_pairs<true>(A));
-    if (2 * xcol >= A.d.inter) return;
-    int e = t1_slot_expert(A, blockIdx.y), p0 = blockIdx.y, n = 1;
-    if (e == -2) {
-        // ids that repeat: the general routing (a slot may hold two positions)
-        const SlotRef sl = WaveRouteView{wave_pairs<false>(A)}.work(blockIdx.y);
-        e = sl.e;
-        p0 = sl.p0;
-        n = sl.n;
+    if (2 * xcol < A.d.inter) {
+        int e = t1_slot_expert(A, blockIdx.y, rin), p0 = blockIdx.y, n = 1;
+        if (e == -2) {
+            // ids that repeat: the general routing (a slot may hold two positions)
+            const SlotRef sl = WaveRouteView{wave_pairs<false>(A)}.work(blockIdx.y);
+            e = sl.e;
+            p0 = sl.p0;
+            n = sl.n;
+        }
+        if (e >= 0) ref_gate_up_t1(A, xs, e, p0, n, xcol, s_cb[wv]);
     }
-    if (e >= 0) ref_gate_up_t1(A, xs, e, p0, n, xcol, s_cb[wv]);
+    // after the wave's own rows, as in bl4_decode_gate_up_t1
+    if (blockIdx.x == 0 && blockIdx.y == 0 && wv == 0) wave_route_publish(A, wave_pairs<true>(A));
 }
 
 template <int TB, bool kPre, int kFmt>
