@@ -314,8 +314,14 @@ __device__ __forceinline__ WaveRoute wave_pairs(const DecodeArgs& A) {
             }
         }
     } else {
+        // the first two tokens' logits in flight together (clamped indices,
+        // in bounds: E <= 64 here), not one round trip per token
+        const int li = min(lane, E - 1);
+        const float v0 = A.logits[li];
+        const float v1 = A.logits[(int64_t)min(1, T - 1) * E + li];
         for (int t = 0; t < T; ++t) {
-            const float v = lane < E ? A.logits[(int64_t)t * E + lane] : -INFINITY;
+            const float raw = t == 0 ? v0 : t == 1 ? v1 : A.logits[(int64_t)t * E + li];
+            const float v = lane < E ? raw : -INFINITY;
             int key = lane < E ? float_key(v) : INT_MIN;
             float mx = 0.f, sum = 1.f;
             if (kWeights) {
