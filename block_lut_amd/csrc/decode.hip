@@ -598,8 +598,10 @@ __global__ __launch_bounds__(1024) void decode_route_kernel(DecodeArgs A) {
 //    a row: with four tokens they pay (T = 32: 155 -> 151 us a layer); with
 //    two the extra loads and registers cost more than the conflicts (T = 8:
 //    70 -> 86 us).
-// Loads past K read nothing (interleaved) or the chunk start (contiguous),
-// and their lookups meet zero tables.
+// Code loads past K read nothing (interleaved: lane-conditional loads, which
+// keep the 256-byte step in the instruction offset; the 4-row loop instead
+// clamps them) or the chunk start (contiguous); their lookups meet zero
+// tables and, interleaved, zeroed activations.
 template <int TB>
 constexpr bool bl4_interleaved() { return TB >= 4; }
 
@@ -638,7 +640,8 @@ __device__ __forceinline__ void load_rows8(const uint8_t* __restrict__ codes, co
 // The activations of the lane's BL4 code dwords in the interleaved map, up
 // to TB vectors: xs[t][4q + i] = columns 8d + 2i, 8d + 2i + 1 of chunk cc
 // (d = l + 64q); zero past K, where the codes meet zero tables.  Vectors past
-// nt are dropped.
+// nt are dropped.  Lane-conditional loads, which keep the 512-column step in
+// the instruction offset (the 8-row loop's registers are tight).
 template <int TB>
 __device__ __forceinline__ void load_xi(const uint16_t* const (&xrow)[TB], int K, int cc, int lane,
                                         uint32_t (&xs)[TB][16]) {
@@ -655,6 +658,43 @@ __device__ __forceinline__ void load_xi(const uint16_t* const (&xrow)[TB], int K
             xs[t][4 * q + 2] = v.z;
             xs[t][4 * q + 3] = v.w;
         }
+    }
+}
+
+// As load_xi, with every load issued (past K the chunk's last 8 columns,
+// zeroed by mask_xi once the weight loads are issued; masking here would make
+// the weight loads wait for these): no load sits under a lane condition, so
+// the compiler's waits cover each row's own loads only (the 4-row loop).
+template <int TB>
+__device__ __forceinline__ void load_xi_all(const uint16_t* const (&xrow)[TB], int K, int cc, int lane,
+                                            uint32_t (&xs)[TB][16]) {
+    const int nd = chunk_dwords(K, cc);
+#pragma unroll
+    for (int t = 0; t < TB; ++t) {
+        const uint16_t* p = xrow[t] + cc * kWChunk;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint4 v = *reinterpret_cast<const uint4*>(p + 8 * min(lane + 64 * q, nd - 1));
+            xs[t][4 * q + 0] = v.x;
+            xs[t][4 * q + 1] = v.y;
+            xs[t][4 * q + 2] = v.z;
+            xs[t][4 * q + 3] = v.w;
+        }
+    }
+}
+
+// Zero the activations load_xi_all read past K (their codes meet zero tables; a
+// zero activation keeps an infinite one out of the sum).
+template <int TB>
+__device__ __forceinline__ void mask_xi(int K, int cc, int lane, uint32_t (&xs)[TB][16]) {
+    const int nd = chunk_dwords(K, cc);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t m = lane + 64 * q < nd ? 0xffffffffu : 0u;
+#pragma unroll
+        for (int t = 0; t < TB; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xs[t][4 * q + i] &= m;
     }
 }
 
@@ -1039,7 +1079,7 @@ __device__ __forceinline__ void bl4_rows4(const uint8_t* __restrict__ codes, con
     const int nch = (K + kWChunk - 1) / kWChunk;
     for (int cc = 0; cc < nch; ++cc) {
         uint32_t xs[TB][16];
-        load_xi<TB>(xrow, K, cc, lane, xs);
+        load_xi_all<TB>(xrow, K, cc, lane, xs);
         __builtin_amdgcn_sched_barrier(0);
         const int nd = chunk_dwords(K, cc);
         const bool ok = cc * kWChunk + 32 * lane < K;
@@ -1049,14 +1089,12 @@ __device__ __forceinline__ void bl4_rows4(const uint8_t* __restrict__ codes, con
         for (int r = 0; r < 4; ++r) {
             const uint32_t ro = (uint32_t)rows[r] * (uint32_t)(K / 2) + cc * (kWChunk / 2);
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                cw[r][q] = 0u;
-                if (lane + 64 * q < nd)
-                    cw[r][q] = *reinterpret_cast<const uint32_t*>(codes + (ro + 4 * lane + 256 * q));
-            }
+            for (int q = 0; q < 4; ++q)
+                cw[r][q] = *reinterpret_cast<const uint32_t*>(codes + (ro + 4u * (uint32_t)min(lane + 64 * q, nd - 1)));
             tw[r] = *reinterpret_cast<const u32x4_t*>(tabs + (ro + (ok ? 16 * lane : 0)));
         }
         __builtin_amdgcn_sched_barrier(0);
+        mask_xi<TB>(K, cc, lane, xs);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             *reinterpret_cast<u32x4_t*>(slot + r * 1024 + 16 * lane) = ok ? tw[r] : z;
@@ -1194,10 +1232,8 @@ __device__ __forceinline__ void gate_up_t1(const DecodeArgs& A, const uint32_t (
     for (int r = 0; r < 4; ++r) {
         const uint32_t ro = (uint32_t)rows[r] * (uint32_t)(H / 2);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            cw[r][q] = 0u;
-            if (8 * (lane + 64 * q) < H) cw[r][q] = *reinterpret_cast<const uint32_t*>(codes + (ro + 4 * lane + 256 * q));
-        }
+        for (int q = 0; q < 4; ++q)
+            cw[r][q] = *reinterpret_cast<const uint32_t*>(codes + (ro + 4u * (uint32_t)min(lane + 64 * q, H / 8 - 1)));
         tw[r] = *reinterpret_cast<const u32x4_t*>(tabs + (ro + (ok ? 16 * lane : 0)));
     }
     __builtin_amdgcn_sched_barrier(0);
