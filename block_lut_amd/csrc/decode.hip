@@ -1586,18 +1586,14 @@ __global__ __launch_bounds__(256, 2) void bl4_decode_down1(DecodeArgs A) {
         // two tokens: passes of up to 2 positions
         for (int tb = 0; tb < (TB == 1 ? 1 : n); tb += TB) {
             const int nt = TB == 1 ? 1 : min(TB, n - tb);
-            // the routing weights: two tokens, from the positions' weight
-            // array with the activations; one token, through the pair index
-            // with the activations and the weight after the lookups (measured
-            // 0.2 us faster per layer than the early weight load)
+            // the routing weights from the positions' weight array, loaded
+            // with the activations
             const uint16_t* xrow[TB];
             float pw[TB];
-            int pair = 0;
 #pragma unroll
             for (int t = 0; t < TB; ++t) {
                 xrow[t] = A.act + (int64_t)(p0 + tb + min(t, nt - 1)) * K;
-                if constexpr (TB == 1) pair = R->perm[p0];
-                else pw[t] = pos_w[p0 + tb + min(t, nt - 1)];
+                pw[t] = pos_w[p0 + tb + min(t, nt - 1)];
             }
             float acc[kD1Rows][TB];
 #pragma unroll
@@ -1605,7 +1601,6 @@ __global__ __launch_bounds__(256, 2) void bl4_decode_down1(DecodeArgs A) {
 #pragma unroll
                 for (int t = 0; t < TB; ++t) acc[r][t] = 0.f;
             bl4_rows4<TB>(wcodes + e * per, wtabs + e * per, rows, K, lane, s_slot[wv], xrow, nt, acc);
-            if constexpr (TB == 1) pw[0] = R->pw[pair];
             if (tb == 0 && a + 4 < kMaxEtot) {
                 e_next = R->act[a + 4];
                 p_next = R->aoff[a + 4];
