@@ -881,18 +881,26 @@ struct Rows8R {
     uint32_t am[kRows];
 };
 
+// The absmax block of the 32 aligned columns starting at flat element 32u of
+// an expert: u / (block_size / 32), clamped to the last block.  32-bit (the
+// host keeps REF experts on these kernels below 2^37 elements); a 64-bit
+// division per row cost ~140 instructions between the rows' loads.
+__device__ __forceinline__ uint32_t ref_block32(uint32_t u, uint32_t q32, uint32_t nb) {
+    return min(u / q32, nb - 1u);
+}
+
 __device__ __forceinline__ void load_rows8r(const uint8_t* __restrict__ codes, const uint16_t* __restrict__ am,
                                             int64_t nb, int bs, const int (&rows)[kRows], int K, int cc, int lane,
                                             Rows8R& b) {
     const bool ok = cc * kWChunk + 32 * lane < K;
+    const uint32_t q32 = (uint32_t)bs / 32u;
 #pragma unroll
     for (int r = 0; r < kRows; ++r) {
         const int64_t off = (int64_t)rows[r] * K + (ok ? cc * kWChunk + 32 * lane : 0);
         b.cw[r][0] = *reinterpret_cast<const u32x4_t*>(codes + off);
         b.cw[r][1] = *reinterpret_cast<const u32x4_t*>(codes + off + 16);
-        int64_t blk = off / bs;
-        blk = blk < nb ? blk : nb - 1;
-        b.am[r] = am[blk];
+        const uint32_t u = (uint32_t)rows[r] * (uint32_t)(K / 32) + (ok ? (uint32_t)(cc * (kWChunk / 32) + lane) : 0u);
+        b.am[r] = am[ref_block32(u, q32, (uint32_t)nb)];
     }
 }
 
@@ -1331,6 +1339,7 @@ __device__ __forceinline__ void ref_gate_up_t1(const DecodeArgs& A, const uint32
     const int64_t nb = w.absmax_per_expert;
     const bool ok = 32 * lane < H;
     const uint2 cbv = reinterpret_cast<const uint2*>(ref_codebook(w, e))[lane];
+    const uint32_t q32 = (uint32_t)w.block_size / 32u;
     u32x4_t cw[4][2];
     uint32_t av[4];
 #pragma unroll
@@ -1338,8 +1347,8 @@ __device__ __forceinline__ void ref_gate_up_t1(const DecodeArgs& A, const uint32
         const int64_t off = (int64_t)rows[r] * H + (ok ? 32 * lane : 0);
         cw[r][0] = *reinterpret_cast<const u32x4_t*>(codes + off);
         cw[r][1] = *reinterpret_cast<const u32x4_t*>(codes + off + 16);
-        const int64_t blk = off / w.block_size;
-        av[r] = am[blk < nb ? blk : nb - 1];
+        const uint32_t u = (uint32_t)rows[r] * (uint32_t)(H / 32) + (ok ? (uint32_t)lane : 0u);
+        av[r] = am[ref_block32(u, q32, (uint32_t)nb)];
     }
     __builtin_amdgcn_sched_barrier(0);
     *reinterpret_cast<uint2*>(slot + 8 * lane) = cbv;
@@ -1704,8 +1713,8 @@ __global__ __launch_bounds__(256, 2) void ref_decode_down1(DecodeArgs A) {
             const int64_t off = u < U ? 32 * u : 0;
             cw[p][0] = *reinterpret_cast<const u32x4_t*>(codes + off);
             cw[p][1] = *reinterpret_cast<const u32x4_t*>(codes + off + 16);
-            const int64_t blk = ((int64_t)h0 * K + off) / w.block_size;
-            av[p] = am[blk < nb ? blk : nb - 1];
+            const uint32_t u32 = (uint32_t)h0 * (uint32_t)(K / 32) + (u < U ? (uint32_t)u : 0u);
+            av[p] = am[ref_block32(u32, (uint32_t)w.block_size / 32u, (uint32_t)nb)];
         }
         __builtin_amdgcn_sched_barrier(0);
         // behind the weight loads: the pair weight and the next slot's fields
@@ -2111,7 +2120,9 @@ bool decode_v2_supported(const lutmoe_moe_desc* d, int T, int k) {
          (int64_t)d->w2.rows * d->w2.cols >= (int64_t(1) << 32)))
         return false;
     if (d->w13.format == LUTMOE_FMT_REF &&
-        (d->w13.block_size <= 0 || d->w13.block_size % 32 || d->w2.block_size <= 0 || d->w2.block_size % 32))
+        (d->w13.block_size <= 0 || d->w13.block_size % 32 || d->w2.block_size <= 0 || d->w2.block_size % 32 ||
+         (int64_t)d->w13.rows * d->w13.cols >= (int64_t(1) << 37) ||
+         (int64_t)d->w2.rows * d->w2.cols >= (int64_t(1) << 37)))   // 32-bit block indices (ref_block32)
         return false;
     return E_tot <= kMaxEtot && P <= kMaxP;
 }
