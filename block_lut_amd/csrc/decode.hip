@@ -1138,12 +1138,14 @@ __device__ __forceinline__ void gate_up_body4(const DecodeArgs& A, const RV& rv,
     const uint8_t* tabs = (const uint8_t*)A.d.w13.tables + sl.e * per;
     for (int tb = 0; tb < sl.n; tb += TB) {
         const int nt = min(TB, sl.n - tb);
+        // the positions' pairs first, all in flight together
+        int pr[TB];
+#pragma unroll
+        for (int t = 0; t < TB; ++t) pr[t] = rv.pair_at(sl.p0 + tb + min(t, nt - 1));
+        __builtin_amdgcn_sched_barrier(0);
         const uint16_t* xrow[TB];
 #pragma unroll
-        for (int t = 0; t < TB; ++t) {
-            const int tok = rv.pair_at(sl.p0 + tb + min(t, nt - 1)) / ke;
-            xrow[t] = A.x + (int64_t)min(max(tok, 0), A.T - 1) * H;
-        }
+        for (int t = 0; t < TB; ++t) xrow[t] = A.x + (int64_t)min(max(pr[t] / ke, 0), A.T - 1) * H;
         float acc[4][TB];
 #pragma unroll
         for (int r = 0; r < 4; ++r)
