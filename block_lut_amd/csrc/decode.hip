@@ -2251,8 +2251,9 @@ int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* t
             const int32_t* inv = ((const RouteOut*)route_ws)->inv;
             return launch_combine(y_ws, inv, T, k + d->num_shared, d->hidden, out, out_dtype, s);
         }
-        if (fmt_idx == 0 && (tb == 1 || (tb == 2 && T == 2)) && d->inter <= 2048) {
-            // one or two tokens, BL4: flat 16-byte units over 4 rows (every lane busy)
+        if (fmt_idx == 0 && (tb == 1 || (tb == 2 && T == 2)) && T * (k + d->num_shared) <= 16 * tb) {
+            // one or two tokens, BL4: 4 output rows a CTA, one slot a wave, the
+            // routing read in place (s_y holds up to 16 positions a token)
             const dim3 g1(d->hidden / kD1Rows);
             if (tb == 1) hipLaunchKernelGGL((bl4_decode_down1<1>), g1, dim3(256), 0, s, A);
             else hipLaunchKernelGGL((bl4_decode_down1<2>), g1, dim3(256), 0, s, A);
