@@ -1223,17 +1223,18 @@ def test_moe_layer_mixtral_shape(gpu):
     assert rel_maxabs(out, ref) <= TOL
 
 
-@pytest.mark.parametrize("T", [3, 20])
-def test_moe_layer_two_chunk_rows(gpu, T):
-    """Decode where both projections span two 2048-column chunks (H = 4096, I = 2304): two-
-    token passes (T = 3) and four-token passes (T = 20, the interleaved code-dword lane map of
-    the 8-row loop) against the oracle on host-dequantised weights."""
+@pytest.mark.parametrize("T,k", [(1, 1), (1, 2), (2, 2), (3, 2), (20, 2)])
+def test_moe_layer_two_chunk_rows(gpu, T, k):
+    """Decode where both projections span two 2048-column chunks (H = 4096, I = 2304): one and
+    two tokens (the one-token down kernel over both chunks, with one or two active experts),
+    two-token passes (T = 3) and four-token passes (T = 20, the interleaved code-dword lane
+    map of the 8-row loop) against the oracle on host-dequantised weights."""
     import torch
     from block_lut_amd import ops
     from block_lut_amd.formats import MoEWeights
     from gpu_weights import DevBL4
-    E, S, k, H, I = 4, 0, 2, 4096, 2304
-    g = torch.Generator(device=gpu).manual_seed(230 + T)
+    E, S, H, I = 4, 0, 4096, 2304
+    g = torch.Generator(device=gpu).manual_seed(230 + 10 * T + k)
     w13 = DevBL4(E, 2 * I, H, g, gpu)
     w2 = DevBL4(E, H, I, g, gpu)
     moe = MoEWeights(w13.stack, w2.stack, H, I, E, S)
