@@ -490,8 +490,8 @@ def test_moe_layer_skewed_routing(gpu, fmt, T):
     assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
 
 
-@pytest.mark.parametrize("block_size,T,path", [(64, 1, 1), (64, 9, 1), (256, 1, 1), (256, 9, 1),
-                                               (64, 40, 2), (192, 40, 2), (256, 300, 2)])
+@pytest.mark.parametrize("block_size,T,path", [(64, 1, 1), (64, 9, 1), (192, 1, 1), (192, 9, 1), (256, 1, 1),
+                                               (256, 9, 1), (64, 40, 2), (192, 40, 2), (256, 300, 2)])
 def test_moe_layer_ref_block_sizes(gpu, block_size, T, path):
     """REF with absmax blocks of 64, 192 and 256 columns.  Decode (path 1) follows the
     reference GEMV's (x * cb) * absmax products (a lane's 32 aligned columns share one block;
