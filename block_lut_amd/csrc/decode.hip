@@ -1064,14 +1064,15 @@ __device__ __forceinline__ void gate_up_body(const DecodeArgs& A, const RV& rv, 
 static_assert(kGuWaves == 1, "gate_up_body4 assumes one wave per CTA");
 template <int TB>
 constexpr bool gu2_for() { return TB == 1; }
-// gate/up with 2 indices a wave (gate_up_body4): one token a pass, and two
-// when a routing kernel ran (T >= 3: 4 rows a wave in the interleaved map
-// keep 44 of 48 lane steps busy at H = 2048 and look up without bank
-// conflicts; T = 8: 68 -> 65 us a layer).  Where every wave routes in
-// registers (T = 2), twice the waves means twice the routing (29.4 -> 30.3 us),
-// and the 8-row body stays.
+// gate/up with 2 indices a wave (gate_up_body4): one token a pass, and two or
+// four when a routing kernel ran (T >= 3: 4 rows a wave in the interleaved
+// map keep 44 of 48 lane steps busy at H = 2048 and look up without bank
+// conflicts, each row waiting for its own loads; T = 8: 68 -> 65 us a layer,
+// T = 17: 119 -> 115 us).  Where every wave routes in registers (T = 2),
+// twice the waves means twice the routing (29.4 -> 30.3 us), and the 8-row
+// body stays.
 template <int TB, bool kPre>
-constexpr bool gu2_gate_up_for() { return TB == 1 || (kPre && TB == 2); }
+constexpr bool gu2_gate_up_for() { return TB == 1 || (kPre && (TB == 2 || TB == 4)); }
 
 // Four BL4 rows over all of K (as bl4_rows8 for 8, in its interleaved lane
 // map: conflict-free lookups, which for one token a pass measured faster,
@@ -2215,7 +2216,7 @@ int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* t
         if ((rc = check_launch())) return rc;
     } else if (stages & LUTMOE_STAGE_GATE_UP) {
         // intermediate indices per CTA (gu2_gate_up_for: 2)
-        const int per_cta = (fmt_idx == 0 && (tb == 1 || (pre && tb == 2))) ? 2 : 4 * kGuWaves;
+        const int per_cta = (fmt_idx == 0 && (tb == 1 || (pre && (tb == 2 || tb == 4)))) ? 2 : 4 * kGuWaves;
         const dim3 grid((d->inter + per_cta - 1) / per_cta, max_work);
         LUTMOE_DECODE_LAUNCH(bl4_decode_gate_up, pre, grid, dim3(64 * kGuWaves), 0)
         if ((rc = check_launch())) return rc;
