@@ -1,30 +1,31 @@
-// Decode-time fused MoE layer on BL4 / NestedLUT weights: two kernels per layer.
+// Decode-time fused MoE layer on BL4 / REF / NestedLUT weights: a gate/up
+// kernel and a down kernel per layer (with a routing kernel before them and a
+// combine kernel after them when many tokens are routed).
 //
-//   bl4_decode_gate_up : routing -> grouped LUT-GEMV over W13 rows of every
-//                        active expert -> SwiGLU -> act[position][I] (bf16)
-//   bl4_decode_down    : routing -> grouped LUT-GEMV over W2 rows of every
-//                        active expert -> per-position results meet in LDS
-//                        -> weighted sum per token in slot order -> out
-// When the T*(k+S) pairs fit one wave (and top-k from logits has E <= 64)
-// every wave of the gate/up kernel computes the routing itself in registers
-// (a few hundred instructions, no LDS, no barrier) and its first CTA writes
-// it, with the pair weights, to the workspace; otherwise decode_route_kernel
-// routes once into the workspace.  The down kernel copies the workspace
-// routing into LDS.
+//   gate/up : routing -> grouped LUT-GEMV over W13 rows of every active
+//             expert -> SwiGLU -> act[position][I] (bf16)
+//   down    : grouped LUT-GEMV over W2 rows of every active expert -> each
+//             position's rows times its routing weight -> per-token sum in
+//             slot order (in LDS, or y[position][H] + combine_kernel)
+// One or two tokens whose pairs fit one wave (top-k from logits needs
+// E <= 64): every gate/up wave routes in registers (one token: only its own
+// slot's expert, from a top-k bitmask) and one wave publishes the routing
+// copy to the workspace, which the down kernel reads in place.  Otherwise
+// decode_route_kernel routes once into the workspace copy.
 //
 // Reference behaviour: LUTFusedMoEMethod.apply, decode branch
 // (vllm_lut/quant_method.py:250-260), routing of moe_layer._routing
 // (vllm_lut/moe_layer.py:358-376), shared experts added with weight 1
 // (customized/deepseek.py:111-115).
 //
-// GEMV layout (see lut_core.h): a wave owns 8 weight rows; in a 512-column
-// chunk lane l = 8g + q reads the code dword q of block g of every row and
-// the same-offset dword of that block's bf16 table (codes and tables are both
-// K/2 bytes per row), stages the tables in its LDS slot and looks each
-// nibble up there.  All chunk loads of a chunk group are issued (activations
-// first, then the weights chunk by chunk, without branches) before any is
-// consumed, so a wave keeps up to 16 KB in flight and starts on chunk 0 while
-// the later chunks are still arriving.
+// GEMV layout (lut_core.h): a wave owns 4 or 8 weight rows and walks K in
+// 2048-column chunks; codes and tables are both K/2 bytes per row, and a
+// row's tables are staged in the wave's LDS slot (block g at 32g), where each
+// nibble is looked up.  Lane maps: interleaved (lane l takes the code dwords
+// l + 64q of the chunk: every lookup step reads 8 blocks' tables in 8
+// distinct bank groups) or contiguous (lane l takes 32 columns).  A chunk's
+// loads are all issued (routing inputs, activations, then the weights) before
+// any is consumed.
 #include <algorithm>
 
 #include "common.h"
@@ -1278,8 +1279,8 @@ __device__ __forceinline__ void gate_up_t1(const DecodeArgs& A, const uint32_t (
 // One token, BL4, H <= 2048: CTAs of 4 independent waves (one dispatch for
 // four, no barrier); wave w of CTA (x, y) takes intermediate indices
 // 2(4x + w), +1 of slot y with its own short slot routing.  The first wave of
-// CTA (0, 0) also computes the full routing with the pair weights and
-// publishes it for the down kernel.
+// CTA (0, 0) also computes the full routing with the pair weights and,
+// after its own rows, publishes it for the down kernel.
 __global__ __launch_bounds__(256, 3) void bl4_decode_gate_up_t1(DecodeArgs A) {
     __shared__ __attribute__((aligned(16))) uint8_t s_slot[4][4 * 1024];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
