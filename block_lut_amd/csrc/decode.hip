@@ -1824,7 +1824,9 @@ __global__ __launch_bounds__(256, TB <= 2 ? 3 : 2) void bl4_decode_down_y(Decode
 // K = 1408 44 of 48 lane steps busy, where 8 rows of one 32-column unit a
 // lane leave 20 of 64 lanes idle); y[pos][h] as bl4_decode_down_y.
 template <int TB>
-__global__ __launch_bounds__(256, 2) void bl4_decode_down_y4(DecodeArgs A, float* __restrict__ y) {
+// (one or two tokens a pass: 4 CTAs a CU, 128 VGPRs: T = 8 64.3 -> 62.4 us,
+// T = 16 92.4 -> 88.5 us a layer against 2 CTAs a CU)
+__global__ __launch_bounds__(256, TB <= 2 ? 4 : 2) void bl4_decode_down_y4(DecodeArgs A, float* __restrict__ y) {
     __shared__ __attribute__((aligned(16))) uint8_t s_slot[4][4 * 1024];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const GlobalRouteView rv{A.route};
