@@ -1078,8 +1078,11 @@ constexpr bool gu2_gate_up_for() { return TB == 1 || (kPre && (TB == 2 || TB == 
 // Four BL4 rows over all of K (as bl4_rows8 for 8, in its interleaved lane
 // map: conflict-free lookups, which for one token a pass measured faster,
 // as in bl4_decode_gate_up_t1): per 2048-column chunk the activations, then
-// the loads of every row, then row by row the table staging and the lookups;
-// the wave's LDS slot holds 4 rows' tables (4 KB).
+// the loads of every row (all issued, none under a lane condition: code
+// loads past K clamped to the chunk's last dword, activations zeroed once
+// the weight loads are issued, so each row waits for its own loads only),
+// then row by row the table staging and the lookups; the wave's LDS slot
+// holds 4 rows' tables (4 KB).
 template <int TB>
 __device__ __forceinline__ void bl4_rows4(const uint8_t* __restrict__ codes, const uint8_t* __restrict__ tabs,
                                           const int (&rows)[4], int K, int lane, uint8_t* slot,
