@@ -2110,12 +2110,13 @@ __global__ __launch_bounds__(256, 2) void nested_gemv_kernel(lutmoe_weights w, i
 
 // tokens per pass: T=1 and T=2 recompute routing per CTA, larger T read it
 // Tokens per pass of the expert loops (fmt_idx: 0 BL4, 1 nested, 2 REF).  Up
-// to 16 tokens most active experts hold one or two of them, and a 4-token BL4
-// pass would spend its FMAs and activation loads on empty positions (Qwen
-// shape, MI355X: 2-token passes take T=4/8/16 from 58/85/121 to 50/72/108 us
-// per layer; at T=32 4-token passes stay ahead, 159 vs 173 us).  The nested
-// kernels lose with 2-token passes at T=16 (113 -> 136 us) and keep 4.
-inline int tb_for(int T, int fmt_idx) { return T <= 1 ? 1 : T <= (fmt_idx == 0 ? 16 : 2) ? 2 : 4; }
+// to 32 tokens most active experts hold a few of them, and a 4-token BL4 pass
+// would spend its FMAs and activation loads on empty positions (Qwen shape,
+// MI355X: 2-token passes take T=4/8/16 from 58/85/121 to 50/72/108 us per
+// layer; with the 4-row loops T=17/24/32 from 115/131/150 to 99/121/146 us).
+// Above 32 tokens (the GEMV path forced) passes take 4.  The nested kernels
+// lose with 2-token passes at T=16 (113 -> 136 us) and keep 4.
+inline int tb_for(int T, int fmt_idx) { return T <= 1 ? 1 : T <= (fmt_idx == 0 ? 32 : 2) ? 2 : 4; }
 
 }  // namespace
 

@@ -407,7 +407,7 @@ def _moe_case(fmt, E, S, H, I, seed):
 
 
 @pytest.mark.parametrize("fmt,T,path", [("bl4", 1, 1), ("bl4", 2, 1), ("bl4", 4, 1), ("bl4", 9, 1),
-                                        ("bl4", 200, 2), ("bl4", 5, 2),
+                                        ("bl4", 40, 1), ("bl4", 200, 2), ("bl4", 5, 2),
                                         ("ref", 1, 1), ("ref", 2, 1), ("ref", 3, 1), ("ref", 9, 1),
                                         ("ref", 150, 2)])
 def test_moe_layer(gpu, fmt, T, path):
@@ -1223,12 +1223,13 @@ def test_moe_layer_mixtral_shape(gpu):
     assert rel_maxabs(out, ref) <= TOL
 
 
-@pytest.mark.parametrize("T,k", [(1, 1), (1, 2), (2, 2), (3, 2), (20, 2)])
+@pytest.mark.parametrize("T,k", [(1, 1), (1, 2), (2, 2), (3, 2), (20, 2), (40, 2)])
 def test_moe_layer_two_chunk_rows(gpu, T, k):
     """Decode where both projections span two 2048-column chunks (H = 4096, I = 2304): one and
     two tokens (the one-token down kernel over both chunks, with one or two active experts),
-    two-token passes (T = 3) and four-token passes (T = 20, the interleaved code-dword lane
-    map of the 8-row loop) against the oracle on host-dequantised weights."""
+    two-token passes (T = 3, 20) and four-token passes (T = 40 on the forced GEMV path, the
+    interleaved code-dword lane map of the 8-row loop) against the oracle on host-dequantised
+    weights."""
     import torch
     from block_lut_amd import ops
     from block_lut_amd.formats import MoEWeights
