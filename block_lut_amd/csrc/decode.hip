@@ -2114,9 +2114,15 @@ __global__ __launch_bounds__(256, 2) void nested_gemv_kernel(lutmoe_weights w, i
 // would spend its FMAs and activation loads on empty positions (Qwen shape,
 // MI355X: 2-token passes take T=4/8/16 from 58/85/121 to 50/72/108 us per
 // layer; with the 4-row loops T=17/24/32 from 115/131/150 to 99/121/146 us).
-// Above 32 tokens (the GEMV path forced) passes take 4.  The nested kernels
-// lose with 2-token passes at T=16 (113 -> 136 us) and keep 4.
-inline int tb_for(int T, int fmt_idx) { return T <= 1 ? 1 : T <= (fmt_idx == 0 ? 32 : 2) ? 2 : 4; }
+// Past 16 tokens that holds while the positions per expert stay few (at most
+// 3 on average, P / min(P, E_tot)); few experts holding many tokens each
+// (top-2 of 8) and more than 32 tokens (the GEMV path forced) take 4.  The
+// nested kernels lose with 2-token passes at T=16 (113 -> 136 us) and keep 4.
+inline int tb_for(int T, int fmt_idx, int P, int E_tot) {
+    if (T <= 1) return 1;
+    if (fmt_idx != 0) return T <= 2 ? 2 : 4;
+    return T <= 16 || (T <= 32 && P <= 3 * std::min(P, E_tot)) ? 2 : 4;
+}
 
 }  // namespace
 
@@ -2179,7 +2185,7 @@ int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* t
     const bool pre = T > 2 || !(P <= 64 && (topk_ids != nullptr || d->num_routed <= 64));
     const bool nested = d->w13.format == LUTMOE_FMT_NESTED;
     const int fmt_idx = nested ? 1 : d->w13.format == LUTMOE_FMT_REF ? 2 : 0;
-    const int tb = tb_for(T, fmt_idx);
+    const int tb = tb_for(T, fmt_idx, P, E_tot);
     A.tb = tb;   // before the routing launch: its chunking reads it
     int rc;
     if (pre && (stages & LUTMOE_STAGE_ROUTE)) {

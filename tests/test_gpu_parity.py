@@ -1227,9 +1227,9 @@ def test_moe_layer_mixtral_shape(gpu):
 def test_moe_layer_two_chunk_rows(gpu, T, k):
     """Decode where both projections span two 2048-column chunks (H = 4096, I = 2304): one and
     two tokens (the one-token down kernel over both chunks, with one or two active experts),
-    two-token passes (T = 3, 20) and four-token passes (T = 40 on the forced GEMV path, the
-    interleaved code-dword lane map of the 8-row loop) against the oracle on host-dequantised
-    weights."""
+    two-token passes (T = 3) and four-token passes (T = 20, ten positions per expert, and
+    T = 40 on the forced GEMV path: the interleaved code-dword lane map of the 8-row loop)
+    against the oracle on host-dequantised weights."""
     import torch
     from block_lut_amd import ops
     from block_lut_amd.formats import MoEWeights
