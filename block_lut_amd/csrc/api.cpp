@@ -77,7 +77,7 @@ int validate_ref_vector(const lutmoe_weights* w) {
 size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct MoeLayout {
-    size_t sync, route, topk_w, topk_ids, pair_ids, pair_w, offsets, perm, inv, active, act, y, total;
+    size_t route, topk_w, topk_ids, pair_ids, pair_w, offsets, perm, inv, active, act, y, total;
 };
 
 // Room for two K-split partial results of the down projection when that is
@@ -89,7 +89,6 @@ MoeLayout moe_layout(const lutmoe_moe_desc* d, int T, int k) {
     const size_t P = (size_t)T * (k + d->num_shared);
     MoeLayout L{};
     size_t o = 0;
-    L.sync = o;     o = align_up(o + decode_sync_bytes());   // always at offset 0
     L.route = o;    o = align_up(o + decode_route_bytes());
     L.topk_w = o;   o = align_up(o + (size_t)T * k * 4);
     L.topk_ids = o; o = align_up(o + (size_t)T * k * 4);
@@ -396,7 +395,7 @@ int moe_forward_impl(const lutmoe_moe_desc* d, const void* x, const float* topk_
     if (gemv) {
         // routing + permutation happen inside both decode kernels
         return launch_decode_v2(d, (const uint16_t*)x, topk_w, topk_ids, logits, T, k, renorm,
-                                scaling, act, ws + L.route, ws + L.sync, (float*)(ws + L.y), out, out_dtype, stages, s);
+                                scaling, act, ws + L.route, (float*)(ws + L.y), out, out_dtype, stages, s);
     }
     int32_t* pair_ids = (int32_t*)(ws + L.pair_ids);
     float* pair_w = (float*)(ws + L.pair_w);

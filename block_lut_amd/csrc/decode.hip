@@ -1866,208 +1866,6 @@ __global__ __launch_bounds__(256, TB <= 2 ? 4 : 2) void bl4_decode_down_y4(Decod
     }
 }
 
-// ---------------------------------------------------------------------------
-// One persistent kernel for the whole layer.  Every CTA routes, then takes
-// work items from a queue in the workspace: first the gate_up items (one per
-// active expert and 16 intermediate indices, as bl4_decode_gate_up's CTAs),
-// then the down items (8 output rows of every active expert, as
-// bl4_decode_down's CTAs).  A down item issues its W2 loads, then waits until
-// every gate_up item has published its act slice, so W13 and W2 stream from
-// HBM together and the layer costs one launch.  Items are taken in queue
-// order, so every gate_up item a down item waits for is already held by a
-// running CTA: no CTA waits on one that may not be resident.  Waits are
-// bounded (20 ms; a CTA that hits the bound sets DecodeSync::err and carries
-// on), and
-// the last CTA to finish puts the counters back to zero for the next call.
-struct DecodeSync {
-    int queue;      // next work item
-    int gu_done;    // gate_up items whose act slice is published
-    int cta_done;   // CTAs finished
-    int err;        // sticky: a wait hit its bound
-};
-constexpr uint64_t kWaitTicks = 2000000;   // 20 ms of the 100 MHz real-time counter
-
-// The persistent kernel is switched off: its first GPU runs did not complete
-// (cause not yet found; the per-stage kernels below run instead).
-constexpr bool kFusedDecodeEnabled = false;
-
-__device__ __forceinline__ int atomic_add_agent(int* p, int v) {
-    return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-template <int TB>
-__device__ __forceinline__ void fused_gate_up_item(const DecodeArgs& A, const RouteOut& R, int a, int slice,
-                                                   uint8_t* slot) {
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int I = A.d.inter, H = A.d.hidden, ke = A.k + A.d.num_shared;
-    const int i0 = (slice * 4 + wv) * 4;
-    if (i0 >= I) return;
-    const int e = R.act[a];
-    const int p0 = R.aoff[a], n = R.an[a];
-    int rows[kRows];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int i = min(i0 + j, I - 1);
-        rows[j] = i;
-        rows[4 + j] = I + i;
-    }
-    const int64_t per = (int64_t)A.d.w13.rows * (H / 2);
-    const uint8_t* codes = (const uint8_t*)A.d.w13.codes + e * per;
-    const uint8_t* tabs = (const uint8_t*)A.d.w13.tables + e * per;
-    for (int tb = 0; tb < n; tb += TB) {
-        const int nt = min(TB, n - tb);
-        const uint16_t* xrow[TB];
-#pragma unroll
-        for (int t = 0; t < TB; ++t) xrow[t] = A.x + (int64_t)(R.perm[p0 + tb + min(t, nt - 1)] / ke) * H;
-        float acc[kRows][TB];
-#pragma unroll
-        for (int r = 0; r < kRows; ++r)
-#pragma unroll
-            for (int t = 0; t < TB; ++t) acc[r][t] = 0.f;
-        bl4_rows8<TB>(codes, tabs, rows, H, lane, slot, xrow, nt, acc);
-        float g[4][TB], u[4][TB];
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int t = 0; t < TB; ++t) {
-                g[j][t] = wave_reduce(acc[j][t]);
-                u[j][t] = wave_reduce(acc[4 + j][t]);
-            }
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int t = 0; t < TB; ++t)
-                if (lane == j * TB + t && t < nt && i0 + j < I)
-                    A.act[(int64_t)(p0 + tb + t) * I + i0 + j] = (uint16_t)f32_to_bf16(silu_mul(g[j][t], u[j][t]));
-    }
-}
-
-template <int TB>
-__device__ __forceinline__ void fused_down_item(const DecodeArgs& A, const RouteOut& R, int hs, int n_gu,
-                                                DecodeSync* sync, uint8_t* slot, float* s_y) {
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int I = A.d.inter, H = A.d.hidden, ke = A.k + A.d.num_shared;
-    const int h0 = hs * kRows;
-    int rows[kRows];
-#pragma unroll
-    for (int r = 0; r < kRows; ++r) rows[r] = min(h0 + r, H - 1);
-    const int64_t per = (int64_t)A.d.w2.rows * (I / 2);
-    const int nch = (I + kWChunk - 1) / kWChunk;
-    // W2 rows of this wave's first expert (first chunk): issued before the wait
-    Rows8 pre;
-    if (wv < R.nact) {
-        const int e = R.act[wv];
-        load_rows8<TB>((const uint8_t*)A.d.w2.codes + e * per, (const uint8_t*)A.d.w2.tables + e * per, rows, I, 0,
-                   lane, pre);
-    }
-    // Wait for every act slice: poll with relaxed loads (no cache
-    // invalidation per poll), bounded in wall time, then one acquire fence
-    // (invalidates this CU's caches, so the act loads below see the slices).
-    if (threadIdx.x == 0) {
-        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-        while (__hip_atomic_load(&sync->gu_done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < n_gu) {
-            if (__builtin_amdgcn_s_memrealtime() - t0 > kWaitTicks) {
-                __hip_atomic_store(&sync->err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                break;
-            }
-            __builtin_amdgcn_s_sleep(8);
-        }
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    }
-    __syncthreads();
-    for (int a = wv; a < R.nact; a += 4) {
-        const int e = R.act[a];
-        const int p0 = R.aoff[a], n = R.an[a];
-        const uint8_t* codes = (const uint8_t*)A.d.w2.codes + e * per;
-        const uint8_t* tabs = (const uint8_t*)A.d.w2.tables + e * per;
-        for (int tb = 0; tb < n; tb += TB) {
-            const int nt = min(TB, n - tb);
-            const uint16_t* xrow[TB];
-#pragma unroll
-            for (int t = 0; t < TB; ++t) xrow[t] = A.act + (int64_t)(p0 + tb + min(t, nt - 1)) * I;
-            float acc[kRows][TB];
-#pragma unroll
-            for (int r = 0; r < kRows; ++r)
-#pragma unroll
-                for (int t = 0; t < TB; ++t) acc[r][t] = 0.f;
-            for (int cc = 0; cc < nch; ++cc) {
-                // the first pass uses the prefetched rows, later ones reload
-                if (!(a == wv && tb == 0 && cc == 0)) load_rows8<TB>(codes, tabs, rows, I, cc, lane, pre);
-                uint32_t xs[TB][16];
-                if constexpr (bl4_interleaved<TB>()) load_xi<TB>(xrow, I, cc, lane, xs);
-                else load_x8<TB>(xrow, I, cc, lane, nt, xs);
-                compute_rows8<TB>(pre, xs, cc * kWChunk + 32 * lane < I, lane, chunk_dwords(I, cc), slot, nt, acc);
-            }
-#pragma unroll
-            for (int t = 0; t < TB; ++t) {
-                const int p = p0 + tb + min(t, nt - 1);
-                const float pw = R.pw[R.perm[p]];
-#pragma unroll
-                for (int r = 0; r < kRows; ++r) {
-                    const float v = wave_reduce(acc[r][t]);
-                    if (lane == r && t < nt) s_y[p * kRows + r] = v * pw;
-                }
-            }
-        }
-    }
-    __syncthreads();
-    const int T = A.T;
-    for (int idx = threadIdx.x; idx < T * kRows; idx += blockDim.x) {
-        const int t = idx / kRows, r = idx % kRows;
-        if (h0 + r >= H) continue;
-        float sum = 0.f;
-        for (int q = 0; q < ke; ++q) {
-            const int pos = R.inv[t * ke + q];
-            if (pos >= 0) sum += s_y[pos * kRows + r];
-        }
-        const int64_t o = (int64_t)t * H + h0 + r;
-        if (A.out_dtype == LUTMOE_DTYPE_F32) ((float*)A.out)[o] = sum;
-        else ((uint16_t*)A.out)[o] = (uint16_t)f32_to_bf16(sum);
-    }
-    __syncthreads();   // s_y is reused by the next item
-}
-
-template <int TB, bool kPre>
-__global__ __launch_bounds__(256) void bl4_decode_fused(DecodeArgs A, DecodeSync* sync) {
-    __shared__ RouteOut R;
-    __shared__ RouteScratch X;
-    __shared__ __attribute__((aligned(16))) uint8_t s_slot[4 * kSlot];
-    __shared__ int s_item;
-    extern __shared__ float s_y[];   // [P][8]
-    get_route<kPre>(A, R, X);
-    const int I = A.d.inter, H = A.d.hidden;
-    const int nsl = (I + 15) / 16;
-    const int n_gu = R.nact * nsl;
-    const int n_all = n_gu + (H + kRows - 1) / kRows;
-    uint8_t* slot = s_slot + (threadIdx.x >> 6) * kSlot;
-    for (;;) {
-        if (threadIdx.x == 0) s_item = atomic_add_agent(&sync->queue, 1);
-        __syncthreads();
-        const int item = s_item;
-        __syncthreads();
-        if (item >= n_all) break;
-        if (item < n_gu) {
-            fused_gate_up_item<TB>(A, R, item / nsl, item % nsl, slot);
-            // publish: every wave's act stores complete in L2, then one
-            // release fence (writes the L2 back) and the count
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            __syncthreads();
-            if (threadIdx.x == 0) {
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-                atomic_add_agent(&sync->gu_done, 1);
-            }
-        } else {
-            fused_down_item<TB>(A, R, item - n_gu, n_gu, sync, slot, s_y);
-        }
-    }
-    if (threadIdx.x == 0 &&
-        __hip_atomic_fetch_add(&sync->cta_done, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == (int)gridDim.x - 1) {
-        __hip_atomic_store(&sync->queue, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(&sync->gu_done, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(&sync->cta_done, 0, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-    }
-}
-
 // Single-matrix NestedLUT GEMV (lutmoe_gemv): y[t][m] = sum_k x[t][k] W_e[m][k]
 // for T vectors, TB at a time; a wave owns 8 rows, a CTA 32.
 template <int TB>
@@ -2157,11 +1955,9 @@ int launch_nested_gemv(const lutmoe_weights* w, int expert, const uint16_t* x, i
 }
 
 size_t decode_route_bytes() { return sizeof(RouteOut) + sizeof(RouteChunks) + sizeof(RoutePosW); }
-size_t decode_sync_bytes() { return sizeof(DecodeSync); }
-
 int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* topk_w,
                      const int32_t* topk_ids, const float* logits, int T, int k, int renorm,
-                     float scaling, uint16_t* act, void* route_ws, void* sync_ws, float* y_ws, void* out,
+                     float scaling, uint16_t* act, void* route_ws, float* y_ws, void* out,
                      int out_dtype, int stages, hipStream_t s) {
     DecodeArgs A;
     A.d = *d;
@@ -2191,18 +1987,6 @@ int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* t
     if (pre && (stages & LUTMOE_STAGE_ROUTE)) {
         hipLaunchKernelGGL(decode_route_kernel, dim3(1), dim3(1024), 0, s, A);
         if ((rc = check_launch())) return rc;
-    }
-    if (kFusedDecodeEnabled && fmt_idx == 0 && stages == LUTMOE_STAGE_ALL && sync_ws) {
-        // one persistent launch: enough CTAs for one item each
-        const int items = max_active * ((d->inter + 15) / 16) + (d->hidden + kRows - 1) / kRows;
-        const size_t lds = (size_t)P * kRows * sizeof(float);
-        DecodeSync* sy = (DecodeSync*)sync_ws;
-        switch (tb) {
-            case 1: hipLaunchKernelGGL((bl4_decode_fused<1, false>), dim3(items), dim3(256), lds, s, A, sy); break;
-            case 2: hipLaunchKernelGGL((bl4_decode_fused<2, false>), dim3(items), dim3(256), lds, s, A, sy); break;
-            default: hipLaunchKernelGGL((bl4_decode_fused<4, true>), dim3(items), dim3(256), lds, s, A, sy); break;
-        }
-        return check_launch();
     }
 #define LUTMOE_DECODE_CASE(N, TB, PRE, FMT, KERNEL, GRID, BLOCK, LDS) \
     case N: hipLaunchKernelGGL((KERNEL<TB, PRE, FMT>), GRID, BLOCK, LDS, s, A); break;

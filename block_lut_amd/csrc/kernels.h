@@ -63,13 +63,9 @@ void set_last_error_text(const char* text);
 // decode.hip (BL4 decode layer, routing recomputed inside each CTA)
 bool decode_v2_supported(const lutmoe_moe_desc* d, int T, int k);
 size_t decode_route_bytes();
-size_t decode_sync_bytes();
-// sync_ws: the persistent kernel's counters (zero before the first call, left
-// zero by every call); with stages == ALL and sync_ws set the layer is one
-// launch, otherwise the per-stage kernels run.
 int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* topk_w,
                      const int32_t* topk_ids, const float* logits, int T, int k, int renorm,
-                     float scaling, uint16_t* act, void* route_ws, void* sync_ws, float* y_ws, void* out,
+                     float scaling, uint16_t* act, void* route_ws, float* y_ws, void* out,
                      int out_dtype, int stages, hipStream_t s);
 
 // route.hip

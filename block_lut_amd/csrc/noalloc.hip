@@ -23,7 +23,6 @@ namespace {
 
 constexpr size_t kScratchBytes = size_t(32) << 20;   // 32 MiB per GPU
 constexpr int kMaxDevices = 64;
-constexpr int kZeroBytes = 256;                      // the layout's counters (offset 0)
 
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
@@ -31,27 +30,16 @@ uint8_t* g_scratch[kMaxDevices];
 int g_setup_rc[kMaxDevices];
 std::once_flag g_once[kMaxDevices];
 
-// Clears the counters at the start of the layout (a kernel, not a memset, so
-// a first call under graph capture records an ordinary kernel node).
-__global__ void zero_bytes_kernel(uint8_t* __restrict__ p, int n) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) p[i] = 0;
-}
-
-// The device address of this device's scratch (set up on the first call on
-// the device: symbol lookup, counters cleared on `s`).
-int device_scratch(uint8_t** out, hipStream_t s) {
+// The device address of this device's scratch (looked up on the first call
+// on the device).  No part of the layer's workspace needs to start at zero:
+// every kernel writes what it later reads within the same call.
+int device_scratch(uint8_t** out) {
     int dev = -1;
     if (hipGetDevice(&dev) != hipSuccess) return LUTMOE_EHIP;
     if (dev < 0 || dev >= kMaxDevices) return LUTMOE_EUNSUPPORTED;
-    std::call_once(g_once[dev], [dev, s]() {
+    std::call_once(g_once[dev], [dev]() {
         void* p = nullptr;
         if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) {
-            g_setup_rc[dev] = LUTMOE_EHIP;
-            return;
-        }
-        hipLaunchKernelGGL(zero_bytes_kernel, dim3(1), dim3(kZeroBytes), 0, s, (uint8_t*)p, kZeroBytes);
-        if (hipGetLastError() != hipSuccess) {
             g_setup_rc[dev] = LUTMOE_EHIP;
             return;
         }
@@ -83,7 +71,7 @@ extern "C" int lutmoe_moe_forward_noalloc(const lutmoe_moe_desc* d, const void* 
     }
     set_last_error_text("");
     uint8_t* ws = nullptr;
-    const int rc = device_scratch(&ws, stream_of(stream));
+    const int rc = device_scratch(&ws);
     if (rc) return rc;
     return moe_forward_impl(d, x, topk_w, topk_ids, nullptr, T, k, 0, 1.0f, out, out_dtype, ws, kScratchBytes,
                             force_path, LUTMOE_STAGE_ALL, stream);

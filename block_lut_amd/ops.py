@@ -232,10 +232,9 @@ def moe_workspace_bytes(moe: MoEWeights, T: int, k: int) -> int:
 
 
 def new_workspace(moe: MoEWeights, T: int, k: int, device) -> torch.Tensor:
-    """A zero-filled workspace for the MoE layer at up to T tokens (the
-    decode kernel's counters at its start must be zero before first use; each
-    call leaves them zero).  Reuse it across calls; do not share it between
-    calls that overlap in time."""
+    """A workspace for the MoE layer at up to T tokens (zero-filled for
+    determinism; no kernel needs it zeroed).  Reuse it across calls; do not
+    share it between calls that overlap in time."""
     return torch.zeros(max(moe_workspace_bytes(moe, T, k), 256), dtype=torch.uint8, device=device)
 
 

@@ -235,11 +235,9 @@ int lutmoe_permute(const int32_t* topk_ids_dev, int T, int k, int E, int32_t* of
 /* ---- fused MoE layer ------------------------------------------------------ */
 
 /* Workspace bytes lutmoe_moe_forward needs for T tokens and top-k.
- * The workspace is device memory, 256-byte aligned, owned by the caller.
- * Its first 256 bytes hold the decode kernel's cross-CTA counters: zero-fill
- * the workspace (or at least those bytes) once before its first use; every
- * call leaves them zero again.  Calls that overlap in time must not share a
- * workspace. */
+ * The workspace is device memory, 256-byte aligned, owned by the caller; its
+ * contents need no initialisation (every kernel writes what it reads within
+ * the call).  Calls that overlap in time must not share a workspace. */
 size_t lutmoe_moe_workspace_size(const lutmoe_moe_desc* d, int T, int k);
 
 /* out[T][H] (out_dtype) = sum_k topk_w[t][k] * FFN_{ids[t][k]}(x[t])
@@ -263,8 +261,7 @@ int lutmoe_moe_forward(const lutmoe_moe_desc* d, const void* x_dev, const float*
  * LUTMOE_EWORKSPACE and a lutmoe_last_error text giving the sizes.  Every call
  * on one GPU shares that GPU's scratch, which keeps the last call's contents:
  * calls that overlap in time on one GPU race (serialise them, e.g. on one
- * stream).  The first call on a device looks up the scratch's address and
- * clears its counters with a kernel on `stream`. */
+ * stream).  The first call on a device looks up the scratch's address. */
 int lutmoe_moe_forward_noalloc(const lutmoe_moe_desc* d, const void* x_dev, const float* topk_w_dev,
                                const int32_t* topk_ids_dev, int T, int k, void* out_dev, int out_dtype,
                                int force_path, void* stream);

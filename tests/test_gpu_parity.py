@@ -741,8 +741,8 @@ def test_moe_layer_from_logits_ties(gpu, T, E, renorm):
 
 
 @pytest.mark.skip(reason="the one-launch persistent decode kernel (bl4_decode_fused) did not complete "
-                         "on its first GPU runs (E=8, S=1, k=2, H=512, I=320, T=1); it is switched off "
-                         "(kFusedDecodeEnabled) until the cause is found on the CPU")
+                         "on its first GPU runs (E=8, S=1, k=2, H=512, I=320, T=1); no cause was shown, "
+                         "and the kernel has been removed (the per-stage kernels run every layer)")
 def test_moe_layer_fused_decode(gpu):
     """Layer through the persistent decode kernel (one launch, all stages) against the
     per-stage kernels (routing + gate/up, then down + combine, in a second workspace) bit
