@@ -740,7 +740,7 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
 #pragma unroll
             for (int i = 0; i < NMT; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                            // 1 MFMA
-                if (!kNested) __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);             // VALU
+                if (!kNested) __builtin_amdgcn_sched_group_barrier(0x002, NMT <= 6 ? 3 : 2, 0);   // VALU
                 __builtin_amdgcn_sched_group_barrier(0x100, (8 + kHalfA + 2 + NMT - 1) / NMT, 0);   // LDS reads
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -755,7 +755,7 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
 #pragma unroll
             for (int i = 0; i < NMT; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                if (!kNested) __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+                if (!kNested) __builtin_amdgcn_sched_group_barrier(0x002, NMT <= 6 ? 3 : 2, 0);
                 __builtin_amdgcn_sched_group_barrier(0x100, (8 + NMT - kHalfA + NMT - 1) / NMT, 0);
             }
             __builtin_amdgcn_sched_barrier(0);
