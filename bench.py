@@ -56,18 +56,32 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def measured_traffic(name="decode_gate_up_traffic.md"):
-    """HBM bytes per launch of the dominant kernel from the committed counter
-    summary (FETCH_SIZE and WRITE_SIZE passes, each scaled by what it reads
-    for a copy of known size); None when the summary is absent."""
+def measured_traffic(name):
+    """HBM bytes per launch of the dominant kernel from a committed counter summary
+    (FETCH_SIZE and WRITE_SIZE passes, each scaled by what it reads for a copy of known
+    size), with the summary's name and the commit it records; (None, None) when the
+    summary is absent."""
     path = os.path.join(ROOT, "profiles", name)
+    traffic, commit = None, None
     try:
         for line in open(path):
             if line.startswith("traffic_bytes_per_launch:"):
-                return int(float(line.split(":", 1)[1]))
+                traffic = int(float(line.split(":", 1)[1]))
+            if line.startswith("measured_at_commit:"):
+                commit = line.split(":", 1)[1].strip()
     except OSError:
-        pass
-    return None
+        return None, None
+    return traffic, f"profiles/{name} (measured at commit {commit})" if traffic is not None else None
+
+
+def decode_kernel_label(T, P, E_tot):
+    """The gate/up kernel the library launches for this batch (the tokens-per-pass rule of
+    decode.hip's tb_for for BL4: one token its own kernel, two-token passes up to 16
+    tokens, and up to 32 while the experts hold at most 3 positions on average)."""
+    if T <= 1:
+        return "bl4_decode_gate_up_t1"
+    tb = 2 if T <= 16 or (T <= 32 and P <= 3 * min(P, E_tot)) else 4
+    return f"bl4_decode_gate_up<{tb}>"
 
 
 def parse():
@@ -130,6 +144,7 @@ def main():
             self.x = torch.randn((T, c["H"]), generator=gen).to(torch.bfloat16).to(dev)
             self.w = torch.empty((T, c["k"]), dtype=torch.float32, device=dev)
             self.ids = torch.empty((T, c["k"]), dtype=torch.int32, device=dev)
+            self.sink = None
             self.out = torch.empty((T, c["H"]), dtype=torch.bfloat16, device=dev)
             self.ws = ops.new_workspace(layer, T, c["k"], dev)
             ops.route_topk(self.logits, c["k"], out_w=self.w, out_ids=self.ids)
@@ -241,7 +256,8 @@ def main():
     us_per_token = ms_per_step * 1e3 / T
     log(f"[bench] {ms_per_step * 1e3:.2f} us/layer-step, {value_tbs:.3f} TB/s")
 
-    # dominant kernel alone: gate/up + SwiGLU grouped LUT-GEMV
+    # dominant kernel alone (gate/up + SwiGLU grouped LUT-GEMV), timed with HIP events
+    # around a graph of its launches on the stream they run on
     g_gu = graph_of([lambda s=s: s.run(stages=N.STAGE_GATE_UP) for s in steps])
     time_graph(g_gu, 4)
     r_gu = max(8, min(32, K // R))
@@ -255,6 +271,7 @@ def main():
     bytes_dn = sum(s.U * c["H"] * c["I"] * BYTES_PER_WEIGHT for s in steps) / len(steps)
     log(f"[bench] gate_up kernel {dur_gu * 1e6:.2f} us ({ach_gu:.0f} GB/s); "
         f"down+combine {dur_dn * 1e6:.2f} us ({bytes_dn / dur_dn / 1e9:.0f} GB/s)")
+    traffic, traffic_src = measured_traffic("decode_gate_up_traffic.md")
 
     result = {
         "metric": METRIC,
@@ -278,21 +295,24 @@ def main():
                    "avg_distinct_experts": round(sum(s.U for s in steps) / len(steps), 3)},
         "us_per_token": round(us_per_token, 3),
         "tokens_per_s": round(T / (ms_per_step / 1e3), 1),
-        # one token: the dedicated kernel; else the template argument = tokens
-        # per pass (2 up to T=16, else 4)
         "roofline": {"bound": "hbm",
-                     "kernel": "bl4_decode_gate_up_t1" if T <= 1 else f"bl4_decode_gate_up<{2 if T <= 16 else 4}>",
+                     "kernel": decode_kernel_label(T, T * (c["k"] + c["S"]), c["E"] + c["S"]),
                      "achieved": round(ach_gu, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(ach_gu / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "frac": round(ach_gu / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_source": traffic_src,
                      "avg_launch_us": round(dur_gu * 1e6, 3),
                      "algorithmic_bytes_per_launch": int(bytes_gu)},
         "kernels": {"decode_down_combine_us": round(dur_dn * 1e6, 3),
                     "decode_down_combine_GBs": round(bytes_dn / dur_dn / 1e9, 1)},
     }
+    floor = stream_floor(N, torch, dev, steps, c, graph_of, time_graph) if T == 1 else {}
+    if floor:
+        floor["decode_T1_floor_over_layer"] = round(floor["decode_T1_stream_floor_all_us"] / (ms_per_step * 1e3), 4)
 
     # ---------------------------------------------------------- extra configs
+    result["extra"] = dict(floor)
     if not a.no_extra:
-        extra = {}
+        extra = dict(floor)
         # hot cache: one layer, same routing every step
         g_hot = graph_of([steps[0].run] * 16)
         time_graph(g_hot, 4)
@@ -392,6 +412,42 @@ def main():
         result["cpu_baseline"] = cpu_baseline(a, c, T)
 
     print(json.dumps(result), flush=True)
+
+
+def stream_floor(N, torch, dev, steps, c, graph_of, time_graph):
+    """HBM floor of the one-token layer: lutmoe_decode_stream_probe launches, whose CTAs
+    issue exactly the weight loads of the one-token gate/up and down kernels for each
+    step's own experts (the same rotating layers) and nothing else, graph-timed like the
+    layer.  "all": both kernels' loads in one launch (the step's bytes); "w13": the gate/up
+    kernel's alone (the gate/up bytes)."""
+    import ctypes
+    lib = N.lib()
+    for s in steps:
+        s.slot_ids = s.ids.reshape(-1).contiguous()
+
+    out = {}
+    for which, name, nb in ((3, "all", lambda s: s.bytes - 2 * c["H"] * 2),
+                            (1, "w13", lambda s: s.bytes_gate_up - c["H"] * 2)):
+        sinks = []
+        for s in steps:
+            d = s.layer.desc()
+            n = int(lib.lutmoe_decode_stream_probe_sink_words(ctypes.byref(d), c["k"], which))
+            sinks.append(torch.empty(max(1, n), dtype=torch.int32, device=dev))
+
+        def probe(s, sink, which=which):
+            d = s.layer.desc()
+            N.check("lutmoe_decode_stream_probe",
+                    lib.lutmoe_decode_stream_probe(ctypes.byref(d), s.slot_ids.data_ptr(), c["k"], which,
+                                                   sink.data_ptr(), torch.cuda.current_stream().cuda_stream))
+        g = graph_of([lambda s=s, k=k: probe(s, k) for s, k in zip(steps, sinks)])
+        time_graph(g, 4)
+        sec = time_graph(g, 16) / (16 * len(steps))
+        by = sum(nb(s) for s in steps) / len(steps)
+        out[f"decode_T1_stream_floor_{name}_us"] = round(sec * 1e6, 3)
+        out[f"decode_T1_stream_floor_{name}_TBs"] = round(by / sec / 1e12, 3)
+        log(f"[bench] stream floor ({name}): {sec * 1e6:.2f} us, {by / sec / 1e12:.3f} TB/s")
+        del g
+    return out
 
 
 def measured_ceilings(torch, dev, d, T=2048):
@@ -573,13 +629,19 @@ def nested_tiers(a, ops, N, torch, dev, NestedExpert, NestedStack, MoEWeights, g
 
 
 def cpu_model() -> str:
+    """The host CPU as /proc/cpuinfo names it, with its family / model / stepping numbers
+    (a virtualised host may report only a short model name)."""
+    info = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if ":" in line:
+                key, val = (t.strip() for t in line.split(":", 1))
+                if key in ("model name", "vendor_id", "cpu family", "model", "stepping") and key not in info:
+                    info[key] = val
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    return (f"{info.get('model name', 'unknown')} ({info.get('vendor_id', '?')} family "
+            f"{info.get('cpu family', '?')} model {info.get('model', '?')} stepping {info.get('stepping', '?')})")
 
 
 def cpu_baseline(a, c, T):

@@ -348,6 +348,21 @@ int lutmoe_permute(const int32_t* topk_ids, int T, int k, int E, int32_t* offset
 
 // -------------------------------------------------------------- MoE layer
 
+size_t lutmoe_decode_stream_probe_sink_words(const lutmoe_moe_desc* d, int k, int which) {
+    if (validate_moe(d) || k <= 0 || which < 1 || which > 3) return 0;
+    return decode_stream_probe_ctas(d, k + d->num_shared, which);
+}
+
+int lutmoe_decode_stream_probe(const lutmoe_moe_desc* d, const int32_t* ids_dev, int k, int which,
+                               uint32_t* sink_dev, void* stream) {
+    int rc = validate_moe(d);
+    if (rc) return rc;
+    if (!ids_dev || !sink_dev || k <= 0 || which < 1 || which > 3) return LUTMOE_EINVAL;
+    if (d->w13.format != LUTMOE_FMT_BL4 || d->hidden > 2048 || d->inter > 2048 || k + d->num_shared > 64)
+        return LUTMOE_EUNSUPPORTED;
+    return launch_decode_stream_probe(d, ids_dev, k + d->num_shared, which, sink_dev, stream_of(stream));
+}
+
 size_t lutmoe_moe_workspace_size(const lutmoe_moe_desc* d, int T, int k) {
     if (!d || T < 0 || k <= 0) return 0;
     return moe_layout(d, T, k).total;

@@ -1906,6 +1906,81 @@ __global__ __launch_bounds__(256, 2) void nested_gemv_kernel(lutmoe_weights w, i
     }
 }
 
+// The HBM floor of the one-token BL4 layer, for measurement: one launch
+// whose CTAs issue exactly the weight loads of the two one-token kernels for
+// the experts ids[y] of the slots y (which & 1: the gate/up kernel's CTAs,
+// bl4_decode_gate_up_t1's grid and per-wave rows; which & 2: the down
+// kernel's, bl4_decode_down1's grid, 4 rows of every slot a CTA) and fold the
+// loaded words into one word per CTA (sink[blockIdx.x]): no routing, lookups
+// or stores, so its time is what streaming the step's bytes in those load
+// patterns costs.  H, I <= 2048.
+__global__ __launch_bounds__(256, 3) void decode_stream_probe(lutmoe_moe_desc d, const int32_t* __restrict__ ids,
+                                                              int ns, int which, uint32_t* __restrict__ sink) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int H = d.hidden, I = d.inter;
+    const int gcols = (I + 7) / 8;
+    const int ng = (which & 1) ? gcols * ns : 0;
+    const int bx = blockIdx.x;
+    uint32_t acc = 0;
+    if (bx < ng) {
+        // bl4_decode_gate_up_t1: CTA (x, y), wave wv: gate rows i0, i0 + 1 and up rows of slot y
+        const int y = bx / gcols, xcol = (bx - y * gcols) * 4 + wv;
+        const int e = min(max(ids[y], 0), d.w13.num_experts - 1);
+        const int i0 = 2 * xcol;
+        if (i0 < I) {
+            const int i1 = min(i0 + 1, I - 1);
+            const int rows[4] = {i0, i1, I + i0, I + i1};
+            const int64_t per = (int64_t)d.w13.rows * (H / 2);
+            const uint8_t* codes = (const uint8_t*)d.w13.codes + e * per;
+            const uint8_t* tabs = (const uint8_t*)d.w13.tables + e * per;
+            const bool ok = 32 * lane < H;
+            uint32_t cw[4][4];
+            u32x4_t tw[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t ro = (uint32_t)rows[r] * (uint32_t)(H / 2);
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    cw[r][q] = *reinterpret_cast<const uint32_t*>(codes +
+                                                                  (ro + 4u * (uint32_t)min(lane + 64 * q, H / 8 - 1)));
+                tw[r] = *reinterpret_cast<const u32x4_t*>(tabs + (ro + (ok ? 16 * lane : 0)));
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                acc ^= cw[r][0] ^ cw[r][1] ^ cw[r][2] ^ cw[r][3] ^ tw[r][0] ^ tw[r][1] ^ tw[r][2] ^ tw[r][3];
+        }
+    } else {
+        // bl4_decode_down1: CTA = output rows h0 .. h0 + 3; wave wv: slots wv, wv + 4, ..
+        const int h0 = (bx - ng) * kD1Rows;
+        const int K = I, nd = K / 8;
+        const int64_t per = (int64_t)d.w2.rows * (K / 2);
+        const bool ok = 32 * lane < K;
+        for (int a = wv; a < ns; a += 4) {
+            const int e = min(max(ids[a], 0), d.w2.num_experts - 1);
+            const uint8_t* codes = (const uint8_t*)d.w2.codes + e * per;
+            const uint8_t* tabs = (const uint8_t*)d.w2.tables + e * per;
+            uint32_t cw[4][4];
+            u32x4_t tw[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t ro = (uint32_t)(h0 + r) * (uint32_t)(K / 2);
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    cw[r][q] = *reinterpret_cast<const uint32_t*>(codes + (ro + 4u * (uint32_t)min(lane + 64 * q, nd - 1)));
+                tw[r] = *reinterpret_cast<const u32x4_t*>(tabs + (ro + (ok ? 16 * lane : 0)));
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                acc ^= cw[r][0] ^ cw[r][1] ^ cw[r][2] ^ cw[r][3] ^ tw[r][0] ^ tw[r][1] ^ tw[r][2] ^ tw[r][3];
+        }
+    }
+    acc = (uint32_t)wave_max_i32((int)(acc & 0x7fffffffu));
+    __shared__ uint32_t s_acc[4];
+    if (lane == 0) s_acc[wv] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) sink[bx] = s_acc[0] ^ s_acc[1] ^ s_acc[2] ^ s_acc[3];
+}
+
 // tokens per pass: T=1 and T=2 recompute routing per CTA, larger T read it
 // Tokens per pass of the expert loops (fmt_idx: 0 BL4, 1 nested, 2 REF).  Up
 // to 32 tokens most active experts hold a few of them, and a 4-token BL4 pass
@@ -1955,6 +2030,17 @@ int launch_nested_gemv(const lutmoe_weights* w, int expert, const uint16_t* x, i
 }
 
 size_t decode_route_bytes() { return sizeof(RouteOut) + sizeof(RouteChunks) + sizeof(RoutePosW); }
+
+size_t decode_stream_probe_ctas(const lutmoe_moe_desc* d, int ns, int which) {
+    return (size_t)((which & 1) ? (d->inter + 7) / 8 * ns : 0) + ((which & 2) ? d->hidden / kD1Rows : 0);
+}
+
+int launch_decode_stream_probe(const lutmoe_moe_desc* d, const int32_t* ids, int ns, int which, uint32_t* sink,
+                               hipStream_t s) {
+    const size_t n = decode_stream_probe_ctas(d, ns, which);
+    hipLaunchKernelGGL(decode_stream_probe, dim3((unsigned)n), dim3(256), 0, s, *d, ids, ns, which, sink);
+    return check_launch();
+}
 int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* topk_w,
                      const int32_t* topk_ids, const float* logits, int T, int k, int renorm,
                      float scaling, uint16_t* act, void* route_ws, float* y_ws, void* out,

@@ -68,6 +68,11 @@ int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* t
                      float scaling, uint16_t* act, void* route_ws, float* y_ws, void* out,
                      int out_dtype, int stages, hipStream_t s);
 
+// decode.hip: the one-token layer's weight loads alone (HBM floor measurement)
+size_t decode_stream_probe_ctas(const lutmoe_moe_desc* d, int ns, int which);
+int launch_decode_stream_probe(const lutmoe_moe_desc* d, const int32_t* ids, int ns, int which, uint32_t* sink,
+                               hipStream_t s);
+
 // route.hip
 int launch_route_topk(const float* logits, int T, int E, int k, int renorm, float scaling,
                       float* w, int32_t* ids, hipStream_t s);

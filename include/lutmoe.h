@@ -290,6 +290,20 @@ int lutmoe_moe_forward_logits(const lutmoe_moe_desc* d, const void* x_dev, const
                               int out_dtype, void* workspace_dev, size_t workspace_bytes,
                               int force_path, int stages, void* stream);
 
+/* ---- measurement ---------------------------------------------------------- */
+
+/* The HBM floor of the one-token BL4 layer (no counterpart in the reference;
+ * for benchmarks): one launch whose CTAs issue the same weight loads as the
+ * one-token kernels (which = 1: the gate/up kernel's grid and W13 rows,
+ * 2: the down kernel's grid and W2 rows, 3: both in one launch) for expert
+ * ids_dev[y] of each slot (int32 [k + num_shared], shared slots included;
+ * clamped into the stacks) and only fold the loaded words into
+ * sink_dev[lutmoe_decode_stream_probe_sink_words(d, k, which)] (uint32).
+ * BL4, H and I <= 2048, k + num_shared <= 64. */
+size_t lutmoe_decode_stream_probe_sink_words(const lutmoe_moe_desc* d, int k, int which);
+int lutmoe_decode_stream_probe(const lutmoe_moe_desc* d, const int32_t* ids_dev, int k, int which,
+                               uint32_t* sink_dev, void* stream);
+
 /* ---- encoders (format producers) ----------------------------------------- */
 
 /* BL4 per-64-block k-means encoder on the GPU: w fp32 [nblocks*64] ->

@@ -740,34 +740,51 @@ def test_moe_layer_from_logits_ties(gpu, T, E, renorm):
     assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
 
 
-@pytest.mark.skip(reason="the one-launch persistent decode kernel (bl4_decode_fused) did not complete "
-                         "on its first GPU runs (E=8, S=1, k=2, H=512, I=320, T=1); no cause was shown, "
-                         "and the kernel has been removed (the per-stage kernels run every layer)")
-def test_moe_layer_fused_decode(gpu):
-    """Layer through the persistent decode kernel (one launch, all stages) against the
-    per-stage kernels (routing + gate/up, then down + combine, in a second workspace) bit
-    for bit, and against the oracle."""
+@pytest.mark.parametrize("fmt,T", [("bl4", 1), ("bl4", 2), ("bl4", 9), ("ref", 1), ("nested", 1)])
+def test_moe_layer_decode_staged_equals_full(gpu, fmt, T):
+    """The decode layer run stage by stage (routing + gate/up, then down + combine, in one
+    workspace) equals the one-call layer bit for bit, and the oracle; the one-token
+    stream probe (the layer's weight loads alone, for the HBM floor) runs through the C
+    ABI with the same grid and leaves one word per CTA."""
+    import ctypes
     import torch
     from block_lut_amd import _native as N
     from block_lut_amd import ops
     from block_lut_amd.formats import MoEWeights
-    E, S, k, H, I, T = 8, 1, 2, 512, 320, 1
-    w13, w2 = _moe_case("bl4", E, S, H, I, seed=21)
+    E, S, k, H, I = 8, 1, 2, 512, 320
+    if fmt == "nested":
+        bits = [2, 3, 4, 2, 3, 4, 3, 2, 4]
+        w13 = NestedExpertset(bits, 2 * I, H, seed=91, n_iter=8)
+        w2 = NestedExpertset(bits, H, I, seed=92, n_iter=8)
+    else:
+        w13, w2 = _moe_case(fmt, E, S, H, I, seed=21 + T)
     moe = MoEWeights(w13.stack(gpu), w2.stack(gpu), H, I, E, S)
     rng = np.random.default_rng(T)
     xb = _x(rng, T, H)
-    lg = rng.standard_normal((T, E)).astype(np.float32)
-    rw, rids = O.route(lg, k)
+    rw, rids = O.route(rng.standard_normal((T, E)).astype(np.float32), k)
     args = (moe, to_dev_bf16(xb, gpu), torch.from_numpy(rw).to(gpu), torch.from_numpy(rids).to(gpu))
-    fused = ops.moe_forward(*args, out_dtype=torch.float32, path=1, workspace=ops.new_workspace(moe, T, k, gpu))
+    full = ops.moe_forward(*args, out_dtype=torch.float32, path=1, workspace=ops.new_workspace(moe, T, k, gpu))
     ws = ops.new_workspace(moe, T, k, gpu)
-    staged = torch.empty_like(fused)
+    staged = torch.empty_like(full)
     ops.moe_forward(*args, out=staged, path=1, workspace=ws, stages=N.STAGE_ROUTE | N.STAGE_GATE_UP)
     ops.moe_forward(*args, out=staged, path=1, workspace=ws, stages=N.STAGE_DOWN)
-    assert torch.equal(fused, staged)
-    ref = O.moe_layer(xb, rids, rw, w13.deq_f32, w2.deq_f32,
-                      shared=[(w13.deq_f32(E + s), w2.deq_f32(E + s)) for s in range(S)])
-    assert rel_maxabs(fused.cpu().numpy(), ref) <= TOL
+    assert torch.equal(full, staged)
+    f13, f2 = _ref_semantics(w13, w2, T, 1) if fmt == "ref" else (w13.deq_f32, w2.deq_f32)
+    ref = O.moe_layer(xb, rids, rw, f13, f2, shared=[(f13(E + s), f2(E + s)) for s in range(S)])
+    assert rel_maxabs(full.cpu().numpy(), ref) <= TOL
+    if fmt == "bl4" and T == 1:
+        d = moe.desc()
+        slot_ids = torch.tensor(list(rids[0]) + [E + s for s in range(S)], dtype=torch.int32, device=gpu)
+        for which in (1, 2, 3):
+            n = N.lib().lutmoe_decode_stream_probe_sink_words(ctypes.byref(d), k, which)
+            assert n == ((I + 7) // 8 * (k + S) if which & 1 else 0) + (H // 4 if which & 2 else 0)
+            sink = torch.full((n + 1,), -7, dtype=torch.int32, device=gpu)
+            N.check("lutmoe_decode_stream_probe",
+                    N.lib().lutmoe_decode_stream_probe(ctypes.byref(d), slot_ids.data_ptr(), k, which,
+                                                       sink.data_ptr(), None))
+            torch.cuda.synchronize()
+            got = sink.cpu().numpy()
+            assert got[n] == -7 and not np.any(got[:n] == -7)
 
 
 @pytest.mark.parametrize("T", [1, 2, 5])
