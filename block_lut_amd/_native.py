@@ -113,6 +113,7 @@ PROTOTYPES = {
     "lutmoe_moe_forward_stages": (I32, [DP, P, P, P, I32, I32, P, I32, P, SZ, I32, I32, P]),
     "lutmoe_moe_forward_logits": (I32, [DP, P, P, I32, I32, I32, F32, P, I32, P, SZ, I32, I32, P]),
     "lutmoe_moe_forward_noalloc": (I32, [DP, P, P, P, I32, I32, P, I32, I32, P]),
+    "lutmoe_noalloc_prepare": (I32, []),
     "lutmoe_bl4_encode": (I32, [P, I64, I32, P, P, P]),
     "lutmoe_ref_encode": (I32, [P, P, I64, I32, P, P, P]),
 }

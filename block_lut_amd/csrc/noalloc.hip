@@ -7,8 +7,10 @@
 // The scratch is one file-scope device array per GPU, kScratchBytes long,
 // held until the process ends.  Host code reaches it only through the device
 // address hipGetSymbolAddress returns for the current device (looked up once
-// per device, on the first call there); the array's name in host code is a
-// host-side stand-in and is never passed to a kernel.  Every call on a GPU
+// per device, by lutmoe_noalloc_prepare or else on the first call there; the
+// lookup may load the library's code object, so it is done before any graph
+// capture); the array's name in host code is a host-side stand-in and is
+// never passed to a kernel.  Every call on a GPU
 // uses that GPU's array, which keeps the last call's contents: calls that
 // overlap in time on one GPU race (serialise them, e.g. on one stream).
 #include <hip/hip_runtime.h>
@@ -51,6 +53,11 @@ int device_scratch(uint8_t** out) {
 }
 
 }  // namespace
+
+extern "C" int lutmoe_noalloc_prepare(void) {
+    uint8_t* ws = nullptr;
+    return device_scratch(&ws);
+}
 
 extern "C" int lutmoe_moe_forward_noalloc(const lutmoe_moe_desc* d, const void* x, const float* topk_w,
                                           const int32_t* topk_ids, int T, int k, void* out, int out_dtype,

@@ -261,7 +261,12 @@ int lutmoe_moe_forward(const lutmoe_moe_desc* d, const void* x_dev, const float*
  * LUTMOE_EWORKSPACE and a lutmoe_last_error text giving the sizes.  Every call
  * on one GPU shares that GPU's scratch, which keeps the last call's contents:
  * calls that overlap in time on one GPU race (serialise them, e.g. on one
- * stream).  The first call on a device looks up the scratch's address. */
+ * stream).  The scratch's address on a device is looked up once, by
+ * lutmoe_noalloc_prepare or else by the first call there; that lookup may load
+ * the library's code object, so code that captures calls into a HIP graph
+ * calls lutmoe_noalloc_prepare (or one lutmoe_moe_forward_noalloc) on the
+ * device before it starts capturing. */
+int lutmoe_noalloc_prepare(void);   /* current device; 0 or LUTMOE_EHIP */
 int lutmoe_moe_forward_noalloc(const lutmoe_moe_desc* d, const void* x_dev, const float* topk_w_dev,
                                const int32_t* topk_ids_dev, int T, int k, void* out_dev, int out_dtype,
                                int force_path, void* stream);

@@ -615,7 +615,7 @@ def silu_mul_f32(g, u) -> np.ndarray:
 
 
 def moe_layer(x_bf16, ids, weights, w13_f32, w2_f32, shared=None, act_round_bf16: bool = True,
-              shared_w=None):
+              shared_w=None, blas_dtype=np.float64):
     """fp32 restatement of the fused-MoE apply (vllm_lut/quant_method.py:230-279,
     vllm_lut/fast_moe.py:30-80) with float64 accumulation:
       gu = x @ W13[e]^T ; a = silu(gu[:, :I]) * gu[:, I:] (fp32) ; a -> bf16 (the input
@@ -627,6 +627,9 @@ def moe_layer(x_bf16, ids, weights, w13_f32, w2_f32, shared=None, act_round_bf16
     shared experts (Qwen's sigmoid(x . g), customized/qwen.py:99-100).
     w2_f32 may return a subset of W2's rows (output columns): the result then has that
     many columns.
+    blas_dtype: the dtype of the two matrix products (float64 by default; float32 for
+    full-shape prefill checks, whose sums of at most a few thousand products carry a
+    relative error near 1e-6, far below the 1e-3 bar); results are accumulated in float64.
     Returns float64 [T, H] (or [T, rows of the W2 given])."""
     x = bf16_to_f32(x_bf16).astype(np.float64)
     ids = np.asarray(ids, np.int64)
@@ -634,13 +637,15 @@ def moe_layer(x_bf16, ids, weights, w13_f32, w2_f32, shared=None, act_round_bf16
     T = x.shape[0]
     out = None
 
+    xb = x.astype(blas_dtype)
+
     def expert(rows, W13, W2):
-        gu = x[rows] @ W13.astype(np.float64).T
+        gu = xb[rows] @ W13.astype(blas_dtype, copy=False).T
         I = W13.shape[0] // 2
         a = silu_mul_f32(gu[:, :I].astype(np.float32), gu[:, I:].astype(np.float32))
         if act_round_bf16:
             a = bf16_to_f32(f32_to_bf16(a))
-        return a.astype(np.float64) @ W2.astype(np.float64).T
+        return (a.astype(blas_dtype) @ W2.astype(blas_dtype, copy=False).T).astype(np.float64)
 
     def acc(rows, y):
         # a token listing an expert twice adds both pairs, as the reference's loop
@@ -648,7 +653,10 @@ def moe_layer(x_bf16, ids, weights, w13_f32, w2_f32, shared=None, act_round_bf16
         nonlocal out
         if out is None:
             out = np.zeros((T, y.shape[1]), np.float64)
-        np.add.at(out, rows, y)
+        if np.unique(rows).size == rows.size:
+            out[rows] += y
+        else:
+            np.add.at(out, rows, y)
 
     for e in np.unique(ids):
         tok, slot = np.nonzero(ids == e)

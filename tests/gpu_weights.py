@@ -116,21 +116,3 @@ class DevNested:
             t = self.tabs[e].cpu().numpy().view(np.uint16)
             self._cache[e] = O.nested_dequant_f32(codes, t, b)
         return self._cache[e]
-
-
-def sample_tokens(rids, T, n_random, rng, extra=()):
-    """Token rows for a sampled check of a prefill-sized layer: the first and last
-    token, the first and last tokens of the most heavily routed expert (its
-    positions span the most tiles, the last one a tail tile), the last token
-    routed to each of a few other experts (tail tiles of their position
-    ranges), and random tokens."""
-    ids = np.asarray(rids)
-    counts = np.bincount(ids.reshape(-1))
-    heavy = int(np.argmax(counts))
-    ht = np.nonzero((ids == heavy).any(axis=1))[0]
-    picks = {0, T - 1, int(ht[0]), int(ht[-1]), int(ht[len(ht) // 2])}
-    for e in rng.choice(np.nonzero(counts)[0], size=min(6, np.count_nonzero(counts)), replace=False):
-        picks.add(int(np.nonzero((ids == e).any(axis=1))[0][-1]))
-    picks.update(int(t) for t in rng.choice(T, size=min(n_random, T), replace=False))
-    picks.update(int(t) for t in extra)
-    return np.array(sorted(picks), np.int64)

@@ -34,6 +34,21 @@ def rel_maxabs(got, ref) -> float:
     return float(np.abs(got - ref).max() / (den if den > 0 else 1.0))
 
 
+def rel_excess_bf16(got, ref) -> float:
+    """For a bf16 result: max over elements of (|got - bf16(ref)| minus one bf16 ulp of
+    bf16(ref), at least 0) / max|ref|.  The result may sit one rounding step from the oracle
+    rounded to bf16 (its fp32 sum and the oracle's float64 sum can round to neighbouring
+    bf16 values); everything beyond that step is held to the same relative bar as an fp32
+    result."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    refb = O.bf16_to_f32(O.f32_to_bf16(ref.astype(np.float32))).astype(np.float64)
+    ulp = np.spacing(np.abs(refb).astype(np.float32)).astype(np.float64) * 65536.0
+    excess = np.maximum(np.abs(got - refb) - ulp, 0.0)
+    den = np.abs(ref).max()
+    return float(excess.max() / (den if den > 0 else 1.0))
+
+
 def golden_codebook() -> np.ndarray:
     """bf16 bits of the reference's shipped Qwen blocklut_256 codebook (derived fixture)."""
     return np.load(os.path.join(GOLDEN, "codebooks.npz"))["qwen_blocklut_256_bf16"]

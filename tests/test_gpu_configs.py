@@ -3,17 +3,17 @@ against the float64 oracle (the Qwen decode layer at T = 1 / 8 / 32 is in
 test_gpu_parity.py).
 
 Weights are random stacks in their wire formats (tests/gpu_weights.py); the oracle
-dequantises them on the host from the codes.  Prefill-sized runs are checked on a
-sample of token rows (and, for Mixtral, of output columns) chosen to include the
-first and last tokens, the most heavily routed expert's first and last tokens and
-the tail tiles of several experts' position ranges.  Bar as in test_gpu_parity.py:
-max|y - y_ref| / max|y_ref| <= 1e-3 over the checked entries, fp32 output.
+dequantises them on the host from the codes.  Every token row of every output is
+checked (Mixtral: every token on 384 sampled output columns, which keeps the host
+copy of its down projection small); the prefill-sized oracles run their matrix
+products in float32 host BLAS (relative error near 1e-6).  Bar as in
+test_gpu_parity.py: max|y - y_ref| / max|y_ref| <= 1e-3, fp32 output.
 """
 import numpy as np
 import pytest
 
 import oracle as O
-from gpu_weights import DevBL4, DevNested, sample_tokens
+from gpu_weights import DevBL4, DevNested
 from lutmoe_testutil import rel_maxabs, to_dev_bf16
 
 pytestmark = pytest.mark.gpu
@@ -44,17 +44,16 @@ def test_config_deepseek_v2_lite_prefill(gpu):
                                  out_dtype=torch.float32).cpu().numpy()
     assert np.isfinite(out).all()
     rw, rids = O.route(lg, k)
-    tok = sample_tokens(rids, T, 24, rng)
-    ref = O.moe_layer(xb[tok], rids[tok], rw[tok], w13.host, w2.host,
-                      shared=[(w13.host(E + s), w2.host(E + s)) for s in range(S)])
-    assert rel_maxabs(out[tok], ref) <= TOL
+    ref = O.moe_layer(xb, rids, rw, w13.host, w2.host,
+                      shared=[(w13.host(E + s), w2.host(E + s)) for s in range(S)], blas_dtype=np.float32)
+    assert rel_maxabs(out, ref) <= TOL
 
 
 def test_config_mixtral_layer(gpu):
     """One Mixtral-8x7B-shaped layer (H4096, I14336, 8 experts top-2 with renormalisation,
     BL4, 1.41 GB resident): decode B=1 (grouped LUT-GEMV) and B=64 (grouped MFMA with the
-    down projection's K split in two), prefill 4096 tokens; every check on sampled token
-    rows and 384 sampled output columns."""
+    down projection's K split in two), prefill 4096 tokens; every token row checked on 384
+    sampled output columns."""
     import torch
     from block_lut_amd import ops
     from block_lut_amd.formats import MoEWeights
@@ -72,9 +71,8 @@ def test_config_mixtral_layer(gpu):
                                      renormalize=True, out_dtype=torch.float32).cpu().numpy()
         assert np.isfinite(out).all(), T
         rw, rids = O.route(lg, k, renormalize=True)
-        tok = np.arange(T) if T == 1 else sample_tokens(rids, T, 8, rng)
-        ref = O.moe_layer(xb[tok], rids[tok], rw[tok], w13.host, lambda e: w2.host(e, rows=cols))
-        assert rel_maxabs(out[tok][:, cols], ref) <= TOL, T
+        ref = O.moe_layer(xb, rids, rw, w13.host, lambda e: w2.host(e, rows=cols), blas_dtype=np.float32)
+        assert rel_maxabs(out[:, cols], ref) <= TOL, T
 
 
 @pytest.mark.parametrize("T", [16, 1024])
@@ -82,8 +80,8 @@ def test_config_nested_tiers_qwen(gpu, T):
     """NestedLUT tiers on the Qwen1.5-MoE shape (H2048, I1408, 60 experts top-4): 20 experts
     each at 2, 3 and 4 bits (seeded permutation); expert popularity p_e ~ rank^-1.1 (Zipf,
     seeded ranks) with Gumbel-top-4 routing (logits = log p_e + Gumbel noise, so the layer's
-    own softmax / top-k makes the selection).  Decode T=16 (every token checked) and
-    prefill T=1024 (sampled tokens, including the heaviest slot)."""
+    own softmax / top-k makes the selection).  Decode T=16 and prefill T=1024, every token
+    checked."""
     import torch
     from block_lut_amd import ops
     from block_lut_amd.formats import MoEWeights
@@ -106,6 +104,5 @@ def test_config_nested_tiers_qwen(gpu, T):
     rw, rids = O.route(lg, k)
     counts = np.bincount(rids.reshape(-1), minlength=E)
     assert counts.max() >= 2 * counts[counts > 0].mean()   # the routing is skewed
-    tok = np.arange(T) if T <= 32 else sample_tokens(rids, T, 24, rng)
-    ref = O.moe_layer(xb[tok], rids[tok], rw[tok], w13.host, w2.host)
-    assert rel_maxabs(out[tok], ref) <= TOL
+    ref = O.moe_layer(xb, rids, rw, w13.host, w2.host, blas_dtype=np.float32)
+    assert rel_maxabs(out, ref) <= TOL

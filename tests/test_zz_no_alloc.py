@@ -79,3 +79,63 @@ def test_noalloc_rejects_layers_beyond_its_scratch(gpu):
     assert str(need) in msg and str(32 << 20) in msg
     torch.cuda.synchronize()
     assert torch.count_nonzero(out) == 0
+
+
+@pytest.mark.parametrize("T,path", [(1, 0), (9, 0), (40, 0)])
+def test_noalloc_graph_capture(gpu, T, path):
+    """lutmoe_noalloc_prepare, then lutmoe_moe_forward_noalloc captured into a HIP graph
+    (torch.cuda.CUDAGraph) and replayed three times with new activations and routing
+    copied into its input buffers between replays, with eager work and synchronisations in
+    between: every replay equals lutmoe_moe_forward with a caller workspace, bit for bit."""
+    import torch
+    from block_lut_amd import _native as N
+    from block_lut_amd import ops
+    from block_lut_amd.formats import MoEWeights
+    E, S, k, H, I = 8, 1, 2, 512, 320
+    w13 = BL4Expertset(E + S, 2 * I, H, seed=83, n_iter=8)
+    w2 = BL4Expertset(E + S, H, I, seed=84, n_iter=8)
+    moe = MoEWeights(w13.stack(gpu), w2.stack(gpu), H, I, E, S)
+    d = moe.desc()
+    assert N.lib().lutmoe_noalloc_prepare() == 0
+    x = torch.zeros((T, H), dtype=torch.bfloat16, device=gpu)
+    w = torch.zeros((T, k), dtype=torch.float32, device=gpu)
+    ids = torch.zeros((T, k), dtype=torch.int32, device=gpu)
+    out = torch.zeros((T, H), dtype=torch.float32, device=gpu)
+
+    def call():
+        N.check("lutmoe_moe_forward_noalloc",
+                N.lib().lutmoe_moe_forward_noalloc(ctypes.byref(d), x.data_ptr(), w.data_ptr(), ids.data_ptr(), T,
+                                                   k, out.data_ptr(), N.DTYPE_F32, path,
+                                                   torch.cuda.current_stream().cuda_stream))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        call()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        call()
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(500 + T)
+    ws = ops.new_workspace(moe, T, k, gpu)
+    for rep in range(3):
+        xb = O.f32_to_bf16(rng.standard_normal((T, H)).astype(np.float32))
+        rw, rids = O.route(rng.standard_normal((T, E)).astype(np.float32), k)
+        x.copy_(to_dev_bf16(xb, gpu))
+        w.copy_(torch.from_numpy(rw).to(gpu))
+        ids.copy_(torch.from_numpy(rids.astype(np.int32)).to(gpu))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        ref_out = torch.full((T, H), float("nan"), dtype=torch.float32, device=gpu)
+        N.check("lutmoe_moe_forward",
+                N.lib().lutmoe_moe_forward(ctypes.byref(d), x.data_ptr(), w.data_ptr(), ids.data_ptr(), T, k,
+                                           ref_out.data_ptr(), N.DTYPE_F32, ws.data_ptr(), ws.numel(), path,
+                                           torch.cuda.current_stream().cuda_stream))
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref_out), (T, rep)
+        ref = O.moe_layer(xb, rids, rw, w13.deq_f32, w2.deq_f32,
+                          shared=[(w13.deq_f32(E + s), w2.deq_f32(E + s)) for s in range(S)])
+        assert rel_maxabs(got.cpu().numpy(), ref) <= 1e-3, (T, rep)
