@@ -394,22 +394,29 @@ def main():
         torch.cuda.empty_cache()
         extra.update(mixtral_stack(ops, torch, dev, rand_stack, MoEWeights, graph_of, time_graph))
         torch.cuda.empty_cache()
-        # switch-base-8 single BL4 linear 768 -> 3072, one token
+        # switch-base-8 single BL4 linear 768 -> 3072, one token of fp32 activations (the
+        # configured precision, fp32 output); the same with the row rounded to bf16 beside it
         st1 = rand_stack(1, 3072, 768)
-        x1 = torch.randn((1, 768), device=dev).to(torch.bfloat16)
-        y1 = torch.empty((1, 3072), dtype=torch.bfloat16, device=dev)
+        for name, xdt in (("switch_linear_768x3072_us", torch.float32),
+                          ("switch_linear_768x3072_bf16x_us", torch.bfloat16)):
+            x1 = torch.randn((1, 768), device=dev).to(xdt)
+            y1 = torch.empty((1, 3072), dtype=torch.float32, device=dev)
 
-        def c1():
-            ops.gemv(st1, x1, out=y1)
-        g = graph_of([c1] * 32)
-        time_graph(g, 2)
-        sec = time_graph(g, 10) / (10 * 32)
-        extra["switch_linear_768x3072_us"] = round(sec * 1e6, 3)
+            def c1(x1=x1, y1=y1):
+                ops.gemv(st1, x1, out=y1)
+            g = graph_of([c1] * 32)
+            time_graph(g, 2)
+            sec = time_graph(g, 10) / (10 * 32)
+            extra[name] = round(sec * 1e6, 3)
+        extra["switch_linear_768x3072_GBs"] = round(3072 * 768 * BYTES_PER_WEIGHT / (extra["switch_linear_768x3072_us"] * 1e-6) / 1e9, 1)
         result["extra"] = extra
 
     # ------------------------------------------------------------ CPU leg
     if not a.no_cpu:
         result["cpu_baseline"] = cpu_baseline(a, c, T)
+        if not a.no_extra:
+            result["extra"].update(cpu_other_workloads(result["extra"].pop("_nested_touched", None)))
+    result.get("extra", {}).pop("_nested_touched", None)
 
     print(json.dumps(result), flush=True)
 
@@ -595,18 +602,22 @@ def nested_tiers(a, ops, N, torch, dev, NestedExpert, NestedStack, MoEWeights, g
 
     nl = 4   # 4 layer copies: about 1.4 GB, past the Infinity Cache
     layers = [MoEWeights(stack(2 * I, H), stack(H, I), H, I, E, 0) for _ in range(nl)]
-    out = {}
+    out = {"_nested_touched": {}}
     for T, path, label in ((16, ops.PATH_GEMV, "decode"), (1024, ops.PATH_MFMA, "prefill")):
         steps = []
+        touched = {2: 0, 3: 0, 4: 0}
         for L in layers:
             g = rng.gumbel(size=(T, E))
             lg = torch.from_numpy((logp[None, :] + g).astype(np.float32)).to(dev)
             ids = np.argsort(-(logp[None, :] + g), axis=1, kind="stable")[:, :k]
             uniq = np.unique(ids)
+            for e in uniq:
+                touched[int(bits[e])] += 1 / nl
             x = torch.randn((T, H), device=dev).to(torch.bfloat16)
             o = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
             ws = ops.new_workspace(L, T, k, dev)
             steps.append((L, lg, x, o, ws, sum(exp_bytes(int(bits[e])) for e in uniq)))
+        out["_nested_touched"][T] = touched
         fns = [(lambda s=s: ops.moe_forward_logits(s[0], s[2], s[1], k, out=s[3], workspace=s[4],
                                                    path=path)) for s in steps]
         g = graph_of(fns)
@@ -642,6 +653,95 @@ def cpu_model() -> str:
         return "unknown"
     return (f"{info.get('model name', 'unknown')} ({info.get('vendor_id', '?')} family "
             f"{info.get('cpu family', '?')} model {info.get('model', '?')} stepping {info.get('stepping', '?')})")
+
+
+def cpu_other_workloads(nested_touched):
+    """The reference's CPU dequant + matmul path (oracle/cpu_baseline.py) beside the other
+    workloads, on the host cores, each on a bounded sample (about 5 s in all):
+      switch-base-8 single linear: fp32 F.linear of one fp32 row over the dequantised
+        [3072, 768] BL4 weights, median of >= 20 calls;
+      DeepSeek-V2-Lite prefill T=2048: the reference's multi-token branch per expert
+        (dequantise W13 and W2, both projections over all 2048 tokens), median over 6
+        experts, times the step's 66 experts;
+      NestedLUT tiers: the same per expert at 2, 3 and 4 bits (2 experts each) for T=16
+        and T=1024, times the step's touched experts per tier (the bench's own routing).
+    Figures: ms per layer step, and the GPU metrics' units (TB/s of algorithmic bytes,
+    TFLOP/s of routed flops)."""
+    import statistics
+    import torch
+    from oracle.cpu_baseline import (bl4_dequant_torch, expert_all_tokens, linear_fp32,
+                                     table_dequant_torch)
+    ncores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(ncores)
+    g = torch.Generator().manual_seed(77)
+    out = {"cpu_other_cores": ncores}
+
+    def timed(fn, n, warm=2):
+        for _ in range(warm):
+            fn()
+        ts = []
+        for _ in range(n):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts)
+
+    def bl4(M, K):
+        return (torch.randint(0, 256, (M, K // 2), dtype=torch.uint8, generator=g),
+                torch.sort(torch.randn((M, K // 64, 16), generator=g) * 0.02, dim=-1).values.to(torch.bfloat16))
+
+    c1 = bl4(3072, 768)
+    x1 = torch.randn((1, 768), generator=g)
+    sec = timed(lambda: linear_fp32(x1, *c1), 40, warm=3)
+    out["cpu_switch_linear_768x3072_us"] = round(sec * 1e6, 1)
+    out["cpu_switch_linear_768x3072_GBs"] = round(3072 * 768 * BYTES_PER_WEIGHT / sec / 1e9, 3)
+
+    H, I = 2048, 1408
+
+    def expert_time(T, make13, make2, n):
+        """Median over n fresh experts of dequantise + both projections over all T tokens;
+        make13 / make2 build an expert's stored weights (untimed) and return its dequantiser."""
+        x = torch.randn((T, H), generator=g).to(torch.bfloat16)
+        ts = []
+        for _ in range(n):
+            deq13, deq2 = make13(), make2()
+            t0 = time.perf_counter()
+            expert_all_tokens(x, deq13(), deq2())
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts)
+
+    def bl4_expert(M, K):
+        st = bl4(M, K)
+        return lambda: bl4_dequant_torch(*st)
+
+    d = DSV2
+    per = expert_time(2048, lambda: bl4_expert(2 * I, H), lambda: bl4_expert(H, I), 6)
+    n_exp = d["E"] + d["S"]
+    step = per * n_exp
+    flops = 6 * d["H"] * d["I"] * 2048 * (d["k"] + d["S"])
+    out["cpu_prefill_dsv2_T2048_ms"] = round(step * 1e3, 1)
+    out["cpu_prefill_dsv2_T2048_TFLOPs"] = round(flops / step / 1e12, 4)
+    out["cpu_prefill_dsv2_T2048_sample"] = (f"median of 6 experts ({per * 1e3:.0f} ms each: dequantise W13 + W2, "
+                                            f"F.linear over all 2048 tokens) x {n_exp} experts")
+    if nested_touched:
+        for T, key in ((16, "decode_T16"), (1024, "prefill_T1024")):
+            tot = 0.0
+            for b in (2, 3, 4):
+                def nested_expert(M, K, b=b):
+                    codes = torch.randint(0, 1 << b, (M, K), dtype=torch.uint8, generator=g)
+                    tab = torch.sort(torch.randn((M, K // 64, 1 << b), generator=g) * 0.02,
+                                     dim=-1).values.to(torch.bfloat16)
+                    return lambda: table_dequant_torch(codes, tab)
+                tb = expert_time(T, lambda: nested_expert(2 * I, H), lambda: nested_expert(H, I), 2)
+                tot += tb * nested_touched[T][b]
+            out[f"cpu_nested_tiers_{key}_ms"] = round(tot * 1e3, 1)
+            if T == 1024:
+                out[f"cpu_nested_tiers_{key}_TFLOPs"] = round(6 * H * I * T * 4 / tot / 1e12, 4)
+        out["cpu_nested_tiers_sample"] = ("per tier the median of 2 experts (dequantise through the tier's "
+                                          "table, F.linear over all tokens) x the step's touched experts "
+                                          "of that tier (average over the bench's 4 layers)")
+    torch.set_num_threads(ncores)
+    return out
 
 
 def cpu_baseline(a, c, T):

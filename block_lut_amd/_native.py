@@ -103,6 +103,7 @@ PROTOTYPES = {
     "lutmoe_ref_quantize": (I32, [P, I32, P, I32, I64, I32, I32, P, P, P]),
     "lutmoe_dequant": (I32, [WP, I32, I32, P, P]),
     "lutmoe_gemv": (I32, [WP, I32, P, I32, P, I32, P]),
+    "lutmoe_gemv_ex": (I32, [WP, I32, P, I32, I32, P, I32, P]),
     "lutmoe_bl4_tables_from_f16": (I32, [P, P, I64, P]),
     "lutmoe_decode_stream_probe_sink_words": (SZ, [DP, I32, I32]),
     "lutmoe_decode_stream_probe": (I32, [DP, P, I32, I32, P, P]),

@@ -294,18 +294,26 @@ int lutmoe_dequant(const lutmoe_weights* w, int e0, int ne, void* out, void* str
     }
 }
 
-int lutmoe_gemv(const lutmoe_weights* w, int expert, const void* x, int T, void* y, int y_dtype,
-                void* stream) {
+int lutmoe_gemv_ex(const lutmoe_weights* w, int expert, const void* x, int x_dtype, int T, void* y, int y_dtype,
+                   void* stream) {
     int rc = validate_weights(w);
     if (rc) return rc;
     if (!x || !y || T < 0 || expert < 0 || expert >= w->num_experts) return LUTMOE_EINVAL;
     if (y_dtype != LUTMOE_DTYPE_BF16 && y_dtype != LUTMOE_DTYPE_F32) return LUTMOE_EINVAL;
+    if (x_dtype != LUTMOE_DTYPE_BF16 && x_dtype != LUTMOE_DTYPE_F32) return LUTMOE_EINVAL;
     if (!aligned(x, 16) || w->cols % 8) return LUTMOE_EALIGN;
     if (T == 0) return LUTMOE_OK;
-    if (w->format == LUTMOE_FMT_NESTED)
+    if (w->format == LUTMOE_FMT_NESTED) {
+        if (x_dtype == LUTMOE_DTYPE_F32) return LUTMOE_EUNSUPPORTED;
         return launch_nested_gemv(w, expert, (const uint16_t*)x, T, y, y_dtype, stream_of(stream));
+    }
     if (w->format == LUTMOE_FMT_REF && (rc = validate_ref_vector(w))) return rc;
-    return launch_bl4_gemv(w, expert, (const uint16_t*)x, T, y, y_dtype, stream_of(stream));
+    return launch_bl4_gemv(w, expert, x, x_dtype == LUTMOE_DTYPE_F32, T, y, y_dtype, stream_of(stream));
+}
+
+int lutmoe_gemv(const lutmoe_weights* w, int expert, const void* x, int T, void* y, int y_dtype,
+                void* stream) {
+    return lutmoe_gemv_ex(w, expert, x, LUTMOE_DTYPE_BF16, T, y, y_dtype, stream);
 }
 
 int lutmoe_bl4_tables_from_f16(const uint16_t* f16, uint16_t* bf16, int64_t n, void* stream) {

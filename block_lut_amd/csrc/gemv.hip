@@ -76,6 +76,28 @@ struct Bl4Dec {
             }
         }
     }
+    // fp32 activations: each looked-up entry widened to fp32 (exact) and
+    // multiplied with its activation by an fp32 FMA
+    template <int TB>
+    __device__ __forceinline__ void dot_f32(int r, const uint8_t* slot, int lane, const float (&xv)[TB][8],
+                                            int nt, float (&acc)[TB]) const {
+        const uint8_t* tb = slot + r * 256 + ((lane >> 3) << 5);
+        const uint32_t w = cw[r];
+        const uint32_t we = (w << 1) & 0x1e1e1e1eu;
+        const uint32_t wo = (w >> 3) & 0x1e1e1e1eu;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float lo = bf16_to_f32(*reinterpret_cast<const uint16_t*>(tb + ((we >> (8 * j)) & 0xffu)));
+            const float hi = bf16_to_f32(*reinterpret_cast<const uint16_t*>(tb + ((wo >> (8 * j)) & 0xffu)));
+#pragma unroll
+            for (int t = 0; t < TB; ++t) {
+                if (t < nt) {
+                    acc[t] = fmaf(xv[t][2 * j], lo, acc[t]);
+                    acc[t] = fmaf(xv[t][2 * j + 1], hi, acc[t]);
+                }
+            }
+        }
+    }
 };
 
 struct RefDec {
@@ -132,6 +154,24 @@ struct RefDec {
 #pragma unroll
         for (int t = 0; t < TB; ++t) acc[t] = kDeq ? acc[t] + s[t] : fmaf(s[t], am[r], acc[t]);
     }
+    // fp32 activations, lut_gemv's product order (x * cb) * absmax
+    template <int TB>
+    __device__ __forceinline__ void dot_f32(int r, const uint8_t*, int, const float (&xv)[TB][8], int nt,
+                                            float (&acc)[TB]) const {
+        float s[TB];
+#pragma unroll
+        for (int t = 0; t < TB; ++t) s[t] = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t word = j < 4 ? cw[r].x : cw[r].y;
+            const float cv = s_cb[(word >> (8 * (j & 3))) & 0xffu];
+#pragma unroll
+            for (int t = 0; t < TB; ++t)
+                if (t < nt) s[t] = fmaf(xv[t][j], cv, s[t]);
+        }
+#pragma unroll
+        for (int t = 0; t < TB; ++t) acc[t] = fmaf(s[t], am[r], acc[t]);
+    }
 };
 
 template <class Dec>
@@ -168,12 +208,40 @@ __device__ __forceinline__ void octet_chunk(Dec& dec, const int (&rows)[kRows], 
     wave_lds_sync();
 }
 
+// The same for fp32 activations (8 floats a lane, two 16-byte loads).
+template <class Dec, int TB>
+__device__ __forceinline__ void octet_chunk_f32(Dec& dec, const int (&rows)[kRows], int c, int nblk_k,
+                                                int lane, uint8_t* slot, const float* const (&xrow)[TB],
+                                                int nt, float (&acc)[kRows][TB]) {
+    const bool ok = (c * 8 + (lane >> 3)) < nblk_k;
+    float xv[TB][8];
+#pragma unroll
+    for (int t = 0; t < TB; ++t) {
+        float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+        if (ok && t < nt) {
+            a = *reinterpret_cast<const float4*>(xrow[t] + c * kChunk + 8 * lane);
+            b = *reinterpret_cast<const float4*>(xrow[t] + c * kChunk + 8 * lane + 4);
+        }
+        xv[t][0] = a.x; xv[t][1] = a.y; xv[t][2] = a.z; xv[t][3] = a.w;
+        xv[t][4] = b.x; xv[t][5] = b.y; xv[t][6] = b.z; xv[t][7] = b.w;
+    }
+    dec.load(rows, c, lane, ok);
+    dec.stage(slot, lane);
+    wave_lds_sync();
+    if (ok) {
+#pragma unroll
+        for (int r = 0; r < kRows; ++r) dec.template dot_f32<TB>(r, slot, lane, xv, nt, acc[r]);
+    }
+    wave_lds_sync();
+}
+
 // -------------------------------------------------------- single-matrix GEMV
 
 // y[t][row] for one expert; CTA = 4 waves, wave w owns rows 8*(4*bx + w) ..
-template <class Dec, int TB>
+// kXF32: x is fp32 [T][K] (else bf16).
+template <class Dec, int TB, bool kXF32>
 __global__ __launch_bounds__(256) void gemv_kernel(lutmoe_weights w, int expert,
-                                                   const uint16_t* __restrict__ x, int T,
+                                                   const void* __restrict__ x, int T,
                                                    void* __restrict__ y, int y_dtype) {
     __shared__ __attribute__((aligned(16))) uint8_t s_slot[4 * kSlot];
     __shared__ float s_cb[256];
@@ -194,15 +262,22 @@ __global__ __launch_bounds__(256) void gemv_kernel(lutmoe_weights w, int expert,
     uint8_t* slot = s_slot + wv * kSlot;
     for (int tb = 0; tb < T; tb += TB) {
         const int nt = min(TB, T - tb);
-        const uint16_t* xrow[TB];
-#pragma unroll
-        for (int t = 0; t < TB; ++t) xrow[t] = x + (int64_t)(tb + min(t, nt - 1)) * K;
         float acc[kRows][TB];
 #pragma unroll
         for (int r = 0; r < kRows; ++r)
 #pragma unroll
             for (int t = 0; t < TB; ++t) acc[r][t] = 0.f;
-        for (int c = 0; c < nch; ++c) octet_chunk<Dec, TB>(dec, rows, c, nblk_k, lane, slot, xrow, nt, acc);
+        if constexpr (kXF32) {
+            const float* xrow[TB];
+#pragma unroll
+            for (int t = 0; t < TB; ++t) xrow[t] = (const float*)x + (int64_t)(tb + min(t, nt - 1)) * K;
+            for (int c = 0; c < nch; ++c) octet_chunk_f32<Dec, TB>(dec, rows, c, nblk_k, lane, slot, xrow, nt, acc);
+        } else {
+            const uint16_t* xrow[TB];
+#pragma unroll
+            for (int t = 0; t < TB; ++t) xrow[t] = (const uint16_t*)x + (int64_t)(tb + min(t, nt - 1)) * K;
+            for (int c = 0; c < nch; ++c) octet_chunk<Dec, TB>(dec, rows, c, nblk_k, lane, slot, xrow, nt, acc);
+        }
 #pragma unroll
         for (int r = 0; r < kRows; ++r) {
 #pragma unroll
@@ -349,22 +424,25 @@ int launch_ref_gemv(const uint16_t* x, const uint8_t* idx, const uint16_t* cb_bf
     return ref_gemv_dispatch<false>(x, idx, cb_bf16, cb_f32, absmax, y, M, K, T, num_blocks, block_size, y_dtype, s);
 }
 
-template <class Dec>
-static int gemv_dispatch(const lutmoe_weights* w, int expert, const uint16_t* x, int T, void* y,
+template <class Dec, bool kXF32>
+static int gemv_dispatch(const lutmoe_weights* w, int expert, const void* x, int T, void* y,
                          int y_dtype, hipStream_t s) {
     const dim3 grid((w->rows + 4 * kRows - 1) / (4 * kRows));
     switch (tb_for(T)) {
-        case 1: hipLaunchKernelGGL((gemv_kernel<Dec, 1>), grid, dim3(256), 0, s, *w, expert, x, T, y, y_dtype); break;
-        case 2: hipLaunchKernelGGL((gemv_kernel<Dec, 2>), grid, dim3(256), 0, s, *w, expert, x, T, y, y_dtype); break;
-        default: hipLaunchKernelGGL((gemv_kernel<Dec, 4>), grid, dim3(256), 0, s, *w, expert, x, T, y, y_dtype); break;
+        case 1: hipLaunchKernelGGL((gemv_kernel<Dec, 1, kXF32>), grid, dim3(256), 0, s, *w, expert, x, T, y, y_dtype); break;
+        case 2: hipLaunchKernelGGL((gemv_kernel<Dec, 2, kXF32>), grid, dim3(256), 0, s, *w, expert, x, T, y, y_dtype); break;
+        default: hipLaunchKernelGGL((gemv_kernel<Dec, 4, kXF32>), grid, dim3(256), 0, s, *w, expert, x, T, y, y_dtype); break;
     }
     return check_launch();
 }
 
-int launch_bl4_gemv(const lutmoe_weights* w, int expert, const uint16_t* x, int T, void* y,
+int launch_bl4_gemv(const lutmoe_weights* w, int expert, const void* x, bool x_f32, int T, void* y,
                     int y_dtype, hipStream_t s) {
-    if (w->format == LUTMOE_FMT_REF) return gemv_dispatch<RefDec>(w, expert, x, T, y, y_dtype, s);
-    return gemv_dispatch<Bl4Dec>(w, expert, x, T, y, y_dtype, s);
+    if (w->format == LUTMOE_FMT_REF)
+        return x_f32 ? gemv_dispatch<RefDec, true>(w, expert, x, T, y, y_dtype, s)
+                     : gemv_dispatch<RefDec, false>(w, expert, x, T, y, y_dtype, s);
+    return x_f32 ? gemv_dispatch<Bl4Dec, true>(w, expert, x, T, y, y_dtype, s)
+                 : gemv_dispatch<Bl4Dec, false>(w, expert, x, T, y, y_dtype, s);
 }
 
 

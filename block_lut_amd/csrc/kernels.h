@@ -33,7 +33,8 @@ int launch_ref_gemv(const uint16_t* x, const uint8_t* idx, const uint16_t* cb_bf
                     const float* cb_f32, const uint16_t* absmax, void* y, int M, int K,
                     int T, int num_blocks, int block_size, int y_dtype, hipStream_t s,
                     bool dequant = false);
-int launch_bl4_gemv(const lutmoe_weights* w, int expert, const uint16_t* x, int T, void* y,
+// BL4 and REF weights; x bf16, or fp32 when x_f32
+int launch_bl4_gemv(const lutmoe_weights* w, int expert, const void* x, bool x_f32, int T, void* y,
                     int y_dtype, hipStream_t s);
 int launch_nested_gemv(const lutmoe_weights* w, int expert, const uint16_t* x, int T,
                        void* y, int y_dtype, hipStream_t s);

@@ -124,11 +124,14 @@ def blocklut_recover(indices: torch.Tensor, absmax: torch.Tensor, lut: torch.Ten
 
 def gemv(w: WeightStack, x: torch.Tensor, expert: int = 0,
          out_dtype: torch.dtype = torch.bfloat16, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """y [T, M] = x [T, K] . W[expert]^T (fp32 accumulation); ``out`` (contiguous
-    [T, M], its dtype bf16 or fp32) receives the result without an allocation."""
+    """y [T, M] = x [T, K] . W[expert]^T (fp32 accumulation); x bf16, or fp32 (BL4 and REF
+    weights); ``out`` (contiguous [T, M], its dtype bf16 or fp32) receives the result
+    without an allocation."""
     squeeze = x.dim() == 1
     x2 = x.unsqueeze(0) if squeeze else x
-    _dev(x2, torch.bfloat16, "x")
+    if x2.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"x must be bf16 or fp32, got {x2.dtype}")
+    _dev(x2, x2.dtype, "x")
     if x2.shape[1] != w.cols:
         raise ValueError(f"x has {x2.shape[1]} features, weights expect {w.cols}")
     if out is None:
@@ -137,8 +140,8 @@ def gemv(w: WeightStack, x: torch.Tensor, expert: int = 0,
         y = _dev(out, out.dtype, "out").view(x2.shape[0], w.rows)
         out_dtype = out.dtype
     d = w.desc()
-    N.check("lutmoe_gemv", N.lib().lutmoe_gemv(ctypes.byref(d), expert, x2.data_ptr(), x2.shape[0],
-                                               y.data_ptr(), _out_code(out_dtype), _stream()))
+    N.check("lutmoe_gemv", N.lib().lutmoe_gemv_ex(ctypes.byref(d), expert, x2.data_ptr(), _out_code(x2.dtype),
+                                                  x2.shape[0], y.data_ptr(), _out_code(out_dtype), _stream()))
     return y[0] if squeeze else y
 
 

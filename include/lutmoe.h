@@ -198,9 +198,18 @@ int lutmoe_merge_bitplane(uint8_t* codes_dev, const uint8_t* plane_dev, int64_t 
 /* Dequantise experts [e0, e0+ne) of a weight stack to bf16 [ne][M][K]. */
 int lutmoe_dequant(const lutmoe_weights* w, int e0, int ne, void* out_dev, void* stream);
 
-/* y[T][M] = x[T][K] . W[expert]^T for one expert (fp32 accumulation). */
+/* y[T][M] = x[T][K] . W[expert]^T for one expert (fp32 accumulation); x bf16. */
 int lutmoe_gemv(const lutmoe_weights* w, int expert, const void* x_dev, int T,
                 void* y_dev, int y_dtype, void* stream);
+
+/* lutmoe_gemv with the activations' dtype given: x_dtype LUTMOE_DTYPE_BF16 or
+ * LUTMOE_DTYPE_F32 (BL4 and REF weights; fp32 x: each weight widened to fp32
+ * and multiplied by an fp32 FMA, REF in lut_gemv's (x * cb) * absmax order --
+ * the reference's CPU dequant + F.linear on fp32 inputs,
+ * vllm_lut/quantizer.py:449-477).  NestedLUT takes bf16 x only
+ * (LUTMOE_EUNSUPPORTED). */
+int lutmoe_gemv_ex(const lutmoe_weights* w, int expert, const void* x_dev, int x_dtype, int T,
+                   void* y_dev, int y_dtype, void* stream);
 
 /* BL4 repack: fp16 codebook entries -> bf16 dequantised entries. */
 int lutmoe_bl4_tables_from_f16(const uint16_t* f16_dev, uint16_t* bf16_dev, int64_t n,

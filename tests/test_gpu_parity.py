@@ -186,6 +186,27 @@ def test_bl4_gemv_c1_shape(gpu, T):
     assert rel_maxabs(y, ref) <= TOL
 
 
+@pytest.mark.parametrize("fmt,T", [("bl4", 1), ("bl4", 3), ("ref", 1), ("ref", 2)])
+def test_gemv_fp32_activations(gpu, fmt, T):
+    """The switch-base-8 single linear at its configured precision: W [3072, 768] from
+    N(0, 0.02) fp32, one (or a few) fp32 N(0, 1) activation rows, fp32 output; BL4 weights
+    are the bf16 table entries, REF ones lut_gemv's unrounded cb * absmax products.  The
+    fp32 path must see the activations' low mantissa bits: the same rows rounded to bf16
+    give a clearly different result."""
+    import torch
+    from block_lut_amd import ops
+    es = (BL4Expertset(1, 3072, 768, seed=0, n_iter=10) if fmt == "bl4" else RefExpertset(1, 3072, 768, seed=0))
+    st = es.stack(gpu)
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((T, 768)).astype(np.float32)
+    y = ops.gemv(st, torch.from_numpy(x).to(gpu), 0, out_dtype=torch.float32).cpu().numpy()
+    wf = (es.deq_f32 if fmt == "bl4" else es.gemv_f32)(0).astype(np.float64)
+    ref = x.astype(np.float64) @ wf.T
+    assert rel_maxabs(y, ref) <= 1e-5
+    ref_b = O.bf16_to_f32(O.f32_to_bf16(x)).astype(np.float64) @ wf.T
+    assert rel_maxabs(ref_b, ref) > 20 * rel_maxabs(y, ref)
+
+
 # ------------------------------------------------------------ NestedLUT
 
 def test_nested_dequant_bitexact(gpu):
