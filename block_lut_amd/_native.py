@@ -71,6 +71,10 @@ class lutmoe_moe_desc(ctypes.Structure):
         ("num_routed", ctypes.c_int32),
         ("num_shared", ctypes.c_int32),
         ("shared_gate", ctypes.c_void_p),
+        ("dense_inter", ctypes.c_int32),
+        ("dense_reserved", ctypes.c_int32),
+        ("dense_w13", ctypes.c_void_p),
+        ("dense_w2", ctypes.c_void_p),
     ]
 
 

@@ -77,7 +77,7 @@ int validate_ref_vector(const lutmoe_weights* w) {
 size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct MoeLayout {
-    size_t route, topk_w, topk_ids, pair_ids, pair_w, offsets, perm, inv, active, act, y, total;
+    size_t route, topk_w, topk_ids, pair_ids, pair_w, offsets, perm, inv, active, act, y, dact, dy, dw, total;
 };
 
 // Room for two K-split partial results of the down projection when that is
@@ -100,6 +100,11 @@ MoeLayout moe_layout(const lutmoe_moe_desc* d, int T, int k) {
     L.active = o;   o = align_up(o + (E_tot + 1) * 4);
     L.act = o;      o = align_up(o + P * d->inter * 2);
     L.y = o;        o = align_up(o + P * d->hidden * 4 * prefill_y_splits(P, d->hidden));
+    // the dense shared expert: its activations, its weighted rows, token weights
+    const size_t Is = d->dense_inter > 0 ? (size_t)d->dense_inter : 0;
+    L.dact = o;     o = align_up(o + (Is ? (size_t)T * Is * 2 : 0));
+    L.dy = o;       o = align_up(o + (Is ? (size_t)T * d->hidden * 4 : 0));
+    L.dw = o;       o = align_up(o + (Is ? (size_t)T * 4 : 0));
     L.total = o;
     return L;
 }
@@ -119,6 +124,13 @@ int validate_moe(const lutmoe_moe_desc* d) {
     if (d->w13.format != d->w2.format) return LUTMOE_EUNSUPPORTED;
     if (H % 64 || I % 64) return LUTMOE_EUNSUPPORTED;
     if (d->shared_gate && !aligned(d->shared_gate, 16)) return LUTMOE_EALIGN;
+    if (d->dense_inter < 0 || d->dense_reserved != 0) return LUTMOE_EINVAL;
+    if (d->dense_inter > 0) {
+        if (!d->dense_w13 || !d->dense_w2) return LUTMOE_EINVAL;
+        if (d->dense_inter % 64) return LUTMOE_EUNSUPPORTED;
+        if (!aligned(d->dense_w13, 16) || !aligned(d->dense_w2, 16)) return LUTMOE_EALIGN;
+        if ((int64_t)2 * d->dense_inter * H >= (1ll << 31)) return LUTMOE_EUNSUPPORTED;
+    }
     if (d->w13.format == LUTMOE_FMT_REF) {
         if ((rc = validate_ref_vector(&d->w13)) || (rc = validate_ref_vector(&d->w2))) return rc;
     }
@@ -415,10 +427,22 @@ int moe_forward_impl(const lutmoe_moe_desc* d, const void* x, const float* topk_
     char* ws = (char*)workspace;
     uint16_t* act = (uint16_t*)(ws + L.act);
     hipStream_t s = stream_of(stream);
+    // the dense shared expert: gate/up with the gate/up stage, its weighted
+    // rows with the down stage, before the kernels that write the output
+    // (which add them)
+    const bool dense = d->dense_inter > 0;
+    const float* addend = dense ? (const float*)(ws + L.dy) : nullptr;
+    if (dense && (stages & LUTMOE_STAGE_GATE_UP) &&
+        (rc = launch_dense_gate_up(d, (const uint16_t*)x, T, !gemv, (uint16_t*)(ws + L.dact), (float*)(ws + L.dw), s)))
+        return rc;
+    if (dense && (stages & LUTMOE_STAGE_DOWN) &&
+        (rc = launch_dense_down(d, (const uint16_t*)(ws + L.dact), T, !gemv, (const float*)(ws + L.dw),
+                                (float*)(ws + L.dy), s)))
+        return rc;
     if (gemv) {
         // routing + permutation happen inside both decode kernels
         return launch_decode_v2(d, (const uint16_t*)x, topk_w, topk_ids, logits, T, k, renorm,
-                                scaling, act, ws + L.route, (float*)(ws + L.y), out, out_dtype, stages, s);
+                                scaling, act, ws + L.route, (float*)(ws + L.y), out, out_dtype, stages, s, addend);
     }
     int32_t* pair_ids = (int32_t*)(ws + L.pair_ids);
     float* pair_w = (float*)(ws + L.pair_w);
@@ -455,7 +479,8 @@ int moe_forward_impl(const lutmoe_moe_desc* d, const void* x, const float* topk_
         int nsplit = 1;
         if ((rc = launch_prefill_down(d, act, r, y, (int)P, (int)prefill_y_splits(P, d->hidden), &nsplit, s)))
             return rc;
-        return launch_combine(y, r.inv, T, ke, d->hidden, out, out_dtype, s, nsplit, (int64_t)P * d->hidden);
+        return launch_combine(y, r.inv, T, ke, d->hidden, out, out_dtype, s, nsplit, (int64_t)P * d->hidden,
+                              addend);
     }
     return LUTMOE_OK;
 }

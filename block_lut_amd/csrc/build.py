@@ -18,7 +18,7 @@ PKG = os.path.dirname(HERE)
 ROOT = os.path.dirname(PKG)
 LIB = os.path.join(PKG, "liblutmoe.so")
 SOURCES = ["api.cpp", "dequant.hip", "gemv.hip", "decode.hip", "route.hip", "gemm.hip",
-           "encode.hip", "noalloc.hip"]
+           "encode.hip", "noalloc.hip", "dense.hip"]
 ARCH = "gfx950"
 
 

@@ -103,7 +103,15 @@ struct DecodeArgs {
     void* out;
     int out_dtype;
     RouteOut* route;           // global copy (precomputed-routing mode)
+    const float* addend;       // NULL or fp32 [T][H]: the dense shared expert's rows
 };
+
+// out[o] = sum (+ addend[o]), one rounding to the output dtype (o = t * H + h).
+__device__ __forceinline__ void store_out(const DecodeArgs& A, int64_t o, float sum) {
+    if (A.addend) sum += A.addend[o];
+    if (A.out_dtype == LUTMOE_DTYPE_F32) ((float*)A.out)[o] = sum;
+    else ((uint16_t*)A.out)[o] = (uint16_t)f32_to_bf16(sum);
+}
 
 // Routing + permutation of all T*(k+S) pairs into LDS; identical in every CTA
 // that runs it.  Cross-lane work is readlane/DPP only (no LDS round trips in
@@ -1497,8 +1505,7 @@ __device__ __forceinline__ void down_body(const DecodeArgs& A, const RV& rv, uin
         }
         if (idx < T * kRows && h0 + r < H) {
             const int64_t o = (int64_t)t * H + h0 + r;
-            if (A.out_dtype == LUTMOE_DTYPE_F32) ((float*)A.out)[o] = sum;
-            else ((uint16_t*)A.out)[o] = (uint16_t)f32_to_bf16(sum);
+            store_out(A, o, sum);
         }
     }
 }
@@ -1544,8 +1551,7 @@ __device__ __forceinline__ void down_body4(const DecodeArgs& A, const RV& rv, ui
         }
         if (idx < T * 4 && h0 + r < H) {
             const int64_t o = (int64_t)t * H + h0 + r;
-            if (A.out_dtype == LUTMOE_DTYPE_F32) ((float*)A.out)[o] = sum;
-            else ((uint16_t*)A.out)[o] = (uint16_t)f32_to_bf16(sum);
+            store_out(A, o, sum);
         }
     }
 }
@@ -1657,8 +1663,7 @@ __global__ __launch_bounds__(256, 2) void bl4_decode_down1(DecodeArgs A) {
         }
         if (lane < kD1Rows * (TB == 1 ? 1 : A.T)) {
             const int64_t o = TB == 1 ? h0 + lane : (int64_t)(lane / kD1Rows) * H + h0 + lane % kD1Rows;
-            if (A.out_dtype == LUTMOE_DTYPE_F32) ((float*)A.out)[o] = sum;
-            else ((uint16_t*)A.out)[o] = (uint16_t)f32_to_bf16(sum);
+            store_out(A, o, sum);
         }
     }
 }
@@ -1766,8 +1771,7 @@ __global__ __launch_bounds__(256, 2) void ref_decode_down1(DecodeArgs A) {
         }
         if (lane < kD1Rows) {
             const int64_t o = h0 + lane;
-            if (A.out_dtype == LUTMOE_DTYPE_F32) ((float*)A.out)[o] = sum;
-            else ((uint16_t*)A.out)[o] = (uint16_t)f32_to_bf16(sum);
+            store_out(A, o, sum);
         }
     }
 }
@@ -2044,8 +2048,9 @@ int launch_decode_stream_probe(const lutmoe_moe_desc* d, const int32_t* ids, int
 int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* topk_w,
                      const int32_t* topk_ids, const float* logits, int T, int k, int renorm,
                      float scaling, uint16_t* act, void* route_ws, float* y_ws, void* out,
-                     int out_dtype, int stages, hipStream_t s) {
-    DecodeArgs A;
+                     int out_dtype, int stages, hipStream_t s, const float* addend) {
+    DecodeArgs A{};
+    A.addend = addend;
     A.d = *d;
     A.x = x;
     A.topk_w = topk_w;
@@ -2133,7 +2138,7 @@ int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* t
 #undef LUTMOE_DOWN_Y
             if ((rc = check_launch())) return rc;
             const int32_t* inv = ((const RouteOut*)route_ws)->inv;
-            return launch_combine(y_ws, inv, T, k + d->num_shared, d->hidden, out, out_dtype, s);
+            return launch_combine(y_ws, inv, T, k + d->num_shared, d->hidden, out, out_dtype, s, 1, 0, addend);
         }
         if (fmt_idx == 0 && (tb == 1 || (tb == 2 && T == 2)) && T * (k + d->num_shared) <= 16 * tb) {
             // one or two tokens, BL4: 4 output rows a CTA, one slot a wave, the

@@ -64,10 +64,19 @@ void set_last_error_text(const char* text);
 // decode.hip (BL4 decode layer, routing recomputed inside each CTA)
 bool decode_v2_supported(const lutmoe_moe_desc* d, int T, int k);
 size_t decode_route_bytes();
+// addend: NULL or fp32 [T][H] added to each output before its rounding
 int launch_decode_v2(const lutmoe_moe_desc* d, const uint16_t* x, const float* topk_w,
                      const int32_t* topk_ids, const float* logits, int T, int k, int renorm,
                      float scaling, uint16_t* act, void* route_ws, float* y_ws, void* out,
-                     int out_dtype, int stages, hipStream_t s);
+                     int out_dtype, int stages, hipStream_t s, const float* addend = nullptr);
+
+// dense.hip: a dense bf16 shared expert (d->dense_inter > 0).  gate_up:
+// tokw[t] = the shared weight of token t, act [T][Is] bf16; down: y [T][H]
+// fp32 = tokw[t] * (act[t] . W2s^T).  mfma: the MFMA tiles, else GEMVs.
+int launch_dense_gate_up(const lutmoe_moe_desc* d, const uint16_t* x, int T, bool mfma, uint16_t* act,
+                         float* tokw, hipStream_t s);
+int launch_dense_down(const lutmoe_moe_desc* d, const uint16_t* act, int T, bool mfma, const float* tokw, float* y,
+                      hipStream_t s);
 
 // decode.hip: the one-token layer's weight loads alone (HBM floor measurement)
 size_t decode_stream_probe_ctas(const lutmoe_moe_desc* d, int ns, int which);
@@ -95,8 +104,10 @@ int launch_router_logits(const uint16_t* x, const uint16_t* gate, int T, int H, 
                          int round_bf16, hipStream_t s);
 // nsplit > 1: y_pos holds nsplit partial results (K splits of the down
 // projection), split_stride floats apart, summed per position first.
+// addend: NULL or fp32 [T][H] added to each token's sum before the rounding.
 int launch_combine(const float* y_pos, const int32_t* inv, int T, int k_eff, int H,
-                   void* out, int out_dtype, hipStream_t s, int nsplit = 1, int64_t split_stride = 0);
+                   void* out, int out_dtype, hipStream_t s, int nsplit = 1, int64_t split_stride = 0,
+                   const float* addend = nullptr);
 
 // gemm.hip (prefill, MFMA)
 int launch_prefill_gate_up(const lutmoe_moe_desc* d, const uint16_t* x, const MoeRouting& r,

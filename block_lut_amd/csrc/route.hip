@@ -364,7 +364,8 @@ __global__ __launch_bounds__(1024) void permute_chunk_kernel(PairSrc ps, int P, 
 // sstride, added in split order.
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ y, const int32_t* __restrict__ inv,
                                                       int T, int ke, int H, void* __restrict__ out,
-                                                      int out_dtype, int nsplit, int64_t sstride) {
+                                                      int out_dtype, int nsplit, int64_t sstride,
+                                                      const float* __restrict__ addend) {
     const int hq = H / 4;
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= (int64_t)T * hq) return;
@@ -379,6 +380,10 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
             v.x += u.x; v.y += u.y; v.z += u.z; v.w += u.w;
         }
         s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
+    }
+    if (addend) {
+        const float4 a = *reinterpret_cast<const float4*>(addend + (int64_t)t * H + h);
+        s.x += a.x; s.y += a.y; s.z += a.z; s.w += a.w;
     }
     if (out_dtype == LUTMOE_DTYPE_F32) {
         *reinterpret_cast<float4*>((float*)out + (int64_t)t * H + h) = s;
@@ -459,10 +464,11 @@ int launch_route_pairs(const int32_t* topk_ids, const float* topk_w, int T, int 
 }
 
 int launch_combine(const float* y_pos, const int32_t* inv, int T, int k_eff, int H, void* out,
-                   int out_dtype, hipStream_t s, int nsplit, int64_t split_stride) {
+                   int out_dtype, hipStream_t s, int nsplit, int64_t split_stride,
+                   const float* addend) {
     const int64_t n = (int64_t)T * (H / 4);
     hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, y_pos,
-                       inv, T, k_eff, H, out, out_dtype, nsplit, split_stride);
+                       inv, T, k_eff, H, out, out_dtype, nsplit, split_stride, addend);
     return check_launch();
 }
 

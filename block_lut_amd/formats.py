@@ -220,7 +220,12 @@ class MoEWeights:
     ``split_shared_ref`` cut its matrices).  Shared slots weigh 1 (DeepSeek's shared
     experts, customized/deepseek.py:111-115) or, with ``shared_gate`` (bf16 [H], the
     weight of Qwen's shared_expert_gate Linear(H, 1)), sigmoid(x . shared_gate) per token
-    (customized/qwen.py:42-43, 99-100)."""
+    (customized/qwen.py:42-43, 99-100).
+
+    ``dense_shared`` = (w13 bf16 [2*Is, H], w2 bf16 [H, Is]): a shared expert kept in dense
+    bf16, as the reference keeps a model's shared experts (bf16 linears beside the LUT
+    experts, vllm_lut/moe_layer.py:186-200, 348-353; customized/qwen.py:40-43, 96-100):
+    every token adds its MLP output, weighted by 1 or by ``shared_gate``'s sigmoid."""
 
     w13: WeightStack
     w2: WeightStack
@@ -229,6 +234,7 @@ class MoEWeights:
     num_routed: int
     num_shared: int = 0
     shared_gate: Optional[torch.Tensor] = None
+    dense_shared: Optional[tuple] = None
     _desc: Optional[N.lutmoe_moe_desc] = field(default=None, repr=False)
 
     def __post_init__(self):
@@ -243,9 +249,20 @@ class MoEWeights:
             g = _dev(self.shared_gate, torch.bfloat16, "shared_gate")
             if g.numel() != self.hidden:
                 raise ValueError(f"shared_gate must hold {self.hidden} values (hidden size)")
-            if self.num_shared == 0:
-                raise ValueError("shared_gate given but the layer has no shared expert slots")
+            if self.num_shared == 0 and self.dense_shared is None:
+                raise ValueError("shared_gate given but the layer has no shared expert")
             self.shared_gate = g.reshape(-1)
+        if self.dense_shared is not None:
+            w13s, w2s = self.dense_shared
+            _dev(w13s, torch.bfloat16, "dense_shared w13")
+            _dev(w2s, torch.bfloat16, "dense_shared w2")
+            if w13s.dim() != 2 or w13s.shape[1] != self.hidden or w13s.shape[0] % 2:
+                raise ValueError("dense_shared w13 must be [2*Is, H]")
+            Is = w13s.shape[0] // 2
+            if Is % 64:
+                raise ValueError("the dense shared expert's intermediate size must be a multiple of 64")
+            if tuple(w2s.shape) != (self.hidden, Is):
+                raise ValueError(f"dense_shared w2 must be [{self.hidden}, {Is}]")
 
     def desc(self) -> N.lutmoe_moe_desc:
         if self._desc is None:
@@ -255,6 +272,10 @@ class MoEWeights:
             d.hidden, d.inter = self.hidden, self.inter
             d.num_routed, d.num_shared = self.num_routed, self.num_shared
             d.shared_gate = None if self.shared_gate is None else self.shared_gate.data_ptr()
+            if self.dense_shared is not None:
+                d.dense_inter = self.dense_shared[0].shape[0] // 2
+                d.dense_w13 = self.dense_shared[0].data_ptr()
+                d.dense_w2 = self.dense_shared[1].data_ptr()
             self._desc = d
         return self._desc
 

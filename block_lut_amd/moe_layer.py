@@ -7,7 +7,10 @@ LUTMoEExpertWrapper  one expert's LUT weights; get_weight dequantises to bf16
 LUTMoELayer     router -> fused LUT MoE -> + always-on shared experts
                 (customized/deepseek.py:111-115), or Qwen's shared expert with
                 its sigmoid gate (customized/qwen.py:99-100) through
-                MoEWeights.shared_gate.  Router: the hand-written gate kernel
+                MoEWeights.shared_gate; shared experts LUT-quantised as extra
+                slots of the stacks, or kept in dense bf16 as the reference
+                keeps them (vllm_lut/moe_layer.py:186-200, 348-353) through
+                MoEWeights.dense_shared, summed in the same layer call.  Router: the hand-written gate kernel
                 (lutmoe_router_logits) for decode batches, torch's GEMM above.
                 router_dtype=bfloat16 (default) is the reference's vLLM layer
                 (vllm_lut/moe_layer.py:301-304, 358-376): bf16 gate logits, top-k
@@ -59,8 +62,8 @@ class LUTMoEExpertWrapper(nn.Module):
 
 
 class LUTMoELayer(nn.Module):
-    """Router + LUT-quantised routed experts (+ shared experts as extra
-    always-on slots of the same stacks)."""
+    """Router + LUT-quantised routed experts (+ shared experts: extra always-on
+    slots of the same stacks, and/or MoEWeights.dense_shared in bf16)."""
 
     ROUTER_KERNEL_MAX_T = 64   # decode batches: the gate kernel; larger: torch's GEMM
 

@@ -97,6 +97,20 @@ typedef struct lutmoe_moe_desc {
     int32_t num_routed;        /* E                                             */
     int32_t num_shared;        /* S                                             */
     const void* shared_gate;   /* bf16 [H] (device) or NULL                     */
+    /* Optional dense bf16 shared expert, as the reference keeps a model's
+     * shared experts (bf16 linears beside the LUT experts,
+     * vllm_lut/moe_layer.py:186-200, 348-353; customized/qwen.py:40-43,
+     * 96-100): dense_inter = its intermediate size Is (0 = none; Is % 64 ==
+     * 0), dense_w13 bf16 [2 Is][H] (gate rows [0, Is), up rows [Is, 2 Is)),
+     * dense_w2 bf16 [H][Is], both row-major and 16-byte aligned.  Every token
+     * adds w * W2s . bf16(silu(Wg x) * (Wu x)) with w = 1, or
+     * sigmoid(x . shared_gate) when shared_gate is set (it then weighs the
+     * LUT shared slots too), to its sum of expert outputs before the one
+     * rounding of the result.  Decode runs it as bf16 GEMVs, prefill on MFMA. */
+    int32_t dense_inter;
+    int32_t dense_reserved;    /* 0 */
+    const void* dense_w13;
+    const void* dense_w2;
 } lutmoe_moe_desc;
 
 /* ---- library ---------------------------------------------------------- */

@@ -252,3 +252,41 @@ def test_decompress_wrappers(gpu):
     short = am[:10]
     assert np.array_equal(bf16_bits(decompress_blocklut(di, to_dev_bf16(short, gpu), dc, 128)),
                           O.ref_dequant(idx, short, cb, 128))
+
+
+@pytest.mark.parametrize("router_dtype,T", [("bf16", 1), ("f32", 6), ("bf16", 80)])
+def test_lut_moe_layer_dense_shared_expert(gpu, router_dtype, T):
+    """LUTMoELayer over LUT routed experts and a shared expert kept in dense bf16 with
+    Qwen's sigmoid gate (the layout of the reference's Qwen2MoE block: bf16 shared MLP and
+    gate beside the LUT experts, customized/qwen.py:40-43, 96-100), bf16 output against the
+    oracle within one bf16 ulp of its rounding plus the bar."""
+    import torch
+    from block_lut_amd.formats import MoEWeights
+    from block_lut_amd.moe_layer import LUTMoELayer
+    from test_gpu_parity import _sigmoid_gate, dense_shared_weights
+    E, k, H, I, Is = 8, 2, 512, 256, 512
+    w13 = BL4Expertset(E, 2 * I, H, seed=541 + T, n_iter=8)
+    w2 = BL4Expertset(E, H, I, seed=542 + T, n_iter=8)
+    d13, d2, h13, h2 = dense_shared_weights(gpu, Is, H, 543 + T)
+    rng = np.random.default_rng(540 + T)
+    gate = O.f32_to_bf16((rng.standard_normal(H) * 0.05).astype(np.float32))
+    moe = MoEWeights(w13.stack(gpu), w2.stack(gpu), H, I, E, 0, dense_shared=(d13, d2),
+                     shared_gate=to_dev_bf16(gate, gpu))
+    gb = O.f32_to_bf16((rng.standard_normal((E, H)) * 0.05).astype(np.float32))
+    dt = torch.bfloat16 if router_dtype == "bf16" else torch.float32
+    layer = LUTMoELayer(moe, to_dev_bf16(gb, gpu), k, router_dtype=dt)
+    xb = _x(rng, T, H)
+    out = layer(to_dev_bf16(xb, gpu))
+    lg = O.bf16_to_f32(xb).astype(np.float64) @ O.bf16_to_f32(gb).astype(np.float64).T
+    if router_dtype == "bf16":
+        lg = O.bf16_to_f32(O.f32_to_bf16(lg.astype(np.float32)))
+    srt = np.sort(lg, axis=1)[:, ::-1]
+    gap = srt[:, k - 1] - srt[:, k]
+    clear = gap > (4 * 2.0 ** -7 * np.abs(srt[:, k - 1]) + 1e-6 if router_dtype == "bf16" else 1e-4)
+    rw, rids = O.route(lg.astype(np.float32), k)
+    if router_dtype == "bf16":
+        rw = O.bf16_to_f32(O.f32_to_bf16(rw))
+    ref = O.moe_layer(xb, rids, rw, w13.deq_f32, w2.deq_f32, shared=[(h13, h2)], shared_w=_sigmoid_gate(xb, gate))
+    got = O.bf16_to_f32(bf16_bits(out))
+    assert clear.any()
+    assert rel_excess_bf16(got[clear], ref[clear]) <= TOL

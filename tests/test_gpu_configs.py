@@ -106,3 +106,37 @@ def test_config_nested_tiers_qwen(gpu, T):
     assert counts.max() >= 2 * counts[counts > 0].mean()   # the routing is skewed
     ref = O.moe_layer(xb, rids, rw, w13.host, w2.host, blas_dtype=np.float32)
     assert rel_maxabs(out, ref) <= TOL
+
+
+@pytest.mark.parametrize("model,T", [("deepseek", 1), ("deepseek", 2048), ("qwen", 1), ("qwen", 8),
+                                     ("qwen", 1024)])
+def test_config_dense_shared_expert(gpu, model, T):
+    """The model shapes with their shared experts kept in dense bf16, as the reference keeps
+    them (vllm_lut/moe_layer.py:186-200, 348-353): DeepSeek-V2-Lite's two shared experts
+    as one 2816-wide bf16 MLP of weight 1 beside 64 routed BL4 experts top-6; Qwen1.5-MoE's
+    5632-wide shared expert with its sigmoid(x . g) gate beside 60 routed experts top-4.
+    Decode and prefill sizes, every token checked."""
+    import torch
+    from block_lut_amd import ops
+    from block_lut_amd.formats import MoEWeights
+    from test_gpu_parity import _sigmoid_gate, dense_shared_weights
+    H, I = 2048, 1408
+    E, k, Is = (64, 6, 2816) if model == "deepseek" else (60, 4, 5632)
+    g = torch.Generator(device=gpu).manual_seed(77 + T)
+    w13 = DevBL4(E, 2 * I, H, g, gpu)
+    w2 = DevBL4(E, H, I, g, gpu)
+    d13, d2, h13, h2 = dense_shared_weights(gpu, Is, H, 78)
+    rng = np.random.default_rng(79 + T)
+    gate = O.f32_to_bf16((rng.standard_normal(H) * 0.05).astype(np.float32)) if model == "qwen" else None
+    moe = MoEWeights(w13.stack, w2.stack, H, I, E, 0, dense_shared=(d13, d2),
+                     shared_gate=None if gate is None else to_dev_bf16(gate, gpu))
+    xb = _x(rng, T, H)
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    out = ops.moe_forward_logits(moe, to_dev_bf16(xb, gpu), torch.from_numpy(lg).to(gpu), k,
+                                 out_dtype=torch.float32).cpu().numpy()
+    assert np.isfinite(out).all()
+    rw, rids = O.route(lg, k)
+    sw = None if gate is None else _sigmoid_gate(xb, gate)
+    ref = O.moe_layer(xb, rids, rw, w13.host, w2.host, shared=[(h13, h2)], shared_w=sw,
+                      blas_dtype=np.float32)
+    assert rel_maxabs(out, ref) <= TOL

@@ -1368,3 +1368,59 @@ def test_moe_layer_paths_agree(gpu):
     a = ops.moe_forward(*args, out_dtype=torch.float32, path=1).cpu().numpy()
     b = ops.moe_forward(*args, out_dtype=torch.float32, path=2).cpu().numpy()
     assert rel_maxabs(a, b) <= TOL
+
+
+# ------------------------------------------------ dense bf16 shared expert
+
+def dense_shared_weights(gpu, Is, H, seed):
+    """A dense bf16 shared expert (N(0, 0.02) on the device) and its float32 host copy."""
+    import torch
+    g = torch.Generator(device=gpu).manual_seed(seed)
+    w13 = (torch.randn((2 * Is, H), generator=g, device=gpu) * 0.02).to(torch.bfloat16)
+    w2 = (torch.randn((H, Is), generator=g, device=gpu) * 0.02).to(torch.bfloat16)
+
+    def host(t):
+        return O.bf16_to_f32(t.view(torch.int16).cpu().numpy().view(np.uint16))
+    return w13, w2, host(w13), host(w2)
+
+
+@pytest.mark.parametrize("T,path,gated,logits", [(1, 1, False, True), (1, 1, True, False), (3, 1, True, True),
+                                                 (9, 1, False, False), (32, 1, True, False), (5, 2, True, False),
+                                                 (300, 2, False, True)])
+def test_moe_layer_dense_shared_expert(gpu, T, path, gated, logits):
+    """A shared expert kept in dense bf16 beside the LUT experts (and a LUT shared slot):
+    every token adds w * W2s . bf16(silu(Wg x) * (Wu x)), w = 1 or sigmoid(x . g) (which
+    then weighs the LUT shared slot too), against the oracle, on the GEMV (decode) and MFMA
+    (prefill) paths; the stages run one by one give the one-call result bit for bit."""
+    import torch
+    from block_lut_amd import _native as N
+    from block_lut_amd import ops
+    from block_lut_amd.formats import MoEWeights
+    E, S, k, H, I, Is = 8, 1, 2, 512, 320, 640
+    w13, w2 = _moe_case("bl4", E, S, H, I, seed=600 + T)
+    d13, d2, h13, h2 = dense_shared_weights(gpu, Is, H, 601 + T)
+    rng = np.random.default_rng(602 + T)
+    gate = O.f32_to_bf16((rng.standard_normal(H) * 0.05).astype(np.float32)) if gated else None
+    moe = MoEWeights(w13.stack(gpu), w2.stack(gpu), H, I, E, S, dense_shared=(d13, d2),
+                     shared_gate=None if gate is None else to_dev_bf16(gate, gpu))
+    xb = _x(rng, T, H)
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    rw, rids = O.route(lg, k)
+    x = to_dev_bf16(xb, gpu)
+    if logits:
+        out = ops.moe_forward_logits(moe, x, torch.from_numpy(lg).to(gpu), k, out_dtype=torch.float32, path=path)
+    else:
+        args = (moe, x, torch.from_numpy(rw).to(gpu), torch.from_numpy(rids).to(gpu))
+        out = ops.moe_forward(*args, out_dtype=torch.float32, path=path)
+        ws = ops.new_workspace(moe, T, k, gpu)
+        staged = torch.empty_like(out)
+        ops.moe_forward(*args, out=staged, path=path, workspace=ws, stages=N.STAGE_ROUTE | N.STAGE_GATE_UP)
+        ops.moe_forward(*args, out=staged, path=path, workspace=ws, stages=N.STAGE_DOWN)
+        assert torch.equal(out, staged)
+    sw = _sigmoid_gate(xb, gate) if gated else None
+    shared = [(w13.deq_f32(E + s), w2.deq_f32(E + s)) for s in range(S)] + [(h13, h2)]
+    ref = O.moe_layer(xb, rids, rw, w13.deq_f32, w2.deq_f32, shared=shared, shared_w=sw)
+    assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
+    # the dense expert moves the result well past the bar: dropping it fails
+    ref_wo = O.moe_layer(xb, rids, rw, w13.deq_f32, w2.deq_f32, shared=shared[:S], shared_w=sw)
+    assert rel_maxabs(ref_wo, ref) > 50 * TOL
