@@ -627,9 +627,11 @@ def moe_layer(x_bf16, ids, weights, w13_f32, w2_f32, shared=None, act_round_bf16
     shared experts (Qwen's sigmoid(x . g), customized/qwen.py:99-100).
     w2_f32 may return a subset of W2's rows (output columns): the result then has that
     many columns.
-    blas_dtype: the dtype of the two matrix products (float64 by default; float32 for
-    full-shape prefill checks, whose sums of at most a few thousand products carry a
-    relative error near 1e-6, far below the 1e-3 bar); results are accumulated in float64.
+    blas_dtype: the dtype of the down projection's product (float64 by default; float32 for
+    full-shape prefill checks: its sums of a few thousand products carry a relative error
+    near 1e-6, far below the 1e-3 bar).  The gate/up product stays float64 whatever
+    blas_dtype is: its result is rounded to bf16, and a float32 sum flips enough of those
+    roundings to move the output by about 3e-4 of its range.  Results accumulate in float64.
     Returns float64 [T, H] (or [T, rows of the W2 given])."""
     x = bf16_to_f32(x_bf16).astype(np.float64)
     ids = np.asarray(ids, np.int64)
@@ -637,10 +639,8 @@ def moe_layer(x_bf16, ids, weights, w13_f32, w2_f32, shared=None, act_round_bf16
     T = x.shape[0]
     out = None
 
-    xb = x.astype(blas_dtype)
-
     def expert(rows, W13, W2):
-        gu = xb[rows] @ W13.astype(blas_dtype, copy=False).T
+        gu = x[rows] @ W13.astype(np.float64).T
         I = W13.shape[0] // 2
         a = silu_mul_f32(gu[:, :I].astype(np.float32), gu[:, I:].astype(np.float32))
         if act_round_bf16:

@@ -6,7 +6,7 @@ Weights are random stacks in their wire formats (tests/gpu_weights.py); the orac
 dequantises them on the host from the codes.  Every token row of every output is
 checked (Mixtral: every token on 384 sampled output columns, which keeps the host
 copy of its down projection small); the prefill-sized oracles run their matrix
-products in float32 host BLAS (relative error near 1e-6).  Bar as in
+down projections in float32 host BLAS (relative error near 1e-6; the gate/up products, rounded to bf16, stay float64).  Bar as in
 test_gpu_parity.py: max|y - y_ref| / max|y_ref| <= 1e-3, fp32 output.
 """
 import numpy as np
