@@ -421,124 +421,218 @@ __device__ __forceinline__ u32x4_t lookup8_ref_combine(const Lookup8& l, float a
     return r;
 }
 
-template <bool kGateUp, int kFmt, int NMT>
-__device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, const uint16_t* __restrict__ src,
-                                                  const MoeRouting& rt, void* __restrict__ dst,
-                                                  const TileInfo ti, uint8_t* ring) {
-    constexpr bool kNested = kFmt == LUTMOE_FMT_NESTED;
-    constexpr bool kRef = kFmt == LUTMOE_FMT_REF;
-    constexpr int kCodesB = RingSlot<kFmt>::kCodes, kSlot = RingSlot<kFmt>::kBytes;
-    constexpr int kNC = kRef ? 4 : 2;   // code registers (u32x4) per lane per K step
-    // ring loads per thread per stage: the tile's NMT activation loads (only
-    // its NMT*32 rows are loaded) and the weight loads
-    constexpr int kDma = NMT + (kRef ? 5 : 4);
-    const lutmoe_weights& w = d.w13;
-    const lutmoe_weights& w2 = d.w2;
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int I = d.inter, H = d.hidden;
-    const int K = kGateUp ? H : I;
-    // K steps [kb0, kb0 + nkb) of this CTA: all of K, or split z of gridDim.z
-    // (down projection only; partial results go to separate y buffers)
-    const int nsplit = kGateUp ? 1 : (int)gridDim.z, zs = kGateUp ? 0 : (int)blockIdx.z;
-    const int kb0 = (K / kBK) * zs / nsplit;
-    const int nkb = (K / kBK) * (zs + 1) / nsplit - kb0;
-    const int n0 = blockIdx.x * (kGateUp ? kBN / 2 : kBN);
-    const int nvalid = min(kBM, ti.n - ti.m0);
-    // down projection: the routing weight of tile row tid, loaded now (two
-    // dependent loads) so that the K loop hides them; the epilogue reads it
-    // from LDS
-    float pw_row = 0.f;
-    if constexpr (!kGateUp) {
-        if (tid < nvalid) pw_row = rt.pair_w[rt.perm[ti.p0 + ti.m0 + tid]];
-    }
+// ---------------------------------------------------------------------------
+// Persistent ring kernel: one CTA per CU walks the tile items -- tile rows in
+// find_tile's order (experts from the last id down, the tail split), the
+// weight-row blocks x of a row consecutive, K splits z outermost -- in snake
+// order: round r takes item r*G + c for even r and r*G + G-1-c for odd r (G
+// CTAs), so the CTA that drew a heavy item in one round draws a light one in
+// the next.  Every wave finds its tiles itself from an LDS copy of the expert
+// offsets (no barrier).  When a tile's K loop ends the ring is free: the next
+// tile's first stages are issued at once and land while this tile's epilogue
+// stores its results straight from the accumulators (no LDS staging).
+struct RingTile {
+    int e, m0, p0, n;   // positions [p0 + m0, p0 + min(n, m0 + 256)) of expert e; e < 0: none
+    int x, z;           // weight-row block, K split
+};
 
-    // ---- loader side (all offsets 32-bit, from scalar bases; the host
-    // checks the sizes).  The tile's first NMT*32 activation rows are
-    // loaded: load j of wave w covers rows 8*NMT*w + 8j .. +7, lane l reads
-    // the (l%8 ^ swz)-th 16 bytes of row 8*NMT*w + 8j + l/8.  Rows past the
-    // tile's positions repeat its last position (never read back).
-    const int wvu = __builtin_amdgcn_readfirstlane(wv);
-    uint32_t a_off[NMT];
-#pragma unroll
-    for (int j = 0; j < NMT; ++j) {
-        const int r = 8 * NMT * wv + 8 * j + (lane >> 3);
-        const int pos = ti.p0 + ti.m0 + min(r, nvalid - 1);
-        const uint32_t row = kGateUp ? (uint32_t)(rt.perm[pos] / rt.k_eff) * (uint32_t)H : (uint32_t)pos * (uint32_t)I;
-        a_off[j] = 2u * (row + 8u * (uint32_t)((lane & 7) ^ a_swz(r)));
+__device__ __forceinline__ int ring_nmt(const RingTile& t) { return (min(kBM, t.n - t.m0) + 31) / 32; }
+
+// The item list of one launch: `rows` tile rows (ttot whole rows, the last
+// `split` of them cut into 128-position halves) x nx weight-row blocks x ns
+// K splits.
+struct TileWalk {
+    const int* off;   // expert offsets (LDS)
+    int et, ttot, split, rows, nx, ns, nitems;
+};
+
+__device__ __forceinline__ TileWalk tile_walk(const int* off, int et, int nx, int ns, int ncu) {
+    const int lane = threadIdx.x & 63;
+    int ttot = 0;
+    for (int c0 = 0; c0 < et; c0 += 64) {
+        const int e = c0 + lane;
+        const int n = e < et ? off[e + 1] - off[e] : 0;
+        ttot += __builtin_amdgcn_readlane(wave_scan_incl((n + kBM - 1) / kBM), 63);
     }
-    // weight row of tile row tr (gate/up: rows 0..127 gate, 128..255 up)
-    auto tile_row = [&](int tr) __attribute__((always_inline)) {
-        if (kGateUp) {
-            const int i = min(n0 + (tr & 127), I - 1);
-            return tr < 128 ? i : I + i;
+    TileWalk w;
+    w.off = off;
+    w.et = et;
+    w.ttot = ttot;
+    w.nx = nx;
+    w.ns = ns;
+    w.split = tail_split_rows(ttot, nx, ncu);
+    w.rows = ttot + w.split;
+    w.nitems = w.rows * nx * ns;
+    return w;
+}
+
+// Item -> tile, by the calling wave alone (uniform result).
+__device__ __forceinline__ RingTile walk_item(const TileWalk& w, int item) {
+    RingTile t{-1, 0, 0, 0, 0, 0};
+    if (item >= w.nitems) return t;
+    t.x = item % w.nx;
+    const int yz = item / w.nx;
+    const int j = yz % w.rows;
+    t.z = yz / w.rows;
+    const int lane = threadIdx.x & 63;
+    const int s0 = w.ttot - w.split;   // first split row
+    int row = j, half = -1;
+    if (j >= s0) {
+        row = s0 + (j - s0) / 2;
+        half = (j - s0) & 1;
+    }
+    int base = 0;   // tile rows of the experts in earlier chunks
+    for (int c0 = 0; c0 < w.et; c0 += 64) {
+        const int e = w.et - 1 - (c0 + lane);
+        int p0 = 0, n = 0;
+        if (e >= 0) {
+            p0 = w.off[e];
+            n = w.off[e + 1] - p0;
         }
-        return min(n0 + tr, H - 1);
-    };
-    const lutmoe_weights& ww = kGateUp ? w : w2;
-    const uint8_t* a_base = (const uint8_t*)src;
-    // BL4 codes / tables: load h of wave w covers tile rows 64w+32h .. +31,
-    // two lanes per row (16 B each), so a row's 32 bytes land contiguous in
-    // LDS.  NestedLUT tier b: a row's K step is 8b code bytes (its two
-    // 32-weight groups) and 2^(b+1) table bytes, both contiguous in HBM:
-    //   codes  b=4: as BL4 (LDS row stride 32, groups at 0 and 16); b=3: as
-    //          BL4 with the second lane reading bytes 8..23, so the groups
-    //          land at 0 and 20 of the 32-byte LDS row and nothing past the
-    //          row's bytes is read; b=2: load 0 covers rows 64w .. +63, one
-    //          lane (16 B) per row (LDS row stride 16), load 1 repeats it
-    //   tables b=4: as BL4; b=3: load 0 covers rows 64w .. +63, one lane
-    //          (16 B) per row, load 1 repeats it; b=2: as BL4 with 4-byte
-    //          loads (LDS row stride 2^(b+1))
-    // so every tier issues four weight loads per stage.
+        const int nt = (n + kBM - 1) / kBM;
+        const int incl = wave_scan_incl(nt);
+        const int excl = incl - nt;
+        const uint64_t hit = __ballot(e >= 0 && row >= base + excl && row < base + incl);
+        if (hit) {
+            const int src = (int)__builtin_ctzll(hit);
+            int m0 = (row - base - excl) * kBM, nn = n;
+            if (half >= 0) {
+                m0 += half * (kBM / 2);
+                nn = min(n, m0 + kBM / 2);
+            }
+            t.e = __builtin_amdgcn_readlane(e, src);
+            t.m0 = __builtin_amdgcn_readlane(m0, src);
+            t.p0 = __builtin_amdgcn_readlane(p0, src);
+            t.n = __builtin_amdgcn_readlane(nn, src);
+            if (t.m0 >= t.n) t.e = -1;   // an empty half
+            return t;
+        }
+        base += __builtin_amdgcn_readlane(incl, 63);
+    }
+    return t;
+}
+
+// K steps [kb0, kb0 + nkb) of a tile: all of K, or split z of ns (down
+// projection only; partial results go to separate y buffers).
+__device__ __forceinline__ void ring_k_range(int K, int z, int ns, int& kb0, int& nkb) {
+    kb0 = (K / kBK) * z / ns;
+    nkb = (K / kBK) * (z + 1) / ns - kb0;
+}
+
+// Loader side of one tile (all offsets 32-bit, from scalar bases; the host
+// checks the sizes).  The tile's first nmt*32 activation rows are loaded:
+// load j of wave w covers rows 8*nmt*w + 8j .. +7, lane l reads the
+// (l%8 ^ swz)-th 16 bytes of row 8*nmt*w + 8j + l/8.  Rows past the tile's
+// positions repeat its last position (never read back).
+//
+// BL4 codes / tables: load h of wave w covers tile rows 64w+32h .. +31, two
+// lanes per row (16 B each), so a row's 32 bytes land contiguous in LDS.
+// NestedLUT tier b: a row's K step is 8b code bytes (its two 32-weight
+// groups) and 2^(b+1) table bytes, both contiguous in HBM:
+//   codes  b=4: as BL4 (LDS row stride 32, groups at 0 and 16); b=3: as
+//          BL4 with the second lane reading bytes 8..23, so the groups land
+//          at 0 and 20 of the 32-byte LDS row and nothing past the row's
+//          bytes is read; b=2: load 0 covers rows 64w .. +63, one lane
+//          (16 B) per row (LDS row stride 16), load 1 repeats it
+//   tables b=4: as BL4; b=3: load 0 covers rows 64w .. +63, one lane (16 B)
+//          per row, load 1 repeats it; b=2: as BL4 with 4-byte loads (LDS
+//          row stride 2^(b+1))
+// so every tier issues four weight loads per stage.  REF: codes 256 rows x
+// 64 B (load h of wave w covers tile rows 64w+16h .. +15, four lanes per
+// row) and one absmax dword per row (lane l of wave w fetches the aligned
+// dword holding row 64w+l's entry for the step).
+template <bool kGateUp, int kFmt>
+struct RingLoader {
+    static constexpr bool kNested = kFmt == LUTMOE_FMT_NESTED;
+    static constexpr bool kRef = kFmt == LUTMOE_FMT_REF;
+    static constexpr int kCodesB = RingSlot<kFmt>::kCodes;
+    const uint8_t* a_base;
     const uint8_t* c_base;
     const uint8_t* t_base;
+    uint32_t a_off[8];
     uint32_t w_off[kRef || kNested ? 4 : 2];
-    uint32_t c_step = 32, t_step = 32;
-    int bits = 4;
-    // REF: absmax block of K step kb of weight row r = min((r*K/64 + kb) / q, nb - 1)
-    // with q = block_size / 64 (whole 64-column steps per block, checked on the host)
-    const uint32_t q = kRef ? (uint32_t)(ww.block_size / 64) : 1u;
-    const uint32_t nb = kRef ? (uint32_t)ww.absmax_per_expert : 1u;
-    uint32_t am_row64 = 0;   // the absmax DMA lane's weight row * K/64
-    if constexpr (kRef) {
-        c_base = uniform_ptr((const uint8_t*)ww.codes + (int64_t)ti.e * ww.rows * ww.cols);
-        t_base = uniform_ptr((const uint8_t*)((const uint16_t*)ww.tables + (int64_t)ti.e * ww.absmax_per_expert));
-        // codes: load h of wave w covers tile rows 64w+16h .. +15, four lanes
-        // (16 B each) per row, so a row's 64 bytes land contiguous in LDS;
-        // absmax: lane l of wave w fetches the aligned dword holding row
-        // 64w+l's entry
+    uint32_t c_step, t_step;
+    uint32_t q, nb, am_row64;   // REF: absmax block of step kb of row r = min((r*K/64 + kb) / q, nb - 1)
+    int bits, wvu, nmt;
+
+    __device__ __forceinline__ void init(const lutmoe_moe_desc& d, const uint16_t* src, const MoeRouting& rt,
+                                         const RingTile& ti, int nmt_) {
+        int tid;
+        asm volatile("v_mov_b32 %0, %1" : "=v"(tid) : "v"((int)threadIdx.x));
+        const int lane = tid & 63, wv = tid >> 6;
+        const int I = d.inter, H = d.hidden;
+        const int K = kGateUp ? H : I;
+        const int n0 = ti.x * (kGateUp ? kBN / 2 : kBN);
+        const int nvalid = min(kBM, ti.n - ti.m0);
+        const lutmoe_weights& ww = kGateUp ? d.w13 : d.w2;
+        nmt = nmt_;
+        wvu = __builtin_amdgcn_readfirstlane(wv);
+        a_base = (const uint8_t*)src;
+        // (gate/up: every row's pair index is loaded, also past nmt, and all
+        // loads are issued before the first use, so that they overlap)
+        int pr[8];
 #pragma unroll
-        for (int h = 0; h < 4; ++h)
-            w_off[h] = (uint32_t)tile_row(64 * wv + 16 * h + (lane >> 2)) * (uint32_t)K + 16u * (uint32_t)(lane & 3);
-        am_row64 = (uint32_t)tile_row(64 * wv + lane) * (uint32_t)(K / 64);
-    } else if constexpr (kNested) {
-        c_base = uniform_ptr(((const uint8_t* const*)ww.codes)[ti.e]);
-        t_base = uniform_ptr((const uint8_t*)((const uint16_t* const*)ww.tables)[ti.e]);
-        bits = __builtin_amdgcn_readfirstlane((int)ww.tier_bits[ti.e]);
-        c_step = 8u * (uint32_t)bits;     // code bytes of a row's K step
-        t_step = 2u << bits;              // table bytes of a row's K step
-        const uint32_t kq = (uint32_t)(K / 64);
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const uint32_t pr = (uint32_t)tile_row(64 * wv + 32 * h + (lane >> 1)) * kq;   // lane pairs
-            const uint32_t sr = (uint32_t)tile_row(64 * wv + lane) * kq;                   // one lane per row
-            w_off[h] = bits == 2 ? sr * 16u : pr * c_step + (uint32_t)(lane & 1) * (bits == 4 ? 16u : 8u);
-            w_off[2 + h] = bits == 3 ? sr * 16u : pr * t_step + (uint32_t)(lane & 1) * (t_step / 2u);
+        for (int j = 0; j < 8; ++j) {
+            const int r = 8 * nmt * wv + 8 * j + (lane >> 3);
+            pr[j] = ti.p0 + ti.m0 + min(r, nvalid - 1);
+            if constexpr (kGateUp) pr[j] = rt.perm[pr[j]];
         }
-    } else {
-        const int64_t per = (int64_t)ww.rows * (ww.cols / 2);
-        c_base = uniform_ptr((const uint8_t*)ww.codes + ti.e * per);
-        t_base = uniform_ptr((const uint8_t*)ww.tables + ti.e * per);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
-            w_off[h] = (uint32_t)tile_row(64 * wv + 32 * h + (lane >> 1)) * (uint32_t)(K / 2) +
-                       16u * (uint32_t)(lane & 1);
+        for (int j = 0; j < 8; ++j) {
+            const int r = 8 * nmt * wv + 8 * j + (lane >> 3);
+            const uint32_t row =
+                kGateUp ? (uint32_t)(pr[j] / rt.k_eff) * (uint32_t)H : (uint32_t)pr[j] * (uint32_t)I;
+            a_off[j] = 2u * (row + 8u * (uint32_t)((lane & 7) ^ a_swz(r)));
+        }
+        // weight row of tile row tr (gate/up: rows 0..127 gate, 128..255 up)
+        auto tile_row = [&](int tr) __attribute__((always_inline)) {
+            if (kGateUp) {
+                const int i = min(n0 + (tr & 127), I - 1);
+                return tr < 128 ? i : I + i;
+            }
+            return min(n0 + tr, H - 1);
+        };
+        c_step = 32;
+        t_step = 32;
+        bits = 4;
+        q = kRef ? (uint32_t)(ww.block_size / 64) : 1u;
+        nb = kRef ? (uint32_t)ww.absmax_per_expert : 1u;
+        am_row64 = 0;
+        if constexpr (kRef) {
+            c_base = uniform_ptr((const uint8_t*)ww.codes + (int64_t)ti.e * ww.rows * ww.cols);
+            t_base = uniform_ptr((const uint8_t*)((const uint16_t*)ww.tables + (int64_t)ti.e * ww.absmax_per_expert));
+#pragma unroll
+            for (int h = 0; h < 4; ++h)
+                w_off[h] = (uint32_t)tile_row(64 * wv + 16 * h + (lane >> 2)) * (uint32_t)K + 16u * (uint32_t)(lane & 3);
+            am_row64 = (uint32_t)tile_row(64 * wv + lane) * (uint32_t)(K / 64);
+        } else if constexpr (kNested) {
+            c_base = uniform_ptr(((const uint8_t* const*)ww.codes)[ti.e]);
+            t_base = uniform_ptr((const uint8_t*)((const uint16_t* const*)ww.tables)[ti.e]);
+            bits = __builtin_amdgcn_readfirstlane((int)ww.tier_bits[ti.e]);
+            c_step = 8u * (uint32_t)bits;     // code bytes of a row's K step
+            t_step = 2u << bits;              // table bytes of a row's K step
+            const uint32_t kq = (uint32_t)(K / 64);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t pr = (uint32_t)tile_row(64 * wv + 32 * h + (lane >> 1)) * kq;   // lane pairs
+                const uint32_t sr = (uint32_t)tile_row(64 * wv + lane) * kq;                   // one lane per row
+                w_off[h] = bits == 2 ? sr * 16u : pr * c_step + (uint32_t)(lane & 1) * (bits == 4 ? 16u : 8u);
+                w_off[2 + h] = bits == 3 ? sr * 16u : pr * t_step + (uint32_t)(lane & 1) * (t_step / 2u);
+            }
+        } else {
+            const int64_t per = (int64_t)ww.rows * (ww.cols / 2);
+            c_base = uniform_ptr((const uint8_t*)ww.codes + ti.e * per);
+            t_base = uniform_ptr((const uint8_t*)ww.tables + ti.e * per);
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                w_off[h] = (uint32_t)tile_row(64 * wv + 32 * h + (lane >> 1)) * (uint32_t)(K / 2) +
+                           16u * (uint32_t)(lane & 1);
+        }
     }
 
-    auto issue = [&](int kb, const uint8_t* sl) __attribute__((always_inline)) {
-        const uint32_t l0 = lds_addr(sl);
-        const uint8_t* ab = a_base + kb * (kBK * 2);
-#pragma unroll
-        for (int j = 0; j < NMT; ++j) dma16(a_off[j], ab, l0 + (8 * NMT * wvu + 8 * j) * 128);
+    // the weight loads of step kb into the slot at LDS address l0
+    __device__ __forceinline__ void issue_w(int kb, uint32_t l0) const {
         if constexpr (kRef) {
             const uint8_t* cb = c_base + kb * 64;
 #pragma unroll
@@ -579,12 +673,102 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
                 dma16(w_off[h], tbp, l0 + kSlotA + kCodesB + wvu * 2048 + h * 1024);
             }
         }
-    };
+    }
+    // stage kb into slot sl, NMT activation loads (NMT == nmt)
+    template <int NMT>
+    __device__ __forceinline__ void issue(int kb, const uint8_t* sl) const {
+        const uint32_t l0 = lds_addr(sl);
+        const uint8_t* ab = a_base + kb * (kBK * 2);
+#pragma unroll
+        for (int j = 0; j < NMT; ++j) dma16(a_off[j], ab, l0 + (8 * NMT * wvu + 8 * j) * 128);
+        issue_w(kb, l0);
+    }
+    // the same with the tile's activation-load count known at run time
+    __device__ __forceinline__ void issue_rt(int kb, const uint8_t* sl) const {
+        const uint32_t l0 = lds_addr(sl);
+        const uint8_t* ab = a_base + kb * (kBK * 2);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (j < nmt) dma16(a_off[j], ab, l0 + (8 * nmt * wvu + 8 * j) * 128);
+        issue_w(kb, l0);
+    }
+};
+
+// A tile's first stages into the ring (and REF's fp32 codebook after them);
+// the ring and the codebook must no longer be read.
+template <bool kGateUp, int kFmt>
+__device__ __forceinline__ void ring_prologue(const lutmoe_moe_desc& d, const uint16_t* src, const MoeRouting& rt,
+                                              const RingTile& t, int ns, uint8_t* ring) {
+    // REF: the expert's codebook entry of this thread, loaded beside the
+    // activation row indices (the compiler's wait for them then covers no
+    // ring load)
+    float cbv = 0.f;
+    if constexpr (kFmt == LUTMOE_FMT_REF) cbv = bf16_to_f32(ref_codebook(kGateUp ? d.w13 : d.w2, t.e)[threadIdx.x]);
+    RingLoader<kGateUp, kFmt> L;
+    L.init(d, src, rt, t, ring_nmt(t));
+    if constexpr (kFmt == LUTMOE_FMT_REF)
+        reinterpret_cast<float*>(ring + kStages * RingSlot<kFmt>::kBytes)[threadIdx.x] = cbv;
+    int kb0, nkb;
+    ring_k_range(kGateUp ? d.hidden : d.inter, t.z, ns, kb0, nkb);
+    const int npro = min(kStages, nkb);
+    for (int st = 0; st < npro; ++st) L.issue_rt(kb0 + st, ring + st * RingSlot<kFmt>::kBytes);
+}
+
+// One tile whose first stages are in the ring (issued by ring_prologue).
+// On return the next tile's first stages are issued (when there is one).
+template <bool kGateUp, int kFmt, int NMT>
+__device__ __forceinline__ void ring_tile_body(const lutmoe_moe_desc& d, const uint16_t* __restrict__ src,
+                                               const MoeRouting& rt, void* __restrict__ dst, const RingTile& ti,
+                                               const RingTile& next, uint8_t* ring, float* s_pw, int ns,
+                                               int64_t split_stride) {
+    constexpr bool kNested = kFmt == LUTMOE_FMT_NESTED;
+    constexpr bool kRef = kFmt == LUTMOE_FMT_REF;
+    constexpr int kCodesB = RingSlot<kFmt>::kCodes, kSlot = RingSlot<kFmt>::kBytes;
+    constexpr int kNC = kRef ? 4 : 2;   // code registers (u32x4) per lane per K step
+    // ring loads per thread per stage: the tile's NMT activation loads (only
+    // its NMT*32 rows are loaded) and the weight loads
+    constexpr int kDma = NMT + (kRef ? 5 : 4);
+    const lutmoe_weights& ww = kGateUp ? d.w13 : d.w2;
+    // the lane index through an opaque move, so that nothing derived from it
+    // is hoisted out of the persistent loop (and kept live across K loops)
+    int tid;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(tid) : "v"((int)threadIdx.x));
+    const int lane = tid & 63, wv = tid >> 6;
+    const int I = d.inter, H = d.hidden;
+    const int K = kGateUp ? H : I;
+    int kb0, nkb;
+    ring_k_range(K, ti.z, ns, kb0, nkb);
+    const int n0 = ti.x * (kGateUp ? kBN / 2 : kBN);
+    const int nvalid = min(kBM, ti.n - ti.m0);
+
+    // every stage issued so far landed (the previous tile's epilogue stores
+    // are done too), the REF codebook is written
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    RingLoader<kGateUp, kFmt> L;
+    L.init(d, src, rt, ti, NMT);
+    // down projection: tile row tid's routing weight, by its pair index
+    // (loaded now) in K step 0 (when that index is back), so that the K loop
+    // hides both loads
+    int pair = 0;
+    float pw_row = 0.f;
+    if constexpr (!kGateUp) {
+        if (tid < nvalid) pair = rt.perm[ti.p0 + ti.m0 + tid];
+    }
 
     // ---- compute side: lane (n = lane%32, h = lane/32), n-tiles 0/1
     const int bn = lane & 31, bh = lane >> 5;
     const int L0 = kGateUp ? 32 * wv + bn : 64 * wv + bn;
     const int L1 = kGateUp ? 128 + 32 * wv + bn : 64 * wv + 32 + bn;
+    const int bits = L.bits;
+    const uint32_t t_step = L.t_step;
+    const uint32_t q = L.q, nb = L.nb;
+    auto tile_row = [&](int tr) __attribute__((always_inline)) {
+        if (kGateUp) {
+            const int i = min(n0 + (tr & 127), I - 1);
+            return tr < 128 ? i : I + i;
+        }
+        return min(n0 + tr, H - 1);
+    };
 
     // BL4: codes[nt] = the lane's 16 code bytes of row Lnt.  NestedLUT:
     // codes[nt] = the lane half's 32-weight group: its 2-bit field words (.x,
@@ -600,9 +784,9 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
     if constexpr (kNested) {
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
-            const uint32_t L = (uint32_t)(nt ? L1 : L0);
-            c_grp[nt] = bits == 2 ? L * 16u + (uint32_t)bh * 8u : L * 32u + (uint32_t)bh * (bits == 4 ? 16u : 20u);
-            t_row[nt] = L * t_step;
+            const uint32_t Lr = (uint32_t)(nt ? L1 : L0);
+            c_grp[nt] = bits == 2 ? Lr * 16u + (uint32_t)bh * 8u : Lr * 32u + (uint32_t)bh * (bits == 4 ? 16u : 20u);
+            t_row[nt] = Lr * t_step;
         }
     }
     if constexpr (kRef) {
@@ -657,8 +841,6 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
         for (int mt = 0; mt < NMT; ++mt)
             if (mt >= mt0 && mt < mt1) af[mt] = *reinterpret_cast<const bf16x8_t*>(p + mt * 4096);
     };
-    // B fragment of k-substep ks: the lane's 8 codes looked up in its rows'
-    // LDS tables of slot `sl` (reads issued here, combined later)
     // B lookups of n-tile nt, k-substep ks (reads issued here, combined later)
     auto frag_b = [&](const uint8_t* sl, const u32x4_t (&codes)[kNC], int ks, int nt) __attribute__((always_inline)) {
         if constexpr (kRef) {
@@ -685,11 +867,7 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[mt][nt][i] = 0.f;
 
-    // prologue: stages 0..2 in flight; wait for stage 0, then issue the LDS
-    // reads of k-substep 0's fragments
-    const int npro = min(kStages, nkb);
-    for (int st = 0; st < npro; ++st) issue(kb0 + st, ring + st * kSlot);
-    ring_wait_barrier<kDma>(npro - 1);
+    // k-substep 0's fragment reads (every stage in the ring landed)
     u32x4_t codes[kNC];
     float am[2] = {0.f, 0.f};
     bf16x8_t bf[2], af[NMT];
@@ -703,7 +881,11 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
     // fragment, then its NMT MFMAs interleaved with the next substep's LDS
     // reads: that substep's n-tile-nt lookups and half of its A fragments,
     // one or two reads per MFMA, so the LDS queue drains while the MFMAs
-    // run and every read has a half-substep of MFMAs to land.
+    // run and every read has a half-substep of MFMAs to land.  Per step kb:
+    // k-substeps 0-2 run from slot kb%3; then a barrier (stage kb+1 landed
+    // everywhere, slot kb%3 no longer read), the refill of slot kb%3 with
+    // stage kb+3, and k-substep 3's MFMAs overlapped with reading and looking
+    // up step kb+1's operands.
     constexpr int kHalfA = (NMT + 1) / 2;
     int slot = 0;
     for (int kb = 0; kb < nkb; ++kb) {
@@ -725,7 +907,10 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
                 // in flight) and every read of this slot is done (its values
                 // are in registers) -> refill it with stage kb+3
                 ring_wait_barrier<kDma>(kb + 2 < nkb ? 1 : 0);
-                if (kb + 3 < nkb) issue(kb0 + kb + 3, sl);
+                if constexpr (!kGateUp) {
+                    if (kb == 0 && tid < nvalid) pw_row = rt.pair_w[pair];
+                }
+                if (kb + 3 < nkb) L.template issue<NMT>(kb0 + kb + 3, sl);
                 read_codes(nsl, codes_n);
                 read_am(nsl, kb0 + kb + 1, am_n);
                 frag_a(nsl, 0, af_n, 0, kHalfA);
@@ -770,93 +955,95 @@ __device__ __forceinline__ void prefill_tile_ring(const lutmoe_moe_desc& d, cons
         }
         slot = nslot;
     }
-    // ---- epilogue through LDS, so global stores are whole lines.  D layout:
-    // lane (n = lane%32, h = lane/32), element i -> row m = 8*(i/4) + 4*h +
-    // (i%4), column n.  All loads landed (none may still write LDS) and all
-    // ring reads done -> the ring is free.
+    // All loads landed (none may still write LDS) and all ring reads are
+    // done -> the ring is free; the rows' routing weights are in s_pw.
+    if constexpr (!kGateUp) s_pw[tid] = pw_row;
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (next.e >= 0) ring_prologue<kGateUp, kFmt>(d, src, rt, next, ns, ring);
+
+    // ---- epilogue, straight from the accumulators.  D layout: lane (n =
+    // lane%32, h = lane/32), element i -> row m = 8*(i/4) + 4*h + (i%4),
+    // column n: each store writes 32 consecutive columns of two rows.  The
+    // stores go through a buffer descriptor over the tile's rows, with 32-bit
+    // offsets; rows past the tile's positions fall outside it and are
+    // dropped.
     if constexpr (kGateUp) {
-        // act tile [256 positions][128 intermediate columns] bf16
-        uint16_t* st = reinterpret_cast<uint16_t*>(ring);
-        const int col = 32 * wv + bn;
+        // act[p][i] = bf16(silu(gate) * up)
+        const int ii = n0 + 32 * wv + bn;
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)((uint16_t*)dst + (int64_t)(ti.p0 + ti.m0) * I), 0, nvalid * I * 2, kBufWord3);
+        const uint32_t vo = (uint32_t)(4 * bh * I + ii) * 2u;
+        if (ii < I) {
+#pragma unroll
+            for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const uint32_t mrow = (uint32_t)(mt * 32 + 8 * (i >> 2) + (i & 3));
+                    __builtin_amdgcn_raw_buffer_store_b16(
+                        (uint16_t)f32_to_bf16(silu_mul(acc[mt][0][i], acc[mt][1][i])), rs,
+                        (int)(vo + mrow * (uint32_t)I * 2u), 0, 0);
+                }
+        }
+    } else {
+        // y[p][h] = acc * routing weight (fp32), K split z into its own y
+        const int h0 = n0 + 64 * wv + bn;
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)((float*)dst + ti.z * split_stride + (int64_t)(ti.p0 + ti.m0) * H), 0, nvalid * H * 4, kBufWord3);
+        const uint32_t vo = (uint32_t)(4 * bh * H + h0) * 4u;
 #pragma unroll
         for (int mt = 0; mt < NMT; ++mt)
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                const int m = mt * 32 + 8 * (i >> 2) + 4 * bh + (i & 3);
-                st[m * 128 + col] = (uint16_t)f32_to_bf16(silu_mul(acc[mt][0][i], acc[mt][1][i]));
+                const int mrow = mt * 32 + 8 * (i >> 2) + (i & 3);
+                const float pw = s_pw[min(mrow + 4 * bh, kBM - 1)];
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt)
+                    if (h0 + 32 * nt < H)
+                        __builtin_amdgcn_raw_buffer_store_b32(
+                            __float_as_uint(acc[mt][nt][i] * pw), rs,
+                            (int)(vo + (uint32_t)mrow * (uint32_t)H * 4u + 128u * (uint32_t)nt), 0, 0);
             }
-        __syncthreads();
-        const int chunk = tid & 15;
-        if (n0 + 8 * chunk < I) {
-            uint16_t* out = (uint16_t*)dst + (int64_t)(ti.p0 + ti.m0) * I + n0 + 8 * chunk;
-            for (int r = tid >> 4; r < nvalid; r += 16)
-                *reinterpret_cast<u32x4_t*>(out + (int64_t)r * I) =
-                    *reinterpret_cast<const u32x4_t*>(&st[r * 128 + 8 * chunk]);
-        }
-    } else {
-        // y_pos tile [256 positions][256 h] fp32 times the routing weight, in
-        // two halves of 128 positions (128 KB of LDS each); the rows' weights
-        // after them
-        float* st = reinterpret_cast<float*>(ring);
-        float* s_pw = reinterpret_cast<float*>(ring + 128 * 256 * 4);
-        static_assert(128 * 256 * 4 + kBM * 4 <= RingSlot<kFmt>::kLds, "epilogue LDS");
-        s_pw[tid] = pw_row;
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-            if (4 * hf < NMT) {
-                if (hf) __syncthreads();
-#pragma unroll
-                for (int mt = 4 * hf; mt < NMT && mt < 4 * hf + 4; ++mt)
-#pragma unroll
-                    for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-                        for (int i = 0; i < 16; ++i) {
-                            const int m = (mt - 4 * hf) * 32 + 8 * (i >> 2) + 4 * bh + (i & 3);
-                            st[m * 256 + 64 * wv + 32 * nt + bn] = acc[mt][nt][i];
-                        }
-                __syncthreads();
-                const int chunk = tid & 63;
-                if (n0 + 4 * chunk < H) {
-                    for (int r = tid >> 6; r < 128 && 128 * hf + r < nvalid; r += 4) {
-                        const int p = ti.p0 + ti.m0 + 128 * hf + r;
-                        const float pw = s_pw[128 * hf + r];
-                        float4 v = *reinterpret_cast<const float4*>(&st[r * 256 + 4 * chunk]);
-                        v.x *= pw;
-                        v.y *= pw;
-                        v.z *= pw;
-                        v.w *= pw;
-                        *reinterpret_cast<float4*>((float*)dst + (int64_t)p * H + n0 + 4 * chunk) = v;
-                    }
-                }
-            }
-        }
     }
 }
+
+constexpr int kOffLds = 1024;   // expert offsets held in LDS: E + S + 1 at most
 
 template <bool kGateUp, int kFmt>
 __global__ __launch_bounds__(256, 1) void prefill_ring_kernel(lutmoe_moe_desc d, const uint16_t* __restrict__ src,
                                                               MoeRouting rt, void* __restrict__ dst, int ncu,
-                                                              int64_t split_stride) {
+                                                              int nx, int ns, int64_t split_stride) {
     __shared__ __attribute__((aligned(16))) uint8_t ring[RingSlot<kFmt>::kLds];
-    const TileInfo ti = find_tile(rt, blockIdx.y, ncu);
-    if (ti.e < 0) return;
-    if (!kGateUp) dst = (float*)dst + blockIdx.z * split_stride;   // this K split's partial y
-    if constexpr (kFmt == LUTMOE_FMT_REF) {
-        // fp32 codebook after the stages (ordered before its first read by
-        // the prologue's barrier)
-        const uint16_t* cb = ref_codebook(kGateUp ? d.w13 : d.w2, ti.e);
-        reinterpret_cast<float*>(ring + kStages * RingSlot<kFmt>::kBytes)[threadIdx.x] = bf16_to_f32(cb[threadIdx.x]);
-    }
-    const int nmt = (min(kBM, ti.n - ti.m0) + 31) / 32;
-    switch (nmt) {
+    __shared__ int s_off[kOffLds];
+    __shared__ float s_pw[kBM];
+    const int et = rt.num_experts_total;   // et + 1 <= kOffLds (checked on the host)
+    for (int i = threadIdx.x; i <= et; i += blockDim.x) s_off[i] = rt.offsets[i];
+    __syncthreads();
+    const TileWalk w = tile_walk(s_off, et, nx, ns, ncu);
+    const int G = gridDim.x, c = blockIdx.x;
+    auto item_of = [&](int r) __attribute__((always_inline)) { return r * G + ((r & 1) ? G - 1 - c : c); };
+    // this CTA's first non-empty item
+    int r = 0;
+    RingTile cur = walk_item(w, item_of(0));
+    while (cur.e < 0 && item_of(r) < w.nitems) cur = walk_item(w, item_of(++r));
+    if (cur.e < 0) return;
+    ring_prologue<kGateUp, kFmt>(d, src, rt, cur, ns, ring);
+    for (;;) {
+        RingTile nxt;
+        do nxt = walk_item(w, item_of(++r));
+        while (nxt.e < 0 && item_of(r) < w.nitems);
+        switch (ring_nmt(cur)) {
 #define LUTMOE_TILE_CASE(n) \
-    case n: prefill_tile_ring<kGateUp, kFmt, n>(d, src, rt, dst, ti, ring); break;
-        LUTMOE_TILE_CASE(1) LUTMOE_TILE_CASE(2) LUTMOE_TILE_CASE(3) LUTMOE_TILE_CASE(4)
-        LUTMOE_TILE_CASE(5) LUTMOE_TILE_CASE(6) LUTMOE_TILE_CASE(7) LUTMOE_TILE_CASE(8)
+    case n: ring_tile_body<kGateUp, kFmt, n>(d, src, rt, dst, cur, nxt, ring, s_pw, ns, split_stride); break;
+            LUTMOE_TILE_CASE(1) LUTMOE_TILE_CASE(2) LUTMOE_TILE_CASE(3) LUTMOE_TILE_CASE(4)
+            LUTMOE_TILE_CASE(5) LUTMOE_TILE_CASE(6) LUTMOE_TILE_CASE(7) LUTMOE_TILE_CASE(8)
 #undef LUTMOE_TILE_CASE
-        default: break;
+            default: break;
+        }
+        if (nxt.e < 0) break;
+        cur = nxt;
     }
+    // no load may still write LDS when the CTA ends
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 template <bool kGateUp>
@@ -882,6 +1069,11 @@ __global__ __launch_bounds__(256, 1) void prefill_ref_kernel(lutmoe_moe_desc d, 
 inline int max_tiles(int P, int E_tot) { return (P + kBM - 1) / kBM + E_tot; }
 // extra grid rows for the tail split (find_tile cuts at most ncu / (2 nx) rows)
 inline int tail_rows_max(int nx, int ncu) { return ncu / (2 * nx) + 1; }
+// persistent ring grid: one CTA per compute unit, at most one per item
+inline int persistent_ctas(int ncu, int64_t items) {
+    const int64_t g = ncu > 0 ? ncu : 256;
+    return (int)(items < g ? (items > 0 ? items : 1) : g);
+}
 
 }  // namespace
 
@@ -904,6 +1096,7 @@ static int cu_count() {
 static bool ring_offsets_fit(const lutmoe_moe_desc* d, const MoeRouting& r, int P) {
     const int64_t lim = int64_t(1) << 32;
     if ((int64_t)r.T * d->hidden * 2 >= lim || (int64_t)P * d->inter * 2 >= lim) return false;
+    if (r.num_experts_total + 1 > kOffLds) return false;   // the offsets' LDS copy
     if (d->w13.format == LUTMOE_FMT_REF) {
         // one expert's codes and absmax by 32-bit offsets; absmax read as
         // aligned dwords (an even count per expert keeps them inside it)
@@ -914,6 +1107,7 @@ static bool ring_offsets_fit(const lutmoe_moe_desc* d, const MoeRouting& r, int 
         }
         return true;
     }
+    if (r.num_experts_total + 1 > kOffLds) return false;   // the offsets' LDS copy
     if (d->w13.format == LUTMOE_FMT_NESTED)
         return (int64_t)d->w13.rows * d->w13.cols < lim && (int64_t)d->w2.rows * d->w2.cols < lim;
     return (int64_t)d->w13.rows * (d->w13.cols / 2) < lim && (int64_t)d->w2.rows * (d->w2.cols / 2) < lim;
@@ -924,18 +1118,22 @@ int launch_prefill_gate_up(const lutmoe_moe_desc* d, const uint16_t* x, const Mo
     const bool ring = ring_offsets_fit(d, r, P);
     if (d->w13.format != LUTMOE_FMT_REF && !ring) return LUTMOE_EUNSUPPORTED;
     const int nx = (d->inter + kBN / 2 - 1) / (kBN / 2), ncu = cu_count();
-    const dim3 grid(nx, max_tiles(P, r.num_experts_total) + tail_rows_max(nx, ncu));
-    if (d->w13.format == LUTMOE_FMT_REF && ring)
-        hipLaunchKernelGGL((prefill_ring_kernel<true, LUTMOE_FMT_REF>), grid, dim3(256), 0, s, *d, x, r, (void*)act,
-                           ncu, (int64_t)0);
-    else if (d->w13.format == LUTMOE_FMT_REF)
+    const int rows = max_tiles(P, r.num_experts_total) + tail_rows_max(nx, ncu);
+    if (d->w13.format == LUTMOE_FMT_REF && !ring) {
+        const dim3 grid(nx, rows);
         hipLaunchKernelGGL((prefill_ref_kernel<true>), grid, dim3(256), 0, s, *d, x, r, (void*)act, ncu);
+        return check_launch();
+    }
+    const dim3 grid(persistent_ctas(ncu, (int64_t)rows * nx));
+    if (d->w13.format == LUTMOE_FMT_REF)
+        hipLaunchKernelGGL((prefill_ring_kernel<true, LUTMOE_FMT_REF>), grid, dim3(256), 0, s, *d, x, r, (void*)act,
+                           ncu, nx, 1, (int64_t)0);
     else if (d->w13.format == LUTMOE_FMT_NESTED)
         hipLaunchKernelGGL((prefill_ring_kernel<true, LUTMOE_FMT_NESTED>), grid, dim3(256), 0, s, *d, x, r,
-                           (void*)act, ncu, (int64_t)0);
+                           (void*)act, ncu, nx, 1, (int64_t)0);
     else
         hipLaunchKernelGGL((prefill_ring_kernel<true, LUTMOE_FMT_BL4>), grid, dim3(256), 0, s, *d, x, r, (void*)act,
-                           ncu, (int64_t)0);
+                           ncu, nx, 1, (int64_t)0);
     return check_launch();
 }
 
@@ -952,20 +1150,23 @@ int launch_prefill_down(const lutmoe_moe_desc* d, const uint16_t* act, const Moe
                            d->w2.cols / kBK >= 2 * kStages ? 2 : 1;
     *nsplit = ns;
     const int ncu_tail = ns > 1 ? 0 : ncu;   // one round: no tail split
-    const dim3 grid(nx, max_tiles(P, E_tot) + tail_rows_max(nx, ncu_tail), ns);
+    const int rows = max_tiles(P, E_tot) + tail_rows_max(nx, ncu_tail);
     const int64_t stride = (int64_t)P * d->hidden;
-    if (d->w2.format == LUTMOE_FMT_REF && ring)
+    if (d->w2.format == LUTMOE_FMT_REF && !ring) {
+        const dim3 grid(nx, rows, ns);
+        hipLaunchKernelGGL((prefill_ref_kernel<false>), grid, dim3(256), 0, s, *d, act, r, (void*)y_pos, ncu);
+        return check_launch();
+    }
+    const dim3 grid(persistent_ctas(ncu, (int64_t)rows * nx * ns));
+    if (d->w2.format == LUTMOE_FMT_REF)
         hipLaunchKernelGGL((prefill_ring_kernel<false, LUTMOE_FMT_REF>), grid, dim3(256), 0, s, *d, act, r,
-                           (void*)y_pos, ncu_tail, stride);
-    else if (d->w2.format == LUTMOE_FMT_REF)
-        hipLaunchKernelGGL((prefill_ref_kernel<false>), grid, dim3(256), 0, s, *d, act, r, (void*)y_pos,
-                           ncu);
+                           (void*)y_pos, ncu_tail, nx, ns, stride);
     else if (d->w2.format == LUTMOE_FMT_NESTED)
         hipLaunchKernelGGL((prefill_ring_kernel<false, LUTMOE_FMT_NESTED>), grid, dim3(256), 0, s, *d, act, r,
-                           (void*)y_pos, ncu_tail, stride);
+                           (void*)y_pos, ncu_tail, nx, ns, stride);
     else
         hipLaunchKernelGGL((prefill_ring_kernel<false, LUTMOE_FMT_BL4>), grid, dim3(256), 0, s, *d, act, r,
-                           (void*)y_pos, ncu_tail, stride);
+                           (void*)y_pos, ncu_tail, nx, ns, stride);
     return check_launch();
 }
 
