@@ -77,7 +77,7 @@ int validate_ref_vector(const lutmoe_weights* w) {
 size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct MoeLayout {
-    size_t route, topk_w, topk_ids, pair_ids, pair_w, offsets, perm, inv, active, act, y, dact, dy, dw, total;
+    size_t route, topk_w, topk_ids, pair_ids, pair_w, offsets, perm, inv, active, sched, act, y, dact, dy, dw, total;
 };
 
 // Room for two K-split partial results of the down projection when that is
@@ -98,6 +98,7 @@ MoeLayout moe_layout(const lutmoe_moe_desc* d, int T, int k) {
     L.perm = o;     o = align_up(o + P * 4);
     L.inv = o;      o = align_up(o + P * 4);
     L.active = o;   o = align_up(o + (E_tot + 1) * 4);
+    L.sched = o;    o = align_up(o + 4 * 4);
     L.act = o;      o = align_up(o + P * d->inter * 2);
     L.y = o;        o = align_up(o + P * d->hidden * 4 * prefill_y_splits(P, d->hidden));
     // the dense shared expert: its activations, its weighted rows, token weights
@@ -455,6 +456,7 @@ int moe_forward_impl(const lutmoe_moe_desc* d, const void* x, const float* topk_
     r.T = T;
     r.k_eff = ke;
     r.num_experts_total = E_tot;
+    r.sched = (int32_t*)(ws + L.sched);
     float* y = (float*)(ws + L.y);
     if (stages & LUTMOE_STAGE_ROUTE) {
         if (by_logits) {
@@ -465,7 +467,7 @@ int moe_forward_impl(const lutmoe_moe_desc* d, const void* x, const float* topk_
             topk_ids = ti;
         }
         if ((rc = launch_route_pairs(topk_ids, topk_w, T, k, E, S, (int32_t*)r.offsets, (int32_t*)r.perm,
-                                     (int32_t*)r.inv, (int32_t*)r.active, pair_ids, pair_w, s)))
+                                     (int32_t*)r.inv, (int32_t*)r.active, pair_ids, pair_w, s, r.sched)))
             return rc;
         if (d->shared_gate && S > 0 &&
             (rc = launch_shared_gate((const uint16_t*)x, (const uint16_t*)d->shared_gate, T, d->hidden, k, S,

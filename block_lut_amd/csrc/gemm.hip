@@ -422,21 +422,193 @@ __device__ __forceinline__ u32x4_t lookup8_ref_combine(const Lookup8& l, float a
 }
 
 // ---------------------------------------------------------------------------
-// Persistent ring kernel: one CTA per CU walks the tile items -- tile rows in
-// find_tile's order (experts from the last id down, the tail split), the
-// weight-row blocks x of a row consecutive, K splits z outermost -- in snake
-// order: round r takes item r*G + c for even r and r*G + G-1-c for odd r (G
-// CTAs), so the CTA that drew a heavy item in one round draws a light one in
-// the next.  Every wave finds its tiles itself from an LDS copy of the expert
-// offsets (no barrier).  When a tile's K loop ends the ring is free: the next
-// tile's first stages are issued at once and land while this tile's epilogue
-// stores its results straight from the accumulators (no LDS staging).
+// Persistent ring kernel: one CTA per CU takes tile items -- a tile row
+// (up to 256 positions of one expert) times one weight-row block x, times
+// one K split z -- from a counter shared by the launch, heaviest first, so
+// the CTA that finishes early takes the next item (greedy longest-first).
+// Every wave finds its items itself from LDS copies of the expert offsets
+// and tier widths (no barrier).  When a tile's K loop ends the ring is free:
+// the next tile's first stages are issued at once and land while this
+// tile's epilogue stores its results straight from the accumulators (no LDS
+// staging).
 struct RingTile {
     int e, m0, p0, n;   // positions [p0 + m0, p0 + min(n, m0 + 256)) of expert e; e < 0: none
     int x, z;           // weight-row block, K split
 };
 
 __device__ __forceinline__ int ring_nmt(const RingTile& t) { return (min(kBM, t.n - t.m0) + 31) / 32; }
+
+// A tile is the same in every lane; this says so to the compiler (whose
+// divergence analysis does not follow the wave-wide searches that found it),
+// so that the addresses derived from it stay scalar.
+__device__ __forceinline__ RingTile uniform_tile(const RingTile& t) {
+    return RingTile{__builtin_amdgcn_readfirstlane(t.e), __builtin_amdgcn_readfirstlane(t.m0),
+                    __builtin_amdgcn_readfirstlane(t.p0), __builtin_amdgcn_readfirstlane(t.n),
+                    __builtin_amdgcn_readfirstlane(t.x), __builtin_amdgcn_readfirstlane(t.z)};
+}
+
+// Tile classes in hand-out order: estimated cost descending.  A class is
+// (m-tiles, tier bits); a tile's time grows by about as much per m-tile as
+// per code bit (NestedLUT tiers), so the 24 NestedLUT classes are ordered by
+// m-tiles + bits, then m-tiles; the formats of one code width use the 8
+// classes m-tiles = 8 .. 1.
+constexpr int kMaxClasses = 24;
+
+__device__ __forceinline__ int tile_class(bool nested, int nmt, int bits) {
+    if (!nested) return 8 - nmt;
+    const int est = nmt + bits;   // 3 .. 12
+    // the classes of every larger estimate come first
+    int start = 0;
+    for (int v = 12; v > est; --v) start += min(8, v - 2) - max(1, v - 4) + 1;
+    return start + (min(8, est - 2) - nmt);
+}
+__device__ __forceinline__ void class_params(bool nested, int c, int& nmt, int& bits) {
+    if (!nested) {
+        nmt = 8 - c;
+        bits = 0;
+        return;
+    }
+    for (int v = 12; v >= 3; --v) {
+        const int hi = min(8, v - 2), lo = max(1, v - 4), k = hi - lo + 1;
+        if (c < k) {
+            nmt = hi - c;
+            bits = v - nmt;
+            return;
+        }
+        c -= k;
+    }
+    nmt = 1;
+    bits = 2;
+}
+
+// Tiles of expert e (n positions) in class (cn, cb): its whole 256-position
+// tiles and its last tile of fewer positions each fall in the class of
+// their m-tiles and the expert's tier.
+__device__ __forceinline__ int class_tiles(int n, int bits_e, bool nested, int cn, int cb) {
+    if (nested && bits_e != cb) return 0;
+    const int full = n >> 8, rn = ((n & (kBM - 1)) + 31) >> 5;
+    return cn == 8 ? full + (rn == 8 ? 1 : 0) : (rn == cn ? 1 : 0);
+}
+
+// The items of one launch: tile rows in class order, the last `split` of
+// them (the lightest) cut into two 128-position halves when they hold more
+// than 128 positions; nsub sub-rows x nx weight-row blocks x ns K splits.
+// Per class c (LDS, written once per CTA by wave 0): its first sub-row
+// sub0[c], its sub-rows nsubc[c], its whole rows before the split whole[c],
+// and (m-tiles | bits << 8) prm[c].
+struct ClassTable {
+    int sub0[kMaxClasses], nsubc[kMaxClasses], whole[kMaxClasses], prm[kMaxClasses];
+    int nsub;
+};
+
+__device__ __forceinline__ void class_table(ClassTable& t, const int* cls, bool nested, int nx, int ncu) {
+    if (threadIdx.x >= 64) return;
+    const int lane = threadIdx.x;
+    const int nc = nested ? kMaxClasses : 8;
+    int cn = 1, cb = 0, cnt = 0;
+    if (lane < nc) {
+        class_params(nested, lane, cn, cb);
+        cnt = cls[lane];
+    }
+    const int r_incl = wave_scan_incl(cnt);
+    const int ttot = __builtin_amdgcn_readlane(r_incl, 63);
+    const int s0 = ttot - tail_split_rows(ttot, nx, ncu);
+    const int a = min(max(s0 - (r_incl - cnt), 0), cnt);   // whole rows of the class
+    const int w = a + (cnt - a) * (cn > 4 ? 2 : 1);
+    const int w_incl = wave_scan_incl(w);
+    if (lane < nc) {
+        t.sub0[lane] = w_incl - w;
+        t.nsubc[lane] = w;
+        t.whole[lane] = a;
+        t.prm[lane] = cn | (cb << 8);
+    }
+    if (lane == 0) t.nsub = __builtin_amdgcn_readlane(w_incl, 63);
+}
+
+struct ItemMap {
+    const int* off;        // expert offsets (LDS)
+    const int8_t* bits;    // NestedLUT tier of each expert (LDS)
+    const ClassTable* ct;  // (LDS)
+    int et, nc, nsub, nx, ns, nitems;
+    bool nested;
+};
+
+__device__ __forceinline__ ItemMap item_map(const int* off, const int8_t* bits, const ClassTable* ct, int et,
+                                            bool nested, int nx, int ns) {
+    ItemMap m;
+    m.off = off;
+    m.bits = bits;
+    m.ct = ct;
+    m.et = et;
+    m.nested = nested;
+    m.nc = nested ? kMaxClasses : 8;
+    m.nx = nx;
+    m.ns = ns;
+    m.nsub = __builtin_amdgcn_readfirstlane(ct->nsub);
+    m.nitems = m.nsub * nx * ns;
+    return m;
+}
+
+// Item -> tile, by the calling wave alone (uniform result); e < 0 past the end.
+__device__ __forceinline__ RingTile map_item(const ItemMap& m, int item) {
+    RingTile t{-1, 0, 0, 0, 0, 0};
+    if (item >= m.nitems) return t;
+    t.x = item % m.nx;
+    int u = item / m.nx;
+    t.z = u / m.nsub;
+    u -= t.z * m.nsub;
+    const int lane = threadIdx.x & 63;
+    // the class holding sub-row u: lane c checks class c
+    int sub0 = 0, nsc = 0;
+    if (lane < m.nc) {
+        sub0 = m.ct->sub0[lane];
+        nsc = m.ct->nsubc[lane];
+    }
+    const uint64_t chit = __ballot(lane < m.nc && u >= sub0 && u < sub0 + nsc);
+    if (!chit) return t;
+    const int c = (int)__builtin_ctzll(chit);
+    const int uu = u - __builtin_amdgcn_readlane(sub0, c);
+    const int a = __builtin_amdgcn_readfirstlane(m.ct->whole[c]);
+    const int prm = __builtin_amdgcn_readfirstlane(m.ct->prm[c]);
+    const int cn = prm & 0xff, cb = prm >> 8;
+    const int sp = cn > 4 ? 2 : 1;
+    int r = uu, half = -1;
+    if (uu >= a) {
+        r = a + (uu - a) / sp;
+        if (sp == 2) half = (uu - a) & 1;
+    }
+    // the r-th tile of the class, experts from the last id down
+    int base = 0;
+    for (int c0 = 0; c0 < m.et; c0 += 64) {
+        const int e = m.et - 1 - (c0 + lane);
+        int p0 = 0, n = 0, k = 0;
+        if (e >= 0) {
+            p0 = m.off[e];
+            n = m.off[e + 1] - p0;
+            k = class_tiles(n, m.nested ? m.bits[e] : 0, m.nested, cn, cb);
+        }
+        const int incl = wave_scan_incl(k);
+        const int excl = incl - k;
+        const uint64_t hit = __ballot(k > 0 && r >= base + excl && r < base + incl);
+        if (hit) {
+            const int src = (int)__builtin_ctzll(hit);
+            const int q = r - base - excl;
+            int m0 = cn == 8 ? q * kBM : (n >> 8) * kBM;
+            int nn = cn == 8 ? min(n, m0 + kBM) : n;
+            if (half >= 0) {
+                m0 += half * (kBM / 2);
+                nn = min(nn, m0 + kBM / 2);
+            }
+            t.e = __builtin_amdgcn_readlane(e, src);
+            t.m0 = __builtin_amdgcn_readlane(m0, src);
+            t.p0 = __builtin_amdgcn_readlane(p0, src);
+            t.n = __builtin_amdgcn_readlane(nn, src);
+            return t;
+        }
+        base += __builtin_amdgcn_readlane(incl, 63);
+    }
+    return t;
+}
 
 // The item list of one launch: `rows` tile rows (ttot whole rows, the last
 // `split` of them cut into 128-position halves) x nx weight-row blocks x ns
@@ -715,12 +887,15 @@ __device__ __forceinline__ void ring_prologue(const lutmoe_moe_desc& d, const ui
 }
 
 // One tile whose first stages are in the ring (issued by ring_prologue).
-// On return the next tile's first stages are issued (when there is one).
-template <bool kGateUp, int kFmt, int NMT>
+// Thread 0 claims the next item from the launch's counter when the tile
+// starts (the returned index is published through s_claim in the last K
+// step, where every load has landed anyway); on return `next` is that item's
+// tile and its first stages are issued (when there is one).
+template <bool kGateUp, int kFmt, int NMT, typename NextFn>
 __device__ __forceinline__ void ring_tile_body(const lutmoe_moe_desc& d, const uint16_t* __restrict__ src,
                                                const MoeRouting& rt, void* __restrict__ dst, const RingTile& ti,
-                                               const RingTile& next, uint8_t* ring, float* s_pw, int ns,
-                                               int64_t split_stride) {
+                                               NextFn next_of, RingTile& next, int* ctr, int* s_claim,
+                                               uint8_t* ring, float* s_pw, int ns, int64_t split_stride) {
     constexpr bool kNested = kFmt == LUTMOE_FMT_NESTED;
     constexpr bool kRef = kFmt == LUTMOE_FMT_REF;
     constexpr int kCodesB = RingSlot<kFmt>::kCodes, kSlot = RingSlot<kFmt>::kBytes;
@@ -744,6 +919,8 @@ __device__ __forceinline__ void ring_tile_body(const lutmoe_moe_desc& d, const u
     // every stage issued so far landed (the previous tile's epilogue stores
     // are done too), the REF codebook is written
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    int claim = 0;
+    if (ctr && threadIdx.x == 0) claim = atomicAdd(ctr, 1);
     RingLoader<kGateUp, kFmt> L;
     L.init(d, src, rt, ti, NMT);
     // down projection: tile row tid's routing weight, by its pair index
@@ -910,6 +1087,7 @@ __device__ __forceinline__ void ring_tile_body(const lutmoe_moe_desc& d, const u
                 if constexpr (!kGateUp) {
                     if (kb == 0 && tid < nvalid) pw_row = rt.pair_w[pair];
                 }
+                if (kb == nkb - 1 && threadIdx.x == 0) *s_claim = claim;
                 if (kb + 3 < nkb) L.template issue<NMT>(kb0 + kb + 3, sl);
                 read_codes(nsl, codes_n);
                 read_am(nsl, kb0 + kb + 1, am_n);
@@ -959,6 +1137,7 @@ __device__ __forceinline__ void ring_tile_body(const lutmoe_moe_desc& d, const u
     // done -> the ring is free; the rows' routing weights are in s_pw.
     if constexpr (!kGateUp) s_pw[tid] = pw_row;
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    next = next_of(*s_claim);
     if (next.e >= 0) ring_prologue<kGateUp, kFmt>(d, src, rt, next, ns, ring);
 
     // ---- epilogue, straight from the accumulators.  D layout: lane (n =
@@ -1008,39 +1187,104 @@ __device__ __forceinline__ void ring_tile_body(const lutmoe_moe_desc& d, const u
 
 constexpr int kOffLds = 1024;   // expert offsets held in LDS: E + S + 1 at most
 
+// sched (gate/up): this launch's item counter and finished-CTA counter, zero
+// at launch (the routing zeroes them; the last CTA to finish zeroes them
+// again).
 template <bool kGateUp, int kFmt>
 __global__ __launch_bounds__(256, 1) void prefill_ring_kernel(lutmoe_moe_desc d, const uint16_t* __restrict__ src,
                                                               MoeRouting rt, void* __restrict__ dst, int ncu,
-                                                              int nx, int ns, int64_t split_stride) {
+                                                              int nx, int ns, int64_t split_stride, int* sched) {
+    constexpr bool kNested = kFmt == LUTMOE_FMT_NESTED;
     __shared__ __attribute__((aligned(16))) uint8_t ring[RingSlot<kFmt>::kLds];
     __shared__ int s_off[kOffLds];
+    __shared__ int8_t s_bits[kNested ? kOffLds : 1];
+    __shared__ int s_cls[kMaxClasses];
+    __shared__ ClassTable s_ct;
     __shared__ float s_pw[kBM];
+    __shared__ int s_claim;
     const int et = rt.num_experts_total;   // et + 1 <= kOffLds (checked on the host)
-    for (int i = threadIdx.x; i <= et; i += blockDim.x) s_off[i] = rt.offsets[i];
+    const int tid = threadIdx.x;
+    for (int i = tid; i <= et; i += blockDim.x) s_off[i] = rt.offsets[i];
+    if constexpr (kNested) {
+        const int8_t* tb = (kGateUp ? d.w13 : d.w2).tier_bits;
+        for (int i = tid; i < et; i += blockDim.x) s_bits[i] = tb[i];
+    }
+    if (tid < kMaxClasses) s_cls[tid] = 0;
     __syncthreads();
+    // tile rows per class (gate/up's item order)
+    for (int e = tid; kGateUp && e < et; e += blockDim.x) {
+        const int n = s_off[e + 1] - s_off[e];
+        const int full = n >> 8, rn = ((n & (kBM - 1)) + 31) >> 5;
+        const int b = kNested ? (int)s_bits[e] : 0;
+        if (full + (rn == 8 ? 1 : 0) > 0) atomicAdd(&s_cls[tile_class(kNested, 8, b)], full + (rn == 8 ? 1 : 0));
+        if (rn > 0 && rn < 8) atomicAdd(&s_cls[tile_class(kNested, rn, b)], 1);
+    }
+    __syncthreads();
+    class_table(s_ct, s_cls, kNested, nx, ncu);
+    __syncthreads();
+    const ItemMap im = item_map(s_off, s_bits, &s_ct, et, kNested, nx, ns);
     const TileWalk w = tile_walk(s_off, et, nx, ns, ncu);
     const int G = gridDim.x, c = blockIdx.x;
-    auto item_of = [&](int r) __attribute__((always_inline)) { return r * G + ((r & 1) ? G - 1 - c : c); };
-    // this CTA's first non-empty item
-    int r = 0;
-    RingTile cur = walk_item(w, item_of(0));
-    while (cur.e < 0 && item_of(r) < w.nitems) cur = walk_item(w, item_of(++r));
-    if (cur.e < 0) return;
-    ring_prologue<kGateUp, kFmt>(d, src, rt, cur, ns, ring);
-    for (;;) {
-        RingTile nxt;
-        do nxt = walk_item(w, item_of(++r));
-        while (nxt.e < 0 && item_of(r) < w.nitems);
-        switch (ring_nmt(cur)) {
-#define LUTMOE_TILE_CASE(n) \
-    case n: ring_tile_body<kGateUp, kFmt, n>(d, src, rt, dst, cur, nxt, ring, s_pw, ns, split_stride); break;
-            LUTMOE_TILE_CASE(1) LUTMOE_TILE_CASE(2) LUTMOE_TILE_CASE(3) LUTMOE_TILE_CASE(4)
-            LUTMOE_TILE_CASE(5) LUTMOE_TILE_CASE(6) LUTMOE_TILE_CASE(7) LUTMOE_TILE_CASE(8)
-#undef LUTMOE_TILE_CASE
-            default: break;
+    // Item order.  Gate/up with widely spread tile sizes (a quarter of the
+    // tile rows or more hold at most 128 positions, as under skewed routing):
+    // longest first from the counter, the first G items to the CTAs in
+    // order.  Otherwise (and always for the down projection) the snake order
+    // over the expert-ordered items, which keeps the heaviest tiles -- whose
+    // epilogues write the most -- spread over the launch.
+    bool dyn = false;
+    if constexpr (kGateUp) {
+        int small = 0, all = 0;
+        for (int k = 0; k < (kNested ? kMaxClasses : 8); ++k) {
+            int cn, cb;
+            class_params(kNested, k, cn, cb);
+            const int cnt = __builtin_amdgcn_readfirstlane(s_cls[k]);
+            all += cnt;
+            if (cn <= 4) small += cnt;
         }
-        if (nxt.e < 0) break;
-        cur = nxt;
+        dyn = __builtin_amdgcn_readfirstlane(4 * small >= all ? 1 : 0) != 0;
+    }
+    int* ctr = dyn ? sched : nullptr;
+    auto snake = [&](int r) __attribute__((always_inline)) { return r * G + ((r & 1) ? G - 1 - c : c); };
+    int r = 0;
+    auto next_of = [&](int v) __attribute__((always_inline)) {
+        if (dyn) return uniform_tile(map_item(im, G + __builtin_amdgcn_readfirstlane(v)));
+        RingTile t;
+        do t = walk_item(w, snake(++r));
+        while (t.e < 0 && snake(r) < w.nitems);
+        return uniform_tile(t);
+    };
+    RingTile cur;
+    if (dyn) {
+        cur = map_item(im, c);
+    } else {
+        cur = walk_item(w, snake(0));
+        while (cur.e < 0 && snake(r) < w.nitems) cur = walk_item(w, snake(++r));
+    }
+    cur = uniform_tile(cur);
+    if (cur.e >= 0) {
+        ring_prologue<kGateUp, kFmt>(d, src, rt, cur, ns, ring);
+        for (;;) {
+            RingTile nxt;
+            switch (ring_nmt(cur)) {
+#define LUTMOE_TILE_CASE(n)                                                                                      \
+    case n:                                                                                                      \
+        ring_tile_body<kGateUp, kFmt, n>(d, src, rt, dst, cur, next_of, nxt, ctr, &s_claim, ring, s_pw, ns,   \
+                                         split_stride);                                                          \
+        break;
+                LUTMOE_TILE_CASE(1) LUTMOE_TILE_CASE(2) LUTMOE_TILE_CASE(3) LUTMOE_TILE_CASE(4)
+                LUTMOE_TILE_CASE(5) LUTMOE_TILE_CASE(6) LUTMOE_TILE_CASE(7) LUTMOE_TILE_CASE(8)
+#undef LUTMOE_TILE_CASE
+                default: nxt.e = -1; break;
+            }
+            if (nxt.e < 0) break;
+            cur = nxt;
+        }
+    }
+    // every claim of this CTA has returned: count it finished; the last one
+    // zeroes both counters for the next launch
+    if (dyn && tid == 0 && atomicAdd(sched + 1, 1) == G - 1) {
+        atomicExch(sched, 0);
+        atomicExch(sched + 1, 0);
     }
     // no load may still write LDS when the CTA ends
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -1127,13 +1371,13 @@ int launch_prefill_gate_up(const lutmoe_moe_desc* d, const uint16_t* x, const Mo
     const dim3 grid(persistent_ctas(ncu, (int64_t)rows * nx));
     if (d->w13.format == LUTMOE_FMT_REF)
         hipLaunchKernelGGL((prefill_ring_kernel<true, LUTMOE_FMT_REF>), grid, dim3(256), 0, s, *d, x, r, (void*)act,
-                           ncu, nx, 1, (int64_t)0);
+                           ncu, nx, 1, (int64_t)0, r.sched);
     else if (d->w13.format == LUTMOE_FMT_NESTED)
         hipLaunchKernelGGL((prefill_ring_kernel<true, LUTMOE_FMT_NESTED>), grid, dim3(256), 0, s, *d, x, r,
-                           (void*)act, ncu, nx, 1, (int64_t)0);
+                           (void*)act, ncu, nx, 1, (int64_t)0, r.sched);
     else
         hipLaunchKernelGGL((prefill_ring_kernel<true, LUTMOE_FMT_BL4>), grid, dim3(256), 0, s, *d, x, r, (void*)act,
-                           ncu, nx, 1, (int64_t)0);
+                           ncu, nx, 1, (int64_t)0, r.sched);
     return check_launch();
 }
 
@@ -1160,13 +1404,13 @@ int launch_prefill_down(const lutmoe_moe_desc* d, const uint16_t* act, const Moe
     const dim3 grid(persistent_ctas(ncu, (int64_t)rows * nx * ns));
     if (d->w2.format == LUTMOE_FMT_REF)
         hipLaunchKernelGGL((prefill_ring_kernel<false, LUTMOE_FMT_REF>), grid, dim3(256), 0, s, *d, act, r,
-                           (void*)y_pos, ncu_tail, nx, ns, stride);
+                           (void*)y_pos, ncu_tail, nx, ns, stride, (int*)nullptr);
     else if (d->w2.format == LUTMOE_FMT_NESTED)
         hipLaunchKernelGGL((prefill_ring_kernel<false, LUTMOE_FMT_NESTED>), grid, dim3(256), 0, s, *d, act, r,
-                           (void*)y_pos, ncu_tail, nx, ns, stride);
+                           (void*)y_pos, ncu_tail, nx, ns, stride, (int*)nullptr);
     else
         hipLaunchKernelGGL((prefill_ring_kernel<false, LUTMOE_FMT_BL4>), grid, dim3(256), 0, s, *d, act, r,
-                           (void*)y_pos, ncu_tail, nx, ns, stride);
+                           (void*)y_pos, ncu_tail, nx, ns, stride, (int*)nullptr);
     return check_launch();
 }
 

@@ -50,6 +50,8 @@ struct MoeRouting {
     int T;
     int k_eff;
     int num_experts_total;    // E + S
+    int32_t* sched;           // [4] item and finished-CTA counters of the gate/up ring kernel (2 spare)
+                              // (zeroed by the routing, and by each ring launch's last CTA)
 };
 
 // api.cpp: the body shared by the MoE layer entry points (arguments as
@@ -94,7 +96,7 @@ int launch_permute(const int32_t* pair_ids, int T, int k_eff, int E_tot, int32_t
 // their ids / weights written to pair_ids / pair_w
 int launch_route_pairs(const int32_t* topk_ids, const float* topk_w, int T, int k, int E, int S,
                        int32_t* offsets, int32_t* perm, int32_t* inv, int32_t* active, int32_t* pair_ids,
-                       float* pair_w, hipStream_t s);
+                       float* pair_w, hipStream_t s, int32_t* sched = nullptr);
 // shared slots k..k+S-1 of every token t: pair_w = sigmoid(x_t . gate)
 int launch_shared_gate(const uint16_t* x, const uint16_t* gate, int T, int H, int k, int S, float* pair_w,
                        hipStream_t s);

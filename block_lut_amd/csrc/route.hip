@@ -174,8 +174,10 @@ __global__ __launch_bounds__(256) void permute_kernel(const int32_t* __restrict_
                                                       int32_t* __restrict__ offsets,
                                                       int32_t* __restrict__ perm,
                                                       int32_t* __restrict__ inv,
-                                                      int32_t* __restrict__ active) {
+                                                      int32_t* __restrict__ active,
+                                                      int32_t* __restrict__ sched) {
     extern __shared__ int32_t s_hist[];          // [E_tot]
+    if (sched && blockIdx.x == 0 && threadIdx.x < 4) sched[threadIdx.x] = 0;
     __shared__ int32_t s_wave[4];
     __shared__ int32_t s_base;
     const int e = blockIdx.x;
@@ -261,7 +263,8 @@ __global__ __launch_bounds__(1024) void permute_chunk_kernel(PairSrc ps, int P, 
                                                              int32_t* __restrict__ perm, int32_t* __restrict__ inv,
                                                              int32_t* __restrict__ active,
                                                              int32_t* __restrict__ pair_ids,
-                                                             float* __restrict__ pair_w) {
+                                                             float* __restrict__ pair_w,
+                                                             int32_t* __restrict__ sched) {
     extern __shared__ int32_t sm[];   // h_all[E_tot] | h_bef[E_tot] | off[E_tot+1] | sub[kPermSub][E_tot]
     int32_t* h_all = sm;
     int32_t* h_bef = sm + E_tot;
@@ -269,6 +272,7 @@ __global__ __launch_bounds__(1024) void permute_chunk_kernel(PairSrc ps, int P, 
     int32_t* sub = sm + 3 * E_tot + 1;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int c0 = blockIdx.x * kPermChunk;
+    if (sched && blockIdx.x == 0 && tid < 4) sched[tid] = 0;
     const uint64_t lt = (1ull << lane) - 1ull;
     for (int i = tid; i < (3 + kPermSub) * E_tot + 1; i += blockDim.x) sm[i] = 0;
     __syncthreads();
@@ -439,7 +443,7 @@ int launch_permute(const int32_t* pair_ids, int T, int k_eff, int E_tot, int32_t
 
 int launch_route_pairs(const int32_t* topk_ids, const float* topk_w, int T, int k, int E, int S,
                        int32_t* offsets, int32_t* perm, int32_t* inv, int32_t* active, int32_t* pair_ids,
-                       float* pair_w, hipStream_t s) {
+                       float* pair_w, hipStream_t s, int32_t* sched) {
     const int ke = k + S, E_tot = E + S;
     const int P = T * ke;
     if (E_tot <= 512) {
@@ -449,7 +453,7 @@ int launch_route_pairs(const int32_t* topk_ids, const float* topk_w, int T, int 
         const size_t lds = ((size_t)(3 + kPermSub) * E_tot + 1) * sizeof(int32_t);
         const PairSrc ps{topk_ids, topk_w, T, k, ke, E};
         hipLaunchKernelGGL(permute_chunk_kernel, dim3(nchunk), dim3(64 * kPermSub), lds, s, ps, P, E_tot, nbits,
-                           offsets, perm, inv, active, pair_ids, pair_w);
+                           offsets, perm, inv, active, pair_ids, pair_w, sched);
         return check_launch();
     }
     int rc;
@@ -459,7 +463,7 @@ int launch_route_pairs(const int32_t* topk_ids, const float* topk_w, int T, int 
         return LUTMOE_EINVAL;
     }
     hipLaunchKernelGGL(permute_kernel, dim3(E_tot), dim3(256), E_tot * sizeof(int32_t), s,
-                       pair_ids ? pair_ids : topk_ids, P, E_tot, offsets, perm, inv, active);
+                       pair_ids ? pair_ids : topk_ids, P, E_tot, offsets, perm, inv, active, sched);
     return check_launch();
 }
 
