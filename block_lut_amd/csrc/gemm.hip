@@ -333,6 +333,13 @@ constexpr int kSlotA = kBM * kBK * 2;              // 32 KB
 constexpr int kSlotB = kBN * 32;                   // 8 KB
 constexpr int kSlotBytes = kSlotA + 2 * kSlotB;    // 48 KB
 constexpr int kStages = 3;
+// Tiles of at most 64 positions (BL4 / NestedLUT): their stages are 24 KB
+// (64 activation rows), so the same LDS holds 6, and 5 stages are in flight
+// while one is read -- a short K step needs that many to cover the latency
+// of its loads.
+constexpr int kSlotAs = 64 * kBK * 2;              // 8 KB
+constexpr int kSlotBytesS = kSlotAs + 2 * kSlotB;  // 24 KB
+constexpr int kStagesS = 6;
 
 // A-row chunk swizzle: distinct for any 8 consecutive rows, and (r&1, swz)
 // distinct for any 16 consecutive rows.
@@ -362,6 +369,13 @@ __device__ __forceinline__ void ring_wait_barrier(int stages_after) {
     if (stages_after >= 2) ring_wait_barrier_n<2 * kDma>();
     else if (stages_after == 1) ring_wait_barrier_n<kDma>();
     else ring_wait_barrier_n<0>();
+}
+// the same for up to 4 stages after the one needed next
+template <int kDma>
+__device__ __forceinline__ void ring_wait_barrier4(int stages_after) {
+    if (stages_after >= 4) ring_wait_barrier_n<4 * kDma>();
+    else if (stages_after == 3) ring_wait_barrier_n<3 * kDma>();
+    else ring_wait_barrier<kDma>(stages_after);
 }
 
 // 4 bytes per lane from sbase + voff into LDS at m0 + 4 * lane.
@@ -803,33 +817,35 @@ struct RingLoader {
         }
     }
 
-    // the weight loads of step kb into the slot at LDS address l0
+    // the weight loads of step kb into the slot at LDS address l0 (SA: the
+    // slot's activation bytes, the weights after them)
+    template <int SA>
     __device__ __forceinline__ void issue_w(int kb, uint32_t l0) const {
         if constexpr (kRef) {
             const uint8_t* cb = c_base + kb * 64;
 #pragma unroll
-            for (int h = 0; h < 4; ++h) dma16(w_off[h], cb, l0 + kSlotA + (64 * wvu + 16 * h) * 64);
+            for (int h = 0; h < 4; ++h) dma16(w_off[h], cb, l0 + SA + (64 * wvu + 16 * h) * 64);
             const uint32_t idx = min((am_row64 + (uint32_t)kb) / q, nb - 1u);
-            dma4((idx & ~1u) * 2u, t_base, l0 + kSlotA + kCodesB + 256 * wvu);
+            dma4((idx & ~1u) * 2u, t_base, l0 + SA + kCodesB + 256 * wvu);
         } else if constexpr (kNested) {
             const uint32_t cs = (uint32_t)kb * c_step, ts = (uint32_t)kb * t_step;
-            const uint32_t tl = l0 + kSlotA + kCodesB + (uint32_t)wvu * 64u * t_step;
+            const uint32_t tl = l0 + SA + kCodesB + (uint32_t)wvu * 64u * t_step;
             if (bits == 4) {
-                const uint32_t cl = l0 + kSlotA + (uint32_t)wvu * 2048u;
+                const uint32_t cl = l0 + SA + (uint32_t)wvu * 2048u;
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     dma16(w_off[h] + cs, c_base, cl + h * 1024);
                     dma16(w_off[2 + h] + ts, t_base, tl + h * 1024);
                 }
             } else if (bits == 3) {
-                const uint32_t cl = l0 + kSlotA + (uint32_t)wvu * 2048u;
+                const uint32_t cl = l0 + SA + (uint32_t)wvu * 2048u;
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     dma16(w_off[h] + cs, c_base, cl + h * 1024);
                     dma16(w_off[2 + h] + ts, t_base, tl);
                 }
             } else {
-                const uint32_t cl = l0 + kSlotA + (uint32_t)wvu * 1024u;
+                const uint32_t cl = l0 + SA + (uint32_t)wvu * 1024u;
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     dma16(w_off[h] + cs, c_base, cl);
@@ -841,28 +857,29 @@ struct RingLoader {
             const uint8_t* tbp = t_base + kb * 32;
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                dma16(w_off[h], cb, l0 + kSlotA + wvu * 2048 + h * 1024);
-                dma16(w_off[h], tbp, l0 + kSlotA + kCodesB + wvu * 2048 + h * 1024);
+                dma16(w_off[h], cb, l0 + SA + wvu * 2048 + h * 1024);
+                dma16(w_off[h], tbp, l0 + SA + kCodesB + wvu * 2048 + h * 1024);
             }
         }
     }
     // stage kb into slot sl, NMT activation loads (NMT == nmt)
-    template <int NMT>
+    template <int NMT, int SA = kSlotA>
     __device__ __forceinline__ void issue(int kb, const uint8_t* sl) const {
         const uint32_t l0 = lds_addr(sl);
         const uint8_t* ab = a_base + kb * (kBK * 2);
 #pragma unroll
         for (int j = 0; j < NMT; ++j) dma16(a_off[j], ab, l0 + (8 * NMT * wvu + 8 * j) * 128);
-        issue_w(kb, l0);
+        issue_w<SA>(kb, l0);
     }
     // the same with the tile's activation-load count known at run time
+    template <int SA = kSlotA>
     __device__ __forceinline__ void issue_rt(int kb, const uint8_t* sl) const {
         const uint32_t l0 = lds_addr(sl);
         const uint8_t* ab = a_base + kb * (kBK * 2);
 #pragma unroll
         for (int j = 0; j < 8; ++j)
             if (j < nmt) dma16(a_off[j], ab, l0 + (8 * nmt * wvu + 8 * j) * 128);
-        issue_w(kb, l0);
+        issue_w<SA>(kb, l0);
     }
 };
 
@@ -882,8 +899,13 @@ __device__ __forceinline__ void ring_prologue(const lutmoe_moe_desc& d, const ui
         reinterpret_cast<float*>(ring + kStages * RingSlot<kFmt>::kBytes)[threadIdx.x] = cbv;
     int kb0, nkb;
     ring_k_range(kGateUp ? d.hidden : d.inter, t.z, ns, kb0, nkb);
-    const int npro = min(kStages, nkb);
-    for (int st = 0; st < npro; ++st) L.issue_rt(kb0 + st, ring + st * RingSlot<kFmt>::kBytes);
+    if (kFmt != LUTMOE_FMT_REF && ring_nmt(t) <= 2) {
+        // the small-tile ring geometry
+        for (int st = 0; st < min(kStagesS, nkb); ++st)
+            L.template issue_rt<kSlotAs>(kb0 + st, ring + st * kSlotBytesS);
+    } else {
+        for (int st = 0; st < min(kStages, nkb); ++st) L.issue_rt(kb0 + st, ring + st * RingSlot<kFmt>::kBytes);
+    }
 }
 
 // One tile whose first stages are in the ring (issued by ring_prologue).
@@ -1044,6 +1066,90 @@ __device__ __forceinline__ void ring_tile_body(const lutmoe_moe_desc& d, const u
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[mt][nt][i] = 0.f;
 
+    // Tiles of at most 64 positions (BL4 / NestedLUT): the table lookups,
+    // not the MFMAs, set the pace, and the LDS serves the random 16-bit
+    // lookups into 32 rows' tables with bank conflicts.  Here each lane
+    // loads its two rows' tables once per K step and looks its codes up in
+    // registers (v_perm_b32 over byte planes).  A step's operand reads are
+    // issued one step ahead of its MFMAs (two register sets), right after
+    // the barrier that lands their stage.
+    auto regtab_loop = [&](auto BC) __attribute__((always_inline)) {
+        constexpr int B = decltype(BC)::value;
+        constexpr int ND = (1 << B) / 2;    // table dwords per row
+        constexpr int NP = (1 << B) / 4;    // plane dwords
+        u32x4_t cds[2][kNC];
+        uint32_t tab[2][2][ND];
+        bf16x8_t afs[2][4][NMT];
+        auto issue_step = [&](const uint8_t* sl, auto Bf) __attribute__((always_inline)) {
+            constexpr int b = decltype(Bf)::value;
+            read_codes(sl + (kSlotAs - kSlotA), cds[b]);   // (read_codes adds kSlotA)
+            const uint8_t* tb = sl + kSlotAs + kCodesB;
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                const uint32_t* tp = reinterpret_cast<const uint32_t*>(tb + t_row[nt]);
+                if constexpr (ND >= 4) {
+#pragma unroll
+                    for (int q = 0; q < ND; q += 4) {
+                        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(tp + q);
+                        tab[b][nt][q] = v[0];
+                        tab[b][nt][q + 1] = v[1];
+                        tab[b][nt][q + 2] = v[2];
+                        tab[b][nt][q + 3] = v[3];
+                    }
+                } else {
+                    tab[b][nt][0] = tp[0];
+                    tab[b][nt][1] = tp[1];
+                }
+            }
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) frag_a(sl, ks, afs[b][ks], 0, NMT);
+        };
+        int slot = 0;
+        auto step = [&](int kb, auto Bf) __attribute__((always_inline)) {
+            constexpr int b = decltype(Bf)::value;
+            uint8_t* sl = ring + slot * kSlotBytesS;
+            const int nslot = slot == kStagesS - 1 ? 0 : slot + 1;
+            // step kb's reads are done (this wait also tells the compiler),
+            // stage kb+1 landed everywhere (stages kb+2 .. kb+5 may still be
+            // in flight) and slot kb%6 is no longer read -> refill it with
+            // stage kb+6, issue step kb+1's reads, then step kb's lookups and
+            // MFMAs from registers
+            __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0)
+            ring_wait_barrier4<kDma>(min(4, nkb - 2 - kb));
+            if constexpr (!kGateUp) {
+                if (kb == 0 && tid < nvalid) pw_row = rt.pair_w[pair];
+            }
+            if (kb == nkb - 1 && threadIdx.x == 0) *s_claim = claim;
+            if (kb + kStagesS < nkb) L.template issue<NMT, kSlotAs>(kb0 + kb + kStagesS, sl);
+            if (kb + 1 < nkb) issue_step(ring + nslot * kSlotBytesS, std::integral_constant<int, 1 - b>{});
+            uint32_t lo[2][NP], hi[2][NP];
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) table_planes<B>(tab[b][nt], lo[nt], hi[nt]);
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) {
+                    const bf16x8_t bfr =
+                        __builtin_bit_cast(bf16x8_t, regtab_lookup8<B>(lo[nt], hi[nt], nested_code(cds[b][nt], ks)));
+#pragma unroll
+                    for (int mt = 0; mt < NMT; ++mt)
+                        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(afs[b][ks][mt], bfr, acc[mt][nt], 0, 0, 0);
+                }
+            slot = nslot;
+        };
+        issue_step(ring, std::integral_constant<int, 0>{});
+        int kb = 0;
+        for (; kb + 1 < nkb; kb += 2) {
+            step(kb, std::integral_constant<int, 0>{});
+            step(kb + 1, std::integral_constant<int, 1>{});
+        }
+        if (kb < nkb) step(kb, std::integral_constant<int, 0>{});
+    };
+    if constexpr (NMT <= 2 && !kRef) {
+        if (!kNested || bits == 4) regtab_loop(std::integral_constant<int, 4>{});
+        else if (bits == 3) regtab_loop(std::integral_constant<int, 3>{});
+        else regtab_loop(std::integral_constant<int, 2>{});
+    } else {
     // k-substep 0's fragment reads (every stage in the ring landed)
     u32x4_t codes[kNC];
     float am[2] = {0.f, 0.f};
@@ -1133,6 +1239,7 @@ __device__ __forceinline__ void ring_tile_body(const lutmoe_moe_desc& d, const u
         }
         slot = nslot;
     }
+    }
     // All loads landed (none may still write LDS) and all ring reads are
     // done -> the ring is free; the rows' routing weights are in s_pw.
     if constexpr (!kGateUp) s_pw[tid] = pw_row;
@@ -1187,9 +1294,8 @@ __device__ __forceinline__ void ring_tile_body(const lutmoe_moe_desc& d, const u
 
 constexpr int kOffLds = 1024;   // expert offsets held in LDS: E + S + 1 at most
 
-// sched (gate/up): this launch's item counter and finished-CTA counter, zero
-// at launch (the routing zeroes them; the last CTA to finish zeroes them
-// again).
+// sched: this launch's item counter and finished-CTA counter, zero at launch
+// (the routing zeroes them; the last CTA to finish zeroes them again).
 template <bool kGateUp, int kFmt>
 __global__ __launch_bounds__(256, 1) void prefill_ring_kernel(lutmoe_moe_desc d, const uint16_t* __restrict__ src,
                                                               MoeRouting rt, void* __restrict__ dst, int ncu,
@@ -1211,8 +1317,8 @@ __global__ __launch_bounds__(256, 1) void prefill_ring_kernel(lutmoe_moe_desc d,
     }
     if (tid < kMaxClasses) s_cls[tid] = 0;
     __syncthreads();
-    // tile rows per class (gate/up's item order)
-    for (int e = tid; kGateUp && e < et; e += blockDim.x) {
+    // tile rows per class
+    for (int e = tid; e < et; e += blockDim.x) {
         const int n = s_off[e + 1] - s_off[e];
         const int full = n >> 8, rn = ((n & (kBM - 1)) + 31) >> 5;
         const int b = kNested ? (int)s_bits[e] : 0;
@@ -1225,14 +1331,14 @@ __global__ __launch_bounds__(256, 1) void prefill_ring_kernel(lutmoe_moe_desc d,
     const ItemMap im = item_map(s_off, s_bits, &s_ct, et, kNested, nx, ns);
     const TileWalk w = tile_walk(s_off, et, nx, ns, ncu);
     const int G = gridDim.x, c = blockIdx.x;
-    // Item order.  Gate/up with widely spread tile sizes (a quarter of the
-    // tile rows or more hold at most 128 positions, as under skewed routing):
-    // longest first from the counter, the first G items to the CTAs in
-    // order.  Otherwise (and always for the down projection) the snake order
-    // over the expert-ordered items, which keeps the heaviest tiles -- whose
-    // epilogues write the most -- spread over the launch.
+    // Item order.  Widely spread tile sizes (a quarter of the tile rows or
+    // more hold at most 128 positions, as under skewed routing): longest
+    // first from the counter, the first G items to the CTAs in order.
+    // Otherwise the snake order over the expert-ordered items, which keeps
+    // the heaviest tiles -- whose epilogues write the most -- spread over
+    // the launch.
     bool dyn = false;
-    if constexpr (kGateUp) {
+    {
         int small = 0, all = 0;
         for (int k = 0; k < (kNested ? kMaxClasses : 8); ++k) {
             int cn, cb;
@@ -1404,13 +1510,13 @@ int launch_prefill_down(const lutmoe_moe_desc* d, const uint16_t* act, const Moe
     const dim3 grid(persistent_ctas(ncu, (int64_t)rows * nx * ns));
     if (d->w2.format == LUTMOE_FMT_REF)
         hipLaunchKernelGGL((prefill_ring_kernel<false, LUTMOE_FMT_REF>), grid, dim3(256), 0, s, *d, act, r,
-                           (void*)y_pos, ncu_tail, nx, ns, stride, (int*)nullptr);
+                           (void*)y_pos, ncu_tail, nx, ns, stride, r.sched + 2);
     else if (d->w2.format == LUTMOE_FMT_NESTED)
         hipLaunchKernelGGL((prefill_ring_kernel<false, LUTMOE_FMT_NESTED>), grid, dim3(256), 0, s, *d, act, r,
-                           (void*)y_pos, ncu_tail, nx, ns, stride, (int*)nullptr);
+                           (void*)y_pos, ncu_tail, nx, ns, stride, r.sched + 2);
     else
         hipLaunchKernelGGL((prefill_ring_kernel<false, LUTMOE_FMT_BL4>), grid, dim3(256), 0, s, *d, act, r,
-                           (void*)y_pos, ncu_tail, nx, ns, stride, (int*)nullptr);
+                           (void*)y_pos, ncu_tail, nx, ns, stride, r.sched + 2);
     return check_launch();
 }
 

@@ -50,7 +50,7 @@ struct MoeRouting {
     int T;
     int k_eff;
     int num_experts_total;    // E + S
-    int32_t* sched;           // [4] item and finished-CTA counters of the gate/up ring kernel (2 spare)
+    int32_t* sched;           // [4] item and finished-CTA counters of the gate/up and down ring kernels
                               // (zeroed by the routing, and by each ring launch's last CTA)
 };
 

@@ -125,6 +125,56 @@ __device__ __forceinline__ u32x4_t lookup8_combine(const Lookup8& l) {
     return r;
 }
 
+// Register tables: a row's bf16 table of 2^B entries (B = 2, 3, 4; dwords
+// T[i] = entries 2i, 2i+1) as two byte planes, lo[k] / hi[k] byte i = low /
+// high byte of entry 4k+i, so that v_perm_b32 looks up four codes at once.
+template <int B>
+__device__ __forceinline__ void table_planes(const uint32_t* T, uint32_t* lo, uint32_t* hi) {
+#pragma unroll
+    for (int k = 0; k < (1 << B) / 4; ++k) {
+        lo[k] = __builtin_amdgcn_perm(T[2 * k + 1], T[2 * k], 0x06040200u);
+        hi[k] = __builtin_amdgcn_perm(T[2 * k + 1], T[2 * k], 0x07050301u);
+    }
+}
+// Plane bytes of the four codes in the bytes of s (each < 2^B).  Eight
+// entries are one v_perm_b32 (byte selects 0-7); sixteen are two, of the
+// low and high halves, and a third that picks per byte by the code's bit 3.
+template <int B>
+__device__ __forceinline__ uint32_t plane_lookup4(const uint32_t* pl, uint32_t s, uint32_t s7, uint32_t sel8) {
+    if constexpr (B == 2) return __builtin_amdgcn_perm(pl[0], pl[0], s);
+    else if constexpr (B == 3) return __builtin_amdgcn_perm(pl[1], pl[0], s);
+    else {
+        const uint32_t p0 = __builtin_amdgcn_perm(pl[1], pl[0], s7);
+        const uint32_t p1 = __builtin_amdgcn_perm(pl[3], pl[2], s7);
+        return __builtin_amdgcn_perm(p1, p0, sel8);
+    }
+}
+// The 8 codes of one BL4 code dword (nibble j = code of weight j) looked up
+// in register planes: dword j = bf16(w_2j) | bf16(w_2j+1) << 16, as
+// lookup8_combine(lookup8_issue(w, ...)).
+template <int B>
+__device__ __forceinline__ u32x4_t regtab_lookup8(const uint32_t* lo, const uint32_t* hi, uint32_t w) {
+    const uint32_t se = w & 0x0f0f0f0fu, so = (w >> 4) & 0x0f0f0f0fu;
+    uint32_t se7 = se, so7 = so, sel_e = 0, sel_o = 0;
+    if constexpr (B == 4) {
+        se7 = se & 0x07070707u;
+        so7 = so & 0x07070707u;
+        sel_e = ((se >> 1) & 0x04040404u) | 0x03020100u;   // byte j: j, or j + 4 for codes >= 8
+        sel_o = ((so >> 1) & 0x04040404u) | 0x03020100u;
+    }
+    const uint32_t le = plane_lookup4<B>(lo, se, se7, sel_e), he = plane_lookup4<B>(hi, se, se7, sel_e);
+    const uint32_t lo_ = plane_lookup4<B>(lo, so, so7, sel_o), ho = plane_lookup4<B>(hi, so, so7, sel_o);
+    // even weights 0, 2 | 4, 6 and odd weights 1, 3 | 5, 7 as bf16 pairs
+    const uint32_t e01 = __builtin_amdgcn_perm(he, le, 0x05010400u), e23 = __builtin_amdgcn_perm(he, le, 0x07030602u);
+    const uint32_t o01 = __builtin_amdgcn_perm(ho, lo_, 0x05010400u), o23 = __builtin_amdgcn_perm(ho, lo_, 0x07030602u);
+    u32x4_t r;
+    r[0] = __builtin_amdgcn_perm(o01, e01, 0x05040100u);
+    r[1] = __builtin_amdgcn_perm(o01, e01, 0x07060302u);
+    r[2] = __builtin_amdgcn_perm(o23, e23, 0x05040100u);
+    r[3] = __builtin_amdgcn_perm(o23, e23, 0x07060302u);
+    return r;
+}
+
 __device__ __forceinline__ u32x4_t lookup8_lds(uint32_t w, uint32_t tab) {
     return lookup8_combine(lookup8_issue(w, tab));
 }
