@@ -511,6 +511,54 @@ def test_moe_layer_skewed_routing(gpu, fmt, T):
     assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
 
 
+@pytest.mark.parametrize("fmt", ["bl4", "ref", "nested"])
+def test_prefill_skewed_routing_staged(gpu, fmt):
+    """Prefill with very uneven tiles: every token picks expert 0 (one tile of 200 positions)
+    and three others of a Zipf-like popularity (tiles of a few to ~60 positions), so the
+    grouped GEMMs hand tiles out longest first from their launch counters and the tiles of
+    at most 64 positions look their tables up in registers (BL4, NestedLUT).  Checked against
+    the oracle; then the stages run one by one in one workspace, gate/up and down twice each
+    after one routing (the counters are zeroed by the routing and by each launch's last CTA),
+    equal to the one-call layer bit for bit."""
+    import torch
+    from block_lut_amd import _native as N
+    from block_lut_amd import ops
+    from block_lut_amd.formats import MoEWeights
+    E, S, k, H, I, T = 24, 0, 4, 512, 320, 200
+    if fmt == "nested":
+        bits = [2, 3, 4] * (E // 3)
+        w13 = NestedExpertset(bits, 2 * I, H, seed=130, n_iter=8)
+        w2 = NestedExpertset(bits, H, I, seed=131, n_iter=8)
+        f13, f2 = w13.deq_f32, w2.deq_f32
+    else:
+        w13, w2 = _moe_case(fmt, E, S, H, I, seed=130)
+        f13, f2 = _ref_semantics(w13, w2, T, 2) if fmt == "ref" else (w13.deq_f32, w2.deq_f32)
+    moe = MoEWeights(w13.stack(gpu), w2.stack(gpu), H, I, E, S)
+    rng = np.random.default_rng(1300)
+    xb = _x(rng, T, H)
+    p = 1.0 / np.arange(1, E) ** 1.1
+    p /= p.sum()
+    rids = np.stack([np.concatenate([[0], 1 + rng.choice(E - 1, size=k - 1, replace=False, p=p)])
+                     for _ in range(T)]).astype(np.int64)
+    rw = rng.random((T, k)).astype(np.float32)
+    counts = np.bincount(rids.ravel(), minlength=E)
+    assert counts[0] == T and np.sum((counts > 0) & (counts <= 64)) >= E // 2
+    args = (moe, to_dev_bf16(xb, gpu), torch.from_numpy(rw).to(gpu), torch.from_numpy(rids).to(gpu))
+    full = ops.moe_forward(*args, out_dtype=torch.float32, path=2, workspace=ops.new_workspace(moe, T, k, gpu))
+    ref = O.moe_layer(xb, rids, rw, f13, f2, shared=[])
+    assert rel_maxabs(full.cpu().numpy(), ref) <= TOL
+    ws = ops.new_workspace(moe, T, k, gpu)
+    staged = torch.empty_like(full)
+    ops.moe_forward(*args, out=staged, path=2, workspace=ws, stages=N.STAGE_ROUTE)
+    for _ in range(2):
+        ops.moe_forward(*args, out=staged, path=2, workspace=ws, stages=N.STAGE_GATE_UP)
+    for _ in range(2):
+        staged.zero_()
+        ops.moe_forward(*args, out=staged, path=2, workspace=ws, stages=N.STAGE_DOWN)
+        torch.cuda.synchronize()
+        assert torch.equal(full, staged)
+
+
 @pytest.mark.parametrize("block_size,T,path", [(64, 1, 1), (64, 9, 1), (192, 1, 1), (192, 9, 1), (256, 1, 1),
                                                (256, 9, 1), (64, 40, 2), (192, 40, 2), (256, 300, 2)])
 def test_moe_layer_ref_block_sizes(gpu, block_size, T, path):
