@@ -540,8 +540,8 @@ __device__ __forceinline__ void class_table(ClassTable& t, const int* cls, bool 
 }
 
 struct ItemMap {
-    const int* off;        // expert offsets (LDS)
-    const int8_t* bits;    // NestedLUT tier of each expert (LDS)
+    const int* off;        // expert offsets (LDS, or global past kOffLds - 1 experts)
+    const int8_t* bits;    // NestedLUT tier of each expert (LDS, or global)
     const ClassTable* ct;  // (LDS)
     int et, nc, nsub, nx, ns, nitems;
     bool nested;
@@ -628,7 +628,7 @@ __device__ __forceinline__ RingTile map_item(const ItemMap& m, int item) {
 // `split` of them cut into 128-position halves) x nx weight-row blocks x ns
 // K splits.
 struct TileWalk {
-    const int* off;   // expert offsets (LDS)
+    const int* off;   // expert offsets (LDS, or global)
     int et, ttot, split, rows, nx, ns, nitems;
 };
 
@@ -1292,7 +1292,7 @@ __device__ __forceinline__ void ring_tile_body(const lutmoe_moe_desc& d, const u
     }
 }
 
-constexpr int kOffLds = 1024;   // expert offsets held in LDS: E + S + 1 at most
+constexpr int kOffLds = 1024;   // expert offsets held in LDS: E + S + 1 at most (more: read in place)
 
 // sched: this launch's item counter and finished-CTA counter, zero at launch
 // (the routing zeroes them; the last CTA to finish zeroes them again).
@@ -1308,28 +1308,35 @@ __global__ __launch_bounds__(256, 1) void prefill_ring_kernel(lutmoe_moe_desc d,
     __shared__ ClassTable s_ct;
     __shared__ float s_pw[kBM];
     __shared__ int s_claim;
-    const int et = rt.num_experts_total;   // et + 1 <= kOffLds (checked on the host)
+    const int et = rt.num_experts_total;
     const int tid = threadIdx.x;
-    for (int i = tid; i <= et; i += blockDim.x) s_off[i] = rt.offsets[i];
-    if constexpr (kNested) {
-        const int8_t* tb = (kGateUp ? d.w13 : d.w2).tier_bits;
-        for (int i = tid; i < et; i += blockDim.x) s_bits[i] = tb[i];
+    // the expert offsets (and NestedLUT tier widths) in LDS, or, past
+    // kOffLds - 1 experts, read in place (generic pointers)
+    const bool in_lds = et < kOffLds;
+    const int* off = in_lds ? (const int*)s_off : rt.offsets;
+    const int8_t* bits = kNested ? (in_lds ? (const int8_t*)s_bits : (kGateUp ? d.w13 : d.w2).tier_bits) : s_bits;
+    if (in_lds) {
+        for (int i = tid; i <= et; i += blockDim.x) s_off[i] = rt.offsets[i];
+        if constexpr (kNested) {
+            const int8_t* tb = (kGateUp ? d.w13 : d.w2).tier_bits;
+            for (int i = tid; i < et; i += blockDim.x) s_bits[i] = tb[i];
+        }
     }
     if (tid < kMaxClasses) s_cls[tid] = 0;
     __syncthreads();
     // tile rows per class
     for (int e = tid; e < et; e += blockDim.x) {
-        const int n = s_off[e + 1] - s_off[e];
+        const int n = off[e + 1] - off[e];
         const int full = n >> 8, rn = ((n & (kBM - 1)) + 31) >> 5;
-        const int b = kNested ? (int)s_bits[e] : 0;
+        const int b = kNested ? (int)bits[e] : 0;
         if (full + (rn == 8 ? 1 : 0) > 0) atomicAdd(&s_cls[tile_class(kNested, 8, b)], full + (rn == 8 ? 1 : 0));
         if (rn > 0 && rn < 8) atomicAdd(&s_cls[tile_class(kNested, rn, b)], 1);
     }
     __syncthreads();
     class_table(s_ct, s_cls, kNested, nx, ncu);
     __syncthreads();
-    const ItemMap im = item_map(s_off, s_bits, &s_ct, et, kNested, nx, ns);
-    const TileWalk w = tile_walk(s_off, et, nx, ns, ncu);
+    const ItemMap im = item_map(off, bits, &s_ct, et, kNested, nx, ns);
+    const TileWalk w = tile_walk(off, et, nx, ns, ncu);
     const int G = gridDim.x, c = blockIdx.x;
     // Item order.  Widely spread tile sizes (a quarter of the tile rows or
     // more hold at most 128 positions, as under skewed routing): longest
@@ -1446,7 +1453,6 @@ static int cu_count() {
 static bool ring_offsets_fit(const lutmoe_moe_desc* d, const MoeRouting& r, int P) {
     const int64_t lim = int64_t(1) << 32;
     if ((int64_t)r.T * d->hidden * 2 >= lim || (int64_t)P * d->inter * 2 >= lim) return false;
-    if (r.num_experts_total + 1 > kOffLds) return false;   // the offsets' LDS copy
     if (d->w13.format == LUTMOE_FMT_REF) {
         // one expert's codes and absmax by 32-bit offsets; absmax read as
         // aligned dwords (an even count per expert keeps them inside it)
@@ -1457,7 +1463,6 @@ static bool ring_offsets_fit(const lutmoe_moe_desc* d, const MoeRouting& r, int 
         }
         return true;
     }
-    if (r.num_experts_total + 1 > kOffLds) return false;   // the offsets' LDS copy
     if (d->w13.format == LUTMOE_FMT_NESTED)
         return (int64_t)d->w13.rows * d->w13.cols < lim && (int64_t)d->w2.rows * d->w2.cols < lim;
     return (int64_t)d->w13.rows * (d->w13.cols / 2) < lim && (int64_t)d->w2.rows * (d->w2.cols / 2) < lim;

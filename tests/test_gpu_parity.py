@@ -559,6 +559,44 @@ def test_prefill_skewed_routing_staged(gpu, fmt):
         assert torch.equal(full, staged)
 
 
+def test_prefill_many_experts(gpu):
+    """More experts than the grouped GEMMs keep offsets of in LDS (1,100 routed + shared):
+    the kernels read the offsets in place; checked against the oracle."""
+    import torch
+    from block_lut_amd import ops
+    from block_lut_amd.formats import MoEWeights
+    from block_lut_amd.formats import BL4Stack
+    E, S, k, H, I, T = 1100, 1, 2, 256, 192, 96
+
+    class RandomBL4:
+        """Random codes and sorted random fp16 tables (no k-means: 1,101 experts)."""
+
+        def __init__(self, M, K, seed):
+            r = np.random.default_rng(seed)
+            self.codes = r.integers(0, 256, (E + S, M, K // 2), dtype=np.uint8)
+            t = np.sort(r.standard_normal((E + S, M, K // 64, 16)).astype(np.float32) * 0.02, axis=-1)
+            self.tables = t.astype(np.float16).view(np.uint16)
+
+        def deq_f32(self, e):
+            return O.bf16_to_f32(O.bl4_dequant(self.codes[e], self.tables[e]))
+
+        def stack(self, device):
+            return BL4Stack.from_fp16(torch.from_numpy(self.codes).to(device), to_dev_f16(self.tables, device))
+
+    w13, w2 = RandomBL4(2 * I, H, 140), RandomBL4(H, I, 141)
+    moe = MoEWeights(w13.stack(gpu), w2.stack(gpu), H, I, E, S)
+    rng = np.random.default_rng(1400)
+    xb = _x(rng, T, H)
+    rids = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int64)
+    rids[: T // 2, 0] = 7   # one expert with many positions, the rest with one or none
+    rw = rng.random((T, k)).astype(np.float32)
+    out = ops.moe_forward(moe, to_dev_bf16(xb, gpu), torch.from_numpy(rw).to(gpu),
+                          torch.from_numpy(rids).to(gpu), out_dtype=torch.float32, path=2)
+    f13, f2 = w13.deq_f32, w2.deq_f32
+    ref = O.moe_layer(xb, rids, rw, f13, f2, shared=[(f13(E + s), f2(E + s)) for s in range(S)])
+    assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
+
+
 @pytest.mark.parametrize("block_size,T,path", [(64, 1, 1), (64, 9, 1), (192, 1, 1), (192, 9, 1), (256, 1, 1),
                                                (256, 9, 1), (64, 40, 2), (192, 40, 2), (256, 300, 2)])
 def test_moe_layer_ref_block_sizes(gpu, block_size, T, path):
