@@ -1,32 +1,27 @@
 // Prefill grouped LUT-GEMM on MFMA (v_mfma_f32_32x32x16_bf16, gfx950).
 //
 // Positions (permuted (token, slot) pairs) of one expert are contiguous, so a
-// tile is up to 256 positions of one expert (tile -> expert found by a scan of
-// the expert offsets, heaviest experts -- the shared ones, stored last --
-// first; no host sync).
-//
-// CTA = 4 waves, tile = (up to) 256 positions x 256 weight rows, K step = 64
+// tile is up to 256 positions of one expert and 256 weight rows; K step = 64
 // (one BL4 codebook block per row).  Wave w owns 64 weight rows (2 MFMA
 // n-tiles) and ALL m-tiles of 32 positions: up to 8 x 2 accumulators of 16
 // fp32 (256 per lane, held in AGPRs); m-tiles past the expert's position count
-// are skipped, so a tile costs what its positions need.  Per K step:
-//   A (activations, bf16) 256 x 64 -> LDS (144-byte padded rows), double
-//     buffered, one barrier per step; stage 1 gathers the rows
-//     x[token(perm[p])] directly (fused permute).
-//   B tables: the 256 rows' 32-byte bf16 tables of block kb -> LDS.
-//   B codes: each lane reads its own 16 bytes (32 codes) of its row straight
-//     from global memory; the four 16-wide k-substeps take bytes 4ks..4ks+3,
-//     i.e. lane half h covers columns 32h + 8ks .. +7 of the block, and the A
-//     fragments use the same column map (a consistent permutation of k leaves
-//     the contraction unchanged).  The lookup table[row][code] (one SDWA add
-//     and one ds_read_u16 per weight) gives the bf16 dequantised weights of
-//     the MFMA B fragment.
-//   The next step's A, tables and codes are loaded into registers while the
-//   current step's MFMAs run.
+// are skipped, so a tile costs what its positions need.
+//
+// prefill_ring_kernel is persistent: one CTA per CU takes tiles one after
+// another (longest first from a launch counter under skewed routing, else a
+// snake order; no host sync).  Operands go global -> LDS by direct loads
+// through a ring of stages (3 of 48 KB; 6 of 24 KB for tiles of at most 64
+// positions), and the next tile's first stages are issued as soon as a K loop
+// ends, so that they land while the epilogue stores straight from the
+// accumulators.  B fragments are the rows' bf16 tables looked up per code (an
+// SDWA add and a ds_read_u16 per weight; tiles of at most 64 positions look
+// the tables up in registers instead).
 //   stage 1 (gate_up): n-tile 0 = gate rows i0+32w.., n-tile 1 = up rows
 //     I+i0+32w..; epilogue act = bf16(silu(g) * u) per position.
 //   stage 2 (down): n-tiles = rows h0+64w.., +32; epilogue y_pos[p][h] =
 //     acc * routing weight (fp32), summed per token by the combine kernel.
+// prefill_ref_kernel (REF stacks the ring cannot address) stages its
+// operands through registers, one tile per CTA (find_tile).
 // Restates the prefill branch of LUTFusedMoEMethod.apply
 // (vllm_lut/quant_method.py:261-277) and the per-expert GEMMs of the
 // llama.cpp mul_mat_id patch (llama-cpp-port/patches/0001:151-208), over the
@@ -320,10 +315,10 @@ __device__ __forceinline__ void prefill_tile_ref(const lutmoe_moe_desc& d, const
 //          fragment read hit distinct LDS banks)
 //   codes  [256 rows] x 32 B             ( 8 KB; bytes 16h.. = columns 32h..32h+31)
 //   tables [256 rows] x 32 B             ( 8 KB; the rows' bf16[16] tables)
-// Each load instruction reads whole 128-byte lines (8 lanes per A row, 2 lanes
-// per 32-byte weight-row segment; NestedLUT tiers below 4 bits pack their
-// shorter rows densely, see prefill_tile_ring).  Only the tile's NMT*32
-// activation rows are loaded.  Every thread issues the same kDma loads per
+// The activation loads read whole 128-byte lines (8 lanes per row), the weight
+// loads each row's 32-byte piece of the K step (2 lanes per row; NestedLUT
+// tiers below 4 bits pack their shorter rows densely, see RingLoader).  Only
+// the tile's NMT*32 activation rows are loaded.  Every thread issues the same kDma loads per
 // stage (NMT + 4 for BL4 and NestedLUT, NMT + 5 for REF), so
 // `s_waitcnt vmcnt(kDma)` means "all but the newest stage have landed".  Per step kb: k-substeps 0-2 run from slot kb%3; then a barrier
 // (stage kb+1 landed everywhere, slot kb%3 no longer read), the refill of slot
@@ -331,7 +326,6 @@ __device__ __forceinline__ void prefill_tile_ref(const lutmoe_moe_desc& d, const
 // looking up step kb+1's operands.
 constexpr int kSlotA = kBM * kBK * 2;              // 32 KB
 constexpr int kSlotB = kBN * 32;                   // 8 KB
-constexpr int kSlotBytes = kSlotA + 2 * kSlotB;    // 48 KB
 constexpr int kStages = 3;
 // Tiles of at most 64 positions (BL4 / NestedLUT): their stages are 24 KB
 // (64 activation rows), so the same LDS holds 6, and 5 stages are in flight
@@ -925,7 +919,6 @@ __device__ __forceinline__ void ring_tile_body(const lutmoe_moe_desc& d, const u
     // ring loads per thread per stage: the tile's NMT activation loads (only
     // its NMT*32 rows are loaded) and the weight loads
     constexpr int kDma = NMT + (kRef ? 5 : 4);
-    const lutmoe_weights& ww = kGateUp ? d.w13 : d.w2;
     // the lane index through an opaque move, so that nothing derived from it
     // is hoisted out of the persistent loop (and kept live across K loops)
     int tid;
