@@ -55,6 +55,16 @@ def build(verbose: bool = False) -> str:
     jobs = min(len(SOURCES), max(1, (os.cpu_count() or 4)))
     with cf.ThreadPoolExecutor(jobs) as ex:
         objs = list(ex.map(lambda s: _compile(s, obj_dir), SOURCES))
+    # the inline-asm LDS-DMA loads against the VALU-SGPR-write hazard (the
+    # compiler does not guard inline asm): a library with one is not linked
+    if HERE not in sys.path:
+        sys.path.insert(0, HERE)
+    import isa_check
+    hazards = isa_check.check_objects(objs)
+    if hazards:
+        raise RuntimeError("LDS-DMA load reads an SGPR a VALU instruction wrote fewer than "
+                           f"{isa_check.WAIT_STATES} wait states earlier:\n" +
+                           "\n".join("  |  ".join(map(str, h)) for h in hazards))
     tmp = LIB + f".tmp{os.getpid()}"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)

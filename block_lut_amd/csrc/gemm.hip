@@ -372,9 +372,16 @@ __device__ __forceinline__ void ring_wait_barrier4(int stages_after) {
     else ring_wait_barrier<kDma>(stages_after);
 }
 
-// 4 bytes per lane from sbase + voff into LDS at m0 + 4 * lane.
+// 4 bytes per lane from sbase + voff into LDS at m0 + 4 * lane.  The load
+// reads sbase as an SGPR pair; a VALU write of an SGPR (v_readlane of a
+// spilled pointer, v_readfirstlane) needs 5 wait states before a VMEM
+// instruction reads it, and the compiler does not insert them in front of
+// inline asm: this rarely issued load carries them itself (s_nop 4).  The
+// ring's dma16 sites have none; the build's ISA check
+// (block_lut_amd/csrc/isa_check.py) verifies every LDS-DMA load of the
+// library.
 __device__ __forceinline__ void dma4(uint32_t voff, const void* sbase, uint32_t m0) {
-    asm volatile("global_load_lds_dword %0, %1" : : "v"(voff), "s"(sbase), "{m0}"(m0) : "memory");
+    asm volatile("s_nop 4\n\tglobal_load_lds_dword %0, %1" : : "v"(voff), "s"(sbase), "{m0}"(m0) : "memory");
 }
 
 template <typename T>
