@@ -12,6 +12,8 @@ typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
 typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4_t;
+typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2_t;
+typedef __attribute__((__vector_size__(2 * sizeof(float)))) float f32x2_t;
 
 constexpr int kBlockBL = 64;   // BL4 / nested: weights per codebook block
 constexpr int kWave = 64;      // CDNA wavefront size
@@ -29,6 +31,14 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
     return u >> 16;
 }
 
+// Two floats -> packed bf16 bits (a in the low half) by the hardware
+// conversion (v_cvt_pk_bf16_f32): round to nearest even with fp32 denormals
+// kept (the kernels' default float mode), the rule of f32_to_bf16 for every
+// non-NaN input.
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+}
+
 __device__ __forceinline__ float f16_to_f32(uint32_t h) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
@@ -43,13 +53,13 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
                                            __builtin_bit_cast(bf16x2_t, b), c, false);
 }
 
-// silu(g) * u = g * u / (1 + exp(-g)), with the hardware reciprocal (1 ulp in
-// fp32; callers round the result to bf16).
 // REF: expert e's bf16[256] codebook (codebook_stride 0: one for all experts).
 __device__ __forceinline__ const uint16_t* ref_codebook(const lutmoe_weights& w, int e) {
     return (const uint16_t*)w.codebook + (int64_t)e * w.codebook_stride;
 }
 
+// silu(g) * u = g * u / (1 + exp(-g)), with the hardware reciprocal (1 ulp in
+// fp32; callers round the result to bf16).
 __device__ __forceinline__ float silu_mul(float g, float u) {
     return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
 }

@@ -1133,7 +1133,7 @@ __device__ __forceinline__ void ring_tile_body(const lutmoe_moe_desc& d, const u
                         __builtin_bit_cast(bf16x8_t, regtab_lookup8<B>(lo[nt], hi[nt], nested_code(cds[b][nt], ks)));
 #pragma unroll
                     for (int mt = 0; mt < NMT; ++mt)
-                        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(afs[b][ks][mt], bfr, acc[mt][nt], 0, 0, 0);
+                        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr, afs[b][ks][mt], acc[mt][nt], 0, 0, 0);
                 }
             slot = nslot;
         };
@@ -1205,7 +1205,7 @@ __device__ __forceinline__ void ring_tile_body(const lutmoe_moe_desc& d, const u
             }
 #pragma unroll
             for (int mt = 0; mt < NMT; ++mt)
-                acc[mt][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mt], bf[0], acc[mt][0], 0, 0, 0);
+                acc[mt][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[0], af[mt], acc[mt][0], 0, 0, 0);
 #pragma unroll
             for (int i = 0; i < NMT; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                            // 1 MFMA
@@ -1220,7 +1220,7 @@ __device__ __forceinline__ void ring_tile_body(const lutmoe_moe_desc& d, const u
             frag_a(rs, ksn, af_n, kHalfA, NMT);
 #pragma unroll
             for (int mt = 0; mt < NMT; ++mt)
-                acc[mt][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mt], bf[1], acc[mt][1], 0, 0, 0);
+                acc[mt][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[1], af[mt], acc[mt][1], 0, 0, 0);
 #pragma unroll
             for (int i = 0; i < NMT; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -1247,48 +1247,61 @@ __device__ __forceinline__ void ring_tile_body(const lutmoe_moe_desc& d, const u
     next = next_of(*s_claim);
     if (next.e >= 0) ring_prologue<kGateUp, kFmt>(d, src, rt, next, ns, ring);
 
-    // ---- epilogue, straight from the accumulators.  D layout: lane (n =
-    // lane%32, h = lane/32), element i -> row m = 8*(i/4) + 4*h + (i%4),
-    // column n: each store writes 32 consecutive columns of two rows.  The
-    // stores go through a buffer descriptor over the tile's rows, with 32-bit
-    // offsets; rows past the tile's positions fall outside it and are
-    // dropped.
+    // ---- epilogue, straight from the accumulators.  The weights are the
+    // MFMAs' A operand, so D is the tile transposed: lane (m = lane%32,
+    // h = lane/32), element i -> tile position 32*mt + m, weight row
+    // 8*(i/4) + 4*h + (i%4) of the n-tile.  A lane holds four runs of 4
+    // consecutive output columns of one position, each stored at once (8
+    // bytes of bf16, 16 of fp32), and the lane pair (m, m+32) writes 8
+    // consecutive columns.  The stores go through a buffer descriptor over
+    // the tile's rows, with 32-bit offsets; rows past the tile's positions
+    // fall outside it and are dropped.  H and I are multiples of 64, so a
+    // wave's columns (32 of gate/up, 64 of down, from a multiple of 32 / 64)
+    // are in range all or none: one wave-uniform test (a lane-dependent one
+    // around each store makes the compiler take the tile for divergent).
+    const int wvs = __builtin_amdgcn_readfirstlane(wv);
     if constexpr (kGateUp) {
         // act[p][i] = bf16(silu(gate) * up)
-        const int ii = n0 + 32 * wv + bn;
+        const int i0 = n0 + 32 * wvs;             // the wave's first column; lane runs at +4h+8g
         const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
             (void*)((uint16_t*)dst + (int64_t)(ti.p0 + ti.m0) * I), 0, nvalid * I * 2, kBufWord3);
-        const uint32_t vo = (uint32_t)(4 * bh * I + ii) * 2u;
-        if (ii < I) {
+        if (i0 < I) {
 #pragma unroll
-            for (int mt = 0; mt < NMT; ++mt)
+            for (int mt = 0; mt < NMT; ++mt) {
+                const uint32_t ro = ((uint32_t)(mt * 32 + bn) * (uint32_t)I + (uint32_t)(i0 + 4 * bh)) * 2u;
 #pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const uint32_t mrow = (uint32_t)(mt * 32 + 8 * (i >> 2) + (i & 3));
-                    __builtin_amdgcn_raw_buffer_store_b16(
-                        (uint16_t)f32_to_bf16(silu_mul(acc[mt][0][i], acc[mt][1][i])), rs,
-                        (int)(vo + mrow * (uint32_t)I * 2u), 0, 0);
+                for (int g = 0; g < 4; ++g) {
+                    float a[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) a[r] = silu_mul(acc[mt][0][4 * g + r], acc[mt][1][4 * g + r]);
+                    const u32x2_t v = {f32x2_to_bf16x2(a[0], a[1]), f32x2_to_bf16x2(a[2], a[3])};
+                    __builtin_amdgcn_raw_buffer_store_b64(v, rs, (int)(ro + 16u * (uint32_t)g), 0, 0);
                 }
+            }
         }
     } else {
         // y[p][h] = acc * routing weight (fp32), K split z into its own y
-        const int h0 = n0 + 64 * wv + bn;
+        const int h0 = n0 + 64 * wvs;             // the wave's first column; lane runs at +4h+32nt+8g
         const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
             (void*)((float*)dst + ti.z * split_stride + (int64_t)(ti.p0 + ti.m0) * H), 0, nvalid * H * 4, kBufWord3);
-        const uint32_t vo = (uint32_t)(4 * bh * H + h0) * 4u;
+        if (h0 < H) {
 #pragma unroll
-        for (int mt = 0; mt < NMT; ++mt)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int mrow = mt * 32 + 8 * (i >> 2) + (i & 3);
-                const float pw = s_pw[min(mrow + 4 * bh, kBM - 1)];
+            for (int mt = 0; mt < NMT; ++mt) {
+                const float pw = s_pw[mt * 32 + bn];
+                const uint32_t ro = ((uint32_t)(mt * 32 + bn) * (uint32_t)H + (uint32_t)(h0 + 4 * bh)) * 4u;
 #pragma unroll
                 for (int nt = 0; nt < 2; ++nt)
-                    if (h0 + 32 * nt < H)
-                        __builtin_amdgcn_raw_buffer_store_b32(
-                            __float_as_uint(acc[mt][nt][i] * pw), rs,
-                            (int)(vo + (uint32_t)mrow * (uint32_t)H * 4u + 128u * (uint32_t)nt), 0, 0);
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const u32x4_t v = {__float_as_uint(acc[mt][nt][4 * g] * pw),
+                                           __float_as_uint(acc[mt][nt][4 * g + 1] * pw),
+                                           __float_as_uint(acc[mt][nt][4 * g + 2] * pw),
+                                           __float_as_uint(acc[mt][nt][4 * g + 3] * pw)};
+                        __builtin_amdgcn_raw_buffer_store_b128(v, rs, (int)(ro + 128u * (uint32_t)nt + 32u * (uint32_t)g),
+                                                               0, 0);
+                    }
             }
+        }
     }
 }
 
