@@ -365,35 +365,47 @@ __global__ __launch_bounds__(1024) void permute_chunk_kernel(PairSrc ps, int P, 
 
 // out[t] = sum over the token's positions p (slot order) of y[p], each y[p]
 // itself the sum of nsplit partial rows (K-split down projection) at stride
-// sstride, added in split order.
+// sstride, added in split order; plus addend[t] when given; one rounding to
+// the output dtype.  CTA (t, x) covers columns [1024x, 1024x + 1024) of token
+// t, 4 a thread: the token's positions are the same in the whole CTA (scalar
+// loads), and a thread issues the loads of all its positions' rows before it
+// adds them (in slot order, as one pass over the positions would).  The rows
+// are read once: non-temporal loads.
+constexpr int kCombineMaxKe = 16;   // k + shared experts (the entry points check it)
+
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ y, const int32_t* __restrict__ inv,
                                                       int T, int ke, int H, void* __restrict__ out,
                                                       int out_dtype, int nsplit, int64_t sstride,
                                                       const float* __restrict__ addend) {
-    const int hq = H / 4;
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= (int64_t)T * hq) return;
-    const int t = (int)(i / hq), h = (int)(i % hq) * 4;
-    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int q = 0; q < ke; ++q) {
-        const int p = inv[(int64_t)t * ke + q];
-        if (p < 0) continue;
-        float4 v = *reinterpret_cast<const float4*>(y + (int64_t)p * H + h);
-        for (int sp = 1; sp < nsplit; ++sp) {
-            const float4 u = *reinterpret_cast<const float4*>(y + sp * sstride + (int64_t)p * H + h);
-            v.x += u.x; v.y += u.y; v.z += u.z; v.w += u.w;
-        }
-        s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
+    const int t = blockIdx.x;
+    const int h = blockIdx.y * 1024 + threadIdx.x * 4;
+    if (h >= H) return;
+    int pos[kCombineMaxKe];
+#pragma unroll
+    for (int q = 0; q < kCombineMaxKe; ++q) pos[q] = q < ke ? inv[(int64_t)t * ke + q] : -1;
+    f32x4_t v[kCombineMaxKe];
+#pragma unroll
+    for (int q = 0; q < kCombineMaxKe; ++q) {
+        v[q] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        if (pos[q] >= 0) v[q] = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(y + (int64_t)pos[q] * H + h));
     }
-    if (addend) {
-        const float4 a = *reinterpret_cast<const float4*>(addend + (int64_t)t * H + h);
-        s.x += a.x; s.y += a.y; s.z += a.z; s.w += a.w;
+    for (int sp = 1; sp < nsplit; ++sp) {
+#pragma unroll
+        for (int q = 0; q < kCombineMaxKe; ++q)
+            if (pos[q] >= 0)
+                v[q] += __builtin_nontemporal_load(
+                    reinterpret_cast<const f32x4_t*>(y + sp * sstride + (int64_t)pos[q] * H + h));
     }
+    f32x4_t sum = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < kCombineMaxKe; ++q)
+        if (pos[q] >= 0) sum += v[q];
+    if (addend) sum += *reinterpret_cast<const f32x4_t*>(addend + (int64_t)t * H + h);
     if (out_dtype == LUTMOE_DTYPE_F32) {
-        *reinterpret_cast<float4*>((float*)out + (int64_t)t * H + h) = s;
+        *reinterpret_cast<f32x4_t*>((float*)out + (int64_t)t * H + h) = sum;
     } else {
-        const uint32_t a = f32_to_bf16(s.x) | (f32_to_bf16(s.y) << 16);
-        const uint32_t b = f32_to_bf16(s.z) | (f32_to_bf16(s.w) << 16);
+        const uint32_t a = f32_to_bf16(sum[0]) | (f32_to_bf16(sum[1]) << 16);
+        const uint32_t b = f32_to_bf16(sum[2]) | (f32_to_bf16(sum[3]) << 16);
         *reinterpret_cast<uint2*>((uint16_t*)out + (int64_t)t * H + h) = make_uint2(a, b);
     }
 }
@@ -470,8 +482,8 @@ int launch_route_pairs(const int32_t* topk_ids, const float* topk_w, int T, int 
 int launch_combine(const float* y_pos, const int32_t* inv, int T, int k_eff, int H, void* out,
                    int out_dtype, hipStream_t s, int nsplit, int64_t split_stride,
                    const float* addend) {
-    const int64_t n = (int64_t)T * (H / 4);
-    hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, y_pos,
+    if (k_eff > kCombineMaxKe) return LUTMOE_EUNSUPPORTED;
+    hipLaunchKernelGGL(combine_kernel, dim3((unsigned)T, (unsigned)((H + 1023) / 1024)), dim3(256), 0, s, y_pos,
                        inv, T, k_eff, H, out, out_dtype, nsplit, split_stride, addend);
     return check_launch();
 }
