@@ -1058,6 +1058,14 @@ __device__ __forceinline__ void ring_tile_body(const lutmoe_moe_desc& d, const u
         else return __builtin_bit_cast(bf16x8_t, lookup8_combine(lk));
     };
 
+    // One MFMA of activation fragment a and weight fragment w.  Gate/up puts
+    // the weights in the A operand, so that its accumulators hold output
+    // columns of one position (see the epilogue); down keeps the activations
+    // in A, so that a store writes whole 128-byte rows of fp32 output.
+    auto mma = [&](const bf16x8_t& a, const bf16x8_t& w, const f32x16_t& c) __attribute__((always_inline)) {
+        if constexpr (kGateUp) return __builtin_amdgcn_mfma_f32_32x32x16_bf16(w, a, c, 0, 0, 0);
+        else return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, w, c, 0, 0, 0);
+    };
     f32x16_t acc[NMT][2];
 #pragma unroll
     for (int mt = 0; mt < NMT; ++mt)
@@ -1133,7 +1141,7 @@ __device__ __forceinline__ void ring_tile_body(const lutmoe_moe_desc& d, const u
                         __builtin_bit_cast(bf16x8_t, regtab_lookup8<B>(lo[nt], hi[nt], nested_code(cds[b][nt], ks)));
 #pragma unroll
                     for (int mt = 0; mt < NMT; ++mt)
-                        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr, afs[b][ks][mt], acc[mt][nt], 0, 0, 0);
+                        acc[mt][nt] = mma(afs[b][ks][mt], bfr, acc[mt][nt]);
                 }
             slot = nslot;
         };
@@ -1205,7 +1213,7 @@ __device__ __forceinline__ void ring_tile_body(const lutmoe_moe_desc& d, const u
             }
 #pragma unroll
             for (int mt = 0; mt < NMT; ++mt)
-                acc[mt][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[0], af[mt], acc[mt][0], 0, 0, 0);
+                acc[mt][0] = mma(af[mt], bf[0], acc[mt][0]);
 #pragma unroll
             for (int i = 0; i < NMT; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                            // 1 MFMA
@@ -1220,7 +1228,7 @@ __device__ __forceinline__ void ring_tile_body(const lutmoe_moe_desc& d, const u
             frag_a(rs, ksn, af_n, kHalfA, NMT);
 #pragma unroll
             for (int mt = 0; mt < NMT; ++mt)
-                acc[mt][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[1], af[mt], acc[mt][1], 0, 0, 0);
+                acc[mt][1] = mma(af[mt], bf[1], acc[mt][1]);
 #pragma unroll
             for (int i = 0; i < NMT; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -1247,21 +1255,20 @@ __device__ __forceinline__ void ring_tile_body(const lutmoe_moe_desc& d, const u
     next = next_of(*s_claim);
     if (next.e >= 0) ring_prologue<kGateUp, kFmt>(d, src, rt, next, ns, ring);
 
-    // ---- epilogue, straight from the accumulators.  The weights are the
-    // MFMAs' A operand, so D is the tile transposed: lane (m = lane%32,
-    // h = lane/32), element i -> tile position 32*mt + m, weight row
-    // 8*(i/4) + 4*h + (i%4) of the n-tile.  A lane holds four runs of 4
-    // consecutive output columns of one position, each stored at once (8
-    // bytes of bf16, 16 of fp32), and the lane pair (m, m+32) writes 8
-    // consecutive columns.  The stores go through a buffer descriptor over
-    // the tile's rows, with 32-bit offsets; rows past the tile's positions
-    // fall outside it and are dropped.  H and I are multiples of 64, so a
-    // wave's columns (32 of gate/up, 64 of down, from a multiple of 32 / 64)
-    // are in range all or none: one wave-uniform test (a lane-dependent one
-    // around each store makes the compiler take the tile for divergent).
-    const int wvs = __builtin_amdgcn_readfirstlane(wv);
+    // ---- epilogue, straight from the accumulators, through buffer
+    // descriptors over the tile's rows (32-bit offsets; rows past the tile's
+    // positions fall outside them and are dropped).
     if constexpr (kGateUp) {
-        // act[p][i] = bf16(silu(gate) * up)
+        // act[p][i] = bf16(silu(gate) * up).  The weights are the MFMAs' A
+        // operand, so D is the tile transposed: lane (m = lane%32, h =
+        // lane/32), element i -> tile position 32*mt + m, weight row
+        // 8*(i/4) + 4*h + (i%4) of the n-tile; a lane holds four runs of 4
+        // consecutive columns of one position, stored 8 bytes at a time with
+        // the hardware's pair conversion to bf16.  I is a multiple of 64, so
+        // a wave's 32 columns (from a multiple of 32) are in range all or
+        // none: one wave-uniform test (a lane-dependent one around each store
+        // makes the compiler take the tile for divergent).
+        const int wvs = __builtin_amdgcn_readfirstlane(wv);
         const int i0 = n0 + 32 * wvs;             // the wave's first column; lane runs at +4h+8g
         const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
             (void*)((uint16_t*)dst + (int64_t)(ti.p0 + ti.m0) * I), 0, nvalid * I * 2, kBufWord3);
@@ -1280,28 +1287,27 @@ __device__ __forceinline__ void ring_tile_body(const lutmoe_moe_desc& d, const u
             }
         }
     } else {
-        // y[p][h] = acc * routing weight (fp32), K split z into its own y
-        const int h0 = n0 + 64 * wvs;             // the wave's first column; lane runs at +4h+32nt+8g
+        // y[p][h] = acc * routing weight (fp32), K split z into its own y.  D
+        // layout: lane (n = lane%32, h = lane/32), element i -> row m =
+        // 8*(i/4) + 4*h + (i%4), column n: each store writes 32 consecutive
+        // columns (128 bytes) of two rows.
+        const int h0 = n0 + 64 * wv + bn;
         const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
             (void*)((float*)dst + ti.z * split_stride + (int64_t)(ti.p0 + ti.m0) * H), 0, nvalid * H * 4, kBufWord3);
-        if (h0 < H) {
+        const uint32_t vo = (uint32_t)(4 * bh * H + h0) * 4u;
 #pragma unroll
-            for (int mt = 0; mt < NMT; ++mt) {
-                const float pw = s_pw[mt * 32 + bn];
-                const uint32_t ro = ((uint32_t)(mt * 32 + bn) * (uint32_t)H + (uint32_t)(h0 + 4 * bh)) * 4u;
+        for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int mrow = mt * 32 + 8 * (i >> 2) + (i & 3);
+                const float pw = s_pw[min(mrow + 4 * bh, kBM - 1)];
 #pragma unroll
                 for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-                    for (int g = 0; g < 4; ++g) {
-                        const u32x4_t v = {__float_as_uint(acc[mt][nt][4 * g] * pw),
-                                           __float_as_uint(acc[mt][nt][4 * g + 1] * pw),
-                                           __float_as_uint(acc[mt][nt][4 * g + 2] * pw),
-                                           __float_as_uint(acc[mt][nt][4 * g + 3] * pw)};
-                        __builtin_amdgcn_raw_buffer_store_b128(v, rs, (int)(ro + 128u * (uint32_t)nt + 32u * (uint32_t)g),
-                                                               0, 0);
-                    }
+                    if (h0 + 32 * nt < H)
+                        __builtin_amdgcn_raw_buffer_store_b32(
+                            __float_as_uint(acc[mt][nt][i] * pw), rs,
+                            (int)(vo + (uint32_t)mrow * (uint32_t)H * 4u + 128u * (uint32_t)nt), 0, 0);
             }
-        }
     }
 }
 
