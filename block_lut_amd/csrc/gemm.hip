@@ -17,7 +17,9 @@
 // SDWA add and a ds_read_u16 per weight; tiles of at most 64 positions look
 // the tables up in registers instead).
 //   stage 1 (gate_up): n-tile 0 = gate rows i0+32w.., n-tile 1 = up rows
-//     I+i0+32w..; epilogue act = bf16(silu(g) * u) per position.
+//     I+i0+32w..; epilogue act = bf16(silu(g) * u) per position.  Its MFMAs
+//     take the weights as the A operand, so a lane's accumulators hold runs
+//     of 4 output columns of one position (8-byte bf16 stores).
 //   stage 2 (down): n-tiles = rows h0+64w.., +32; epilogue y_pos[p][h] =
 //     acc * routing weight (fp32), summed per token by the combine kernel.
 // prefill_ref_kernel (REF stacks the ring cannot address) stages its
