@@ -10,7 +10,7 @@ import pytest
 
 import oracle as O
 from lutmoe_testutil import (BL4Expertset, NestedExpertset, RefExpertset, bf16_bits, golden_codebook,
-                             rel_maxabs, to_dev_bf16, to_dev_f16)
+                             rel_excess_bf16, rel_maxabs, to_dev_bf16, to_dev_f16)
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-3
@@ -509,6 +509,36 @@ def test_moe_layer_skewed_routing(gpu, fmt, T):
                           torch.from_numpy(rids).to(gpu), out_dtype=torch.float32, path=1)
     ref = O.moe_layer(xb, rids, rw, f13, f2, shared=[])
     assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
+
+
+@pytest.mark.parametrize("T,path,out_bf16", [(3, 1, False), (40, 2, False), (40, 2, True)])
+def test_moe_layer_max_slots(gpu, T, path, out_bf16):
+    """k + shared experts = 16, the entry points' maximum: each token's 16 positions meet in
+    the combine kernel (the prefill path's, and the decode path's from three tokens on),
+    with some routed pairs dropped (id -1: no position, skipped by the combine).  The
+    oracle takes a dropped pair as expert 0 at weight 0, which adds exactly nothing."""
+    import torch
+    from block_lut_amd import ops
+    from block_lut_amd.formats import MoEWeights
+    E, S, k, H, I = 24, 4, 12, 256, 192
+    w13, w2 = _moe_case("bl4", E, S, H, I, seed=130 + T)
+    moe = MoEWeights(w13.stack(gpu), w2.stack(gpu), H, I, E, S)
+    rng = np.random.default_rng(1300 + T)
+    xb = _x(rng, T, H)
+    rids = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
+    rids[::3, 5] = -1                     # one dropped pair in every third token
+    rids[1, [0, 7]] = -1                  # two in token 1
+    rw = rng.uniform(0.05, 1.0, size=(T, k)).astype(np.float32)
+    out = ops.moe_forward(moe, to_dev_bf16(xb, gpu), torch.from_numpy(rw).to(gpu),
+                          torch.from_numpy(rids).to(gpu),
+                          out_dtype=torch.bfloat16 if out_bf16 else torch.float32, path=path)
+    keep = rids >= 0
+    ref = O.moe_layer(xb, np.where(keep, rids, 0), np.where(keep, rw, 0.0).astype(np.float32),
+                      w13.deq_f32, w2.deq_f32, shared=[(w13.deq_f32(E + s), w2.deq_f32(E + s)) for s in range(S)])
+    if out_bf16:
+        assert rel_excess_bf16(O.bf16_to_f32(bf16_bits(out)), ref) <= TOL
+    else:
+        assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
 
 
 @pytest.mark.parametrize("fmt", ["bl4", "ref", "nested"])
