@@ -1015,6 +1015,45 @@ __device__ __forceinline__ void expert_rows8(const lutmoe_weights& w, int e, con
     }
 }
 
+// Pass width: f(PassW<N>{}, n) runs one pass of n tokens with register
+// arrays for N.  A pass of exactly one (two) tokens runs at N = 1 (2), any
+// other at N = TB: the dot products of a token past n would otherwise still
+// be computed (the compiler turns the per-token guard into selects), and in
+// skewed routing most chunks hold one or two tokens.  n is made wave-uniform
+// so that the choice is one scalar branch per pass (BL4, same box: T = 8/16/32
+// 62.4/94.7/150.6 -> 61.2/93.7/147.7 us).  kNarrow = false keeps N = TB and
+// the pass as it was: for REF, whose rows compute the reference's one-token
+// product order at N = 1 and its dequantised-weight order above (chosen by the
+// layer's token count), and for NestedLUT, whose kernels hold three tiers'
+// code and measured slower with three pass widths each (T = 16 tier workload
+// 121 -> 123 us) and with only the uniform token count (121 -> 128 us: the
+// per-token guards then become branches instead of selects).
+template <int N>
+struct PassW {
+    static constexpr int value = N;
+};
+template <int TB, bool kNarrow, class F>
+__device__ __forceinline__ void by_pass_width(int nt, F&& f) {
+    if constexpr (!kNarrow) {
+        f(PassW<TB>{}, nt);
+        return;
+    }
+    nt = __builtin_amdgcn_readfirstlane(nt);
+    if constexpr (TB >= 2) {
+        if (nt == 1) {
+            f(PassW<1>{}, 1);
+            return;
+        }
+    }
+    if constexpr (TB >= 4) {
+        if (nt == 2) {
+            f(PassW<2>{}, 2);
+            return;
+        }
+    }
+    f(PassW<TB>{}, nt);
+}
+
 // Gate/up for one routing view: CTA (x, y) covers 4*kGuWaves intermediate
 // indices of active slot y, wave wv 4 of them (4 gate rows + 4 up rows);
 // SwiGLU of the two projections -> act (bf16).  One-wave CTAs (16 KB of
@@ -1036,31 +1075,34 @@ __device__ __forceinline__ void gate_up_body(const DecodeArgs& A, const RV& rv, 
         rows[4 + j] = I + i;
     }
     uint8_t* slot = s_slot + wv * kSlot;
+    constexpr bool kNarrow = kFmt == LUTMOE_FMT_BL4;
     for (int tb = 0; tb < sl.n; tb += TB) {
-        const int nt = min(TB, sl.n - tb);
-        const uint16_t* xrow[TB];
+        by_pass_width<TB, kNarrow>(min(TB, sl.n - tb), [&](auto W, int nt) __attribute__((always_inline)) {
+            constexpr int N = decltype(W)::value;
+            const uint16_t* xrow[N];
 #pragma unroll
-        for (int t = 0; t < TB; ++t) {
-            const int tok = rv.pair_at(sl.p0 + tb + min(t, nt - 1)) / ke;
-            xrow[t] = A.x + (int64_t)min(max(tok, 0), A.T - 1) * H;   // in bounds whatever the routing holds
-        }
-        float acc[kRows][TB];
+            for (int t = 0; t < N; ++t) {
+                const int tok = rv.pair_at(sl.p0 + tb + min(t, nt - 1)) / ke;
+                xrow[t] = A.x + (int64_t)min(max(tok, 0), A.T - 1) * H;   // in bounds whatever the routing holds
+            }
+            float acc[kRows][N];
 #pragma unroll
-        for (int r = 0; r < kRows; ++r)
+            for (int r = 0; r < kRows; ++r)
 #pragma unroll
-            for (int t = 0; t < TB; ++t) acc[r][t] = 0.f;
-        expert_rows8<kFmt, TB>(A.d.w13, sl.e, rows, H, lane, slot, xrow, nt, acc);
-        const int j = lane >> 3;
+                for (int t = 0; t < N; ++t) acc[r][t] = 0.f;
+            expert_rows8<kFmt, N>(A.d.w13, sl.e, rows, H, lane, slot, xrow, nt, acc);
+            const int j = lane >> 3;
 #pragma unroll
-        for (int t = 0; t < TB; ++t) {
-            float v[kRows];
+            for (int t = 0; t < N; ++t) {
+                float v[kRows];
 #pragma unroll
-            for (int r = 0; r < kRows; ++r) v[r] = acc[r][t];
-            const float g = wave_reduce8(v);       // lane l: row l >> 3 (gate j for l < 32)
-            const float u = from_upper_half(g);    // up row j
-            if (lane < 32 && (lane & 7) == 0 && t < nt && i0 + j < I)
-                A.act[(int64_t)(sl.p0 + tb + t) * I + i0 + j] = (uint16_t)f32_to_bf16(silu_mul(g, u));
-        }
+                for (int r = 0; r < kRows; ++r) v[r] = acc[r][t];
+                const float g = wave_reduce8(v);       // lane l: row l >> 3 (gate j for l < 32)
+                const float u = from_upper_half(g);    // up row j
+                if (lane < 32 && (lane & 7) == 0 && t < nt && i0 + j < I)
+                    A.act[(int64_t)(sl.p0 + tb + t) * I + i0 + j] = (uint16_t)f32_to_bf16(silu_mul(g, u));
+            }
+        });
     }
 }
 
@@ -1150,31 +1192,33 @@ __device__ __forceinline__ void gate_up_body4(const DecodeArgs& A, const RV& rv,
     const uint8_t* codes = (const uint8_t*)A.d.w13.codes + sl.e * per;
     const uint8_t* tabs = (const uint8_t*)A.d.w13.tables + sl.e * per;
     for (int tb = 0; tb < sl.n; tb += TB) {
-        const int nt = min(TB, sl.n - tb);
-        // the positions' pairs first, all in flight together
-        int pr[TB];
+        by_pass_width<TB, true>(min(TB, sl.n - tb), [&](auto W, int nt) __attribute__((always_inline)) {
+            constexpr int N = decltype(W)::value;
+            // the positions' pairs first, all in flight together
+            int pr[N];
 #pragma unroll
-        for (int t = 0; t < TB; ++t) pr[t] = rv.pair_at(sl.p0 + tb + min(t, nt - 1));
-        __builtin_amdgcn_sched_barrier(0);
-        const uint16_t* xrow[TB];
+            for (int t = 0; t < N; ++t) pr[t] = rv.pair_at(sl.p0 + tb + min(t, nt - 1));
+            __builtin_amdgcn_sched_barrier(0);
+            const uint16_t* xrow[N];
 #pragma unroll
-        for (int t = 0; t < TB; ++t) xrow[t] = A.x + (int64_t)min(max(pr[t] / ke, 0), A.T - 1) * H;
-        float acc[4][TB];
+            for (int t = 0; t < N; ++t) xrow[t] = A.x + (int64_t)min(max(pr[t] / ke, 0), A.T - 1) * H;
+            float acc[4][N];
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
+            for (int r = 0; r < 4; ++r)
 #pragma unroll
-            for (int t = 0; t < TB; ++t) acc[r][t] = 0.f;
-        bl4_rows4<TB>(codes, tabs, rows, H, lane, slot, xrow, nt, acc);
+                for (int t = 0; t < N; ++t) acc[r][t] = 0.f;
+            bl4_rows4<N>(codes, tabs, rows, H, lane, slot, xrow, nt, acc);
 #pragma unroll
-        for (int t = 0; t < TB; ++t) {
-            const float g0 = wave_reduce(acc[0][t]), g1 = wave_reduce(acc[1][t]);
-            const float u0 = wave_reduce(acc[2][t]), u1 = wave_reduce(acc[3][t]);
-            if (lane == 0 && t < nt) {
-                uint16_t* a = A.act + (int64_t)(sl.p0 + tb + t) * I;
-                a[i0] = (uint16_t)f32_to_bf16(silu_mul(g0, u0));
-                if (i0 + 1 < I) a[i0 + 1] = (uint16_t)f32_to_bf16(silu_mul(g1, u1));
+            for (int t = 0; t < N; ++t) {
+                const float g0 = wave_reduce(acc[0][t]), g1 = wave_reduce(acc[1][t]);
+                const float u0 = wave_reduce(acc[2][t]), u1 = wave_reduce(acc[3][t]);
+                if (lane == 0 && t < nt) {
+                    uint16_t* a = A.act + (int64_t)(sl.p0 + tb + t) * I;
+                    a[i0] = (uint16_t)f32_to_bf16(silu_mul(g0, u0));
+                    if (i0 + 1 < I) a[i0 + 1] = (uint16_t)f32_to_bf16(silu_mul(g1, u1));
+                }
             }
-        }
+        });
     }
 }
 
@@ -1795,33 +1839,36 @@ __global__ __launch_bounds__(256, TB <= 2 ? 3 : 2) void bl4_decode_down_y(Decode
 #pragma unroll
     for (int r = 0; r < kRows; ++r) rows[r] = min(h0 + r, H - 1);
     uint8_t* slot = s_slot + wv * kSlot;
+    constexpr bool kNarrow = kFmt == LUTMOE_FMT_BL4;
     for (int tb = 0; tb < sl.n; tb += TB) {
-        const int nt = min(TB, sl.n - tb);
-        const uint16_t* xrow[TB];
+        by_pass_width<TB, kNarrow>(min(TB, sl.n - tb), [&](auto W, int nt) __attribute__((always_inline)) {
+            constexpr int N = decltype(W)::value;
+            const uint16_t* xrow[N];
 #pragma unroll
-        for (int t = 0; t < TB; ++t) xrow[t] = A.act + (int64_t)(sl.p0 + tb + min(t, nt - 1)) * I;
-        float acc[kRows][TB];
+            for (int t = 0; t < N; ++t) xrow[t] = A.act + (int64_t)(sl.p0 + tb + min(t, nt - 1)) * I;
+            float acc[kRows][N];
 #pragma unroll
-        for (int r = 0; r < kRows; ++r)
+            for (int r = 0; r < kRows; ++r)
 #pragma unroll
-            for (int t = 0; t < TB; ++t) acc[r][t] = 0.f;
-        // the positions' routing weights (one load each, from the positions'
-        // weight array) issued ahead of the weight loads, which hide them
-        float pwv[TB];
+                for (int t = 0; t < N; ++t) acc[r][t] = 0.f;
+            // the positions' routing weights (one load each, from the positions'
+            // weight array) issued ahead of the weight loads, which hide them
+            float pwv[N];
 #pragma unroll
-        for (int t = 0; t < TB; ++t) pwv[t] = rv.weight_at(sl.p0 + tb + min(t, nt - 1));
-        expert_rows8<kFmt, TB>(A.d.w2, sl.e, rows, I, lane, slot, xrow, nt, acc);
+            for (int t = 0; t < N; ++t) pwv[t] = rv.weight_at(sl.p0 + tb + min(t, nt - 1));
+            expert_rows8<kFmt, N>(A.d.w2, sl.e, rows, I, lane, slot, xrow, nt, acc);
 #pragma unroll
-        for (int t = 0; t < TB; ++t) {
-            const int p = sl.p0 + tb + min(t, nt - 1);
-            const float pw = pwv[t];
-            float v[kRows];
+            for (int t = 0; t < N; ++t) {
+                const int p = sl.p0 + tb + min(t, nt - 1);
+                const float pw = pwv[t];
+                float v[kRows];
 #pragma unroll
-            for (int r = 0; r < kRows; ++r) v[r] = acc[r][t];
-            const float yv = wave_reduce8(v);   // lane l: row l >> 3
-            const int r = lane >> 3;
-            if ((lane & 7) == 0 && t < nt && h0 + r < H) y[(int64_t)p * H + h0 + r] = yv * pw;
-        }
+                for (int r = 0; r < kRows; ++r) v[r] = acc[r][t];
+                const float yv = wave_reduce8(v);   // lane l: row l >> 3
+                const int r = lane >> 3;
+                if ((lane & 7) == 0 && t < nt && h0 + r < H) y[(int64_t)p * H + h0 + r] = yv * pw;
+            }
+        });
     }
 }
 
@@ -1848,25 +1895,28 @@ __global__ __launch_bounds__(256, TB <= 2 ? 4 : 2) void bl4_decode_down_y4(Decod
     const uint8_t* codes = (const uint8_t*)A.d.w2.codes + sl.e * per;
     const uint8_t* tabs = (const uint8_t*)A.d.w2.tables + sl.e * per;
     for (int tb = 0; tb < sl.n; tb += TB) {
-        const int nt = min(TB, sl.n - tb);
-        const uint16_t* xrow[TB];
+        by_pass_width<TB, true>(min(TB, sl.n - tb), [&](auto W, int nt) __attribute__((always_inline)) {
+            constexpr int N = decltype(W)::value;
+            const uint16_t* xrow[N];
 #pragma unroll
-        for (int t = 0; t < TB; ++t) xrow[t] = A.act + (int64_t)(sl.p0 + tb + min(t, nt - 1)) * I;
-        float acc[4][TB];
+            for (int t = 0; t < N; ++t) xrow[t] = A.act + (int64_t)(sl.p0 + tb + min(t, nt - 1)) * I;
+            float acc[4][N];
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
+            for (int r = 0; r < 4; ++r)
 #pragma unroll
-            for (int t = 0; t < TB; ++t) acc[r][t] = 0.f;
-        float pwv[TB];
+                for (int t = 0; t < N; ++t) acc[r][t] = 0.f;
+            float pwv[N];
 #pragma unroll
-        for (int t = 0; t < TB; ++t) pwv[t] = rv.weight_at(sl.p0 + tb + min(t, nt - 1));
-        bl4_rows4<TB>(codes, tabs, rows, I, lane, s_slot[wv], xrow, nt, acc);
+            for (int t = 0; t < N; ++t) pwv[t] = rv.weight_at(sl.p0 + tb + min(t, nt - 1));
+            bl4_rows4<N>(codes, tabs, rows, I, lane, s_slot[wv], xrow, nt, acc);
 #pragma unroll
-        for (int t = 0; t < TB; ++t) {
-            const float yv = wave_reduce4(acc[0][t], acc[1][t], acc[2][t], acc[3][t]);   // lane 16r: row r
-            const int r = lane >> 4;
-            if ((lane & 15) == 0 && t < nt && h0 + r < H) y[(int64_t)(sl.p0 + tb + t) * H + h0 + r] = yv * pwv[t];
-        }
+            for (int t = 0; t < N; ++t) {
+                const float yv = wave_reduce4(acc[0][t], acc[1][t], acc[2][t], acc[3][t]);   // lane 16r: row r
+                const int r = lane >> 4;
+                if ((lane & 15) == 0 && t < nt && h0 + r < H)
+                    y[(int64_t)(sl.p0 + tb + t) * H + h0 + r] = yv * pwv[t];
+            }
+        });
     }
 }
 
