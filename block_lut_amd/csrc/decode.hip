@@ -790,7 +790,9 @@ struct Rows8N {
     u32x4_t tw[kRows];
 };
 
-template <int kBits>
+// kRegTab: each lane loads its block's whole table (b <= 3: 2^(b+1) <= 16
+// bytes) for register lookups instead of its share of it.
+template <int kBits, bool kRegTab = false>
 __device__ __forceinline__ void load_rows8n(const NestedView& v, const int (&rows)[kRows], int K, int cc,
                                             int lane, Rows8N& b) {
     const bool ok = cc * kWChunk + 32 * lane < K;
@@ -818,8 +820,13 @@ __device__ __forceinline__ void load_rows8n(const NestedView& v, const int (&row
             b.f2[r] = 0u;
             b.f3[r] = 0u;
         }
-        const uint32_t tofs = ((i0 >> 6) << (v.bits + 1)) + ((uint32_t)(lane & 1) << v.bits);
-        b.tw[r] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(v.table, (int)tofs, 0, 0));
+        const uint32_t tofs = ((i0 >> 6) << (v.bits + 1)) + (kRegTab ? 0u : (uint32_t)(lane & 1) << v.bits);
+        if constexpr (kRegTab && kBits == 2) {   // the 8-byte table only
+            const auto q = __builtin_amdgcn_raw_buffer_load_b64(v.table, (int)tofs, 0, 0);
+            b.tw[r] = u32x4_t{q[0], q[1], 0u, 0u};
+        } else {
+            b.tw[r] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(v.table, (int)tofs, 0, 0));
+        }
     }
 }
 
@@ -875,6 +882,69 @@ __device__ __forceinline__ void nested_rows8(const NestedView& v, const int (&ro
     if (v.bits == 2) nested_rows8_tier<TB, 2>(v, rows, K, lane, slot, xrow, nt, acc);
     else if (v.bits == 3) nested_rows8_tier<TB, 3>(v, rows, K, lane, slot, xrow, nt, acc);
     else nested_rows8_tier<TB, 4>(v, rows, K, lane, slot, xrow, nt, acc);
+}
+
+// Tiers of 2 and 3 bits looked up in registers: the lane's block table (at
+// most 8 entries; a 2-bit table's upper four are zero and never selected) as
+// byte planes, one v_perm_b32 per plane and four
+// codes (regtab_lookup8), so these experts use no LDS.  The pairs and the
+// order of the dot products are those of the LDS lookup (bit-identical sums).
+template <int TB>
+__device__ __forceinline__ void compute_rows8n_reg(const Rows8N& b, const uint32_t (&xs)[TB][16], bool ok, int nt,
+                                                   float (&acc)[kRows][TB]) {
+    const uint32_t m = ok ? ~0u : 0u;   // lanes past K: zero tables
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+        __builtin_amdgcn_sched_barrier(0);   // row by row, as the LDS path (register pressure)
+        const uint32_t T[4] = {b.tw[r][0] & m, b.tw[r][1] & m, b.tw[r][2] & m, b.tw[r][3] & m};
+        uint32_t lo[2], hi[2];
+        table_planes<3>(T, lo, hi);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const u32x4_t pr = regtab_lookup8<3>(lo, hi, nested_code8<3>(b.f01[r][0], b.f01[r][1], b.f2[r], 0u, j));
+#pragma unroll
+            for (int t = 0; t < TB; ++t) {
+                if (t < nt) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[r][t] = dot2_bf16(pr[i], xs[t][4 * j + i], acc[r][t]);
+                }
+            }
+        }
+    }
+}
+
+// One-token passes (most passes of skewed routing) look the 2- and 3-bit
+// tiers up in registers, with no LDS: one code path for both (a 2-bit group's
+// missing bit-2 word is zero, so nested_code8<3> yields its codes; the loads
+// keep the tier's own width, so nothing past the expert's bytes is read).
+// The 4-bit tier and wider passes keep the LDS lookups, one code path per
+// tier: merging tiers behind one load raises the register count of the
+// four-token pass, whose register lookups would spill.
+__device__ __forceinline__ void nested_rows8_reg(const NestedView& v, const int (&rows)[kRows], int K, int lane,
+                                                 const uint16_t* const (&xrow)[1], int nt, float (&acc)[kRows][1]) {
+    const int nch = (K + kWChunk - 1) / kWChunk;
+    for (int cc = 0; cc < nch; ++cc) {
+        Rows8N b;
+        uint32_t xs[1][16];
+        load_x8<1>(xrow, K, cc, lane, nt, xs);
+        __builtin_amdgcn_sched_barrier(0);
+        if (v.bits == 3) load_rows8n<3, true>(v, rows, K, cc, lane, b);
+        else load_rows8n<2, true>(v, rows, K, cc, lane, b);
+        __builtin_amdgcn_sched_barrier(0);
+        compute_rows8n_reg<1>(b, xs, cc * kWChunk + 32 * lane < K, nt, acc);
+    }
+}
+
+template <int TB>
+__device__ __forceinline__ void nested_rows8_any(const NestedView& v, const int (&rows)[kRows], int K, int lane,
+                                                 uint8_t* slot, const uint16_t* const (&xrow)[TB], int nt,
+                                                 float (&acc)[kRows][TB]) {
+    if constexpr (TB == 1) {
+        if (v.bits == 4) nested_rows8_tier<1, 4>(v, rows, K, lane, slot, xrow, nt, acc);
+        else nested_rows8_reg(v, rows, K, lane, xrow, nt, acc);
+    } else {
+        nested_rows8<TB>(v, rows, K, lane, slot, xrow, nt, acc);
+    }
 }
 
 // ---- REF experts (the reference's uint8 codes, bf16 absmax per block_size
@@ -1005,7 +1075,7 @@ __device__ __forceinline__ void expert_rows8(const lutmoe_weights& w, int e, con
                                              int lane, uint8_t* slot, const uint16_t* const (&xrow)[TB], int nt,
                                              float (&acc)[kRows][TB]) {
     if constexpr (kFmt == LUTMOE_FMT_NESTED) {
-        nested_rows8<TB>(nested_view(w, e), rows, K, lane, slot, xrow, nt, acc);
+        nested_rows8_any<TB>(nested_view(w, e), rows, K, lane, slot, xrow, nt, acc);
     } else if constexpr (kFmt == LUTMOE_FMT_REF) {
         ref_rows8<TB>(w, e, rows, K, lane, slot, xrow, nt, acc);
     } else {
@@ -1016,42 +1086,39 @@ __device__ __forceinline__ void expert_rows8(const lutmoe_weights& w, int e, con
 }
 
 // Pass width: f(PassW<N>{}, n) runs one pass of n tokens with register
-// arrays for N.  A pass of exactly one (two) tokens runs at N = 1 (2), any
-// other at N = TB: the dot products of a token past n would otherwise still
-// be computed (the compiler turns the per-token guard into selects), and in
-// skewed routing most chunks hold one or two tokens.  n is made wave-uniform
-// so that the choice is one scalar branch per pass (BL4, same box: T = 8/16/32
-// 62.4/94.7/150.6 -> 61.2/93.7/147.7 us).  kNarrow = false keeps N = TB and
-// the pass as it was: for REF, whose rows compute the reference's one-token
-// product order at N = 1 and its dequantised-weight order above (chosen by the
-// layer's token count), and for NestedLUT, whose kernels hold three tiers'
-// code and measured slower with three pass widths each (T = 16 tier workload
-// 121 -> 123 us) and with only the uniform token count (121 -> 128 us: the
-// per-token guards then become branches instead of selects).
+// arrays for N.  The dot products of a token past n would otherwise still be
+// computed (the compiler turns the per-token guard into selects), and in
+// skewed routing most chunks hold one or two tokens.  Modes:
+//   kPassAll  N = TB always: REF, whose rows compute the reference's
+//             one-token product order at N = 1 and its dequantised-weight
+//             order above, chosen by the layer's token count;
+//   kPass14   N = 1 for one token, else TB with n as it was (NestedLUT);
+//   kPass124  N = 1 or 2 for exactly that many tokens, else TB, with n made
+//             wave-uniform (BL4, same box: T = 8/16/32 62.4/94.7/150.6 ->
+//             61.2/93.7/147.7 us).
+// The choice is one scalar branch per pass.
 template <int N>
 struct PassW {
     static constexpr int value = N;
 };
-template <int TB, bool kNarrow, class F>
+enum { kPassAll, kPass14, kPass124 };
+template <int TB, int kMode, class F>
 __device__ __forceinline__ void by_pass_width(int nt, F&& f) {
-    if constexpr (!kNarrow) {
+    if constexpr (kMode == kPassAll || TB == 1) {
         f(PassW<TB>{}, nt);
-        return;
+    } else if constexpr (kMode == kPass14) {
+        if (__builtin_amdgcn_readfirstlane(nt) == 1) f(PassW<1>{}, 1);
+        else f(PassW<TB>{}, nt);
+    } else {
+        nt = __builtin_amdgcn_readfirstlane(nt);
+        if (nt == 1) f(PassW<1>{}, 1);
+        else if (TB >= 4 && nt == 2) f(PassW<(TB >= 4 ? 2 : TB)>{}, 2);
+        else f(PassW<TB>{}, nt);
     }
-    nt = __builtin_amdgcn_readfirstlane(nt);
-    if constexpr (TB >= 2) {
-        if (nt == 1) {
-            f(PassW<1>{}, 1);
-            return;
-        }
-    }
-    if constexpr (TB >= 4) {
-        if (nt == 2) {
-            f(PassW<2>{}, 2);
-            return;
-        }
-    }
-    f(PassW<TB>{}, nt);
+}
+template <int kFmt>
+constexpr int pass_mode() {
+    return kFmt == LUTMOE_FMT_BL4 ? kPass124 : kFmt == LUTMOE_FMT_NESTED ? kPass14 : kPassAll;
 }
 
 // Gate/up for one routing view: CTA (x, y) covers 4*kGuWaves intermediate
@@ -1075,9 +1142,8 @@ __device__ __forceinline__ void gate_up_body(const DecodeArgs& A, const RV& rv, 
         rows[4 + j] = I + i;
     }
     uint8_t* slot = s_slot + wv * kSlot;
-    constexpr bool kNarrow = kFmt == LUTMOE_FMT_BL4;
     for (int tb = 0; tb < sl.n; tb += TB) {
-        by_pass_width<TB, kNarrow>(min(TB, sl.n - tb), [&](auto W, int nt) __attribute__((always_inline)) {
+        by_pass_width<TB, pass_mode<kFmt>()>(min(TB, sl.n - tb), [&](auto W, int nt) __attribute__((always_inline)) {
             constexpr int N = decltype(W)::value;
             const uint16_t* xrow[N];
 #pragma unroll
@@ -1192,7 +1258,7 @@ __device__ __forceinline__ void gate_up_body4(const DecodeArgs& A, const RV& rv,
     const uint8_t* codes = (const uint8_t*)A.d.w13.codes + sl.e * per;
     const uint8_t* tabs = (const uint8_t*)A.d.w13.tables + sl.e * per;
     for (int tb = 0; tb < sl.n; tb += TB) {
-        by_pass_width<TB, true>(min(TB, sl.n - tb), [&](auto W, int nt) __attribute__((always_inline)) {
+        by_pass_width<TB, kPass124>(min(TB, sl.n - tb), [&](auto W, int nt) __attribute__((always_inline)) {
             constexpr int N = decltype(W)::value;
             // the positions' pairs first, all in flight together
             int pr[N];
@@ -1839,9 +1905,8 @@ __global__ __launch_bounds__(256, TB <= 2 ? 3 : 2) void bl4_decode_down_y(Decode
 #pragma unroll
     for (int r = 0; r < kRows; ++r) rows[r] = min(h0 + r, H - 1);
     uint8_t* slot = s_slot + wv * kSlot;
-    constexpr bool kNarrow = kFmt == LUTMOE_FMT_BL4;
     for (int tb = 0; tb < sl.n; tb += TB) {
-        by_pass_width<TB, kNarrow>(min(TB, sl.n - tb), [&](auto W, int nt) __attribute__((always_inline)) {
+        by_pass_width<TB, pass_mode<kFmt>()>(min(TB, sl.n - tb), [&](auto W, int nt) __attribute__((always_inline)) {
             constexpr int N = decltype(W)::value;
             const uint16_t* xrow[N];
 #pragma unroll
@@ -1895,7 +1960,7 @@ __global__ __launch_bounds__(256, TB <= 2 ? 4 : 2) void bl4_decode_down_y4(Decod
     const uint8_t* codes = (const uint8_t*)A.d.w2.codes + sl.e * per;
     const uint8_t* tabs = (const uint8_t*)A.d.w2.tables + sl.e * per;
     for (int tb = 0; tb < sl.n; tb += TB) {
-        by_pass_width<TB, true>(min(TB, sl.n - tb), [&](auto W, int nt) __attribute__((always_inline)) {
+        by_pass_width<TB, kPass124>(min(TB, sl.n - tb), [&](auto W, int nt) __attribute__((always_inline)) {
             constexpr int N = decltype(W)::value;
             const uint16_t* xrow[N];
 #pragma unroll
