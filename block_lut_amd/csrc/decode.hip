@@ -889,8 +889,12 @@ __device__ __forceinline__ void nested_rows8(const NestedView& v, const int (&ro
 // byte planes, one v_perm_b32 per plane and four
 // codes (regtab_lookup8), so these experts use no LDS.  The pairs and the
 // order of the dot products are those of the LDS lookup (bit-identical sums).
+// Every token of the pass is computed (a token past the pass's count repeats
+// its last one and is not stored): per-token guards here become branches
+// that keep the lookups' results live across them, and the four-token pass
+// then spills.
 template <int TB>
-__device__ __forceinline__ void compute_rows8n_reg(const Rows8N& b, const uint32_t (&xs)[TB][16], bool ok, int nt,
+__device__ __forceinline__ void compute_rows8n_reg(const Rows8N& b, const uint32_t (&xs)[TB][16], bool ok,
                                                    float (&acc)[kRows][TB]) {
     const uint32_t m = ok ? ~0u : 0u;   // lanes past K: zero tables
 #pragma unroll
@@ -903,35 +907,30 @@ __device__ __forceinline__ void compute_rows8n_reg(const Rows8N& b, const uint32
         for (int j = 0; j < 4; ++j) {
             const u32x4_t pr = regtab_lookup8<3>(lo, hi, nested_code8<3>(b.f01[r][0], b.f01[r][1], b.f2[r], 0u, j));
 #pragma unroll
-            for (int t = 0; t < TB; ++t) {
-                if (t < nt) {
+            for (int t = 0; t < TB; ++t)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) acc[r][t] = dot2_bf16(pr[i], xs[t][4 * j + i], acc[r][t]);
-                }
-            }
+                for (int i = 0; i < 4; ++i) acc[r][t] = dot2_bf16(pr[i], xs[t][4 * j + i], acc[r][t]);
         }
     }
 }
 
-// One-token passes (most passes of skewed routing) look the 2- and 3-bit
-// tiers up in registers, with no LDS: one code path for both (a 2-bit group's
-// missing bit-2 word is zero, so nested_code8<3> yields its codes; the loads
-// keep the tier's own width, so nothing past the expert's bytes is read).
-// The 4-bit tier and wider passes keep the LDS lookups, one code path per
-// tier: merging tiers behind one load raises the register count of the
-// four-token pass, whose register lookups would spill.
+// The 2- and 3-bit tiers looked up in registers (no LDS), one code path for
+// both (a 2-bit group's missing bit-2 word is zero, so nested_code8<3> yields
+// its codes; the loads keep the tier's own width, so nothing past the
+// expert's bytes is read); the 4-bit tier keeps the LDS lookups.
+template <int TB>
 __device__ __forceinline__ void nested_rows8_reg(const NestedView& v, const int (&rows)[kRows], int K, int lane,
-                                                 const uint16_t* const (&xrow)[1], int nt, float (&acc)[kRows][1]) {
+                                                 const uint16_t* const (&xrow)[TB], int nt, float (&acc)[kRows][TB]) {
     const int nch = (K + kWChunk - 1) / kWChunk;
     for (int cc = 0; cc < nch; ++cc) {
         Rows8N b;
-        uint32_t xs[1][16];
-        load_x8<1>(xrow, K, cc, lane, nt, xs);
+        uint32_t xs[TB][16];
+        load_x8<TB>(xrow, K, cc, lane, nt, xs);
         __builtin_amdgcn_sched_barrier(0);
         if (v.bits == 3) load_rows8n<3, true>(v, rows, K, cc, lane, b);
         else load_rows8n<2, true>(v, rows, K, cc, lane, b);
         __builtin_amdgcn_sched_barrier(0);
-        compute_rows8n_reg<1>(b, xs, cc * kWChunk + 32 * lane < K, nt, acc);
+        compute_rows8n_reg<TB>(b, xs, cc * kWChunk + 32 * lane < K, acc);
     }
 }
 
@@ -939,12 +938,8 @@ template <int TB>
 __device__ __forceinline__ void nested_rows8_any(const NestedView& v, const int (&rows)[kRows], int K, int lane,
                                                  uint8_t* slot, const uint16_t* const (&xrow)[TB], int nt,
                                                  float (&acc)[kRows][TB]) {
-    if constexpr (TB == 1) {
-        if (v.bits == 4) nested_rows8_tier<1, 4>(v, rows, K, lane, slot, xrow, nt, acc);
-        else nested_rows8_reg(v, rows, K, lane, xrow, nt, acc);
-    } else {
-        nested_rows8<TB>(v, rows, K, lane, slot, xrow, nt, acc);
-    }
+    if (v.bits == 4) nested_rows8_tier<TB, 4>(v, rows, K, lane, slot, xrow, nt, acc);
+    else nested_rows8_reg<TB>(v, rows, K, lane, xrow, nt, acc);
 }
 
 // ---- REF experts (the reference's uint8 codes, bf16 absmax per block_size
