@@ -62,7 +62,9 @@ struct RouteOut {
 // heavily routed expert does not hold the layer up behind many passes of
 // TB tokens.  C = TB * round(mean positions per active slot / TB), at least
 // TB: routing where every expert gets about as many positions keeps one chunk
-// per slot.  Stored in the workspace right after the RouteOut copy.
+// per slot.  NestedLUT at two tokens a pass: C = TB (one pass a chunk; its
+// register lookups make a chunk's weights cheaper to read again than to look
+// up twice).  Stored in the workspace right after the RouteOut copy.
 struct RouteChunks {
     int nchunk;
     int ce[kMaxP];                      // expert of chunk c
@@ -566,7 +568,7 @@ __device__ __forceinline__ void put_chunks(const DecodeArgs& A, const RouteOut& 
     const int TB = A.tb;   // tokens per pass
     const int pv = nact > 0 ? R.aoff[nact - 1] + R.an[nact - 1] : 0;
     const int navg = nact > 0 ? (pv + nact - 1) / nact : 1;
-    const int C = TB * max(1, (navg + TB / 2) / TB);
+    const int C = A.d.w13.format == LUTMOE_FMT_NESTED && TB == 2 ? TB : TB * max(1, (navg + TB / 2) / TB);
     const int n = tid < nact ? R.an[tid] : 0;
     const int nc = (n + C - 1) / C;
     const int incl = wave_scan_incl(nc);
@@ -2103,10 +2105,14 @@ __global__ __launch_bounds__(256, 3) void decode_stream_probe(lutmoe_moe_desc d,
 // layer; with the 4-row loops T=17/24/32 from 115/131/150 to 99/121/146 us).
 // Past 16 tokens that holds while the positions per expert stay few (at most
 // 3 on average, P / min(P, E_tot)); few experts holding many tokens each
-// (top-2 of 8) and more than 32 tokens (the GEMV path forced) take 4.  The
-// nested kernels lose with 2-token passes at T=16 (113 -> 136 us) and keep 4.
+// (top-2 of 8) and more than 32 tokens (the GEMV path forced) take 4.
+// NestedLUT takes 2 up to 16 tokens, with chunks of one pass each (the
+// routing kernel's chunking): its kernels then fit three waves a SIMD
+// (T = 16 tier workload 95.6 -> 92.8 us; 2-token passes over 4-token chunks,
+// which look every weight up twice, took 95.5 -> 99.5 us).  REF keeps 4.
 inline int tb_for(int T, int fmt_idx, int P, int E_tot) {
     if (T <= 1) return 1;
+    if (fmt_idx == 1) return T <= 16 ? 2 : 4;
     if (fmt_idx != 0) return T <= 2 ? 2 : 4;
     return T <= 16 || (T <= 32 && P <= 3 * std::min(P, E_tot)) ? 2 : 4;
 }
