@@ -252,11 +252,14 @@ def test_nested_gemv(gpu, bits, M, K, T):
     assert rel_maxabs(y, ref) <= TOL
 
 
-@pytest.mark.parametrize("T,path", [(1, 1), (4, 1), (9, 1), (150, 2), (5, 2)])
+@pytest.mark.parametrize("T,path", [(1, 1), (2, 1), (4, 1), (9, 1), (40, 1), (150, 2), (5, 2)])
 def test_moe_layer_nested_tiers(gpu, T, path):
     """MoE layer over NestedLUT experts of mixed tiers (decode GEMV and the
     grouped MFMA path): routed experts at tiers 2/3/4 and a tier-4 shared
-    expert, against the dense restatement of the tier-b weights."""
+    expert, against the dense restatement of the tier-b weights.  Decode
+    passes: one token (T=1), two tokens with the routing in each wave (T=2),
+    two tokens a pass and chunk (T=4, 9), four tokens a pass with one-token
+    passes beside them (T=40)."""
     import torch
     from block_lut_amd import ops
     from block_lut_amd.formats import MoEWeights
@@ -482,7 +485,7 @@ def test_moe_layer_repeated_ids(gpu, fmt, T, path):
     assert rel_maxabs(out.cpu().numpy(), ref) <= TOL
 
 
-@pytest.mark.parametrize("fmt,T", [("bl4", 16), ("bl4", 40), ("ref", 16), ("nested", 16)])
+@pytest.mark.parametrize("fmt,T", [("bl4", 16), ("bl4", 40), ("ref", 16), ("nested", 16), ("nested", 40)])
 def test_moe_layer_skewed_routing(gpu, fmt, T):
     """Decode with one heavily routed expert: every token picks expert 0 plus k-1 others, so
     expert 0 holds T positions while the mean slot holds about 3, and the routing kernel
