@@ -888,9 +888,9 @@ __device__ __forceinline__ void nested_rows8(const NestedView& v, const int (&ro
 
 // Tiers of 2 and 3 bits looked up in registers: the lane's block table (at
 // most 8 entries; a 2-bit table's upper four are zero and never selected) as
-// byte planes, one v_perm_b32 per plane and four
-// codes (regtab_lookup8), so these experts use no LDS.  The pairs and the
-// order of the dot products are those of the LDS lookup (bit-identical sums).
+// byte planes, one v_perm_b32 per plane and four codes (regtab_lookup8), so
+// these experts use no LDS.  The pairs and the order of the dot products are
+// those of the LDS lookup (bit-identical sums).
 // Every token of the pass is computed (a token past the pass's count repeats
 // its last one and is not stored): per-token guards here become branches
 // that keep the lookups' results live across them, and the four-token pass
@@ -1089,7 +1089,10 @@ __device__ __forceinline__ void expert_rows8(const lutmoe_weights& w, int e, con
 //   kPassAll  N = TB always: REF, whose rows compute the reference's
 //             one-token product order at N = 1 and its dequantised-weight
 //             order above, chosen by the layer's token count;
-//   kPass14   N = 1 for one token, else TB with n as it was (NestedLUT);
+//   kPass14   N = 1 for one token, else TB with n as it was (NestedLUT: a
+//             third width made its kernels too large for the instruction
+//             cache, and a wave-uniform n turned the per-token guards of the
+//             LDS path into branches, both slower);
 //   kPass124  N = 1 or 2 for exactly that many tokens, else TB, with n made
 //             wave-uniform (BL4, same box: T = 8/16/32 62.4/94.7/150.6 ->
 //             61.2/93.7/147.7 us).
