@@ -336,6 +336,12 @@ constexpr int kStages = 3;
 constexpr int kSlotAs = 64 * kBK * 2;              // 8 KB
 constexpr int kSlotBytesS = kSlotAs + 2 * kSlotB;  // 24 KB
 constexpr int kStagesS = 6;
+// A tile's CTA claims its next item (longest first from the launch counter)
+// right after the barrier of its second-to-last K step: that barrier waits
+// for every ring load and no stage is issued after it, so the atomic is the
+// only memory operation in flight (no ring wait counts it), and the CTA that
+// frees up first takes the next item
+constexpr int kClaimLead = 2;
 
 // A-row chunk swizzle: distinct for any 8 consecutive rows, and (r&1, swz)
 // distinct for any 16 consecutive rows.
@@ -912,9 +918,10 @@ __device__ __forceinline__ void ring_prologue(const lutmoe_moe_desc& d, const ui
 }
 
 // One tile whose first stages are in the ring (issued by ring_prologue).
-// Thread 0 claims the next item from the launch's counter when the tile
-// starts (the returned index is published through s_claim in the last K
-// step, where every load has landed anyway); on return `next` is that item's
+// Thread 0 claims the next item from the launch's counter after the barrier
+// of the second-to-last K step (kClaimLead; the returned index is published
+// through s_claim in the last K step), so that the items go out longest
+// first to whichever CTA frees up first; on return `next` is that item's
 // tile and its first stages are issued (when there is one).
 template <bool kGateUp, int kFmt, int NMT, typename NextFn>
 __device__ __forceinline__ void ring_tile_body(const lutmoe_moe_desc& d, const uint16_t* __restrict__ src,
@@ -944,7 +951,7 @@ __device__ __forceinline__ void ring_tile_body(const lutmoe_moe_desc& d, const u
     // are done too), the REF codebook is written
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     int claim = 0;
-    if (ctr && threadIdx.x == 0) claim = atomicAdd(ctr, 1);
+    const int kc = max(0, nkb - kClaimLead);   // the K step that claims the next item
     RingLoader<kGateUp, kFmt> L;
     L.init(d, src, rt, ti, NMT);
     // down projection: tile row tid's routing weight, by its pair index
@@ -1126,6 +1133,7 @@ __device__ __forceinline__ void ring_tile_body(const lutmoe_moe_desc& d, const u
             // MFMAs from registers
             __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0)
             ring_wait_barrier4<kDma>(min(4, nkb - 2 - kb));
+            if (ctr && kb == kc && threadIdx.x == 0) claim = atomicAdd(ctr, 1);
             if constexpr (!kGateUp) {
                 if (kb == 0 && tid < nvalid) pw_row = rt.pair_w[pair];
             }
@@ -1200,6 +1208,7 @@ __device__ __forceinline__ void ring_tile_body(const lutmoe_moe_desc& d, const u
                 // in flight) and every read of this slot is done (its values
                 // are in registers) -> refill it with stage kb+3
                 ring_wait_barrier<kDma>(kb + 2 < nkb ? 1 : 0);
+                if (ctr && kb == kc && threadIdx.x == 0) claim = atomicAdd(ctr, 1);
                 if constexpr (!kGateUp) {
                     if (kb == 0 && tid < nvalid) pw_row = rt.pair_w[pair];
                 }
