@@ -175,6 +175,39 @@ __device__ __forceinline__ u32x4_t regtab_lookup8(const uint32_t* lo, const uint
     return r;
 }
 
+// regtab_lookup8 without its last step: the 8 weights in the order
+// w0, w2, w4, w6, w1, w3, w5, w7 (an MFMA operand whose partner operand holds
+// its 8 k-values in the same order gives the same products)
+template <int B>
+__device__ __forceinline__ u32x4_t regtab_lookup8_eo(const uint32_t* lo, const uint32_t* hi, uint32_t w) {
+    const uint32_t se = w & 0x0f0f0f0fu, so = (w >> 4) & 0x0f0f0f0fu;
+    uint32_t se7 = se, so7 = so, sel_e = 0, sel_o = 0;
+    if constexpr (B == 4) {
+        se7 = se & 0x07070707u;
+        so7 = so & 0x07070707u;
+        sel_e = ((se >> 1) & 0x04040404u) | 0x03020100u;
+        sel_o = ((so >> 1) & 0x04040404u) | 0x03020100u;
+    }
+    const uint32_t le = plane_lookup4<B>(lo, se, se7, sel_e), he = plane_lookup4<B>(hi, se, se7, sel_e);
+    const uint32_t lo_ = plane_lookup4<B>(lo, so, so7, sel_o), ho = plane_lookup4<B>(hi, so, so7, sel_o);
+    u32x4_t r;
+    r[0] = __builtin_amdgcn_perm(he, le, 0x05010400u);    // w0, w2
+    r[1] = __builtin_amdgcn_perm(he, le, 0x07030602u);    // w4, w6
+    r[2] = __builtin_amdgcn_perm(ho, lo_, 0x05010400u);   // w1, w3
+    r[3] = __builtin_amdgcn_perm(ho, lo_, 0x07030602u);   // w5, w7
+    return r;
+}
+// 8 bf16 in column order (dword j = columns 2j, 2j+1) -> the order of
+// regtab_lookup8_eo
+__device__ __forceinline__ u32x4_t eo_order(const u32x4_t& a) {
+    u32x4_t r;
+    r[0] = __builtin_amdgcn_perm(a[1], a[0], 0x05040100u);
+    r[1] = __builtin_amdgcn_perm(a[3], a[2], 0x05040100u);
+    r[2] = __builtin_amdgcn_perm(a[1], a[0], 0x07060302u);
+    r[3] = __builtin_amdgcn_perm(a[3], a[2], 0x07060302u);
+    return r;
+}
+
 __device__ __forceinline__ u32x4_t lookup8_lds(uint32_t w, uint32_t tab) {
     return lookup8_combine(lookup8_issue(w, tab));
 }
