@@ -888,15 +888,16 @@ __device__ __forceinline__ void nested_rows8(const NestedView& v, const int (&ro
 
 // Tiers of 2 and 3 bits looked up in registers: the lane's block table (at
 // most 8 entries; a 2-bit table's upper four are zero and never selected) as
-// byte planes, one v_perm_b32 per plane and four codes (regtab_lookup8), so
-// these experts use no LDS.  The pairs and the order of the dot products are
-// those of the LDS lookup (bit-identical sums).
+// byte planes, one v_perm_b32 per plane and four codes, so these experts use
+// no LDS.  The weights come in regtab_lookup8_eo's order (w0, w2 | w4, w6 |
+// w1, w3 | w5, w7: four v_perm fewer per 8 weights than column order) and
+// meet activations put in the same order once per chunk (xe).
 // Every token of the pass is computed (a token past the pass's count repeats
 // its last one and is not stored): per-token guards here become branches
 // that keep the lookups' results live across them, and the four-token pass
 // then spills.
 template <int TB>
-__device__ __forceinline__ void compute_rows8n_reg(const Rows8N& b, const uint32_t (&xs)[TB][16], bool ok,
+__device__ __forceinline__ void compute_rows8n_reg(const Rows8N& b, const uint32_t (&xe)[TB][16], bool ok,
                                                    float (&acc)[kRows][TB]) {
     const uint32_t m = ok ? ~0u : 0u;   // lanes past K: zero tables
 #pragma unroll
@@ -907,11 +908,11 @@ __device__ __forceinline__ void compute_rows8n_reg(const Rows8N& b, const uint32
         table_planes<3>(T, lo, hi);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const u32x4_t pr = regtab_lookup8<3>(lo, hi, nested_code8<3>(b.f01[r][0], b.f01[r][1], b.f2[r], 0u, j));
+            const u32x4_t pr = regtab_lookup8_eo<3>(lo, hi, nested_code8<3>(b.f01[r][0], b.f01[r][1], b.f2[r], 0u, j));
 #pragma unroll
             for (int t = 0; t < TB; ++t)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) acc[r][t] = dot2_bf16(pr[i], xs[t][4 * j + i], acc[r][t]);
+                for (int i = 0; i < 4; ++i) acc[r][t] = dot2_bf16(pr[i], xe[t][4 * j + i], acc[r][t]);
         }
     }
 }
@@ -932,7 +933,16 @@ __device__ __forceinline__ void nested_rows8_reg(const NestedView& v, const int 
         if (v.bits == 3) load_rows8n<3, true>(v, rows, K, cc, lane, b);
         else load_rows8n<2, true>(v, rows, K, cc, lane, b);
         __builtin_amdgcn_sched_barrier(0);
-        compute_rows8n_reg<TB>(b, xs, cc * kWChunk + 32 * lane < K, acc);
+        uint32_t xe[TB][16];   // the activations in regtab_lookup8_eo's order
+#pragma unroll
+        for (int t = 0; t < TB; ++t)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const u32x4_t o = eo_order(u32x4_t{xs[t][4 * j], xs[t][4 * j + 1], xs[t][4 * j + 2], xs[t][4 * j + 3]});
+#pragma unroll
+                for (int i = 0; i < 4; ++i) xe[t][4 * j + i] = o[i];
+            }
+        compute_rows8n_reg<TB>(b, xe, cc * kWChunk + 32 * lane < K, acc);
     }
 }
 
