@@ -966,6 +966,14 @@ __device__ __forceinline__ void ring_tile_body(const lutmoe_moe_desc& d, const u
         else
             return c[ks];
     };
+    // the same for a tier known at compile time (Bt: 2, 3 or 4): the words
+    // the tier does not have are not read
+    auto nested_code_b = [&](auto Bt, const u32x4_t& c, int ks) __attribute__((always_inline)) {
+        if constexpr (kNested)
+            return nested_code8<decltype(Bt)::value>(c[0], c[1], c[2], c[3], ks);
+        else
+            return c[ks];
+    };
     const int sw = a_swz(bn);   // = a_swz(mt * 32 + bn) for every m-tile
     // A fragments of m-tiles [mt0, mt1) of k-substep ks
     auto frag_a = [&](const uint8_t* sl, int ks, bf16x8_t (&af)[NMT], int mt0, int mt1) __attribute__((always_inline)) {
@@ -1078,14 +1086,14 @@ __device__ __forceinline__ void ring_tile_body(const lutmoe_moe_desc& d, const u
 #pragma unroll
                     for (int nt = 0; nt < 2; ++nt) {
                         const bf16x8_t bfr = __builtin_bit_cast(
-                            bf16x8_t, regtab_lookup8_eo<B>(lo[nt], hi[nt], nested_code(cds[b][nt], ks)));
+                            bf16x8_t, regtab_lookup8_eo<B>(lo[nt], hi[nt], nested_code_b(BC, cds[b][nt], ks)));
                         acc[0][nt] = mma(a0, bfr, acc[0][nt]);
                     }
                 } else {
 #pragma unroll
                     for (int nt = 0; nt < 2; ++nt) {
                         const bf16x8_t bfr = __builtin_bit_cast(
-                            bf16x8_t, regtab_lookup8<B>(lo[nt], hi[nt], nested_code(cds[b][nt], ks)));
+                            bf16x8_t, regtab_lookup8<B>(lo[nt], hi[nt], nested_code_b(BC, cds[b][nt], ks)));
 #pragma unroll
                         for (int mt = 0; mt < NMT; ++mt)
                             acc[mt][nt] = mma(afs[b][ks][mt], bfr, acc[mt][nt]);
