@@ -351,9 +351,15 @@ __device__ __forceinline__ int a_swz(int r) { return ((r >> 1) ^ (r << 2)) & 7; 
 // are scalar adds).  Issued as inline asm so the compiler does not track it:
 // the ring's explicit vmcnt waits and barriers order it, and no
 // compiler-visible global load is in flight between the first of these and
-// the final vmcnt(0).
+// the final vmcnt(0).  The load reads sbase as an SGPR pair, which needs 5
+// wait states after a VALU write of it (or of a dead carry the compiler put
+// there just before computing the base with SALU adds); the compiler does not
+// insert them in front of inline asm, so the load carries them (s_nop 4:
+// DeepSeek T=2048 534.5-544.8 us with it against 534.9-545.3 us without,
+// same box; a build that moved the prefill K loop into a lambda had placed
+// such a carry write four instructions before a ring load).
 __device__ __forceinline__ void dma16(uint32_t voff, const void* sbase, uint32_t m0) {
-    asm volatile("global_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase), "{m0}"(m0) : "memory");
+    asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase), "{m0}"(m0) : "memory");
 }
 
 // Wait until at most `after` ring loads of this thread are in flight (the
@@ -383,10 +389,9 @@ __device__ __forceinline__ void ring_wait_barrier4(int stages_after) {
 // reads sbase as an SGPR pair; a VALU write of an SGPR (v_readlane of a
 // spilled pointer, v_readfirstlane) needs 5 wait states before a VMEM
 // instruction reads it, and the compiler does not insert them in front of
-// inline asm: this rarely issued load carries them itself (s_nop 4).  The
-// ring's dma16 sites have none; the build's ISA check
-// (block_lut_amd/csrc/isa_check.py) verifies every LDS-DMA load of the
-// library.
+// inline asm: this load carries them itself (s_nop 4), as dma16 does; the
+// build's ISA check (block_lut_amd/csrc/isa_check.py) verifies every LDS-DMA
+// load of the library.
 __device__ __forceinline__ void dma4(uint32_t voff, const void* sbase, uint32_t m0) {
     asm volatile("s_nop 4\n\tglobal_load_lds_dword %0, %1" : : "v"(voff), "s"(sbase), "{m0}"(m0) : "memory");
 }
