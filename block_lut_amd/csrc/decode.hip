@@ -896,7 +896,7 @@ __device__ __forceinline__ void nested_rows8(const NestedView& v, const int (&ro
 // its last one and is not stored): per-token guards here become branches
 // that keep the lookups' results live across them, and the four-token pass
 // then spills.
-template <int TB>
+template <int TB, int kBits>
 __device__ __forceinline__ void compute_rows8n_reg(const Rows8N& b, const uint32_t (&xe)[TB][16], bool ok,
                                                    float (&acc)[kRows][TB]) {
     const uint32_t m = ok ? ~0u : 0u;   // lanes past K: zero tables
@@ -905,10 +905,11 @@ __device__ __forceinline__ void compute_rows8n_reg(const Rows8N& b, const uint32
         __builtin_amdgcn_sched_barrier(0);   // row by row, as the LDS path (register pressure)
         const uint32_t T[4] = {b.tw[r][0] & m, b.tw[r][1] & m, b.tw[r][2] & m, b.tw[r][3] & m};
         uint32_t lo[2], hi[2];
-        table_planes<3>(T, lo, hi);
+        table_planes<kBits>(T, lo, hi);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const u32x4_t pr = regtab_lookup8_eo<3>(lo, hi, nested_code8<3>(b.f01[r][0], b.f01[r][1], b.f2[r], 0u, j));
+            const u32x4_t pr =
+                regtab_lookup8_eo<kBits>(lo, hi, nested_code8<kBits>(b.f01[r][0], b.f01[r][1], b.f2[r], 0u, j));
 #pragma unroll
             for (int t = 0; t < TB; ++t)
 #pragma unroll
@@ -917,11 +918,11 @@ __device__ __forceinline__ void compute_rows8n_reg(const Rows8N& b, const uint32
     }
 }
 
-// The 2- and 3-bit tiers looked up in registers (no LDS), one code path for
-// both (a 2-bit group's missing bit-2 word is zero, so nested_code8<3> yields
-// its codes; the loads keep the tier's own width, so nothing past the
-// expert's bytes is read); the 4-bit tier keeps the LDS lookups.
-template <int TB>
+// The 2- and 3-bit tiers looked up in registers (no LDS), one code path per
+// tier (codes and planes of the tier's own width: T = 16 90-92 -> 87-90 us
+// against one path for both; the loads read nothing past the expert's
+// bytes); the 4-bit tier keeps the LDS lookups.
+template <int TB, int kBits>
 __device__ __forceinline__ void nested_rows8_reg(const NestedView& v, const int (&rows)[kRows], int K, int lane,
                                                  const uint16_t* const (&xrow)[TB], int nt, float (&acc)[kRows][TB]) {
     const int nch = (K + kWChunk - 1) / kWChunk;
@@ -930,8 +931,7 @@ __device__ __forceinline__ void nested_rows8_reg(const NestedView& v, const int 
         uint32_t xs[TB][16];
         load_x8<TB>(xrow, K, cc, lane, nt, xs);
         __builtin_amdgcn_sched_barrier(0);
-        if (v.bits == 3) load_rows8n<3, true>(v, rows, K, cc, lane, b);
-        else load_rows8n<2, true>(v, rows, K, cc, lane, b);
+        load_rows8n<kBits, true>(v, rows, K, cc, lane, b);
         __builtin_amdgcn_sched_barrier(0);
         uint32_t xe[TB][16];   // the activations in regtab_lookup8_eo's order
 #pragma unroll
@@ -942,7 +942,7 @@ __device__ __forceinline__ void nested_rows8_reg(const NestedView& v, const int 
 #pragma unroll
                 for (int i = 0; i < 4; ++i) xe[t][4 * j + i] = o[i];
             }
-        compute_rows8n_reg<TB>(b, xe, cc * kWChunk + 32 * lane < K, acc);
+        compute_rows8n_reg<TB, kBits>(b, xe, cc * kWChunk + 32 * lane < K, acc);
     }
 }
 
@@ -951,7 +951,8 @@ __device__ __forceinline__ void nested_rows8_any(const NestedView& v, const int 
                                                  uint8_t* slot, const uint16_t* const (&xrow)[TB], int nt,
                                                  float (&acc)[kRows][TB]) {
     if (v.bits == 4) nested_rows8_tier<TB, 4>(v, rows, K, lane, slot, xrow, nt, acc);
-    else nested_rows8_reg<TB>(v, rows, K, lane, xrow, nt, acc);
+    else if (v.bits == 3) nested_rows8_reg<TB, 3>(v, rows, K, lane, xrow, nt, acc);
+    else nested_rows8_reg<TB, 2>(v, rows, K, lane, xrow, nt, acc);
 }
 
 // ---- REF experts (the reference's uint8 codes, bf16 absmax per block_size
